@@ -1,0 +1,172 @@
+/*
+ * xtu_moe_amd.h -- C ABI of the MI355X (gfx950) quantized MoE expert path.
+ *
+ * Plain pointers (device addresses as integers on the Python side), sizes and
+ * a hipStream_t; every entry point returns a hipError_t (0 = success,
+ * hipErrorInvalidValue = 1 for rejected arguments, otherwise the launch
+ * status from hipPeekAtLastError; execution errors surface at the next
+ * synchronisation).  The caller owns all buffers.  Entry points never
+ * allocate and never synchronise, so they may be recorded into a HIP graph.
+ *
+ * Weight formats (fmt): 0 BF16, 1 FP8 e4m3 + 128x128 fp32 block scales,
+ * 2 MXFP4 (e2m1 + e8m0 per 32 k), 3 NVFP4 (e2m1 + e4m3 per 16 k + fp32
+ * per-expert global scale).  Weights are in the P16 panel layout: per
+ * expert, a [N][K] matrix is stored as
+ * [N/16][K/SB][4][16][16 B] with SB = 128 (fp4), 64 (fp8), 32 (bf16) k per
+ * super-block; fp4 scales as [N/16][K/128][4][16] (MXFP4, 1 B) or
+ * [N/16][K/128][4][16][2] (NVFP4); fp8 block scales as [N/128][K/128] fp32.
+ * w13 rows [0, I) are the gate projection, [I, 2I) the up projection.
+ *
+ * Citations are to the reference (yeungtuzi/vllm-xtu-moe) interface each
+ * entry point replaces.
+ */
+#ifndef XTU_MOE_AMD_H
+#define XTU_MOE_AMD_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- library */
+const char* xtu_version(void);
+const char* xtu_error_string(int err);
+
+/* ---------------------------------------------------------------- routing
+ * Replaces the router the hook obtains from vLLM's router factory
+ * (vllm_xiaotu_moe/mixed_experts.py:991-1078 _get_router/_select_topk;
+ * hybrid_model.py:1877 fused_topk_bias).  One wave per token; ties broken
+ * toward the lower expert index.  logits [T][E] fp32; outputs [T][K].
+ *   softmax:  w = exp(l - lmax) / sum over the K chosen (renormalize=1)
+ *   grouped:  s = sigmoid(l), selection by s + bias, group score = sum of the
+ *             two best in the group, topk_group groups kept, then
+ *             w = s / sum(s of chosen) * routed_scaling (renormalize=1). */
+hipError_t xtu_route_softmax_topk(const float* logits, int T, int E, int K, int renormalize,
+                                  int32_t* topk_ids, float* topk_weights, hipStream_t stream);
+hipError_t xtu_route_grouped_sigmoid(const float* logits, const float* bias, int T, int E,
+                                     int n_group, int topk_group, int K, float routed_scaling,
+                                     int renormalize, int32_t* topk_ids, float* topk_weights,
+                                     hipStream_t stream);
+
+/* ----------------------------------------------------------- segmentation
+ * Replaces _build_segmentation / _build_segmentation_reuse
+ * (vllm_xiaotu_moe/gpu_prefill.py:800-887) and moe4_smallm._segmentation
+ * (vllm_xiaotu_moe/moe4_smallm.py:97-129).  Flat pairs a = t*K + k, then the
+ * shared-expert pairs a = T*K + t*n_shared + s (bucket E + s, weight 1).
+ * Invalid ids (< 0 or >= E) -- and zero weights when drop_zero -- go to the
+ * trash bucket E + n_shared.  Stable order by bucket.  id_map (nullable,
+ * int32 [E]) translates ids before bucketing (pool slots / ring order).
+ * Outputs (device): sorted_pair/sorted_tok/sorted_wts/inv [A];
+ * seg_start [NB+1] (NB = E + n_shared + 1); active [NB] + n_active[1] (the
+ * non-empty non-trash buckets, ascending); tile_expert/tile_row0
+ * [xtu_segment_max_tiles] + n_tiles[1] (bm-row tiles per bucket);
+ * expert_tile_start [NB+1] (first tile of each bucket).
+ * workspace: xtu_segment_workspace_bytes(T, K, E, n_shared) bytes. */
+size_t xtu_segment_workspace_bytes(int T, int K, int E, int n_shared);
+int xtu_segment_max_tiles(int T, int K, int E, int n_shared, int bm);
+hipError_t xtu_segment(const int32_t* topk_ids, const float* topk_weights, const int32_t* id_map,
+                       int T, int K, int E, int n_shared, int drop_zero, int bm, void* workspace,
+                       int32_t* sorted_pair, int32_t* sorted_tok, float* sorted_wts, int32_t* inv,
+                       int32_t* seg_start, int32_t* active, int32_t* n_active,
+                       int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
+                       int32_t* expert_tile_start, hipStream_t stream);
+
+/* --------------------------------------------------- skinny-M (decode) path
+ * Replaces moe4_smallm_gu2 / moe4_smallm_dn2 (xiaotu_moe/csrc/moe4_smallm.cu:
+ * 395-430) and the FP8 pair kernels _gate_up_pairs_kernel / _act_pairs_kernel
+ * / _down_pairs_kernel (vllm_xiaotu_moe/decode_moe_fp8.py:23-101).  At most 16
+ * pairs per expert (callers route T <= 16 here).  One workgroup per (weight
+ * panel group, active expert); slots beyond *n_active exit at once.
+ * gate_up writes act bf16 [A][I] = SwiGLU-clamp(x W_gate^T, x W_up^T) per
+ * sorted pair row; down writes y fp32 [A][H].  w/s_estride: bytes between
+ * experts (0 = dense); slot_map (nullable): expert -> weight slot. */
+hipError_t xtu_decode_gate_up(int fmt, const void* x, int H, int I, const void* w13,
+                              const void* s13, const float* gs13, long w_estride, long s_estride,
+                              const int32_t* slot_map, const int32_t* sorted_tok,
+                              const int32_t* seg_start, const int32_t* active,
+                              const int32_t* n_active, int max_active, void* act, float limit,
+                              float alpha, float beta, hipStream_t stream);
+hipError_t xtu_decode_down(int fmt, const void* act, int H, int I, const void* w2, const void* s2,
+                           const float* gs2, long w_estride, long s_estride,
+                           const int32_t* slot_map, const int32_t* seg_start,
+                           const int32_t* active, const int32_t* n_active, int max_active,
+                           float* y, hipStream_t stream);
+
+/* ------------------------------------------------ grouped GEMM (prefill) path
+ * Replaces _gate_up_kernel / _down_kernel (vllm_xiaotu_moe/gpu_prefill.py:
+ * 232-390) and gate_up_kernel_fp8 / down_kernel_fp8
+ * (vllm_xiaotu_moe/gpu_prefill_fp8.py:101-205) plus the bmm FP8 path
+ * (gpu_prefill_fp8.py:1172).  M tiles of xtu_gemm_tile_m(fmt) rows from the
+ * segmentation tile list, range [*tile_lo, *tile_hi) (device pointers, e.g.
+ * expert_tile_start + e0 / + e1); max_tiles bounds the grid.
+ * Requires H % 256 == 0, I % 128 == 0. */
+int xtu_gemm_tile_m(int fmt);
+hipError_t xtu_gemm_gate_up(int fmt, const void* x, const int32_t* sorted_tok, int H, int I,
+                            const void* w13, const void* s13, const float* gs13, long w_estride,
+                            long s_estride, const int32_t* slot_map, const int32_t* seg_start,
+                            const int32_t* tile_expert, const int32_t* tile_row0,
+                            const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                            void* act, float limit, float alpha, float beta, hipStream_t stream);
+hipError_t xtu_gemm_down(int fmt, const void* act, int H, int I, const void* w2, const void* s2,
+                         const float* gs2, long w_estride, long s_estride,
+                         const int32_t* slot_map, const int32_t* seg_start,
+                         const int32_t* tile_expert, const int32_t* tile_row0,
+                         const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles, float* y,
+                         hipStream_t stream);
+
+/* Weighted unpermute.  Replaces the atomic_add epilogue of _down_kernel
+ * (gpu_prefill.py:380-385) and the per-token ordered sum of MOE_V2::forward_many
+ * (xiaotu_moe/csrc/moe/moe_v2.hpp:920-930): out[t] = sum_k w[t,k] * y[inv[t*K+k]]
+ * in k order over pairs whose sorted position is below *trash_start (the
+ * segmentation's seg_start[E + n_shared]) and whose weight is non-zero, plus
+ * the shared rows.  out is bf16 (out_bf16 = 1) or fp32 [T][H]. */
+hipError_t xtu_combine(const float* y, const int32_t* inv, const float* topk_weights,
+                       const int32_t* trash_start, int T, int K, int n_shared, int H, void* out,
+                       int out_bf16, hipStream_t stream);
+
+/* -------------------------------------- INT8-activation x FP4-code (ALIGN) path
+ * Replaces the engine's ALIGN integer path (xiaotu_moe/csrc/moe/
+ * moe_v2_packed4_w4a8.inc:478-586 xiaotu_predecode_block, :661-715
+ * xiaotu_quant_row_align_into, :811-858 xiaotu_i8_align_tile).
+ * xtu_i8_prepare expands MXFP4 weights (P16) of E experts into shifted int8
+ * w8' (P16 with 16 int8 per chunk, N*K bytes per expert) and emin [E][N];
+ * *dmax (zero on entry) receives the largest shift (the path needs <= 3).
+ * xtu_i8_quant_rows: per-row power-of-two int8 quantisation of bf16 rows.
+ * The GEMMs accumulate in int32 (optionally stored to acc_out [A][N]) and
+ * apply 2^(emin-128+crow) in fp32; epilogues as the bf16 GEMMs. */
+size_t xtu_i8_weight_bytes(int N, int K);
+hipError_t xtu_i8_prepare(const void* w, const void* s, int E, int N, int K, void* w8, void* emin,
+                          int32_t* dmax, hipStream_t stream);
+hipError_t xtu_i8_quant_rows(const void* rows_bf16, int M, int K, int8_t* a8, int32_t* crow,
+                             hipStream_t stream);
+hipError_t xtu_i8_gemm_gate_up(const int8_t* a8, const int32_t* crow, const int32_t* sorted_tok,
+                               int H, int I, const void* w8, const void* emin,
+                               const int32_t* slot_map, const int32_t* seg_start,
+                               const int32_t* tile_expert, const int32_t* tile_row0,
+                               const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                               void* act, int32_t* acc_out, float limit, float alpha, float beta,
+                               hipStream_t stream);
+hipError_t xtu_i8_gemm_down(const int8_t* a8, const int32_t* crow, int H, int I, const void* w8,
+                            const void* emin, const int32_t* slot_map, const int32_t* seg_start,
+                            const int32_t* tile_expert, const int32_t* tile_row0,
+                            const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                            float* y, int32_t* acc_out, hipStream_t stream);
+
+/* -------------------------------------------------------------- probes
+ * No reference counterpart: in-bounds checks of the device builtins this
+ * library relies on (scaled fp4/fp8 converters, MFMA lane layouts, the
+ * fixed-sequence exp/sigmoid), compared with host expectations by tests. */
+hipError_t xtu_probe_fp4(const float* scales, int nscale, uint32_t* out, hipStream_t stream);
+hipError_t xtu_probe_fp4_mul(const float* scales, int nscale, uint32_t* out, hipStream_t stream);
+hipError_t xtu_probe_fp8(uint32_t* out, hipStream_t stream);
+hipError_t xtu_probe_mfma(int which, const void* A, const void* B, void* C, hipStream_t stream);
+hipError_t xtu_probe_exp(const float* x, int n, float* e, float* s, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XTU_MOE_AMD_H */

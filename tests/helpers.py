@@ -1,0 +1,77 @@
+"""Shared test helpers: seeded synthetic layers and the parity tolerance."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle
+from xtu_moe_amd import formats as F
+
+# bf16 layer outputs vs the dequantized-fp32 oracle
+MAX_ABS = 2e-2
+REL_L2 = 5e-3
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def check_close(out, ref, *, bf16_out: bool, what: str = ""):
+    """fp32 outputs: max-abs <= 2e-2 and rel-L2 <= 5e-3.  bf16 outputs: the same
+    rel-L2, and max-abs <= 2e-2 plus half a bf16 ulp of the reference value
+    (the final rounding of the output itself)."""
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(out - ref)
+    slack = np.abs(ref) * 2.0 ** -8 if bf16_out else 0.0
+    worst = float(np.max(err - slack)) if err.size else 0.0
+    r = rel_l2(out, ref)
+    assert worst <= MAX_ABS, f"{what}: max-abs excess {worst:.3e} > {MAX_ABS}"
+    assert r <= REL_L2, f"{what}: rel-L2 {r:.3e} > {REL_L2}"
+    return r
+
+
+def make_dense_layer(fmt: int, E_total: int, H: int, I: int, seed: int = 0, std: float = 0.02):
+    """Dense checkpoint tensors (CPU torch) of E_total experts drawn N(0, std) and quantised."""
+    g = torch.Generator().manual_seed(seed)
+    w13 = torch.randn((E_total, 2 * I, H), generator=g) * std
+    w2 = torch.randn((E_total, H, I), generator=g) * std
+    w13q, s13, gs13 = F.quantize(fmt, w13)
+    w2q, s2, gs2 = F.quantize(fmt, w2)
+    return dict(w13=w13q, s13=s13, gs13=gs13, w2=w2q, s2=s2, gs2=gs2)
+
+
+def dense_to_numpy(fmt: int, d: dict) -> dict:
+    out = {}
+    for k, v in d.items():
+        if v is None:
+            out[k] = None
+        elif fmt == F.FMT_BF16 and k in ("w13", "w2"):
+            out[k] = v.contiguous().view(torch.int16).numpy().view(np.uint16)
+        else:
+            out[k] = v.contiguous().numpy()
+    return out
+
+
+def bf16_tensor_to_bits(x: torch.Tensor) -> np.ndarray:
+    return x.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def oracle_layer(fmt, dn: dict, x_bits, ids, wts, E, NS, H, I, limit=0.0):
+    return oracle.moe_layer(fmt, x_bits, ids, wts, E, NS, H, I, dn["w13"], dn["s13"], dn["w2"],
+                            dn["s2"], dn["gs13"], dn["gs2"], limit=limit)
+
+
+def random_routing(T, K, E, seed=0, invalid_frac=0.0, zero_frac=0.0):
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32) if T else np.zeros((0, K), np.int32)
+    wts = rng.random((T, K)).astype(np.float32) + 0.05
+    if invalid_frac > 0:
+        m = rng.random((T, K)) < invalid_frac
+        ids[m] = rng.choice([-1, E, E + 3], size=int(m.sum()))
+    if zero_frac > 0:
+        m = rng.random((T, K)) < zero_frac
+        wts[m] = 0.0
+    return ids, wts

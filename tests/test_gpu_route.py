@@ -1,0 +1,110 @@
+"""Routing and segmentation on the GPU: bit-exact against the oracle.
+
+Routing: ids, weights and their order.  Segmentation: sorted_pair / sorted_tok /
+sorted_wts / inv / seg_start / active / tile lists, including invalid ids
+(-1, >= E -> trash bucket), zero weights (kept, or dropped with drop_zero),
+shared-expert pairs and an id translation map."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import random_routing
+from xtu_moe_amd import layer as L
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu_route(logits, **kw):
+    w, i = L.route(torch.from_numpy(logits).cuda(), **kw)
+    torch.cuda.synchronize()
+    return i.cpu().numpy(), w.cpu().numpy()
+
+
+@pytest.mark.parametrize("T,E,K", [(1, 8, 2), (128, 8, 2), (4, 512, 10), (8192, 512, 10),
+                                   (33, 256, 8), (3, 64, 1)])
+def test_softmax_topk_bit_exact(T, E, K):
+    rng = np.random.default_rng(T * 7 + E)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    if T > 4:   # plant exact ties so the tie-break is exercised
+        logits[::3, 1] = logits[::3, 5]
+        logits[1::5, : E // 2] = np.round(logits[1::5, : E // 2] * 2) / 2
+    ids, wts = _gpu_route(logits, top_k=K, scoring="softmax")
+    rids, rwts = oracle.route_softmax_topk(logits, K)
+    np.testing.assert_array_equal(ids, rids)
+    np.testing.assert_array_equal(wts.view(np.uint32), rwts.view(np.uint32))
+
+
+def test_softmax_not_renormalized_bit_exact():
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((17, 64)).astype(np.float32)
+    ids, wts = _gpu_route(logits, top_k=4, scoring="softmax", renormalize=False)
+    rids, rwts = oracle.route_softmax_topk(logits, 4, renormalize=False)
+    np.testing.assert_array_equal(ids, rids)
+    np.testing.assert_array_equal(wts.view(np.uint32), rwts.view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 2, 4, 61, 8192])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_grouped_sigmoid_bit_exact(T, with_bias):
+    rng = np.random.default_rng(T + 11 * with_bias)
+    E, G, TG, K = 256, 8, 4, 8
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32) if with_bias else None
+    ids, wts = _gpu_route(logits, top_k=K, scoring="sigmoid", n_group=G, topk_group=TG,
+                          routed_scaling_factor=2.5,
+                          bias=None if bias is None else torch.from_numpy(bias).cuda())
+    rids, rwts = oracle.route_grouped_sigmoid(logits, bias, G, TG, K, 2.5)
+    np.testing.assert_array_equal(ids, rids)
+    np.testing.assert_array_equal(wts.view(np.uint32), rwts.view(np.uint32))
+
+
+def _gpu_segment(ids, wts, E, NS, drop_zero, id_map=None, bm=128):
+    T, K = ids.shape
+    seg = L.segmentation(T, K, E, NS, bm, torch.device("cuda"))
+    idm = None if id_map is None else torch.from_numpy(id_map).cuda()
+    seg.run(torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(), idm, drop_zero)
+    torch.cuda.synchronize()
+    return seg
+
+
+@pytest.mark.parametrize("T,K,E,NS", [(1, 8, 256, 1), (4, 8, 256, 1), (128, 2, 8, 0),
+                                      (8192, 8, 256, 1), (8192, 10, 512, 1), (5000, 3, 40, 2),
+                                      (0, 4, 16, 1)])
+@pytest.mark.parametrize("drop_zero", [False, True])
+def test_segmentation_bit_exact(T, K, E, NS, drop_zero):
+    ids, wts = random_routing(T, K, E, seed=T + K, invalid_frac=0.05, zero_frac=0.05)
+    seg = _gpu_segment(ids, wts, E, NS, drop_zero)
+    ref = oracle.segment(ids, wts, E, NS, drop_zero)
+    A = seg.A
+    np.testing.assert_array_equal(seg.seg_start.cpu().numpy(), ref["seg_start"])
+    for k in ("sorted_pair", "sorted_tok", "inv"):
+        np.testing.assert_array_equal(getattr(seg, k).cpu().numpy()[:A], ref[k])
+    np.testing.assert_array_equal(seg.sorted_wts.cpu().numpy()[:A].view(np.uint32),
+                                  ref["sorted_wts"].view(np.uint32))
+    counts = np.diff(ref["seg_start"])[: E + NS]
+    nz = np.nonzero(counts)[0]
+    assert int(seg.n_active.item()) == len(nz)
+    np.testing.assert_array_equal(seg.active.cpu().numpy()[: len(nz)], nz)
+    # tile list: bm-row tiles of every non-trash bucket, in bucket order
+    tiles = [(e, ref["seg_start"][e] + j * 128) for e in range(E + NS)
+             for j in range((counts[e] + 127) // 128)]
+    assert int(seg.n_tiles.item()) == len(tiles)
+    if tiles:
+        np.testing.assert_array_equal(seg.tile_expert.cpu().numpy()[: len(tiles)], [t[0] for t in tiles])
+        np.testing.assert_array_equal(seg.tile_row0.cpu().numpy()[: len(tiles)], [t[1] for t in tiles])
+    ets = np.concatenate([[0], np.cumsum((counts + 127) // 128)])
+    np.testing.assert_array_equal(seg.expert_tile_start.cpu().numpy()[: E + NS + 1], ets)
+
+
+def test_segmentation_id_map():
+    T, K, E = 300, 4, 32
+    ids, wts = random_routing(T, K, E, seed=9, invalid_frac=0.02)
+    rng = np.random.default_rng(1)
+    id_map = rng.permutation(E).astype(np.int32)
+    id_map[3] = -1     # an expert mapped away -> trash
+    seg = _gpu_segment(ids, wts, E, 0, True, id_map=id_map)
+    mapped = np.where((ids >= 0) & (ids < E), id_map[np.clip(ids, 0, E - 1)], ids).astype(np.int32)
+    ref = oracle.segment(mapped, wts, E, 0, True)
+    np.testing.assert_array_equal(seg.seg_start.cpu().numpy(), ref["seg_start"])
+    np.testing.assert_array_equal(seg.sorted_pair.cpu().numpy()[: seg.A], ref["sorted_pair"])

@@ -1,0 +1,383 @@
+// INT8-activation x FP4-code expert path (ALIGN rule), exact int32 accumulation.
+//
+//   activation row a (fp32 of bf16): m = max|a|, crow = ceil(log2(m/127)) from
+//     the exponent field, a8 = clamp(rne(a * 2^-crow), +-127)
+//   weight row n of MXFP4: w4 = 2*e2m1 in {0,+-1,+-2,+-3,+-4,+-6,+-8,+-12},
+//     emin_n = min over the row's e8m0 bytes b, w8' = w4 << (b - emin_n)
+//     (requires b - emin_n <= 3 so |w8'| <= 96 fits int8)
+//   ACC = sum_k a8 * w8'  (int32, exact; |ACC| <= 127*96*K)
+//   C   = float(ACC) * 2^(emin_n - 128 + crow)
+//
+// The shifted int8 weights are expanded once per layer (xtu_i8_prepare) into
+// the P16 panel layout with 16 int8 per chunk, next to a per-row emin; the
+// GEMM then runs v_mfma_i32_32x32x32_i8 on LDS tiles with the same tile list
+// and epilogues as the bf16 grouped GEMM.
+#include "weight_format.hpp"
+
+namespace xtu {
+namespace {
+
+constexpr int kBK = 64;
+constexpr int kBN = 256;
+constexpr int kLDB = kBK + 16;   // LDS pitch in bytes
+
+__device__ __forceinline__ int w4_of(uint32_t nib) {
+  const int m = nib & 7;
+  const int mag = m < 4 ? m : ((4 + (m & 1) * 2) << ((m >> 1) & 1));
+  return (nib & 8) ? -mag : mag;
+}
+
+// per row n: emin = min over its K/32 e8m0 scale bytes (packed P16 scale layout)
+__global__ __launch_bounds__(256) void i8_emin_kernel(const uint8_t* __restrict__ s, int N, int K,
+                                                      long s_estride, uint8_t* __restrict__ emin,
+                                                      int32_t* __restrict__ dmax) {
+  const int e = blockIdx.y;
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  const int p = n / 16, r = n % 16;
+  const long nsbk = K / 128;
+  const uint8_t* se = s + (long)e * s_estride;
+  int mn = 255, mx = 0;
+  for (long sb = 0; sb < nsbk; ++sb)
+    for (int q = 0; q < 4; ++q) {
+      const int b = se[((long)p * nsbk + sb) * 64 + q * 16 + r];
+      mn = min(mn, b);
+      mx = max(mx, b);
+    }
+  emin[(long)e * N + n] = (uint8_t)mn;
+  atomicMax(dmax, mx - mn);
+}
+
+// one thread per fp4 chunk: 32 codes -> 32 int8 w8' in two int8 chunks
+__global__ __launch_bounds__(256) void i8_expand_kernel(const uint8_t* __restrict__ w,
+                                                        const uint8_t* __restrict__ s, int N, int K,
+                                                        long w_estride, long s_estride,
+                                                        const uint8_t* __restrict__ emin,
+                                                        uint8_t* __restrict__ w8, long w8_estride) {
+  const int e = blockIdx.y;
+  const long c = (long)blockIdx.x * 256 + threadIdx.x;   // chunk index inside the expert
+  const long nchunks = (long)N * K / 32;
+  if (c >= nchunks) return;
+  const long nsb4 = K / 128, nsb8 = K / 64;
+  // fp4 layout: [p][sb4][q4][r] chunks
+  const long p = c / (nsb4 * 64);
+  const long rem = c % (nsb4 * 64);
+  const long sb4 = rem / 64;
+  const int q4 = (int)(rem % 64) / 16, r = (int)(rem % 16);
+  const int n = (int)(p * 16 + r);
+  const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(w + (long)e * w_estride + c * 16);
+  const int b = s[(long)e * s_estride + (p * nsb4 + sb4) * 64 + q4 * 16 + r];
+  const int d = b - emin[(long)e * N + n];
+  const int k0 = (int)(sb4 * 128 + q4 * 32);
+  uint32_t outw[8];
+#pragma unroll
+  for (int dw = 0; dw < 4; ++dw) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      const uint32_t byte = (raw[dw] >> (8 * bb)) & 0xffu;
+      const uint32_t v0 = (uint32_t)(w4_of(byte & 15u) * (1 << d)) & 0xffu;
+      const uint32_t v1 = (uint32_t)(w4_of(byte >> 4) * (1 << d)) & 0xffu;
+      const int j = bb * 2;   // k offset inside this dword's 8 values
+      if (j < 4) lo |= (v0 << (8 * j)) | (v1 << (8 * (j + 1)));
+      else hi |= (v0 << (8 * (j - 4))) | (v1 << (8 * (j - 3)));
+    }
+    outw[dw * 2] = lo;
+    outw[dw * 2 + 1] = hi;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int kk = k0 + 16 * h;
+    const long sb8 = kk / 64;
+    const int q8 = (kk % 64) / 16;
+    uint8_t* dst = w8 + (long)e * w8_estride + ((p * nsb8 + sb8) * 1024) + (q8 * 16 + r) * 16;
+    u32x4_t v = {outw[4 * h], outw[4 * h + 1], outw[4 * h + 2], outw[4 * h + 3]};
+    *reinterpret_cast<u32x4_t*>(dst) = v;
+  }
+}
+
+// one wave per row: crow and a8 of a bf16 row of length K (K % 512 == 0 not
+// required; K % 8 == 0)
+__global__ __launch_bounds__(256) void i8_quant_rows_kernel(const uint16_t* __restrict__ src,
+                                                            int M, int K, int8_t* __restrict__ a8,
+                                                            int32_t* __restrict__ crow) {
+  const int row = blockIdx.x * 4 + threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  if (row >= M) return;
+  const uint16_t* s = src + (long)row * K;
+  float m = 0.f;
+  for (int k = lane * 8; k < K; k += 512) {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(s + k);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m = fmaxf(m, fabsf(__uint_as_float(v[i] << 16)));
+      m = fmaxf(m, fabsf(__uint_as_float(v[i] & 0xffff0000u)));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  int c = 0;
+  if (m > 0.f) {
+    const uint32_t b = __float_as_uint(m);
+    const int ef = (int)((b >> 23) & 0xffu);
+    if (ef == 0xff) c = 120;
+    else if (ef == 0) c = -120;
+    else c = (ef - 127) - 6 + (((b & 0x7fffffu) > 8257536u) ? 1 : 0);
+    c = max(-120, min(120, c));
+  }
+  const float inv = __uint_as_float((uint32_t)(127 - c) << 23);
+  for (int k = lane * 8; k < K; k += 512) {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(s + k);
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float f0 = __uint_as_float(v[i] << 16), f1 = __uint_as_float(v[i] & 0xffff0000u);
+      const int q0 = (int)fminf(fmaxf(__builtin_rintf(f0 * inv), -127.f), 127.f);
+      const int q1 = (int)fminf(fmaxf(__builtin_rintf(f1 * inv), -127.f), 127.f);
+      const uint32_t pr = ((uint32_t)q0 & 0xffu) | (((uint32_t)q1 & 0xffu) << 8);
+      packed[i / 2] |= pr << (16 * (i % 2));
+    }
+    *reinterpret_cast<uint2*>(a8 + (long)row * K + k) = make_uint2(packed[0], packed[1]);
+  }
+  if (lane == 0) crow[row] = c;
+}
+
+struct I8GemmArgs {
+  const int8_t* a;            // gate/up: a8 of hidden rows [T][K]; down: a8 of act rows [A][K]
+  const int32_t* crow;        // per A row (token for gate/up, pair row for down)
+  const int32_t* sorted_tok;
+  const uint8_t* w8;          // expanded weights (P16, 16 int8 per chunk)
+  const uint8_t* emin;        // [E][N]
+  const int32_t* seg_start;
+  const int32_t* tile_expert;
+  const int32_t* tile_row0;
+  const int32_t* tile_lo;     // m-tile range [*tile_lo, *tile_hi) of the tile list
+  const int32_t* tile_hi;
+  const int32_t* slot_map;    // expert -> weight slot (null: identity)
+  void* out;
+  int32_t* acc_out;           // optional raw int32 accumulators [A][N] (tests)
+  int H, I;
+  long w_estride;
+  float limit, alpha, beta;
+};
+
+template <int BM, bool GU>
+__global__ __launch_bounds__(256) void i8_gemm_kernel(I8GemmArgs a) {
+  constexpr int MT = BM / 32;
+  constexpr int A_CH = BM * kBK / 16 / 256;   // 16-byte A chunks per thread
+  constexpr int CPP = (kBK / 16) * 16;        // B chunks per panel per K step
+  constexpr int B_CH = 16 * CPP / 256;
+  __shared__ __attribute__((aligned(16))) int8_t As[BM * kLDB];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[kBN * kLDB];
+
+  const int tile = a.tile_lo[0] + blockIdx.x;
+  if (tile >= a.tile_hi[0]) return;
+  const int e = a.tile_expert[tile];
+  const int ws = a.slot_map ? a.slot_map[e] : e;
+  const int row0 = a.tile_row0[tile];
+  const int rows = min(BM, a.seg_start[e + 1] - row0);
+  const int nb = blockIdx.y;
+  const int K = GU ? a.H : a.I;
+  const int N = GU ? 2 * a.I : a.H;
+  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
+  const long nsbk = K / 64;
+  const uint8_t* wexp = a.w8 + (long)ws * a.w_estride;
+
+  const int8_t* asrc[A_CH];
+#pragma unroll
+  for (int i = 0; i < A_CH; ++i) {
+    const int c = i * 256 + tid, r = c / 4;
+    if (r < rows) {
+      const long src = GU ? (long)a.sorted_tok[row0 + r] : (long)(row0 + r);
+      asrc[i] = a.a + src * K + (c % 4) * 16;
+    } else {
+      asrc[i] = nullptr;
+    }
+  }
+  long bpanel[B_CH];
+  int boff[B_CH];
+#pragma unroll
+  for (int i = 0; i < B_CH; ++i) {
+    const int c = i * 256 + tid, pl = c / CPP;
+    boff[i] = c % CPP;
+    if (GU) bpanel[i] = pl < 8 ? (long)nb * 8 + pl : (long)(a.I / 16) + nb * 8 + (pl - 8);
+    else bpanel[i] = (long)nb * 16 + pl;
+  }
+  u32x4_t areg[A_CH], breg[B_CH];
+  auto gload = [&](int kk) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (asrc[i]) v = *reinterpret_cast<const u32x4_t*>(asrc[i] + kk);
+      areg[i] = v;
+    }
+    const long sb = kk / 64;
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i)
+      breg[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(wexp + (bpanel[i] * nsbk + sb) * 1024 + boff[i] * 16));
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int c = i * 256 + tid;
+      *reinterpret_cast<u32x4_t*>(&As[(c / 4) * kLDB + (c % 4) * 16]) = areg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) {
+      const int c = i * 256 + tid, pl = c / CPP;
+      const int r = boff[i] % 16, qr = boff[i] / 16;
+      *reinterpret_cast<u32x4_t*>(&Bs[(pl * 16 + r) * kLDB + qr * 16]) = breg[i];
+    }
+  };
+  const int jt0 = GU ? 32 * w : 64 * w;
+  const int jt1 = GU ? 128 + 32 * w : 64 * w + 32;
+  i32x16_t acc[MT][2];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[m][n][i] = 0;
+
+  const int nk = K / kBK;
+  gload(0);
+  for (int kt = 0; kt < nk; ++kt) {
+    __syncthreads();
+    lstore();
+    __syncthreads();
+    if (kt + 1 < nk) gload((kt + 1) * kBK);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 32; ++ks) {
+      const int kofs = ks * 32 + (lane / 32) * 16;
+      const i32x4_t b0 = *reinterpret_cast<const i32x4_t*>(&Bs[(jt0 + lane % 32) * kLDB + kofs]);
+      const i32x4_t b1 = *reinterpret_cast<const i32x4_t*>(&Bs[(jt1 + lane % 32) * kLDB + kofs]);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const i32x4_t av = *reinterpret_cast<const i32x4_t*>(&As[(m * 32 + lane % 32) * kLDB + kofs]);
+        acc[m][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, acc[m][0], 0, 0, 0);
+        acc[m][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, acc[m][1], 0, 0, 0);
+      }
+    }
+  }
+
+  const int ncol = lane % 32;
+  long gcol0, gcol1;   // global weight rows of the two column tiles
+  if (GU) {
+    gcol0 = (long)nb * 128 + 32 * w + ncol;
+    gcol1 = (long)a.I + nb * 128 + 32 * w + ncol;
+  } else {
+    gcol0 = (long)nb * 256 + jt0 + ncol;
+    gcol1 = (long)nb * 256 + jt1 + ncol;
+  }
+  const int em0 = a.emin[(long)ws * N + gcol0];
+  const int em1 = a.emin[(long)ws * N + gcol1];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = m * 32 + (i / 4) * 8 + (lane / 32) * 4 + (i % 4);
+      if (r < rows) {
+        const long prow = row0 + r;
+        const int cr = a.crow[GU ? (long)a.sorted_tok[prow] : prow];
+        const float sc0 = ldexpf(1.0f, em0 - 128 + cr);
+        const float sc1 = ldexpf(1.0f, em1 - 128 + cr);
+        const float c0 = (float)acc[m][0][i] * sc0;
+        const float c1 = (float)acc[m][1][i] * sc1;
+        if (a.acc_out) {
+          a.acc_out[prow * N + gcol0] = acc[m][0][i];
+          a.acc_out[prow * N + gcol1] = acc[m][1][i];
+        }
+        if (GU) {
+          uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
+          act[prow * a.I + gcol0] = f32_to_bf16(silu_gate(c0, c1, a.limit, a.alpha, a.beta));
+        } else {
+          float* y = reinterpret_cast<float*>(a.out);
+          y[prow * a.H + gcol0] = c0;
+          y[prow * a.H + gcol1] = c1;
+        }
+      }
+    }
+}
+
+}  // namespace
+}  // namespace xtu
+
+using namespace xtu;
+
+extern "C" {
+
+size_t xtu_i8_weight_bytes(int N, int K) { return (size_t)N * (size_t)K; }
+
+hipError_t xtu_i8_prepare(const void* w, const void* s, int E, int N, int K, void* w8,
+                          void* emin, int32_t* dmax, hipStream_t stream) {
+  // dmax must hold 0 on entry; it receives the largest b - emin over all rows
+  XTU_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0);
+  XTU_CHECK_ARG(w && s && w8 && emin && dmax);
+  (void)hipGetLastError();
+  const long w_es = (long)N * K / 2, s_es = (long)N * K / 32, w8_es = (long)N * K;
+  i8_emin_kernel<<<dim3((N + 255) / 256, E), 256, 0, stream>>>((const uint8_t*)s, N, K, s_es,
+                                                               (uint8_t*)emin, dmax);
+  const long nch = (long)N * K / 32;
+  i8_expand_kernel<<<dim3((unsigned)((nch + 255) / 256), E), 256, 0, stream>>>(
+      (const uint8_t*)w, (const uint8_t*)s, N, K, w_es, s_es, (const uint8_t*)emin,
+      (uint8_t*)w8, w8_es);
+  return hipPeekAtLastError();
+}
+
+hipError_t xtu_i8_quant_rows(const void* rows_bf16, int M, int K, int8_t* a8, int32_t* crow,
+                             hipStream_t stream) {
+  XTU_CHECK_ARG(M >= 0 && K > 0 && K % 8 == 0);
+  if (M == 0) return hipSuccess;
+  XTU_CHECK_ARG(rows_bf16 && a8 && crow);
+  (void)hipGetLastError();
+  i8_quant_rows_kernel<<<(M + 3) / 4, 256, 0, stream>>>((const uint16_t*)rows_bf16, M, K, a8, crow);
+  return hipPeekAtLastError();
+}
+
+static hipError_t i8_gemm(bool gu, I8GemmArgs a, int max_tiles, hipStream_t stream) {
+  if (gu) {
+    a.w_estride = 2L * a.I * a.H;
+    i8_gemm_kernel<128, true><<<dim3(max_tiles, a.I / 128), 256, 0, stream>>>(a);
+  } else {
+    a.w_estride = (long)a.H * a.I;
+    i8_gemm_kernel<128, false><<<dim3(max_tiles, a.H / 256), 256, 0, stream>>>(a);
+  }
+  return hipPeekAtLastError();
+}
+
+hipError_t xtu_i8_gemm_gate_up(const int8_t* a8, const int32_t* crow, const int32_t* sorted_tok,
+                               int H, int I, const void* w8, const void* emin,
+                               const int32_t* slot_map, const int32_t* seg_start,
+                               const int32_t* tile_expert, const int32_t* tile_row0,
+                               const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                               void* act, int32_t* acc_out, float limit, float alpha, float beta,
+                               hipStream_t stream) {
+  XTU_CHECK_ARG(H > 0 && I > 0 && H % 256 == 0 && I % 128 == 0 && max_tiles >= 0);
+  XTU_CHECK_ARG(a8 && crow && sorted_tok && w8 && emin && seg_start && tile_expert && tile_row0 &&
+                tile_lo && tile_hi && act);
+  if (max_tiles == 0) return hipSuccess;
+  (void)hipGetLastError();
+  I8GemmArgs a{a8, crow, sorted_tok, (const uint8_t*)w8, (const uint8_t*)emin, seg_start,
+               tile_expert, tile_row0, tile_lo, tile_hi, slot_map, act, acc_out, H, I, 0,
+               limit, alpha, beta};
+  return i8_gemm(true, a, max_tiles, stream);
+}
+
+hipError_t xtu_i8_gemm_down(const int8_t* a8, const int32_t* crow, int H, int I, const void* w8,
+                            const void* emin, const int32_t* slot_map, const int32_t* seg_start,
+                            const int32_t* tile_expert, const int32_t* tile_row0,
+                            const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                            float* y, int32_t* acc_out, hipStream_t stream) {
+  XTU_CHECK_ARG(H > 0 && I > 0 && H % 256 == 0 && I % 128 == 0 && max_tiles >= 0);
+  XTU_CHECK_ARG(a8 && crow && w8 && emin && seg_start && tile_expert && tile_row0 && tile_lo &&
+                tile_hi && y);
+  if (max_tiles == 0) return hipSuccess;
+  (void)hipGetLastError();
+  I8GemmArgs a{a8, crow, nullptr, (const uint8_t*)w8, (const uint8_t*)emin, seg_start,
+               tile_expert, tile_row0, tile_lo, tile_hi, slot_map, y, acc_out, H, I, 0, 0.f,
+               1.f, 0.f};
+  return i8_gemm(false, a, max_tiles, stream);
+}
+
+}  // extern "C"

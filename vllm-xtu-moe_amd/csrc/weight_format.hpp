@@ -1,0 +1,91 @@
+// Per-format description of one 16-byte weight chunk in the P16 panel layout
+// and its conversion to bf16 MFMA operands (exact for every format).
+#pragma once
+
+#include "xtu_common.hpp"
+
+namespace xtu {
+
+template <int FMT>
+struct WFmt;
+
+// MXFP4: 32 e2m1 codes per chunk, one e8m0 byte per chunk.
+template <>
+struct WFmt<kMXFP4> {
+  static constexpr int kCK = 32;       // k per chunk
+  static constexpr int kWords = 16;    // bf16 pairs per chunk
+  static constexpr int kSB = 128;      // k per super-block (4 chunks)
+  static constexpr int kSPU = 1;       // super-blocks per 128-k unit
+  static __host__ __device__ constexpr long w_bytes(long N, long K) { return N * K / 2; }
+  static __host__ __device__ constexpr long s_bytes(long N, long K) { return N * K / 32; }
+};
+
+// NVFP4: 32 e2m1 codes per chunk, two e4m3 bytes (one per 16 k) per chunk,
+// plus a per-expert fp32 global scale applied to the GEMM result.
+template <>
+struct WFmt<kNVFP4> {
+  static constexpr int kCK = 32;
+  static constexpr int kWords = 16;
+  static constexpr int kSB = 128;
+  static constexpr int kSPU = 1;
+  static __host__ __device__ constexpr long w_bytes(long N, long K) { return N * K / 2; }
+  static __host__ __device__ constexpr long s_bytes(long N, long K) { return N * K / 16; }
+};
+
+// FP8 e4m3: 16 codes per chunk; one fp32 scale per 128x128 block.
+template <>
+struct WFmt<kFP8> {
+  static constexpr int kCK = 16;
+  static constexpr int kWords = 8;
+  static constexpr int kSB = 64;
+  static constexpr int kSPU = 2;
+  static __host__ __device__ constexpr long w_bytes(long N, long K) { return N * K; }
+  static __host__ __device__ constexpr long s_bytes(long N, long K) { return (N / 128) * (K / 128) * 4; }
+};
+
+// BF16: 8 values per chunk, no scale.
+template <>
+struct WFmt<kBF16> {
+  static constexpr int kCK = 8;
+  static constexpr int kWords = 4;
+  static constexpr int kSB = 32;
+  static constexpr int kSPU = 4;
+  static __host__ __device__ constexpr long w_bytes(long N, long K) { return N * K * 2; }
+  static __host__ __device__ constexpr long s_bytes(long, long) { return 0; }
+};
+
+// Decode one chunk into bf16 pair words.  `sc` points at this expert's fp4
+// scale array; `sb_index` is the (panel, super-block) index; `lane` = 16q+r.
+template <int FMT>
+__device__ __forceinline__ void load_chunk_scale(const uint8_t* __restrict__ sc, long sb_index,
+                                                 int lane, float& s0, float& s1) {
+  if constexpr (FMT == kMXFP4) {
+    s0 = e8m0_to_f32(sc[sb_index * 64 + lane]);
+    s1 = s0;
+  } else if constexpr (FMT == kNVFP4) {
+    const uint16_t v = *reinterpret_cast<const uint16_t*>(sc + (sb_index * 64 + lane) * 2);
+    s0 = e4m3_to_f32(v & 0xffu);
+    s1 = e4m3_to_f32(v >> 8);
+  } else {
+    s0 = s1 = 1.0f;
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ void decode_chunk(const u32x4_t raw, float s0, float s1,
+                                             uint32_t* words) {
+  if constexpr (FMT == kMXFP4) {
+    fp4x32_to_bf16(raw, s0, words);
+  } else if constexpr (FMT == kNVFP4) {
+    fp4x32_to_bf16_2s(raw, s0, s1, words);
+  } else if constexpr (FMT == kFP8) {
+    fp8x16_to_bf16(raw, words);
+  } else {
+    words[0] = raw[0];
+    words[1] = raw[1];
+    words[2] = raw[2];
+    words[3] = raw[3];
+  }
+}
+
+}  // namespace xtu

@@ -1,0 +1,191 @@
+"""Expert-weight formats: quantisers for synthetic data and the P16 packing.
+
+Checkpoint ("dense") layouts follow the reference engine
+(xiaotu_moe/csrc/moe/moe_v2.hpp:454-470, moe_v2_packed4_w4a8.inc:1966-1976,
+moe_v2_fp8.hpp:1-11):
+
+* MXFP4: codes [E][N][K/2] u8 (low nibble = even k), e8m0 [E][N][K/32] u8;
+* NVFP4: codes as MXFP4, e4m3 [E][N][K/16] u8, fp32 global scale [E];
+* FP8:   e4m3 [E][N][K] u8, fp32 block scales [E][N/128][K/128];
+* BF16:  [E][N][K] bf16.
+
+The device layout is P16: per expert, [N/16][K/SB][4][16][16 bytes] where a
+16-byte chunk holds 32 fp4 codes, 16 fp8 codes or 8 bf16 values of one row,
+so a wave64 loading 16 bytes per lane reads one contiguous KiB
+(lane = 16 * chunk + row).  fp4 scales follow the same (panel, super-block,
+chunk, row) order; fp8 block scales keep their dense layout.
+
+The quantisers are the build's own (OCP MX rule for MXFP4, amax/448 blocks for
+FP8, two-level amax scaling for NVFP4); the codes they produce are the test
+and benchmark inputs, not a parity subject.
+"""
+from __future__ import annotations
+
+import torch
+
+FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4 = 0, 1, 2, 3
+FMT_NAMES = {FMT_BF16: "bf16", FMT_FP8: "fp8", FMT_MXFP4: "mxfp4", FMT_NVFP4: "nvfp4"}
+
+E2M1_VALUES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+               -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0)
+
+
+def fmt_of(name) -> int:
+    if isinstance(name, int):
+        return name
+    inv = {v: k for k, v in FMT_NAMES.items()}
+    return inv[str(name).lower()]
+
+
+# ------------------------------------------------------------------ quantisers
+def _e2m1_codes(v: torch.Tensor) -> torch.Tensor:
+    """Round-to-nearest-even onto the e2m1 grid, saturating at +-6 -> 4-bit codes."""
+    a = v.abs()
+    mag = ((a > 0.25).to(torch.uint8) + (a >= 0.75).to(torch.uint8) + (a > 1.25).to(torch.uint8)
+           + (a >= 1.75).to(torch.uint8) + (a > 2.5).to(torch.uint8) + (a >= 3.5).to(torch.uint8)
+           + (a > 5.0).to(torch.uint8))
+    sign = ((v < 0) & (mag > 0)).to(torch.uint8) << 3
+    return mag | sign
+
+
+def _pack_nibbles(codes: torch.Tensor) -> torch.Tensor:
+    return codes[..., 0::2] | (codes[..., 1::2] << 4)
+
+
+def quantize_mxfp4(w: torch.Tensor):
+    """w [..., N, K] float -> (codes [..., N, K/2] u8, e8m0 [..., N, K/32] u8)."""
+    *lead, N, K = w.shape
+    wb = w.float().reshape(*lead, N, K // 32, 32)
+    amax = wb.abs().amax(-1)
+    e = torch.floor(torch.log2(amax.clamp_min(2.0 ** -126))) - 2.0
+    e = torch.where(amax > 0, e, torch.full_like(e, -127.0)).clamp(-127.0, 127.0)
+    scale = torch.exp2(e)
+    codes = _e2m1_codes(wb / scale[..., None]).reshape(*lead, N, K)
+    return _pack_nibbles(codes).contiguous(), (e + 127.0).to(torch.uint8).contiguous()
+
+
+def quantize_nvfp4(w: torch.Tensor):
+    """w [E, N, K] -> (codes [E,N,K/2] u8, e4m3 scale bytes [E,N,K/16] u8, gs [E] fp32)."""
+    E, N, K = w.shape
+    wf = w.float()
+    amax_t = wf.abs().reshape(E, -1).amax(-1)
+    gs = (amax_t / (448.0 * 6.0)).clamp_min(1e-30)
+    wb = wf.reshape(E, N, K // 16, 16)
+    sblk = (wb.abs().amax(-1) / 6.0) / gs[:, None, None]
+    s8 = sblk.clamp(max=448.0).to(torch.float8_e4m3fn)
+    sq = s8.float() * gs[:, None, None]
+    v = torch.where(sq[..., None] > 0, wb / sq[..., None].clamp_min(1e-30), torch.zeros_like(wb))
+    codes = _e2m1_codes(v).reshape(E, N, K)
+    return _pack_nibbles(codes).contiguous(), s8.view(torch.uint8).contiguous(), gs.float().contiguous()
+
+
+def quantize_fp8_block(w: torch.Tensor):
+    """w [..., N, K] -> (e4m3 codes [..., N, K] u8, fp32 scales [..., N/128, K/128])."""
+    *lead, N, K = w.shape
+    wb = w.float().reshape(*lead, N // 128, 128, K // 128, 128)
+    amax = wb.abs().amax(dim=(-3, -1))
+    s = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    q = (wb / s[..., :, None, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.view(torch.uint8).reshape(*lead, N, K).contiguous(), s.float().contiguous()
+
+
+def quantize(fmt: int, w: torch.Tensor):
+    """Dense checkpoint tensors (w, s, gs) of `w` [E, N, K] in format `fmt`."""
+    if fmt == FMT_MXFP4:
+        c, s = quantize_mxfp4(w)
+        return c, s, None
+    if fmt == FMT_NVFP4:
+        return quantize_nvfp4(w)
+    if fmt == FMT_FP8:
+        c, s = quantize_fp8_block(w)
+        return c, s, None
+    return w.to(torch.bfloat16).contiguous(), None, None
+
+
+# ---------------------------------------------------------------- dequantisers
+def e4m3_table(device=None) -> torch.Tensor:
+    return torch.arange(256, dtype=torch.uint8, device=device).view(torch.float8_e4m3fn).float()
+
+
+def dequantize(fmt: int, w: torch.Tensor, s=None, gs=None) -> torch.Tensor:
+    """Dense checkpoint tensors -> fp32 [E, N, K] (exact)."""
+    if fmt == FMT_BF16:
+        return w.float()
+    if fmt == FMT_FP8:
+        v = w.view(torch.float8_e4m3fn).float()
+        E, N, K = v.shape
+        return (v.reshape(E, N // 128, 128, K // 128, 128) * s[:, :, None, :, None]).reshape(E, N, K)
+    lut = torch.tensor(E2M1_VALUES, dtype=torch.float32, device=w.device)
+    lo, hi = lut[(w & 15).long()], lut[(w >> 4).long()]
+    v = torch.stack([lo, hi], -1).reshape(*w.shape[:-1], w.shape[-1] * 2)
+    if fmt == FMT_MXFP4:
+        return v * torch.exp2(s.float() - 127.0).repeat_interleave(32, -1)
+    sc = e4m3_table(w.device)[s.long()] * gs[:, None, None]
+    return v * sc.repeat_interleave(16, -1)
+
+
+# ---------------------------------------------------------------------- packing
+def row_bytes(fmt: int, K: int) -> int:
+    return {FMT_BF16: 2 * K, FMT_FP8: K, FMT_MXFP4: K // 2, FMT_NVFP4: K // 2}[fmt]
+
+
+def pack_weight(fmt: int, w: torch.Tensor) -> torch.Tensor:
+    """Dense [E, N, K(packed)] -> P16 bytes [E, N*row_bytes] u8."""
+    E, N = w.shape[0], w.shape[1]
+    b = w.contiguous().view(torch.uint8).reshape(E, N, -1)
+    RB = b.shape[-1]
+    assert N % 16 == 0 and RB % 64 == 0, (N, RB)
+    p = b.reshape(E, N // 16, 16, RB // 64, 4, 16).permute(0, 1, 3, 4, 2, 5)
+    return p.contiguous().reshape(E, N * RB)
+
+
+def unpack_weight(fmt: int, p: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """P16 bytes -> dense checkpoint tensor (inverse of pack_weight)."""
+    E = p.shape[0]
+    RB = row_bytes(fmt, K)
+    d = p.reshape(E, N // 16, RB // 64, 4, 16, 16).permute(0, 1, 4, 2, 3, 5).contiguous()
+    d = d.reshape(E, N, RB)
+    return d.view(torch.bfloat16) if fmt == FMT_BF16 else d
+
+
+def pack_scales(fmt: int, s, N: int, K: int):
+    """Dense scales -> P16 scale layout (fp4) / unchanged (fp8) / None (bf16)."""
+    if s is None or fmt == FMT_BF16:
+        return None
+    E = s.shape[0]
+    if fmt == FMT_MXFP4:
+        return s.reshape(E, N // 16, 16, K // 128, 4).permute(0, 1, 3, 4, 2).contiguous().reshape(E, -1)
+    if fmt == FMT_NVFP4:
+        return (s.reshape(E, N // 16, 16, K // 128, 4, 2).permute(0, 1, 3, 4, 2, 5)
+                .contiguous().reshape(E, -1))
+    return s.float().contiguous().reshape(E, -1)
+
+
+def unpack_scales(fmt: int, p, N: int, K: int):
+    if p is None or fmt == FMT_BF16:
+        return None
+    E = p.shape[0]
+    if fmt == FMT_MXFP4:
+        return p.reshape(E, N // 16, K // 128, 4, 16).permute(0, 1, 4, 2, 3).contiguous().reshape(E, N, K // 32)
+    if fmt == FMT_NVFP4:
+        return (p.reshape(E, N // 16, K // 128, 4, 16, 2).permute(0, 1, 4, 2, 3, 5)
+                .contiguous().reshape(E, N, K // 16))
+    return p.reshape(E, N // 128, K // 128)
+
+
+def expert_bytes(fmt: int, H: int, I: int) -> int:
+    """HBM bytes of one expert (w13 + s13 + w2 + s2) in format `fmt`."""
+    w = 3 * H * I * {FMT_BF16: 2.0, FMT_FP8: 1.0, FMT_MXFP4: 0.5, FMT_NVFP4: 0.5}[fmt]
+    if fmt == FMT_MXFP4:
+        s = 3 * H * I / 32
+    elif fmt == FMT_NVFP4:
+        s = 3 * H * I / 16 + 8
+    elif fmt == FMT_FP8:
+        s = 3 * (H // 128) * (I // 128) * 4
+    else:
+        s = 0
+    return int(w + s)
+
+
+def bf16_bits(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16).contiguous().view(torch.int16)

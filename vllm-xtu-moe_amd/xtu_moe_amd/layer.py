@@ -1,0 +1,251 @@
+"""One MoE layer's routed (+ shared) experts on the gfx950 HIP library.
+
+    routing output -> segmentation -> gate/up (+ SwiGLU-clamp) -> down
+                   -> weighted unpermute (combine)
+
+The shapes follow the reference's layer entry (vllm_xiaotu_moe/gpu_prefill.py:
+2566-2780 gpu_moe_layer): x [T, H] bf16, topk_ids [T, K] int32, topk_weights
+[T, K] fp32, output [T, H] bf16 (or fp32).  Device buffers are cached per
+shape for the life of the process (as the reference does with its
+`_reuse_moe` / tile rings), so steady-state calls allocate nothing.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .formats import (FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4, pack_scales, pack_weight)
+
+DECODE_MAX_TOKENS = 16
+
+
+def _p(t) -> int:
+    return 0 if t is None else int(t.data_ptr())
+
+
+def _stream(stream=None) -> int:
+    if stream is None:
+        return int(torch.cuda.current_stream().cuda_stream)
+    return int(stream.cuda_stream) if hasattr(stream, "cuda_stream") else int(stream)
+
+
+class ExpertWeights:
+    """Resident weights of one layer in the P16 panel layout.
+
+    Experts [0, E) are routed; [E, E + n_shared) are shared experts that every
+    token uses with weight 1.  Tensors: w13/w2 u8 [E+NS, bytes], s13/s2 (u8
+    P16 scales for fp4, fp32 block scales for fp8, None for bf16), gs13/gs2
+    fp32 [E+NS] (NVFP4 global scales) or None.
+    """
+
+    def __init__(self, fmt, H, I, E, n_shared, w13, s13, w2, s2, gs13=None, gs2=None):
+        self.fmt, self.H, self.I, self.E, self.n_shared = int(fmt), int(H), int(I), int(E), int(n_shared)
+        self.w13, self.s13, self.w2, self.s2, self.gs13, self.gs2 = w13, s13, w2, s2, gs13, gs2
+        self._i8 = None
+        if self.H % 256 or self.I % 128:
+            raise ValueError(f"unsupported shape H={H} I={I} (need H % 256 == 0, I % 128 == 0)")
+
+    @property
+    def n_experts(self) -> int:
+        return self.E + self.n_shared
+
+    @property
+    def device(self):
+        return self.w13.device
+
+    @classmethod
+    def from_dense(cls, fmt, w13, s13, w2, s2, gs13=None, gs2=None, *, E=None, n_shared=0,
+                   device=None):
+        """Pack dense checkpoint tensors (experts [0,E) routed, the rest shared)."""
+        fmt = int(fmt)
+        Et = w13.shape[0]
+        N13 = w13.shape[1]
+        I = N13 // 2
+        H = w2.shape[1]
+        dev = torch.device(device) if device is not None else w13.device
+
+        def mv(t):
+            return None if t is None else t.to(dev).contiguous()
+
+        w13p = pack_weight(fmt, mv(w13))
+        w2p = pack_weight(fmt, mv(w2))
+        s13p = pack_scales(fmt, mv(s13), 2 * I, H)
+        s2p = pack_scales(fmt, mv(s2), H, I)
+        E = Et - n_shared if E is None else E
+        return cls(fmt, H, I, E, n_shared, w13p, s13p, w2p, s2p, mv(gs13), mv(gs2))
+
+    # ---------------------------------------------------------------- INT8
+    def int8_planes(self):
+        """Shifted int8 weights + per-row emin for the INT8 ALIGN path (MXFP4 only)."""
+        if self._i8 is not None:
+            return self._i8
+        if self.fmt != FMT_MXFP4:
+            raise ValueError("the INT8-activation path needs MXFP4 (e8m0) weights")
+        n = self.n_experts
+        dev = self.device
+        out = []
+        st = _stream()
+        dmax = torch.zeros(1, dtype=torch.int32, device=dev)
+        for (w, s, N, K) in ((self.w13, self.s13, 2 * self.I, self.H), (self.w2, self.s2, self.H, self.I)):
+            w8 = torch.empty((n, N * K), dtype=torch.uint8, device=dev)
+            emin = torch.empty((n, N), dtype=torch.uint8, device=dev)
+            _lib.call("xtu_i8_prepare", _p(w), _p(s), n, N, K, _p(w8), _p(emin), _p(dmax), st)
+            out += [w8, emin]
+        d = int(dmax.item())
+        if d > 3:
+            raise ValueError(f"INT8 ALIGN path needs per-row e8m0 spread <= 3, got {d}")
+        self._i8 = tuple(out)
+        return self._i8
+
+
+class _Segmentation:
+    """Device buffers of one segmentation shape (process-lifetime cache)."""
+
+    def __init__(self, T, K, E, NS, bm, device):
+        self.T, self.K, self.E, self.NS, self.bm = T, K, E, NS, bm
+        A = T * K + T * NS
+        NB = E + NS + 1
+        self.A, self.NB = A, NB
+        i32 = dict(dtype=torch.int32, device=device)
+        self.ws = torch.empty(int(_lib.call("xtu_segment_workspace_bytes", T, K, E, NS)),
+                              dtype=torch.uint8, device=device)
+        Am = max(A, 1)
+        self.sorted_pair = torch.empty(Am, **i32)
+        self.sorted_tok = torch.empty(Am, **i32)
+        self.sorted_wts = torch.empty(Am, dtype=torch.float32, device=device)
+        self.inv = torch.empty(Am, **i32)
+        self.seg_start = torch.empty(NB + 1, **i32)
+        self.active = torch.empty(NB, **i32)
+        self.n_active = torch.empty(1, **i32)
+        self.max_tiles = int(_lib.call("xtu_segment_max_tiles", T, K, E, NS, bm))
+        self.tile_expert = torch.empty(self.max_tiles, **i32)
+        self.tile_row0 = torch.empty(self.max_tiles, **i32)
+        self.n_tiles = torch.empty(1, **i32)
+        self.expert_tile_start = torch.empty(NB + 1, **i32)
+
+    def run(self, ids, wts, id_map=None, drop_zero=True, stream=None):
+        _lib.call("xtu_segment", _p(ids), _p(wts), _p(id_map), self.T, self.K, self.E, self.NS,
+                  int(drop_zero), self.bm, _p(self.ws), _p(self.sorted_pair), _p(self.sorted_tok),
+                  _p(self.sorted_wts), _p(self.inv), _p(self.seg_start), _p(self.active),
+                  _p(self.n_active), _p(self.tile_expert), _p(self.tile_row0), _p(self.n_tiles),
+                  _p(self.expert_tile_start), _stream(stream))
+        return self
+
+    def tile_range_ptrs(self, b0: int, b1: int):
+        """Device pointers to expert_tile_start[b0] and [b1] (m-tile range of buckets [b0, b1))."""
+        base = _p(self.expert_tile_start)
+        return base + 4 * int(b0), base + 4 * int(b1)
+
+
+_SEG_CACHE: dict = {}
+_BUF_CACHE: dict = {}
+
+
+def segmentation(T, K, E, NS, bm, device) -> _Segmentation:
+    key = (T, K, E, NS, bm, str(device))
+    s = _SEG_CACHE.get(key)
+    if s is None:
+        s = _Segmentation(T, K, E, NS, bm, device)
+        _SEG_CACHE[key] = s
+    return s
+
+
+def _buf(name, shape, dtype, device):
+    key = (name, tuple(shape), dtype, str(device))
+    t = _BUF_CACHE.get(key)
+    if t is None:
+        t = torch.empty(shape, dtype=dtype, device=device)
+        _BUF_CACHE[key] = t
+    return t
+
+
+def route(logits, *, top_k, scoring="softmax", renormalize=True, bias=None, n_group=1,
+          topk_group=1, routed_scaling_factor=1.0, ids_out=None, wts_out=None, stream=None):
+    """Top-k routing on the GPU.  Returns (topk_weights fp32 [T,K], topk_ids int32 [T,K])."""
+    lg = logits.float().contiguous() if logits.dtype != torch.float32 or not logits.is_contiguous() else logits
+    T, E = lg.shape
+    dev = lg.device
+    ids = ids_out if ids_out is not None else torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    wts = wts_out if wts_out is not None else torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    st = _stream(stream)
+    if scoring == "softmax":
+        _lib.call("xtu_route_softmax_topk", _p(lg), T, E, top_k, int(renormalize), _p(ids), _p(wts), st)
+    elif scoring == "sigmoid":
+        b = None if bias is None else bias.float().contiguous()
+        _lib.call("xtu_route_grouped_sigmoid", _p(lg), _p(b), T, E, int(n_group), int(topk_group),
+                  top_k, float(routed_scaling_factor), int(renormalize), _p(ids), _p(wts), st)
+    else:
+        raise ValueError(f"unsupported scoring function {scoring!r}")
+    return wts, ids
+
+
+def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0, swiglu_alpha=1.0,
+                swiglu_beta=0.0, out=None, out_dtype=torch.bfloat16, path="auto", int8=False,
+                drop_zero=True, id_map=None, slot_map=None, stream=None, return_seg=False):
+    """Routed (+shared) experts of one layer; returns out [T, H].
+
+    path: "auto" (decode kernels for T <= 16, grouped GEMMs otherwise),
+    "decode" or "gemm".  int8: INT8-activation x FP4-code ALIGN path (MXFP4).
+    id_map: int32 [E] applied to topk_ids before bucketing; slot_map: int32
+    [E+NS] bucket -> weight slot.
+    """
+    if x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError("x must be contiguous bf16 [T, H]")
+    T, K = topk_ids.shape
+    H, I, E, NS = W.H, W.I, W.E, W.n_shared
+    if x.shape != (T, H):
+        raise ValueError(f"x shape {tuple(x.shape)} != ({T}, {H})")
+    dev = x.device
+    ids = topk_ids if (topk_ids.dtype == torch.int32 and topk_ids.is_contiguous()) else topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights if (topk_weights.dtype == torch.float32 and topk_weights.is_contiguous()) else topk_weights.float().contiguous()
+    st = _stream(stream)
+    fmt = W.fmt
+    if path == "auto":
+        path = "decode" if (T <= DECODE_MAX_TOKENS and not int8) else "gemm"
+    if path == "decode" and T > DECODE_MAX_TOKENS:
+        raise ValueError(f"decode path handles at most {DECODE_MAX_TOKENS} tokens")
+    bm = 128 if int8 else int(_lib.call("xtu_gemm_tile_m", fmt))
+    seg = segmentation(T, K, E, NS, bm, dev).run(ids, wts, id_map, drop_zero, st)
+    A = seg.A
+    odt = out_dtype if out is None else out.dtype
+    if out is None:
+        out = torch.empty((T, H), dtype=odt, device=dev)
+    if T == 0:
+        return (out, seg) if return_seg else out
+    act = _buf("act", (max(A, 1), I), torch.bfloat16, dev)
+    y = _buf("y", (max(A, 1), H), torch.float32, dev)
+    lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
+    if path == "decode":
+        max_active = min(E, T * K) + NS
+        _lib.call("xtu_decode_gate_up", fmt, _p(x), H, I, _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0,
+                  _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
+                  _p(seg.n_active), max_active, _p(act), lim, al, be, st)
+        _lib.call("xtu_decode_down", fmt, _p(act), H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
+                  _p(slot_map), _p(seg.seg_start), _p(seg.active), _p(seg.n_active), max_active,
+                  _p(y), st)
+    elif int8:
+        w13_8, emin13, w2_8, emin2 = W.int8_planes()
+        a8x = _buf("a8x", (T, H), torch.int8, dev)
+        crx = _buf("crx", (T,), torch.int32, dev)
+        a8a = _buf("a8a", (max(A, 1), I), torch.int8, dev)
+        cra = _buf("cra", (max(A, 1),), torch.int32, dev)
+        lo, hi = seg.tile_range_ptrs(0, E + NS)
+        _lib.call("xtu_i8_quant_rows", _p(x), T, H, _p(a8x), _p(crx), st)
+        _lib.call("xtu_i8_gemm_gate_up", _p(a8x), _p(crx), _p(seg.sorted_tok), H, I, _p(w13_8),
+                  _p(emin13), _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
+                  _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), 0, lim, al, be, st)
+        _lib.call("xtu_i8_quant_rows", _p(act), A, I, _p(a8a), _p(cra), st)
+        _lib.call("xtu_i8_gemm_down", _p(a8a), _p(cra), H, I, _p(w2_8), _p(emin2), _p(slot_map),
+                  _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo, hi,
+                  seg.max_tiles, _p(y), 0, st)
+    else:
+        lo, hi = seg.tile_range_ptrs(0, E + NS)
+        _lib.call("xtu_gemm_gate_up", fmt, _p(x), _p(seg.sorted_tok), H, I, _p(W.w13), _p(W.s13),
+                  _p(W.gs13), 0, 0, _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
+                  _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), lim, al, be, st)
+        _lib.call("xtu_gemm_down", fmt, _p(act), H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
+                  _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo, hi,
+                  seg.max_tiles, _p(y), st)
+    _lib.call("xtu_combine", _p(y), _p(seg.inv), _p(wts), _p(seg.seg_start) + 4 * (E + NS), T, K,
+              NS, H, _p(out), int(odt == torch.bfloat16), st)
+    return (out, seg) if return_seg else out
