@@ -1,0 +1,342 @@
+"""Benchmark of the quantized MoE expert layer on one MI355X.
+
+Default workload: DeepSeek-V3-shaped MoE layer at decode with MXFP4 experts
+(H=7168, 256 routed experts + 1 shared, I=2048, grouped-sigmoid routing with
+8 groups / top-4 groups / top-8 and routed scaling 2.5), T = 1, 2, 4 tokens.
+A step is one pass of the layer (routing from logits -> segmentation ->
+gate/up+SwiGLU -> down -> combine) over a fresh batch of synthetic tokens
+(x ~ N(0,1) bf16, logits ~ N(0,1)), weights N(0,0.02) quantised and resident in
+HBM.  Every timed step starts with the 256 MB last-level cache flushed (a
+1 GiB read-modify-write of a scratch buffer outside the timed events), so
+weights stream from HBM as they do when 61 layers take turns.
+
+The JSON line reports tokens/s at the largest T (value), the layer time, and:
+  roofline      the dominant kernel (gate/up) against HBM (decode) or MFMA
+                (prefill): algorithmic bytes or FLOPs per launch over its
+                average duration from HIP events on its stream;
+  cpu_baseline  the reference xiaotu-moe AVX-512 engine (oracle/_ref, built
+                from the reference sources) on the host cores, on a bounded
+                sample of the same workload.
+Other workloads (--workload): ds-v3-fp8-prefill, qwen3-next-int8,
+qwen3-next-nvfp4, mixtral-tiny-bf16.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "vllm-xtu-moe_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "int8": 5000.0, "fp4": 10100.0}
+
+WORKLOADS = {
+    "ds-v3-mxfp4-decode": dict(fmt="mxfp4", E=256, NS=1, H=7168, I=2048, K=8, router="grouped",
+                               Ts=[1, 2, 4], limit=0.0, int8=False, graph=True),
+    "ds-v3-fp8-prefill": dict(fmt="fp8", E=256, NS=1, H=7168, I=2048, K=8, router="grouped",
+                              Ts=[8192], limit=0.0, int8=False, graph=False),
+    "qwen3-next-int8": dict(fmt="mxfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
+                            Ts=[1, 4, 8192], limit=7.0, int8=True, graph=False),
+    "qwen3-next-nvfp4": dict(fmt="nvfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
+                             Ts=[1, 4, 8192], limit=7.0, int8=False, graph=True),
+    "mixtral-tiny-bf16": dict(fmt="bf16", E=8, NS=0, H=1024, I=2048, K=2, router="softmax",
+                              Ts=[128], limit=0.0, int8=False, graph=False),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="ds-v3-mxfp4-decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--no-flush", action="store_true", help="keep caches warm between steps")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the expert-parallel design is described in DESIGN.md); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from xtu_moe_amd import _lib
+    from xtu_moe_amd import formats as F
+    from xtu_moe_amd.layer import _p, _stream, moe_forward, route, segmentation
+    from xtu_moe_amd.synthetic import synth_layer
+
+    cfg = WORKLOADS[args.workload]
+    fmt = F.fmt_of(cfg["fmt"])
+    E, NS, H, I, K = cfg["E"], cfg["NS"], cfg["H"], cfg["I"], cfg["K"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.load()
+    t0 = time.time()
+    W = synth_layer(fmt, E, NS, H, I, seed=0, device=dev)
+    if cfg["int8"]:
+        W.int8_planes()
+    torch.cuda.synchronize()
+    log(f"[bench] built {E}+{NS} experts fmt={cfg['fmt']} in {time.time() - t0:.1f}s")
+    flush = torch.empty(256 << 20, dtype=torch.float32, device=dev)   # 1 GiB
+    gen = torch.Generator(device=dev).manual_seed(1234)
+
+    if cfg["router"] == "grouped":
+        rkw = dict(top_k=K, scoring="sigmoid", n_group=8, topk_group=4, routed_scaling_factor=2.5)
+    else:
+        rkw = dict(top_k=K, scoring="softmax")
+    router_w = None
+    if args.workload == "mixtral-tiny-bf16":
+        router_w = torch.randn((E, H), generator=gen, device=dev) * 0.02
+
+    e_bytes13 = F.expert_bytes(fmt, H, I) * (2 * I * H) // (3 * H * I)   # w13 + s13 share
+    e_bytes = F.expert_bytes(fmt, H, I)
+    nsteps = args.warmup + args.steps
+    results = {}
+    for T in cfg["Ts"]:
+        xs = [torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16) for _ in range(min(nsteps, 8))]
+        if router_w is not None:
+            lgs = [(x.float() @ router_w.t()).contiguous() for x in xs]
+        else:
+            lgs = [torch.randn((T, E), generator=gen, device=dev) for _ in range(nsteps)]
+        x_st = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+        lg_st = torch.empty((T, E), dtype=torch.float32, device=dev)
+        out_st = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+        ids_st = torch.empty((T, K), dtype=torch.int32, device=dev)
+        wts_st = torch.empty((T, K), dtype=torch.float32, device=dev)
+
+        rt = dict(logits=lg_st, scoring=rkw["scoring"], n_group=rkw.get("n_group", 1),
+                  topk_group=rkw.get("topk_group", 1),
+                  routed_scaling_factor=rkw.get("routed_scaling_factor", 1.0))
+
+        def step():
+            moe_forward(x_st, ids_st, wts_st, W, swiglu_limit=cfg["limit"], out=out_st,
+                        int8=cfg["int8"], router=rt)
+
+        def load(s):
+            x_st.copy_(xs[s % len(xs)])
+            lg_st.copy_(lgs[s % len(lgs)])
+
+        load(0)
+        step()
+        torch.cuda.synchronize()
+        use_graph = cfg["graph"] and T <= 16
+        graph = None
+        if use_graph:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(2):
+                    step()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                step()
+            torch.cuda.synchronize()
+
+        def run_layer():
+            if graph is not None:
+                graph.replay()
+            else:
+                step()
+
+        # ---- whole layer, cold cache per step
+        for s in range(args.warmup):
+            load(s)
+            run_layer()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+        n_active = []
+        wall0 = time.time()
+        for s in range(args.steps):
+            load(args.warmup + s)
+            if not args.no_flush:
+                flush.add_(1.0)
+            ev[s][0].record()
+            run_layer()
+            ev[s][1].record()
+        torch.cuda.synchronize()
+        wall = time.time() - wall0
+        layer_ms = [a.elapsed_time(b) for a, b in ev]
+        # distinct experts per step (algorithmic bytes), re-derived outside timing
+        for s in range(args.steps):
+            load(args.warmup + s)
+            w_, i_ = route(lg_st, **rkw)
+            n_active.append(len(torch.unique(i_)) + NS)
+
+        # ---- dominant kernel alone (gate/up), cold cache, same stream
+        seg = None
+        gu_ms = []
+        bm = 128 if cfg["int8"] else int(_lib.call("xtu_gemm_tile_m", fmt))
+        decode = T <= 16 and not cfg["int8"]
+        act = torch.empty((T * K + T * NS, I), dtype=torch.bfloat16, device=dev)
+        for s in range(args.steps):
+            load(args.warmup + s)
+            w_, i_ = route(lg_st, **rkw)
+            seg = segmentation(T, K, E, NS, bm, dev).run(i_, w_)
+            st = _stream()
+            if cfg["int8"]:
+                w13_8, emin13, _, _ = W.int8_planes()
+                a8x = torch.empty((T, H), dtype=torch.int8, device=dev)
+                crx = torch.empty(T, dtype=torch.int32, device=dev)
+                _lib.call("xtu_i8_quant_rows", _p(x_st), T, H, _p(a8x), _p(crx), st)
+            if not args.no_flush:
+                flush.add_(1.0)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            if decode:
+                _lib.call("xtu_decode_gate_up", fmt, _p(x_st), T, H, I, _p(W.w13), _p(W.s13),
+                          _p(W.gs13), 0, 0, 0, _p(seg.sorted_tok), _p(seg.seg_start),
+                          _p(seg.active), _p(seg.n_active), min(E, T * K) + NS, _p(act),
+                          cfg["limit"], 1.0, 0.0, st)
+            elif cfg["int8"]:
+                lo, hi = seg.tile_range_ptrs(0, E + NS)
+                _lib.call("xtu_i8_gemm_gate_up", _p(a8x), _p(crx), _p(seg.sorted_tok), H, I,
+                          _p(w13_8), _p(emin13), 0, _p(seg.seg_start), _p(seg.tile_expert),
+                          _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), 0, cfg["limit"],
+                          1.0, 0.0, st)
+            else:
+                lo, hi = seg.tile_range_ptrs(0, E + NS)
+                _lib.call("xtu_gemm_gate_up", fmt, _p(x_st), _p(seg.sorted_tok), H, I, _p(W.w13),
+                          _p(W.s13), _p(W.gs13), 0, 0, 0, _p(seg.seg_start), _p(seg.tile_expert),
+                          _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), cfg["limit"], 1.0,
+                          0.0, st)
+            b.record()
+            torch.cuda.synchronize()
+            gu_ms.append(a.elapsed_time(b))
+
+        A = T * K + T * NS
+        mean_layer = float(np.mean(layer_ms))
+        mean_gu = float(np.mean(gu_ms))
+        mean_active = float(np.mean(n_active))
+        layer_bytes = mean_active * e_bytes + 2 * T * H * 2
+        gu_bytes = mean_active * e_bytes13 + T * H * 2 + A * I * 2
+        gu_flops = 2.0 * A * (2 * I) * H
+        results[T] = dict(T=T, layer_ms=mean_layer, layer_ms_min=float(np.min(layer_ms)),
+                          tok_s=T / (mean_layer / 1e3), distinct_experts=mean_active,
+                          layer_GBs=layer_bytes / (mean_layer / 1e3) / 1e9,
+                          gate_up_ms=mean_gu, gate_up_GBs=gu_bytes / (mean_gu / 1e3) / 1e9,
+                          gate_up_TFLOPs=gu_flops / (mean_gu / 1e3) / 1e12,
+                          graph=graph is not None, wall_s=wall)
+        log(f"[bench] T={T}: layer {mean_layer * 1e3:.1f} us ({results[T]['layer_GBs']:.0f} GB/s), "
+            f"gate_up {mean_gu * 1e3:.1f} us ({results[T]['gate_up_GBs']:.0f} GB/s, "
+            f"{results[T]['gate_up_TFLOPs']:.0f} TFLOP/s), |D|={mean_active:.1f}")
+
+    Th = max(cfg["Ts"])
+    r = results[Th]
+    decode_head = Th <= 16
+    if decode_head:
+        roof = dict(bound="hbm", achieved=r["gate_up_GBs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=r["gate_up_GBs"] / HBM_PEAK_GBS, traffic=None,
+                    kernel="decode_gate_up_kernel")
+    else:
+        dt = "int8" if cfg["int8"] else "bf16"
+        roof = dict(bound="mfma", achieved=r["gate_up_TFLOPs"], peak=PEAK_TFLOPS[dt],
+                    unit="TFLOP/s", frac=r["gate_up_TFLOPs"] / PEAK_TFLOPS[dt], traffic=None,
+                    kernel=("i8_gemm_kernel" if cfg["int8"] else "moe_gemm_kernel"),
+                    frac_of_fp8_peak=r["gate_up_TFLOPs"] / PEAK_TFLOPS["fp8"])
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(cfg, W, Th, rkw, args.cpu_seconds, dev)
+        except Exception as exc:  # noqa: BLE001
+            log(f"[bench] cpu baseline unavailable: {type(exc).__name__}: {exc}")
+            cpu = None
+
+    line = {
+        "metric": "MoE-layer ms & tok/s (decode T=1-4, prefill T=8192); HBM GB/s / MFMA % peak",
+        "value": r["tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r["layer_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"mxfp4": "bf16-mfma/e2m1+e8m0", "fp8": "bf16-mfma/e4m3+f32-block",
+                  "nvfp4": "bf16-mfma/e2m1+e4m3", "bf16": "bf16"}[cfg["fmt"]]
+                 if not cfg["int8"] else "int8-mfma/int32-acc",
+        "data": "synthetic (seeded N(0,1) tokens and logits, N(0,0.02) weights quantised)",
+        "config": {"workload": args.workload, "T": Th, "hidden": H, "intermediate": I,
+                   "routed_experts": E, "shared_experts": NS, "top_k": K,
+                   "weights": cfg["fmt"], "int8_activation": cfg["int8"],
+                   "cache_flushed_per_step": not args.no_flush,
+                   "per_T": {str(t): v for t, v in results.items()}},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(cfg, W, T, rkw, seconds, dev):
+    """Reference engine (oracle/_ref) on the host cores over a bounded sample."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from xtu_moe_amd.layer import route
+    from xtu_moe_amd.synthetic import dense_experts
+
+    E, NS, H, I, K = cfg["E"], cfg["NS"], cfg["H"], cfg["I"], cfg["K"]
+    Ts = min(T, 256)   # prefill: a 256-token slice of the batch
+    g = torch.Generator(device=dev).manual_seed(99)
+    logits = torch.randn((Ts, E), generator=g, device=dev)
+    w, i = route(logits, **rkw)
+    ids = i.cpu().numpy()
+    wts = w.cpu().numpy()
+    used = np.unique(ids)
+    remap = np.full(E, -1, np.int32)
+    remap[used] = np.arange(len(used), dtype=np.int32)
+    U = len(used)
+    experts = list(used) + [E + s for s in range(NS)]
+    dn = dense_experts(W, experts)
+    cids = remap[ids]
+    if NS:
+        cids = np.concatenate([cids, np.tile(np.arange(U, U + NS, dtype=np.int32), (Ts, 1))], 1)
+        wts = np.concatenate([wts, np.ones((Ts, NS), np.float32)], 1)
+    x = oracle.f32_to_bf16_bits(np.random.default_rng(5).standard_normal((Ts, H)).astype(np.float32))
+    threads = int(os.environ.get("XIAOTU_MOE_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    os.environ["XIAOTU_MOE_THREADS"] = str(threads)
+    fmt = {"mxfp4": oracle.FMT_MXFP4, "nvfp4": oracle.FMT_NVFP4, "fp8": oracle.FMT_FP8,
+           "bf16": oracle.FMT_BF16}[cfg["fmt"]]
+    eng = oracle.RefEngine(fmt, U + NS, K + NS, H, I, dn["w13"], dn["s13"], dn["w2"], dn["s2"],
+                           dn["gs13"], dn["gs2"], limit=cfg["limit"])
+    L = oracle.ref_lib()
+    if cfg["int8"]:
+        L.xref_set_int8(1, 1 << 30)
+    out = np.zeros((Ts, H), np.float32)
+    for _ in range(2):
+        eng.forward(x, cids, wts, out)
+    times = []
+    t_end = time.time() + seconds
+    while time.time() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        eng.forward(x, cids, wts, out)
+        times.append(time.perf_counter() - t0)
+    if cfg["int8"]:
+        L.xref_set_int8(0, 0)
+    med = float(np.median(times))
+    isa = {2: "avx512_vnni", 1: "avx512", 0: "scalar"}[int(L.xref_isa())]
+    return dict(value=Ts / med, unit="tok/s", cores=threads, kind="reference",
+                ms_per_layer=med * 1e3,
+                sample=(f"reference MOE_V2::forward_many ({isa}), {Ts} tokens x {K}+{NS} experts "
+                        f"({U + NS} distinct), median of {len(times)} calls after 2 warm-ups"))
+
+
+if __name__ == "__main__":
+    main()

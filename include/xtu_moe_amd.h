@@ -74,6 +74,24 @@ hipError_t xtu_segment(const int32_t* topk_ids, const float* topk_weights, const
                        int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
                        int32_t* expert_tile_start, hipStream_t stream);
 
+/* Small batches (A = T*K + T*n_shared <= xtu_route_segment_small_max_pairs()):
+ * routing and the whole segmentation in one workgroup, same outputs as
+ * xtu_route_* followed by xtu_segment.  mode 0 = softmax routing, 1 = grouped
+ * sigmoid routing (topk_ids/topk_weights are written), 2 = ids/weights given
+ * (read).  Replaces, for decode, the router call plus _build_segmentation
+ * (gpu_prefill.py:849-887) and the in-kernel dispatch scan of
+ * moe4_smallm_gu2/dn2 (moe4_smallm.cu:193-206, :266-281). */
+int xtu_route_segment_small_max_pairs(void);
+hipError_t xtu_route_segment_small(int mode, const float* logits, const float* bias,
+                                   int32_t* topk_ids, float* topk_weights, int T, int E, int K,
+                                   int n_group, int topk_group, float routed_scaling,
+                                   int renormalize, const int32_t* id_map, int n_shared,
+                                   int drop_zero, int bm, int32_t* sorted_pair,
+                                   int32_t* sorted_tok, float* sorted_wts, int32_t* inv,
+                                   int32_t* seg_start, int32_t* active, int32_t* n_active,
+                                   int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
+                                   int32_t* expert_tile_start, hipStream_t stream);
+
 /* --------------------------------------------------- skinny-M (decode) path
  * Replaces moe4_smallm_gu2 / moe4_smallm_dn2 (xiaotu_moe/csrc/moe4_smallm.cu:
  * 395-430) and the FP8 pair kernels _gate_up_pairs_kernel / _act_pairs_kernel
@@ -81,19 +99,34 @@ hipError_t xtu_segment(const int32_t* topk_ids, const float* topk_weights, const
  * pairs per expert (callers route T <= 16 here).  One workgroup per (weight
  * panel group, active expert); slots beyond *n_active exit at once.
  * gate_up writes act bf16 [A][I] = SwiGLU-clamp(x W_gate^T, x W_up^T) per
- * sorted pair row; down writes y fp32 [A][H].  w/s_estride: bytes between
- * experts (0 = dense); slot_map (nullable): expert -> weight slot. */
-hipError_t xtu_decode_gate_up(int fmt, const void* x, int H, int I, const void* w13,
+ * sorted pair row; down writes y fp32 [A][H].  T = tokens of the batch (the
+ * activation rows of up to min(T, 4) tokens per expert are staged in LDS).
+ * w/s_estride: bytes between experts (0 = dense); slot_map (nullable):
+ * expert -> weight slot. */
+hipError_t xtu_decode_gate_up(int fmt, const void* x, int T, int H, int I, const void* w13,
                               const void* s13, const float* gs13, long w_estride, long s_estride,
                               const int32_t* slot_map, const int32_t* sorted_tok,
                               const int32_t* seg_start, const int32_t* active,
                               const int32_t* n_active, int max_active, void* act, float limit,
                               float alpha, float beta, hipStream_t stream);
-hipError_t xtu_decode_down(int fmt, const void* act, int H, int I, const void* w2, const void* s2,
+hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const void* w2, const void* s2,
                            const float* gs2, long w_estride, long s_estride,
                            const int32_t* slot_map, const int32_t* seg_start,
                            const int32_t* active, const int32_t* n_active, int max_active,
                            float* y, hipStream_t stream);
+
+/* down projection fused with the weighted unpermute for decode (T <= 16): one
+ * workgroup per 16-row panel of W2 sweeps every active expert and writes
+ * out[T][H] (bf16 or fp32) directly, summing per-wave partials in a fixed
+ * order.  Replaces moe4_smallm_dn2 + its caller's accumulation
+ * (moe4_smallm.cu:260-333, moe4_smallm.py:293-309). */
+hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int H, int I, const void* w2,
+                                   const void* s2, const float* gs2, long w_estride,
+                                   long s_estride, const int32_t* slot_map,
+                                   const int32_t* sorted_tok, const float* sorted_wts,
+                                   const int32_t* seg_start, const int32_t* active,
+                                   const int32_t* n_active, void* out, int out_bf16,
+                                   hipStream_t stream);
 
 /* ------------------------------------------------ grouped GEMM (prefill) path
  * Replaces _gate_up_kernel / _down_kernel (vllm_xiaotu_moe/gpu_prefill.py:

@@ -108,3 +108,46 @@ def test_segmentation_id_map():
     ref = oracle.segment(mapped, wts, E, 0, True)
     np.testing.assert_array_equal(seg.seg_start.cpu().numpy(), ref["seg_start"])
     np.testing.assert_array_equal(seg.sorted_pair.cpu().numpy()[: seg.A], ref["sorted_pair"])
+
+
+@pytest.mark.parametrize("T,E,K,NS,mode", [(1, 256, 8, 1, 1), (4, 256, 8, 1, 1), (16, 256, 8, 1, 1),
+                                           (1, 512, 10, 1, 0), (4, 512, 10, 1, 0), (13, 8, 2, 0, 0),
+                                           (16, 64, 4, 2, 2), (64, 128, 8, 0, 2)])
+def test_fused_small_route_segment_bit_exact(T, E, K, NS, mode):
+    """One-launch routing + segmentation for small batches == router + segmentation."""
+    rng = np.random.default_rng(T * 13 + E)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    dev = torch.device("cuda")
+    seg = L.segmentation(T, K, E, NS, 128, dev)
+    assert seg.small
+    if mode == 2:
+        ids_np, wts_np = random_routing(T, K, E, seed=T, invalid_frac=0.1, zero_frac=0.1)
+        ids = torch.from_numpy(ids_np).to(dev)
+        wts = torch.from_numpy(wts_np).to(dev)
+        seg.run_small(2, ids, wts, drop_zero=True)
+    else:
+        ids = torch.empty((T, K), dtype=torch.int32, device=dev)
+        wts = torch.empty((T, K), dtype=torch.float32, device=dev)
+        kw = dict(n_group=8, topk_group=4, routed_scaling=2.5) if mode == 1 else {}
+        seg.run_small(mode, ids, wts, logits=torch.from_numpy(logits).to(dev), **kw)
+        if mode == 1:
+            ids_np, wts_np = oracle.route_grouped_sigmoid(logits, None, 8, 4, K, 2.5)
+        else:
+            ids_np, wts_np = oracle.route_softmax_topk(logits, K)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_np)
+    np.testing.assert_array_equal(wts.cpu().numpy().view(np.uint32), wts_np.view(np.uint32))
+    ref = oracle.segment(ids_np, wts_np, E, NS, True)
+    A = seg.A
+    np.testing.assert_array_equal(seg.seg_start.cpu().numpy(), ref["seg_start"])
+    for k in ("sorted_pair", "sorted_tok", "inv"):
+        np.testing.assert_array_equal(getattr(seg, k).cpu().numpy()[:A], ref[k])
+    np.testing.assert_array_equal(seg.sorted_wts.cpu().numpy()[:A].view(np.uint32),
+                                  ref["sorted_wts"].view(np.uint32))
+    counts = np.diff(ref["seg_start"])[: E + NS]
+    nz = np.nonzero(counts)[0]
+    assert int(seg.n_active.item()) == len(nz)
+    np.testing.assert_array_equal(seg.active.cpu().numpy()[: len(nz)], nz)
+    ets = np.concatenate([[0], np.cumsum((counts + 127) // 128)])
+    np.testing.assert_array_equal(seg.expert_tile_start.cpu().numpy()[: E + NS + 1], ets)
+    assert int(seg.n_tiles.item()) == ets[-1]

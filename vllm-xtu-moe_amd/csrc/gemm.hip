@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a) {
 
   u32x4_t areg[A_CH];
   u32x4_t breg[B_CH];
-  float bs0[B_CH], bs1[B_CH];
+  uint32_t bsraw[B_CH];
 
   auto gload = [&](int kk) {
 #pragma unroll
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a) {
       const uint8_t* region = wexp + (bpanel[i] * nsbk + sb) * 1024 + qbase * 256;
       breg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(region + boff[i] * 16));
       const int lane_eq = qbase * 16 + boff[i];   // (q, r) position inside the super-block
-      load_chunk_scale<FMT>(sexp, bpanel[i] * nsbk + sb, lane_eq, bs0[i], bs1[i]);
+      bsraw[i] = load_chunk_scale_raw<FMT>(sexp, bpanel[i] * nsbk + sb, lane_eq);
     }
   };
   auto lstore = [&]() {
@@ -128,7 +128,9 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a) {
       const int c = i * 256 + tid, pl = c / CPP;
       const int r = boff[i] % 16, qr = boff[i] / 16;
       uint32_t words[F::kWords];
-      decode_chunk<FMT>(breg[i], bs0[i], bs1[i], words);
+      float s0, s1;
+      chunk_scale<FMT>(bsraw[i], s0, s1);
+      decode_chunk<FMT>(breg[i], s0, s1, words);
       uint16_t* dst = &Bs[(pl * 16 + r) * kLDK + qr * F::kCK];
 #pragma unroll
       for (int j = 0; j < F::kWords / 4; ++j) {

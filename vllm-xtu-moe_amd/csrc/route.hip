@@ -22,41 +22,55 @@ __device__ __forceinline__ bool better(float sa, int ia, float sb, int ib) {
   return (sa > sb) || (sa == sb && ia < ib);
 }
 
-// wave argmax of (s, i) pairs under `better`; every lane gets the winner.
-__device__ __forceinline__ void wave_argmax(float& s, int& i) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float os = __shfl_xor(s, off, kWave);
-    const int oi = __shfl_xor(i, off, kWave);
-    if (better(os, oi, s, i)) {
-      s = os;
-      i = oi;
-    }
+// One DPP step of the wave argmax: combine with the lane selected by `ctrl`
+// (lanes whose source is masked keep their own value).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void dpp_argmax_step(float& s, int& i) {
+  const float os = __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(s), __float_as_int(s), CTRL, ROW_MASK, 0xF, false));
+  const int oi = __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xF, false);
+  if (better(os, oi, s, i)) {
+    s = os;
+    i = oi;
   }
 }
 
-// MODE 0: softmax top-k (renormalised or not).  MODE 1: grouped sigmoid.
-template <int MODE>
-__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
-                                                    const float* __restrict__ bias, int T, int E,
-                                                    int K, int n_group, int topk_group,
-                                                    float scale, int renorm,
-                                                    int32_t* __restrict__ ids,
-                                                    float* __restrict__ wts) {
-  __shared__ float sb[4][1024];   // selection score per expert, per wave
-  const int wv = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int t = blockIdx.x * 4 + wv;
-  if (t >= T) return;
-  const float* l = logits + (size_t)t * E;
+// wave argmax of (s, i) pairs under `better`; every lane gets the winner.
+// quad xor 1, quad xor 2, half-row mirror, row mirror, row_bcast15, row_bcast31
+// leave the maximum in lane 63, which is then read back as a uniform value.
+__device__ __forceinline__ void wave_argmax(float& s, int& i) {
+  dpp_argmax_step<0xB1, 0xF>(s, i);   // quad_perm [1,0,3,2]
+  dpp_argmax_step<0x4E, 0xF>(s, i);   // quad_perm [2,3,0,1]
+  dpp_argmax_step<0x141, 0xF>(s, i);  // row_half_mirror
+  dpp_argmax_step<0x140, 0xF>(s, i);  // row_mirror
+  dpp_argmax_step<0x142, 0xA>(s, i);  // row_bcast15 into rows 1, 3
+  dpp_argmax_step<0x143, 0xC>(s, i);  // row_bcast31 into rows 2, 3
+  s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
+  i = __builtin_amdgcn_readlane(i, 63);
+}
+
+__device__ __forceinline__ float lane_read(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Route one token with one wave.  MODE 0: softmax top-k, MODE 1: grouped
+// sigmoid.  NPER = experts per lane (E <= 64 * NPER); sb is this wave's LDS
+// scratch of E floats.  On return lanes k < K hold the k-th choice in
+// (id, weight); the fp32 weight sequence is the one the host oracle restates.
+template <int MODE, int NPER>
+__device__ __forceinline__ void route_one_token(const float* __restrict__ l,
+                                                const float* __restrict__ bias, int E, int K,
+                                                int n_group, int topk_group, float scale,
+                                                int renorm, float* sb, int lane, int& my_id,
+                                                float& my_w) {
+#pragma clang fp contract(off)
   const float NEG = -__builtin_inff();
-  float sel_score[kMaxPerLane];   // selection score (logit, or sigmoid+bias)
-  float wt_score[kMaxPerLane];    // weight score (sigmoid) for MODE 1
-  const int nper = (E + kWave - 1) / kWave;
+  float sel[NPER], wsc[NPER];
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
+  for (int j = 0; j < NPER; ++j) {
     const int e = lane + kWave * j;
     float v = NEG, w = 0.f;
-    if (j < nper && e < E) {
+    if (e < E) {
       const float x = l[e];
       if (MODE == 0) {
         v = x;
@@ -64,33 +78,38 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
         w = xtu_sigmoid(x);
         v = w + (bias ? bias[e] : 0.0f);
       }
-      sb[wv][e] = v;
     }
-    sel_score[j] = v;
-    wt_score[j] = w;
+    sel[j] = v;
+    wsc[j] = w;
   }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-
-  // group mask (MODE 1): bit j set when group j is kept
   uint64_t gmask = ~0ull;
   int gsz = E;
   if (MODE == 1) {
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+      const int e = lane + kWave * j;
+      if (e < E) sb[e] = sel[j];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     gsz = E / n_group;
     float g = NEG;
     if (lane < n_group) {
+      // two best (score desc, index asc) of the group, kept in registers
+      float v1 = NEG, v2 = NEG;
       int i1 = -1, i2 = -1;
       for (int q = 0; q < gsz; ++q) {
         const int e = lane * gsz + q;
-        const float v = sb[wv][e];
-        if (i1 < 0 || better(v, e, sb[wv][i1], i1)) {
-          i2 = i1;
-          i1 = e;
-        } else if (i2 < 0 || better(v, e, sb[wv][i2], i2)) {
-          i2 = e;
+        const float v = sb[e];
+        if (i1 < 0 || better(v, e, v1, i1)) {
+          v2 = v1; i2 = i1;
+          v1 = v; i1 = e;
+        } else if (i2 < 0 || better(v, e, v2, i2)) {
+          v2 = v; i2 = e;
         }
       }
-      g = (gsz >= 2) ? (sb[wv][i1] + sb[wv][i2]) : sb[wv][i1];
+      g = (gsz >= 2) ? (v1 + v2) : v1;
     }
     gmask = 0;
     bool taken = false;
@@ -102,70 +121,77 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
       gmask |= 1ull << i;
     }
   }
-
-  float chosen_w[16];
-  float chosen_s[16];
-  int chosen_i[16];
-  uint32_t used = 0;   // bit j: this lane's expert lane+64j already chosen
+  uint32_t used = 0;
+  my_id = -1;
+  float my_s = 0.f, my_wsc = 0.f;
   for (int k = 0; k < K; ++k) {
     float s = NEG;
     int i = 0x7fffffff;
-    float w = 0.f;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
+    for (int j = 0; j < NPER; ++j) {
       const int e = lane + kWave * j;
-      if (j < nper && e < E && !((used >> j) & 1u) && ((gmask >> (e / gsz)) & 1ull)) {
-        if (better(sel_score[j], e, s, i)) {
-          s = sel_score[j];
+      if (e < E && !((used >> j) & 1u) && ((gmask >> (e / gsz)) & 1ull)) {
+        if (better(sel[j], e, s, i)) {
+          s = sel[j];
           i = e;
-          w = wt_score[j];
         }
       }
     }
     wave_argmax(s, i);
-    // the owner of the winner marks it and broadcasts its weight score
-    const int owner = i % kWave;
-    if (lane == owner) used |= 1u << (i / kWave);
-    float wsc = 0.f;
+    const int owner = i % kWave, jw = i / kWave;
+    float w = 0.f;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j)
-      if (lane == owner && lane + kWave * j == i) wsc = wt_score[j];
-    wsc = __shfl(wsc, owner, kWave);
-    (void)w;
-    if (k < 16) {
-      chosen_s[k] = s;
-      chosen_w[k] = wsc;
-      chosen_i[k] = i;
+    for (int j = 0; j < NPER; ++j)
+      if (j == jw) w = wsc[j];
+    if (lane == owner) used |= 1u << jw;
+    w = lane_read(w, owner);
+    if (lane == k) {
+      my_id = i;
+      my_s = s;
+      my_wsc = w;
     }
   }
-  if (lane != 0) return;
-  {
-#pragma clang fp contract(off)
   if (MODE == 0) {
-    const float lmax = chosen_s[0];
-    float ev[16];
+    const float lmax = lane_read(my_s, 0);
+    const float ev = (lane < K) ? xtu_expf(my_s - lmax) : 0.f;
     float sum = 0.0f;
-    for (int k = 0; k < K; ++k) {
-      ev[k] = xtu_expf(chosen_s[k] - lmax);
-      sum = sum + ev[k];
+    if (renorm) {
+      for (int k = 0; k < K; ++k) sum = sum + lane_read(ev, k);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NPER; ++j) {
+        const int e = lane + kWave * j;
+        const float x = (e < E) ? xtu_expf(l[e] - lmax) : 0.f;
+        for (int q = 0; q < kWave; ++q)
+          if (q + kWave * j < E) sum = sum + lane_read(x, q);
+      }
     }
-    if (!renorm) {
-      sum = 0.0f;
-      for (int e = 0; e < E; ++e) sum = sum + xtu_expf(l[e] - lmax);
-    }
-    for (int k = 0; k < K; ++k) {
-      ids[(size_t)t * K + k] = chosen_i[k];
-      wts[(size_t)t * K + k] = __fdiv_rn(ev[k], sum);
-    }
+    my_w = __fdiv_rn(ev, sum);
   } else {
     float sum = 0.0f;
-    for (int k = 0; k < K; ++k) sum = sum + chosen_w[k];
-    for (int k = 0; k < K; ++k) {
-      ids[(size_t)t * K + k] = chosen_i[k];
-      wts[(size_t)t * K + k] =
-          renorm ? __fdiv_rn(chosen_w[k], sum) * scale : chosen_w[k] * scale;
-    }
+    for (int k = 0; k < K; ++k) sum = sum + lane_read(my_wsc, k);
+    my_w = renorm ? __fdiv_rn(my_wsc, sum) * scale : my_wsc * scale;
   }
+}
+
+template <int MODE, int NPER>
+__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
+                                                    const float* __restrict__ bias, int T, int E,
+                                                    int K, int n_group, int topk_group,
+                                                    float scale, int renorm,
+                                                    int32_t* __restrict__ ids,
+                                                    float* __restrict__ wts) {
+  __shared__ float sb[4][64 * NPER];
+  const int wv = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int t = blockIdx.x * 4 + wv;
+  if (t >= T) return;   // no block-wide barrier below
+  int id;
+  float w;
+  route_one_token<MODE, NPER>(logits + (size_t)t * E, bias, E, K, n_group, topk_group, scale,
+                              renorm, sb[wv], lane, id, w);
+  if (lane < K) {
+    ids[(size_t)t * K + lane] = id;
+    wts[(size_t)t * K + lane] = w;
   }
 }
 
@@ -396,6 +422,188 @@ __global__ __launch_bounds__(kSegThreads) void seg_scatter_kernel(
   }
 }
 
+// ----------------------------------------------------------------------------
+// Small batches (decode): routing and the whole segmentation in one
+// workgroup.  A = T*K + T*NS <= 1024 pairs, NB <= 2048 buckets.  Same
+// outputs, same order and same fp32 sequence as the multi-launch path.
+// ----------------------------------------------------------------------------
+constexpr int kSmallMaxA = 1024;
+constexpr int kSmallMaxNB = 2048;
+
+// In-place exclusive scan of a[0, n) (n <= 2048) by 256 threads; returns the total.
+__device__ int block_excl_scan_256(int* a, int n, int* wsum) {
+  const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
+  const int per = (n + 255) / 256;
+  int loc[8];
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int idx = tid * per + i;
+    const int v = (i < per && idx < n) ? a[idx] : 0;
+    loc[i] = s;
+    s += v;
+  }
+  int incl = s;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int o = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += o;
+  }
+  if (lane == kWave - 1) wsum[wv] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int q = 0; q < wv; ++q) base += wsum[q];
+  const int total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  const int ex = base + incl - s;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int idx = tid * per + i;
+    if (i < per && idx < n) a[idx] = ex + loc[i];
+  }
+  __syncthreads();
+  return total;
+}
+
+struct SmallArgs {
+  const float* logits;
+  const float* bias;
+  int32_t* ids;
+  float* wts;
+  const int32_t* id_map;
+  int T, K, E, n_group, topk_group, renorm, NS, drop_zero, bm;
+  float scale;
+  int32_t *sorted_pair, *sorted_tok, *inv, *seg_start, *active, *n_active;
+  float* sorted_wts;
+  int32_t *tile_expert, *tile_row0, *n_tiles, *expert_tile_start;
+};
+
+// MODE 0: softmax routing, 1: grouped sigmoid routing, 2: ids/wts given.
+template <int MODE, int NPER>
+__global__ __launch_bounds__(256) void route_seg_small_kernel(SmallArgs a) {
+  __shared__ float sb[4][64 * NPER];
+  __shared__ int s_ids[kSmallMaxA];
+  __shared__ float s_w[kSmallMaxA];
+  __shared__ int s_bk[kSmallMaxA];
+  __shared__ int s_cnt[kSmallMaxNB];
+  __shared__ int s_act[kSmallMaxNB];
+  __shared__ int s_til[kSmallMaxNB];
+  __shared__ int s_wsum[4];
+  const int tid = threadIdx.x, wv = tid / kWave, lane = tid % kWave;
+  const int T = a.T, K = a.K, E = a.E, NS = a.NS;
+  const int TK = T * K, A = TK + T * NS, NB = E + NS + 1;
+  if (MODE < 2) {
+    for (int t = wv; t < T; t += 4) {
+      int id;
+      float w;
+      route_one_token<MODE < 2 ? MODE : 0, NPER>(a.logits + (size_t)t * E, a.bias, E, K,
+                                                  a.n_group, a.topk_group, a.scale, a.renorm,
+                                                  sb[wv], lane, id, w);
+      if (lane < K) {
+        a.ids[t * K + lane] = id;
+        a.wts[t * K + lane] = w;
+        s_ids[t * K + lane] = id;
+        s_w[t * K + lane] = w;
+      }
+    }
+  } else {
+    for (int p = tid; p < TK; p += 256) {
+      s_ids[p] = a.ids[p];
+      s_w[p] = a.wts[p];
+    }
+  }
+  for (int e = tid; e < NB; e += 256) s_cnt[e] = 0;
+  __syncthreads();
+  for (int p = tid; p < A; p += 256) {
+    int b;
+    if (p < TK) {
+      int e = s_ids[p];
+      if (a.id_map && e >= 0 && e < E) e = a.id_map[e];
+      b = (e < 0 || e >= E) ? (E + NS) : e;
+      if (a.drop_zero && s_w[p] == 0.0f) b = E + NS;
+    } else {
+      b = E + (p - TK) % NS;
+    }
+    s_bk[p] = b;
+    atomicAdd(&s_cnt[b], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < NB; e += 256) {
+    const int c = s_cnt[e];
+    const bool expert = e < NB - 1;
+    s_act[e] = (expert && c > 0) ? 1 : 0;
+    s_til[e] = expert ? (c + a.bm - 1) / a.bm : 0;
+  }
+  __syncthreads();
+  block_excl_scan_256(s_cnt, NB, s_wsum);
+  const int n_act = block_excl_scan_256(s_act, NB, s_wsum);
+  const int n_til = block_excl_scan_256(s_til, NB, s_wsum);
+  for (int e = tid; e < NB; e += 256) {
+    const int st = s_cnt[e];
+    const int en = (e + 1 < NB) ? s_cnt[e + 1] : A;
+    const int c = en - st;
+    a.seg_start[e] = st;
+    a.expert_tile_start[e] = s_til[e];
+    if (e == NB - 1) {
+      a.seg_start[NB] = A;
+      a.expert_tile_start[NB] = n_til;
+    }
+    if (e < NB - 1 && c > 0) {
+      a.active[s_act[e]] = e;
+      const int nt = (c + a.bm - 1) / a.bm;
+      for (int j = 0; j < nt; ++j) {
+        a.tile_expert[s_til[e] + j] = e;
+        a.tile_row0[s_til[e] + j] = st + j * a.bm;
+      }
+    }
+  }
+  if (tid == 0) {
+    a.n_active[0] = n_act;
+    a.n_tiles[0] = n_til;
+  }
+  for (int p = tid; p < A; p += 256) {
+    const int b = s_bk[p];
+    int r = 0;
+    for (int q = 0; q < p; ++q) r += (s_bk[q] == b) ? 1 : 0;
+    const int pos = s_cnt[b] + r;
+    a.sorted_pair[pos] = p;
+    a.inv[p] = pos;
+    if (p < TK) {
+      a.sorted_tok[pos] = p / K;
+      a.sorted_wts[pos] = s_w[p];
+    } else {
+      a.sorted_tok[pos] = (p - TK) / NS;
+      a.sorted_wts[pos] = 1.0f;
+    }
+  }
+}
+
+template <int MODE>
+void launch_small(const SmallArgs& a, hipStream_t stream) {
+  if (a.E <= 64) route_seg_small_kernel<MODE, 1><<<1, 256, 0, stream>>>(a);
+  else if (a.E <= 256) route_seg_small_kernel<MODE, 4><<<1, 256, 0, stream>>>(a);
+  else if (a.E <= 512) route_seg_small_kernel<MODE, 8><<<1, 256, 0, stream>>>(a);
+  else route_seg_small_kernel<MODE, 16><<<1, 256, 0, stream>>>(a);
+}
+
+template <int MODE>
+void launch_route(const float* logits, const float* bias, int T, int E, int K, int n_group,
+                  int topk_group, float scale, int renorm, int32_t* ids, float* wts,
+                  hipStream_t stream) {
+  const dim3 grid((T + 3) / 4);
+  if (E <= 64)
+    route_kernel<MODE, 1><<<grid, 256, 0, stream>>>(logits, bias, T, E, K, n_group, topk_group,
+                                                    scale, renorm, ids, wts);
+  else if (E <= 256)
+    route_kernel<MODE, 4><<<grid, 256, 0, stream>>>(logits, bias, T, E, K, n_group, topk_group,
+                                                    scale, renorm, ids, wts);
+  else if (E <= 512)
+    route_kernel<MODE, 8><<<grid, 256, 0, stream>>>(logits, bias, T, E, K, n_group, topk_group,
+                                                    scale, renorm, ids, wts);
+  else
+    route_kernel<MODE, 16><<<grid, 256, 0, stream>>>(logits, bias, T, E, K, n_group, topk_group,
+                                                     scale, renorm, ids, wts);
+}
+
 }  // namespace
 }  // namespace xtu
 
@@ -409,8 +617,8 @@ hipError_t xtu_route_softmax_topk(const float* logits, int T, int E, int K, int 
   XTU_CHECK_ARG(T == 0 || (logits && topk_ids && topk_weights));
   if (T == 0) return hipSuccess;
   (void)hipGetLastError();
-  route_kernel<0><<<(T + 3) / 4, 256, 0, stream>>>(logits, nullptr, T, E, K, 1, 1, 1.0f,
-                                                   renormalize, topk_ids, topk_weights);
+  launch_route<0>(logits, nullptr, T, E, K, 1, 1, 1.0f, renormalize, topk_ids, topk_weights,
+                  stream);
   return hipPeekAtLastError();
 }
 
@@ -424,9 +632,8 @@ hipError_t xtu_route_grouped_sigmoid(const float* logits, const float* bias, int
   XTU_CHECK_ARG(T == 0 || (logits && topk_ids && topk_weights));
   if (T == 0) return hipSuccess;
   (void)hipGetLastError();
-  route_kernel<1><<<(T + 3) / 4, 256, 0, stream>>>(logits, bias, T, E, K, n_group, topk_group,
-                                                   routed_scaling, renormalize, topk_ids,
-                                                   topk_weights);
+  launch_route<1>(logits, bias, T, E, K, n_group, topk_group, routed_scaling, renormalize,
+                  topk_ids, topk_weights, stream);
   return hipPeekAtLastError();
 }
 
@@ -471,6 +678,37 @@ hipError_t xtu_segment(const int32_t* topk_ids, const float* topk_weights,
     seg_scatter_kernel<<<nblocks, kSegThreads, 5 * NB * sizeof(int), stream>>>(
         a, bcnt, seg_start, sorted_pair, sorted_tok, sorted_wts, inv);
   }
+  return hipPeekAtLastError();
+}
+
+int xtu_route_segment_small_max_pairs(void) { return kSmallMaxA; }
+
+hipError_t xtu_route_segment_small(int mode, const float* logits, const float* bias,
+                                   int32_t* topk_ids, float* topk_weights, int T, int E, int K,
+                                   int n_group, int topk_group, float routed_scaling,
+                                   int renormalize, const int32_t* id_map, int n_shared,
+                                   int drop_zero, int bm, int32_t* sorted_pair,
+                                   int32_t* sorted_tok, float* sorted_wts, int32_t* inv,
+                                   int32_t* seg_start, int32_t* active, int32_t* n_active,
+                                   int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
+                                   int32_t* expert_tile_start, hipStream_t stream) {
+  XTU_CHECK_ARG(mode >= 0 && mode <= 2 && T >= 0 && E > 0 && E <= 1024 && K > 0 && K <= 16 &&
+                K <= E && n_shared >= 0 && bm > 0);
+  XTU_CHECK_ARG((long)T * K + (long)T * n_shared <= kSmallMaxA && E + n_shared + 1 <= kSmallMaxNB);
+  if (mode == 1)
+    XTU_CHECK_ARG(n_group > 0 && n_group <= 64 && E % n_group == 0 && topk_group > 0 &&
+                  topk_group <= n_group && K <= topk_group * (E / n_group));
+  XTU_CHECK_ARG(topk_ids && topk_weights && (mode == 2 || T == 0 || logits));
+  XTU_CHECK_ARG(sorted_pair && sorted_tok && sorted_wts && inv && seg_start && active &&
+                n_active && tile_expert && tile_row0 && n_tiles && expert_tile_start);
+  SmallArgs a{logits, bias, topk_ids, topk_weights, id_map, T, K, E, n_group, topk_group,
+              renormalize, n_shared, drop_zero, bm, routed_scaling, sorted_pair, sorted_tok, inv,
+              seg_start, active, n_active, sorted_wts, tile_expert, tile_row0, n_tiles,
+              expert_tile_start};
+  (void)hipGetLastError();
+  if (mode == 0) launch_small<0>(a, stream);
+  else if (mode == 1) launch_small<1>(a, stream);
+  else launch_small<2>(a, stream);
   return hipPeekAtLastError();
 }
 

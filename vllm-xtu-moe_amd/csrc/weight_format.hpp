@@ -54,21 +54,39 @@ struct WFmt<kBF16> {
   static __host__ __device__ constexpr long s_bytes(long, long) { return 0; }
 };
 
-// Decode one chunk into bf16 pair words.  `sc` points at this expert's fp4
-// scale array; `sb_index` is the (panel, super-block) index; `lane` = 16q+r.
+// Raw scale bits of one chunk (no use of the value, so the load does not
+// stall the issue of the loads that follow it).  `sc` points at this expert's
+// fp4 scale array; `sb_index` is the (panel, super-block) index; `lane` = 16q+r.
 template <int FMT>
-__device__ __forceinline__ void load_chunk_scale(const uint8_t* __restrict__ sc, long sb_index,
-                                                 int lane, float& s0, float& s1) {
+__device__ __forceinline__ uint32_t load_chunk_scale_raw(const uint8_t* __restrict__ sc,
+                                                         long sb_index, int lane) {
   if constexpr (FMT == kMXFP4) {
-    s0 = e8m0_to_f32(sc[sb_index * 64 + lane]);
+    return sc[sb_index * 64 + lane];
+  } else if constexpr (FMT == kNVFP4) {
+    return *reinterpret_cast<const uint16_t*>(sc + (sb_index * 64 + lane) * 2);
+  } else {
+    return 0u;
+  }
+}
+
+// Branch-free decode of the raw scale bits into the chunk's scale(s).
+template <int FMT>
+__device__ __forceinline__ void chunk_scale(uint32_t raw, float& s0, float& s1) {
+  if constexpr (FMT == kMXFP4) {
+    s0 = e8m0_to_f32(raw);
     s1 = s0;
   } else if constexpr (FMT == kNVFP4) {
-    const uint16_t v = *reinterpret_cast<const uint16_t*>(sc + (sb_index * 64 + lane) * 2);
-    s0 = e4m3_to_f32(v & 0xffu);
-    s1 = e4m3_to_f32(v >> 8);
+    s0 = e4m3_to_f32(raw & 0xffu);
+    s1 = e4m3_to_f32((raw >> 8) & 0xffu);
   } else {
     s0 = s1 = 1.0f;
   }
+}
+
+template <int FMT>
+__device__ __forceinline__ void load_chunk_scale(const uint8_t* __restrict__ sc, long sb_index,
+                                                 int lane, float& s0, float& s1) {
+  chunk_scale<FMT>(load_chunk_scale_raw<FMT>(sc, sb_index, lane), s0, s1);
 }
 
 template <int FMT>

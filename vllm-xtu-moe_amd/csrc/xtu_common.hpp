@@ -52,9 +52,8 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
 // e8m0 byte -> 2^(b-127) as fp32 (b = 0 gives 2^-127, a subnormal; b = 255 inf).
 __device__ __forceinline__ float e8m0_to_f32(uint32_t b) {
   b &= 255u;
-  if (b == 0) return __uint_as_float(0x00400000u);
-  if (b == 255) return __uint_as_float(0x7f800000u);
-  return __uint_as_float(b << 23);
+  const float v = __uint_as_float(b << 23);   // 255 -> +inf
+  return b == 0 ? __uint_as_float(0x00400000u) : v;
 }
 
 // ---------------------------------------------------------------------------

@@ -21,14 +21,20 @@ SIGNATURES = {
     "xtu_error_string": (ctypes.c_char_p, [_i]),
     "xtu_route_softmax_topk": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "xtu_route_grouped_sigmoid": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp]),
+    "xtu_route_segment_small_max_pairs": (_i, []),
+    "xtu_route_segment_small": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _i,
+                                     _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _vp]),
     "xtu_segment_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "xtu_segment_max_tiles": (_i, [_i, _i, _i, _i, _i]),
     "xtu_segment": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp,
                          _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "xtu_decode_gate_up": (_i, [_i, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp,
-                                _i, _vp, _f, _f, _f, _vp]),
-    "xtu_decode_down": (_i, [_i, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _i, _vp,
-                             _vp]),
+    "xtu_decode_gate_up": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
+                                _vp, _i, _vp, _f, _f, _f, _vp]),
+    "xtu_decode_down": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _i,
+                             _vp, _vp]),
+    "xtu_decode_down_combine": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp,
+                                     _vp, _vp, _vp, _vp, _i, _vp]),
     "xtu_gemm_tile_m": (_i, [_i]),
     "xtu_gemm_gate_up": (_i, [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
                               _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
@@ -51,6 +57,7 @@ SIGNATURES = {
 
 # entry points whose int return value is a size/count, not a status
 _NOT_STATUS = {"xtu_version", "xtu_error_string", "xtu_segment_workspace_bytes",
+               "xtu_route_segment_small_max_pairs",
                "xtu_segment_max_tiles", "xtu_gemm_tile_m", "xtu_i8_weight_bytes"}
 
 _LIB = None

@@ -17,6 +17,10 @@ from . import _lib
 from .formats import (FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4, pack_scales, pack_weight)
 
 DECODE_MAX_TOKENS = 16
+SMALL_MAX_PAIRS = 1024
+# decode: down projection fused with the weighted unpermute (one launch, no y
+# buffer) or split into down (y rows) + combine
+DECODE_FUSED_DOWN = False
 
 
 def _p(t) -> int:
@@ -131,6 +135,23 @@ class _Segmentation:
                   _p(self.expert_tile_start), _stream(stream))
         return self
 
+    def run_small(self, mode, ids, wts, *, logits=None, bias=None, n_group=1, topk_group=1,
+                  routed_scaling=1.0, renormalize=True, id_map=None, drop_zero=True, stream=None):
+        """Routing (mode 0 softmax / 1 grouped sigmoid, writing ids and wts) or
+        given ids (mode 2) plus the whole segmentation, in one launch."""
+        _lib.call("xtu_route_segment_small", int(mode), _p(logits), _p(bias), _p(ids), _p(wts),
+                  self.T, self.E, self.K, int(n_group), int(topk_group), float(routed_scaling),
+                  int(renormalize), _p(id_map), self.NS, int(drop_zero), self.bm,
+                  _p(self.sorted_pair), _p(self.sorted_tok), _p(self.sorted_wts), _p(self.inv),
+                  _p(self.seg_start), _p(self.active), _p(self.n_active), _p(self.tile_expert),
+                  _p(self.tile_row0), _p(self.n_tiles), _p(self.expert_tile_start),
+                  _stream(stream))
+        return self
+
+    @property
+    def small(self) -> bool:
+        return self.A <= SMALL_MAX_PAIRS and self.E + self.NS + 1 <= 2048 and self.K <= 16
+
     def tile_range_ptrs(self, b0: int, b1: int):
         """Device pointers to expert_tile_start[b0] and [b1] (m-tile range of buckets [b0, b1))."""
         base = _p(self.expert_tile_start)
@@ -181,13 +202,16 @@ def route(logits, *, top_k, scoring="softmax", renormalize=True, bias=None, n_gr
 
 def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0, swiglu_alpha=1.0,
                 swiglu_beta=0.0, out=None, out_dtype=torch.bfloat16, path="auto", int8=False,
-                drop_zero=True, id_map=None, slot_map=None, stream=None, return_seg=False):
+                drop_zero=True, id_map=None, slot_map=None, stream=None, return_seg=False,
+                router=None):
     """Routed (+shared) experts of one layer; returns out [T, H].
 
     path: "auto" (decode kernels for T <= 16, grouped GEMMs otherwise),
     "decode" or "gemm".  int8: INT8-activation x FP4-code ALIGN path (MXFP4).
     id_map: int32 [E] applied to topk_ids before bucketing; slot_map: int32
-    [E+NS] bucket -> weight slot.
+    [E+NS] bucket -> weight slot.  router: dict(logits=, scoring=, bias=,
+    n_group=, topk_group=, routed_scaling_factor=, renormalize=) routes from
+    logits first, writing topk_ids / topk_weights (int32 / fp32 buffers).
     """
     if x.dtype != torch.bfloat16 or not x.is_contiguous():
         raise ValueError("x must be contiguous bf16 [T, H]")
@@ -196,6 +220,10 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     if x.shape != (T, H):
         raise ValueError(f"x shape {tuple(x.shape)} != ({T}, {H})")
     dev = x.device
+    if router is not None and not (topk_ids.dtype == torch.int32 and topk_ids.is_contiguous()
+                                   and topk_weights.dtype == torch.float32
+                                   and topk_weights.is_contiguous()):
+        raise ValueError("with router=, topk_ids / topk_weights are int32 / fp32 output buffers")
     ids = topk_ids if (topk_ids.dtype == torch.int32 and topk_ids.is_contiguous()) else topk_ids.to(torch.int32).contiguous()
     wts = topk_weights if (topk_weights.dtype == torch.float32 and topk_weights.is_contiguous()) else topk_weights.float().contiguous()
     st = _stream(stream)
@@ -205,7 +233,26 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     if path == "decode" and T > DECODE_MAX_TOKENS:
         raise ValueError(f"decode path handles at most {DECODE_MAX_TOKENS} tokens")
     bm = 128 if int8 else int(_lib.call("xtu_gemm_tile_m", fmt))
-    seg = segmentation(T, K, E, NS, bm, dev).run(ids, wts, id_map, drop_zero, st)
+    seg = segmentation(T, K, E, NS, bm, dev)
+    if router is not None:
+        mode = 1 if router.get("scoring", "softmax") == "sigmoid" else 0
+        if seg.small and T > 0:
+            seg.run_small(mode, ids, wts, logits=router["logits"], bias=router.get("bias"),
+                          n_group=router.get("n_group", 1), topk_group=router.get("topk_group", 1),
+                          routed_scaling=router.get("routed_scaling_factor", 1.0),
+                          renormalize=router.get("renormalize", True), id_map=id_map,
+                          drop_zero=drop_zero, stream=st)
+        else:
+            route(router["logits"], top_k=K, scoring=router.get("scoring", "softmax"),
+                  renormalize=router.get("renormalize", True), bias=router.get("bias"),
+                  n_group=router.get("n_group", 1), topk_group=router.get("topk_group", 1),
+                  routed_scaling_factor=router.get("routed_scaling_factor", 1.0), ids_out=ids,
+                  wts_out=wts, stream=st)
+            seg.run(ids, wts, id_map, drop_zero, st)
+    elif seg.small and T > 0:
+        seg.run_small(2, ids, wts, id_map=id_map, drop_zero=drop_zero, stream=st)
+    else:
+        seg.run(ids, wts, id_map, drop_zero, st)
     A = seg.A
     odt = out_dtype if out is None else out.dtype
     if out is None:
@@ -217,10 +264,16 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
     if path == "decode":
         max_active = min(E, T * K) + NS
-        _lib.call("xtu_decode_gate_up", fmt, _p(x), H, I, _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0,
+        _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0,
                   _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
                   _p(seg.n_active), max_active, _p(act), lim, al, be, st)
-        _lib.call("xtu_decode_down", fmt, _p(act), H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
+        if DECODE_FUSED_DOWN:
+            _lib.call("xtu_decode_down_combine", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2),
+                      _p(W.gs2), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.sorted_wts),
+                      _p(seg.seg_start), _p(seg.active), _p(seg.n_active), _p(out),
+                      int(odt == torch.bfloat16), st)
+            return (out, seg) if return_seg else out
+        _lib.call("xtu_decode_down", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.active), _p(seg.n_active), max_active,
                   _p(y), st)
     elif int8:
