@@ -96,11 +96,12 @@ hipError_t xtu_route_segment_small(int mode, const float* logits, const float* b
  * Replaces moe4_smallm_gu2 / moe4_smallm_dn2 (xiaotu_moe/csrc/moe4_smallm.cu:
  * 395-430) and the FP8 pair kernels _gate_up_pairs_kernel / _act_pairs_kernel
  * / _down_pairs_kernel (vllm_xiaotu_moe/decode_moe_fp8.py:23-101).  At most 16
- * pairs per expert (callers route T <= 16 here).  One workgroup per (weight
- * panel group, active expert); slots beyond *n_active exit at once.
+ * pairs per expert (callers route T <= 16 here).  One workgroup per (active
+ * expert, weight panel group); slots beyond *n_active exit at once.
  * gate_up writes act bf16 [A][I] = SwiGLU-clamp(x W_gate^T, x W_up^T) per
- * sorted pair row; down writes y fp32 [A][H].  T = tokens of the batch (the
- * activation rows of up to min(T, 4) tokens per expert are staged in LDS).
+ * sorted pair row; down writes y fp32 [A][H].  T = tokens of the batch (up
+ * to 72 KiB of an expert's activation rows are staged in LDS, the rest read
+ * from global memory).
  * w/s_estride: bytes between experts (0 = dense); slot_map (nullable):
  * expert -> weight slot. */
 hipError_t xtu_decode_gate_up(int fmt, const void* x, int T, int H, int I, const void* w13,
@@ -114,19 +115,6 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
                            const int32_t* slot_map, const int32_t* seg_start,
                            const int32_t* active, const int32_t* n_active, int max_active,
                            float* y, hipStream_t stream);
-
-/* down projection fused with the weighted unpermute for decode (T <= 16): one
- * workgroup per 16-row panel of W2 sweeps every active expert and writes
- * out[T][H] (bf16 or fp32) directly, summing per-wave partials in a fixed
- * order.  Replaces moe4_smallm_dn2 + its caller's accumulation
- * (moe4_smallm.cu:260-333, moe4_smallm.py:293-309). */
-hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int H, int I, const void* w2,
-                                   const void* s2, const float* gs2, long w_estride,
-                                   long s_estride, const int32_t* slot_map,
-                                   const int32_t* sorted_tok, const float* sorted_wts,
-                                   const int32_t* seg_start, const int32_t* active,
-                                   const int32_t* n_active, void* out, int out_bf16,
-                                   hipStream_t stream);
 
 /* ------------------------------------------------ grouped GEMM (prefill) path
  * Replaces _gate_up_kernel / _down_kernel (vllm_xiaotu_moe/gpu_prefill.py:

@@ -10,11 +10,20 @@ from helpers import (bf16_tensor_to_bits, check_close, dense_to_numpy, make_dens
                      oracle_layer, random_routing)
 from xtu_moe_amd import _lib
 from xtu_moe_amd import formats as F
+from xtu_moe_amd import layer as L
 from xtu_moe_amd.layer import ExpertWeights, _p, _stream, moe_forward
 
 pytestmark = pytest.mark.gpu
 
 FMTS = [F.FMT_MXFP4, F.FMT_NVFP4, F.FMT_FP8, F.FMT_BF16]
+
+
+def _poison_scratch():
+    """Fill the layer's cached intermediate buffers with NaN so a row the
+    kernels fail to write shows up in the output."""
+    for t in L._BUF_CACHE.values():
+        if t.is_floating_point():
+            t.fill_(float("nan"))
 
 
 def _case(fmt, E, NS, H, I, T, K, seed=0, invalid=0.0, zero=0.0, limit=0.0, path="auto",
@@ -25,6 +34,7 @@ def _case(fmt, E, NS, H, I, T, K, seed=0, invalid=0.0, zero=0.0, limit=0.0, path
     ids, wts = random_routing(T, K, E, seed=seed + 1, invalid_frac=invalid, zero_frac=zero)
     g = torch.Generator().manual_seed(seed + 2)
     x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+    _poison_scratch()
     out = moe_forward(x.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(), W,
                       swiglu_limit=limit, path=path, out_dtype=out_dtype)
     torch.cuda.synchronize()

@@ -1,24 +1,33 @@
 // Skinny-M (decode) expert kernels: a handful of tokens per expert, so the
-// layer is a weight stream.  Every wave reads one contiguous KiB of its
-// panel per step (16 bytes per lane, the P16 layout), dequantises it in
-// registers to bf16 and feeds v_mfma_f32_16x16x32_bf16 with the expert's
-// tokens as the 16-row A operand (rows beyond the expert's token count are
-// zero).  The K range of a panel is split over KSPLIT waves of the same
-// workgroup and reduced through LDS in a fixed order, so results are
-// deterministic.  Empty expert slots (beyond n_active) exit at once; experts
-// nobody routed to (or only with zero weight) are never read.
+// layer is a weight stream.  A wave owns a contiguous range of 128-k units of
+// one 16-row panel; it issues the loads of up to NU units at once (one
+// contiguous KiB per format chunk: 16 bytes per lane, the P16 layout), then
+// consumes them in issue order: dequantise in registers to bf16 and feed
+// v_mfma_f32_16x16x32_bf16 with the expert's tokens as the 16-row A operand
+// (from LDS).  The code of one round is straight-line, so every wait is for
+// exactly the unit about to be used.
 //
-// gate/up: one workgroup per (gate panel p, active expert); waves [0,KSPLIT)
-//   stream gate rows 16p.., waves [KSPLIT, 2KSPLIT) the matching up rows
-//   I+16p.., so the SwiGLU of row n is formed in the reduction step and only
-//   the bf16 activation row is written.
-// down:    one workgroup per (PPB panels of W2, active expert); y is fp32.
+// One workgroup per work item: (active expert, gate panel) for gate/up,
+// (active expert, PPB panels of W2) for down.  Expert slots beyond n_active
+// exit at once; experts nobody routed to (or only with zero weight) are never
+// read.  The K range of a panel is split over KSPLIT waves and reduced through
+// LDS in a fixed order, so results are deterministic.  A lane whose token
+// slot is empty reads any staged row: MFMA output row m depends on A row m
+// only, and rows beyond the expert's token count are never written.
+//
+// gate/up: waves [0,KSPLIT) stream gate rows 16p.., waves [KSPLIT, 2KSPLIT)
+//   the matching up rows I+16p.., so the SwiGLU of row n is formed in the
+//   reduction step and only the bf16 activation row is written.
+// down: y is fp32; with KSPLIT = 1 each wave writes its panel directly.
 #include "weight_format.hpp"
 
 namespace xtu {
 namespace {
 
 constexpr int kWave = 64;
+constexpr int kMaxTok = 16;             // tokens per expert on this path
+constexpr int kLdsBudget = 72 * 1024;   // bytes of staged rows per workgroup
+constexpr int kRegChunks = 4;           // 16-byte row pieces per thread staged through registers
 
 struct DecodeArgs {
   const uint16_t* x;         // gate/up: hidden rows [T][H]; down: act rows [A][I]
@@ -31,411 +40,459 @@ struct DecodeArgs {
   const int32_t* n_active;
   const int32_t* slot_map;   // expert -> weight slot (null: identity)
   void* out;                 // gate/up: act bf16 [A][I]; down: y fp32 [A][H]
-  int H, I;
+  int T, H, I;
   long w_estride, s_estride;
   float limit, alpha, beta;
-  const float* sorted_wts;   // down+combine: pair weight per sorted row
-  int lds_rows;              // activation rows staged in LDS (<= kLdsRows)
+  int rows;                  // rows the LDS stage holds
+  int ksplit, ppb;           // waves per panel K range; panels per workgroup (down)
 };
 
-// Activation rows of one expert staged in LDS: rows m < min(na, kLdsRows) of
-// length K (bf16); rows kLdsRows <= m < na are read from global memory.
-constexpr int kLdsRows = 4;
+// Units issued per round: about 80 VGPRs of weights in flight per wave, and
+// fewer than 64 outstanding vector-memory instructions.
+template <int FMT>
+constexpr int round_units() {
+  return FMT == kBF16 ? 4 : (FMT == kFP8 ? 8 : 16);
+}
 
-// launch shape (waves per workgroup split K; D = 128-k units in flight per wave)
-#ifndef XTU_GU_KSPLIT
-#define XTU_GU_KSPLIT 4
-#endif
-#ifndef XTU_GU_D
-#define XTU_GU_D 4
-#endif
-#ifndef XTU_GU_MAXGRID
-#define XTU_GU_MAXGRID 1024
-#endif
-#ifndef XTU_DN_KSPLIT
-#define XTU_DN_KSPLIT 2
-#endif
-#ifndef XTU_DN_PPB
-#define XTU_DN_PPB 2
-#endif
-#ifndef XTU_DN_D
-#define XTU_DN_D 4
-#endif
-#ifndef XTU_DN_MAXGRID
-#define XTU_DN_MAXGRID 2048
-#endif
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+}
 
-// One batch of D 128-k units of a panel held in registers: weight chunks, raw
-// scale bits, and (FP8) the block scale of each unit.
-template <int FMT, int D>
-struct WBatch {
-  u32x4_t raw[D][WFmt<FMT>::kSPU];
-  uint32_t sraw[D][WFmt<FMT>::kSPU];
-  float bsc[D];
-};
+// Buffer resource dword 3 for raw (untyped, stride-0) buffers on gfx9-class
+// parts.  Loads past num_records return zero instead of touching memory.
+constexpr int kRawBufferFlags = 0x00020000;
+constexpr int kAuxNontemporal = 2;
 
-// Stream position of one wave inside one panel of one expert.
-struct PanelPos {
-  const uint8_t* wp;   // this lane's bytes in (panel, super-block 0)
-  const uint8_t* sp;   // expert's scale array
-  long sbase;          // panel * super-blocks per row
-  int panel, K_total;
+// Wave-uniform buffer descriptors of one panel's weight stream.
+template <int FMT>
+struct Stream {
+  __amdgpu_buffer_rsrc_t w;   // the panel's super-blocks
+  __amdgpu_buffer_rsrc_t s;   // fp4: the panel's scale groups; fp8: its block-scale row
 };
 
 template <int FMT>
-__device__ __forceinline__ PanelPos panel_pos(const DecodeArgs& a, int ws, int panel, int K_total,
-                                              int lane) {
+__device__ __forceinline__ Stream<FMT> make_stream(const DecodeArgs& a, int ws, int panel, int K) {
   using F = WFmt<FMT>;
-  const long nsbk = K_total / F::kSB;
-  PanelPos p;
-  p.wp = a.w + (long)ws * a.w_estride + ((long)panel * nsbk) * 1024 + lane * 16;
-  p.sp = a.s + (long)ws * a.s_estride;
-  p.sbase = (long)panel * nsbk;
-  p.panel = panel;
-  p.K_total = K_total;
-  return p;
+  const long nsb = K / F::kSB;
+  const uint8_t* sx = a.s + (long)ws * a.s_estride;
+  Stream<FMT> st;
+  st.w = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.w + (long)ws * a.w_estride + (long)panel * nsb * 1024), 0, (int)(nsb * 1024),
+      kRawBufferFlags);
+  if constexpr (FMT == kMXFP4 || FMT == kNVFP4) {
+    const long gbytes = scale_groups(K, F::kUG) * 1024;
+    st.s = __builtin_amdgcn_make_buffer_rsrc((void*)(sx + (long)panel * gbytes), 0, (int)gbytes,
+                                             kRawBufferFlags);
+  } else if constexpr (FMT == kFP8) {
+    st.s = __builtin_amdgcn_make_buffer_rsrc((void*)(sx + (long)(panel / 8) * (K / 128) * 4), 0,
+                                             (K / 128) * 4, kRawBufferFlags);
+  } else {
+    st.s = st.w;
+  }
+  return st;
 }
 
-// Issue the loads of units [ub, ub + D) (units >= u1 re-read unit ub, unused).
-template <int FMT, int D>
-__device__ __forceinline__ void issue_batch(WBatch<FMT, D>& b, const PanelPos& p, int ub, int u1,
-                                            int lane) {
+// One round of one lane: the weight chunks of NU units and their scales.
+// fp4: the 16-byte scale groups covering the round, rotated so that unit i's
+// scale sits at byte i * kSBY of sw; fp8: lane l holds the block scale of
+// unit ub + l.
+template <int FMT, int NU>
+struct Round {
   using F = WFmt<FMT>;
+  static constexpr int kGroups = F::kSBY ? (15 + NU * F::kSBY + 15) / 16 : 0;
+  u32x4_t w[NU][F::kSPU];
+  uint32_t sw[kGroups > 0 ? 4 * kGroups : 1];
+  float bsv;
+};
+
+// Loads of the round [ub, min(ub + NU, u1)): scales first, then weights, all
+// unconditional (an index past the range re-reads unit u1 - 1, which is never
+// consumed twice), so the wait counts stay exact.
+template <int FMT, int NU>
+__device__ __forceinline__ void issue_round(Round<FMT, NU>& r, const Stream<FMT>& st, int ub,
+                                            int u1, uint32_t lane) {
+  using F = WFmt<FMT>;
+  if constexpr (Round<FMT, NU>::kGroups > 0) {
+    const int g0 = ub / F::kUG;
 #pragma unroll
-  for (int i = 0; i < D; ++i) {
-    const int u = (ub + i < u1) ? ub + i : ub;
-#pragma unroll
-    for (int j = 0; j < F::kSPU; ++j) {
-      const long sb = (long)u * F::kSPU + j;
-      b.raw[i][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.wp + sb * 1024));
-      b.sraw[i][j] = load_chunk_scale_raw<FMT>(p.sp, p.sbase + sb, lane);
+    for (int j = 0; j < Round<FMT, NU>::kGroups; ++j) {
+      const u32x4_t v = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(st.s, (int)lane * 16, (g0 + j) * 1024,
+                                                         kAuxNontemporal));
+      r.sw[4 * j] = v[0];
+      r.sw[4 * j + 1] = v[1];
+      r.sw[4 * j + 2] = v[2];
+      r.sw[4 * j + 3] = v[3];
     }
-    if constexpr (FMT == kFP8)
-      b.bsc[i] = reinterpret_cast<const float*>(p.sp)[(long)(p.panel / 8) * (p.K_total / 128) + u];
+  } else if constexpr (FMT == kFP8) {
+    r.bsv = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(st.s, (int)lane * 4, ub * 4, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int u = ub + i < u1 ? ub + i : u1 - 1;
+#pragma unroll
+    for (int j = 0; j < F::kSPU; ++j)
+      r.w[i][j] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(st.w, (int)lane * 16,
+                                                         (u * F::kSPU + j) * 1024,
+                                                         kAuxNontemporal));
   }
 }
 
-// MFMA the batch into acc.  The activation fragment of lane (q, m) for unit
-// u, step st is row m, k = u*128 + q*kCK + 8*st (fp4; likewise for the other
-// formats through kSB / kCK): from LDS (LDS_ONLY: row index clamped to the
-// zero row) or, for rows beyond the staged ones, from global memory.
-template <int FMT, int D, bool LDS_ONLY>
-__device__ __forceinline__ void compute_batch(const WBatch<FMT, D>& b, f32x4_t& acc,
-                                              const uint16_t* __restrict__ arow_z,
-                                              const uint16_t* __restrict__ arow_l,
-                                              const uint16_t* __restrict__ arow_g, int ub, int u1,
-                                              int q) {
+// Shift the scale words down by `off` bytes (wave-uniform, 0..15).
+template <int N>
+__device__ __forceinline__ void shift_bytes_down(uint32_t (&v)[N], int off) {
+  if (off & 4) {
+#pragma unroll
+    for (int j = 0; j < N - 1; ++j) v[j] = v[j + 1];
+    v[N - 1] = 0u;
+  }
+  if (off & 8) {
+#pragma unroll
+    for (int j = 0; j < N - 2; ++j) v[j] = v[j + 2];
+    v[N - 2] = v[N - 1] = 0u;
+  }
+  const int b = off & 3;
+  if (b) {
+#pragma unroll
+    for (int j = 0; j < N - 1; ++j) v[j] = __builtin_amdgcn_alignbyte(v[j + 1], v[j], b);
+    v[N - 1] >>= 8 * b;
+  }
+}
+
+// acc += x_rows (16 x 128) * W_unit^T (128 x 16) for unit u.  The A fragment
+// of lane (q, m) for step st of super-block j is row m at k = kb + q*kCK +
+// 8*st; xa points at that row's k = q*kCK in LDS, xg (if set) at the same
+// place in global memory for a row the stage does not hold.
+template <int FMT, bool LDS_ONLY>
+__device__ __forceinline__ void mma_unit(const u32x4_t (&w)[WFmt<FMT>::kSPU], uint32_t sraw,
+                                         float bs, f32x4_t& acc, int u, const uint16_t* xa,
+                                         const uint16_t* xg) {
   using F = WFmt<FMT>;
   constexpr int ST = F::kWords / 4;
+  f32x4_t part = {0.f, 0.f, 0.f, 0.f};
+  float s0, s1;
+  chunk_scale<FMT>(sraw, s0, s1);
 #pragma unroll
-  for (int i = 0; i < D; ++i) {
-    const int u = ub + i;
-    if (u >= u1) break;
-    f32x4_t part = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < F::kSPU; ++j) {
+    uint32_t words[F::kWords];
+    decode_chunk<FMT>(w[j], s0, s1, words);
+    const int kb = (u * F::kSPU + j) * F::kSB;
 #pragma unroll
-    for (int j = 0; j < F::kSPU; ++j) {
-      const long sb = (long)u * F::kSPU + j;
-      uint32_t words[F::kWords];
-      float s0, s1;
-      chunk_scale<FMT>(b.sraw[i][j], s0, s1);
-      decode_chunk<FMT>(b.raw[i][j], s0, s1, words);
-#pragma unroll
-      for (int st = 0; st < ST; ++st) {
-        const long k = sb * F::kSB + q * F::kCK + 8 * st;
-        u32x4_t av = {0u, 0u, 0u, 0u};
-        if constexpr (LDS_ONLY) {
-          av = *reinterpret_cast<const u32x4_t*>(arow_z + k);
-        } else {
-          if (arow_l) av = *reinterpret_cast<const u32x4_t*>(arow_l + k);
-          else if (arow_g) av = *reinterpret_cast<const u32x4_t*>(arow_g + k);
-        }
-        const bf16x8_t bv = as_bf16x8(words[4 * st], words[4 * st + 1], words[4 * st + 2],
-                                      words[4 * st + 3]);
-        if constexpr (FMT == kFP8)
-          part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), bv, part, 0, 0, 0);
-        else
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), bv, acc, 0, 0, 0);
+    for (int st = 0; st < ST; ++st) {
+      u32x4_t av;
+      if constexpr (LDS_ONLY) {
+        av = *reinterpret_cast<const u32x4_t*>(xa + kb + 8 * st);
+      } else {
+        if (xg) av = *reinterpret_cast<const u32x4_t*>(xg + kb + 8 * st);
+        else av = *reinterpret_cast<const u32x4_t*>(xa + kb + 8 * st);
       }
+      const bf16x8_t bv = as_bf16x8(words[4 * st], words[4 * st + 1], words[4 * st + 2],
+                                    words[4 * st + 3]);
+      if constexpr (FMT == kFP8)
+        part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), bv, part, 0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), bv, acc, 0, 0, 0);
     }
-    if constexpr (FMT == kFP8) {
-      // one fp32 block scale per (128 rows, 128 k): exact fp32 promotion
+  }
+  if constexpr (FMT == kFP8) {
+    // one fp32 block scale per (128 rows, 128 k): exact fp32 promotion
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(b.bsc[i], part[r], acc[r]);
+    for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(bs, part[i], acc[i]);
+  }
+}
+
+template <int FMT, int NU, bool LDS_ONLY>
+__device__ __forceinline__ void consume_round(Round<FMT, NU>& r, f32x4_t& acc, int ub, int u1,
+                                              const uint16_t* xa, const uint16_t* xg) {
+  using F = WFmt<FMT>;
+  if constexpr (Round<FMT, NU>::kGroups > 0) shift_bytes_down(r.sw, (ub % F::kUG) * F::kSBY);
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    if (ub + i < u1) {
+      uint32_t sraw = 0u;
+      float bs = 1.0f;
+      if constexpr (FMT == kMXFP4) sraw = r.sw[i / 4] >> (8 * (i % 4));
+      else if constexpr (FMT == kNVFP4) sraw = r.sw[i / 2] >> (16 * (i % 2));
+      else if constexpr (FMT == kFP8)
+        bs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r.bsv), i));
+      mma_unit<FMT, LDS_ONLY>(r.w[i], sraw, bs, acc, ub + i, xa, xg);
     }
   }
 }
 
-// Finish a panel whose first batch (units [u0, u0 + D)) is already in flight
-// in b0: a two-buffer pipeline keeps the next batch's loads issued while the
-// current one is computed.
-template <int FMT, int D, bool LDS_ONLY>
-__device__ __forceinline__ f32x4_t panel_finish(WBatch<FMT, D>& b0, const PanelPos& p,
-                                                const DecodeArgs& a, const uint16_t* xs,
-                                                const uint16_t* xg, int na, int u0, int u1,
-                                                int lane) {
-  const int q = lane / 16, m = lane % 16;
-  const uint16_t* arow_z = xs + (m < na ? m : a.lds_rows) * p.K_total;
-  const uint16_t* arow_l = (m < na && m < a.lds_rows) ? xs + m * p.K_total : nullptr;
-  const uint16_t* arow_g = (m < na && m >= a.lds_rows) ? xg + (long)m * p.K_total : nullptr;
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  WBatch<FMT, D> b1;
-  for (int ub = u0; ub < u1; ub += 2 * D) {
-    if (ub + D < u1) issue_batch<FMT, D>(b1, p, ub + D, u1, lane);
-    compute_batch<FMT, D, LDS_ONLY>(b0, acc, arow_z, arow_l, arow_g, ub, u1, q);
-    if (ub + 2 * D < u1) issue_batch<FMT, D>(b0, p, ub + 2 * D, u1, lane);
-    if (ub + D < u1) compute_batch<FMT, D, LDS_ONLY>(b1, acc, arow_z, arow_l, arow_g, ub + D, u1, q);
+// Rounds after the first (shapes with more than NU units per wave).
+template <int FMT, int NU, bool LDS_ONLY>
+__device__ __forceinline__ f32x4_t more_rounds(f32x4_t acc, const Stream<FMT>& st, int ub, int u1,
+                                               uint32_t lane, const uint16_t* xa,
+                                               const uint16_t* xg) {
+  for (; ub < u1; ub += NU) {
+    Round<FMT, NU> r;
+    issue_round<FMT, NU>(r, st, ub, u1, lane);
+    consume_round<FMT, NU, LDS_ONLY>(r, acc, ub, u1, xa, xg);
   }
   return acc;
 }
 
-// Copy rows src_row(r), r < nr, each K bf16 long, into xs; row zero_row is zero.
-template <typename RowFn>
-__device__ __forceinline__ void stage_rows(uint16_t* xs, int nr, int zero_row, int K,
-                                           RowFn src_row) {
-  const int per_row = K / 8;   // 16-byte pieces
-  for (int c = threadIdx.x; c < nr * per_row; c += blockDim.x) {
-    const int r = c / per_row, k = (c % per_row) * 8;
-    *reinterpret_cast<u32x4_t*>(xs + r * K + k) = *reinterpret_cast<const u32x4_t*>(src_row(r) + k);
-  }
-  const u32x4_t z = {0u, 0u, 0u, 0u};
-  for (int c = threadIdx.x; c < per_row; c += blockDim.x)
-    *reinterpret_cast<u32x4_t*>(xs + zero_row * K + c * 8) = z;
+struct Item {
+  int e, r0, na, ws, sub;
+};
+
+__device__ __forceinline__ Item item_at(const DecodeArgs& a, int it, int per_expert) {
+  Item c;
+  const int slot = it / per_expert;
+  c.sub = it - slot * per_expert;
+  c.e = a.active[slot];
+  c.r0 = a.seg_start[c.e];
+  c.na = min(a.seg_start[c.e + 1] - c.r0, kMaxTok);
+  c.ws = a.slot_map ? a.slot_map[c.e] : c.e;
+  return c;
 }
 
-template <int FMT, int KSPLIT, int D>
-__global__ __launch_bounds__(128 * KSPLIT) void decode_gate_up_kernel(DecodeArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs_dyn[];   // kLdsRows x H
-  __shared__ f32x4_t red[2 * KSPLIT][kWave];
-  const int npan = a.I / 16;
-  const int items = a.n_active[0] * npan;   // (active expert, gate panel) pairs
-  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int half = w / KSPLIT, ks = w % KSPLIT;
-  const int nunits = a.H / 128;
-  const int u0 = ks * nunits / KSPLIT, u1 = (ks + 1) * nunits / KSPLIT;
-  int cur_e = -1;
-  for (int it = blockIdx.x; it < items; it += gridDim.x) {   // uniform loop bound
-    const int slot = it / npan, p = it % npan;
-    const int e = a.active[slot];
-    const int r0 = a.seg_start[e];
-    const int na = min(a.seg_start[e + 1] - r0, 16);
-    const int panel = half ? (npan + p) : p;
-    const int ws = a.slot_map ? a.slot_map[e] : e;
-    const PanelPos pos = panel_pos<FMT>(a, ws, panel, a.H, lane);
-    WBatch<FMT, D> b0;
-    issue_batch<FMT, D>(b0, pos, u0, u1, lane);   // in flight while the rows are staged
-    if (e != cur_e) {   // uniform: stage this expert's token rows once
-      __syncthreads();
-      stage_rows(xs_dyn, min(na, a.lds_rows), a.lds_rows, a.H,
-                 [&](int r) { return a.x + (long)a.sorted_tok[r0 + r] * a.H; });
-      __syncthreads();
-      cur_e = e;
-    }
-    const int m = lane % 16;
-    const uint16_t* xg = (m < na && m >= a.lds_rows) ? a.x + (long)a.sorted_tok[r0 + m] * a.H - (long)m * a.H : nullptr;
-    if (na <= a.lds_rows)   // uniform per item
-      red[w][lane] = panel_finish<FMT, D, true>(b0, pos, a, xs_dyn, xg, na, u0, u1, lane);
-    else
-      red[w][lane] = panel_finish<FMT, D, false>(b0, pos, a, xs_dyn, xg, na, u0, u1, lane);
-    __syncthreads();
-    const int t = threadIdx.x;
-    if (t < 256) {
-      const int mm = t / 16, n = t % 16;
-      if (mm < na) {
-        const int l = (mm / 4) * 16 + n, i = mm % 4;
-        float g = 0.f, u = 0.f;
+// Store the register-staged row pieces (piece index threadIdx.x + j*blockDim)
+// and copy any remaining pieces directly.
+template <typename SrcFn>
+__device__ __forceinline__ void finish_stage(uint16_t* xs, const u32x4_t (&xv)[kRegChunks],
+                                             int nchunks, SrcFn src) {
 #pragma unroll
-        for (int k = 0; k < KSPLIT; ++k) {
-          g += red[k][l][i];
-          u += red[KSPLIT + k][l][i];
-        }
-        if constexpr (FMT == kNVFP4) {
-          const float gsv = a.gs ? a.gs[ws] : 1.0f;
-          g *= gsv;
-          u *= gsv;
-        }
-        uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
-        act[(long)(r0 + mm) * a.I + 16 * p + n] = f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
-      }
-    }
-    __syncthreads();   // red is rewritten by the next item
+  for (int j = 0; j < kRegChunks; ++j) {
+    const int c = threadIdx.x + j * blockDim.x;
+    if (c < nchunks) *reinterpret_cast<u32x4_t*>(xs + c * 8) = xv[j];
   }
+  for (int c = threadIdx.x + kRegChunks * blockDim.x; c < nchunks; c += blockDim.x)
+    *reinterpret_cast<u32x4_t*>(xs + c * 8) = *reinterpret_cast<const u32x4_t*>(src(c));
 }
 
-template <int FMT, int KSPLIT, int PPB, int D>
-__global__ __launch_bounds__(64 * KSPLIT * PPB) void decode_down_kernel(DecodeArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs_dyn[];   // kLdsRows x I
-  __shared__ f32x4_t red[KSPLIT * PPB][kWave];
-  const int npb = a.H / 16 / PPB;
-  const int items = a.n_active[0] * npb;
-  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int pp = w / KSPLIT, ks = w % KSPLIT;
-  const int nunits = a.I / 128;
-  const int u0 = ks * nunits / KSPLIT, u1 = (ks + 1) * nunits / KSPLIT;
-  int cur_e = -1;
-  for (int it = blockIdx.x; it < items; it += gridDim.x) {
-    const int slot = it / npb, pb = it % npb;
-    const int e = a.active[slot];
-    const int r0 = a.seg_start[e];
-    const int na = min(a.seg_start[e + 1] - r0, 16);
-    const int ws = a.slot_map ? a.slot_map[e] : e;
-    const int panel = pb * PPB + pp;
-    const PanelPos pos = panel_pos<FMT>(a, ws, panel, a.I, lane);
-    WBatch<FMT, D> b0;
-    issue_batch<FMT, D>(b0, pos, u0, u1, lane);
-    if (e != cur_e) {
-      __syncthreads();
-      stage_rows(xs_dyn, min(na, a.lds_rows), a.lds_rows, a.I,
-                 [&](int r) { return a.x + (long)(r0 + r) * a.I; });
-      __syncthreads();
-      cur_e = e;
-    }
-    const uint16_t* xg = a.x + (long)r0 * a.I;
-    if (na <= a.lds_rows)
-      red[w][lane] = panel_finish<FMT, D, true>(b0, pos, a, xs_dyn, xg, na, u0, u1, lane);
-    else
-      red[w][lane] = panel_finish<FMT, D, false>(b0, pos, a, xs_dyn, xg, na, u0, u1, lane);
-    __syncthreads();
-    float gsv = 1.0f;
-    if constexpr (FMT == kNVFP4) gsv = a.gs ? a.gs[ws] : 1.0f;
-    float* y = reinterpret_cast<float*>(a.out);
-    for (int t = threadIdx.x; t < PPB * 256; t += 64 * KSPLIT * PPB) {
-      const int pq = t / 256, mm = (t % 256) / 16, n = t % 16;
-      if (mm < na) {
-        const int l = (mm / 4) * 16 + n, i = mm % 4;
-        float v = 0.f;
-#pragma unroll
-        for (int k = 0; k < KSPLIT; ++k) v += red[pq * KSPLIT + k][l][i];
-        y[(long)(r0 + mm) * a.H + 16 * (pb * PPB + pq) + n] = v * gsv;
-      }
-    }
-    __syncthreads();
-  }
-}
-
-template <int FMT, int NW, int UNR>
-__global__ __launch_bounds__(64 * NW) void decode_down_combine_kernel(DecodeArgs a, int T,
-                                                                      int out_bf16) {
+// GENERIC: more than one round per wave, or token rows beyond the stage; the
+// fast instantiation holds neither (the host checks the shape) and stages the
+// batch's T rows through XC register pieces per thread.
+template <int FMT, bool GENERIC, int XC>
+__global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
   using F = WFmt<FMT>;
-  constexpr int ST = F::kWords / 4;
-  __shared__ float acc_s[NW][16][16];
-  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int panel = blockIdx.x;
-  for (int i = threadIdx.x; i < NW * 256; i += 64 * NW) (&acc_s[0][0][0])[i] = 0.f;
-  __syncthreads();
-  const int nu = a.I / 128;
-  const int items = a.n_active[0] * nu;
-  const int q = lane / 16, tslot = lane % 16;
-  const long nsbk = a.I / F::kSB;
-  for (int jb = w; jb < items; jb += NW * UNR) {
-    u32x4_t raw[UNR][F::kSPU];
-    uint32_t sraw[UNR][F::kSPU];
-    u32x4_t av[UNR][F::kSPU][ST];
-    float bsc[UNR];
-    int tok[UNR][4];
-    float wt[UNR][4];
+  constexpr int NU = round_units<FMT>();
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // rows x H
+  __shared__ f32x4_t red[8][kWave];
+  const int npan = a.I / 16;
+  if ((int)blockIdx.x >= a.n_active[0] * npan) return;   // whole workgroup
+  const int ksplit = a.ksplit;
+  const int w = wave_id();
+  const uint32_t lane = threadIdx.x % kWave;
+  const int half = w / ksplit, ks = w - half * ksplit;
+  const int nunits = a.H / 128;
+  const int u0 = ks * nunits / ksplit, u1 = (ks + 1) * nunits / ksplit;
+  const int q = lane / 16, m = lane % 16;
+  const Item c = item_at(a, blockIdx.x, npan);
+  const int per_row = a.H / 8;        // 16-byte pieces per row
+  const Stream<FMT> st = make_stream<FMT>(a, c.ws, half ? npan + c.sub : c.sub, a.H);
+  Round<FMT, NU> r;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if (!GENERIC) {
+    // every token row of the batch is staged (x rows 0..T-1 are contiguous):
+    // lane m reads the row of its expert's m-th token.  Issue order: token
+    // ids, rows, weights, so the row stores wait for the rows only and the
+    // units are consumed as they arrive.
+    const int tok = a.sorted_tok[c.r0 + min(m, c.na - 1)];
+    const int nchunks = a.T * per_row;
+    u32x4_t xv[XC];
 #pragma unroll
-    for (int b = 0; b < UNR; ++b) {
-      const int j = jb + b * NW;
-      const bool ok = j < items;
-      const int slot = ok ? j / nu : 0, u = ok ? j % nu : 0;
-      const int e = a.active[slot];
-      const int r0 = a.seg_start[e];
-      const int na = ok ? min(a.seg_start[e + 1] - r0, 16) : 0;
-      const int ws = a.slot_map ? a.slot_map[e] : e;
-      const uint8_t* wp = a.w + (long)ws * a.w_estride + ((long)panel * nsbk) * 1024 + lane * 16;
-      const uint8_t* sp = a.s + (long)ws * a.s_estride;
-      const uint16_t* arow = tslot < na ? a.x + (long)(r0 + tslot) * a.I : nullptr;
-#pragma unroll
-      for (int jj = 0; jj < F::kSPU; ++jj) {
-        const long sb = (long)u * F::kSPU + jj;
-        const u32x4_t z = {0u, 0u, 0u, 0u};
-        raw[b][jj] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp + sb * 1024));
-        if (!ok) raw[b][jj] = z;
-        sraw[b][jj] = load_chunk_scale_raw<FMT>(sp, (long)panel * nsbk + sb, lane);
-#pragma unroll
-        for (int st = 0; st < ST; ++st) {
-          av[b][jj][st] = z;
-          if (arow) av[b][jj][st] = *reinterpret_cast<const u32x4_t*>(arow + sb * F::kSB + q * F::kCK + 8 * st);
-        }
-      }
-      bsc[b] = 1.0f;
-      if constexpr (FMT == kFP8)
-        if (ok) bsc[b] = reinterpret_cast<const float*>(sp)[(long)(panel / 8) * (a.I / 128) + u];
-      float gsv = 1.0f;
-      if constexpr (FMT == kNVFP4) gsv = (ok && a.gs) ? a.gs[ws] : 1.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = 4 * q + i;
-        tok[b][i] = (m < na) ? a.sorted_tok[r0 + m] : -1;
-        wt[b][i] = (m < na) ? a.sorted_wts[r0 + m] * gsv : 0.f;
-      }
+    for (int j = 0; j < XC; ++j) {
+      const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
+      xv[j] = *reinterpret_cast<const u32x4_t*>(a.x + (long)cc * 8);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    issue_round<FMT, NU>(r, st, u0, u1, lane);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int b = 0; b < UNR; ++b) {
-      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < XC; ++j) {
+      const int cc = threadIdx.x + j * blockDim.x;
+      if (cc < nchunks) *reinterpret_cast<u32x4_t*>(xs + cc * 8) = xv[j];
+    }
+    __syncthreads();
+    consume_round<FMT, NU, true>(r, acc, u0, u1, xs + tok * a.H + q * F::kCK, nullptr);
+  } else {
+    // the expert's first `rows` token rows are staged, the rest read from
+    // global memory; more than one round per wave when K needs it
+    const int nr = min(c.na, a.rows);
+    const int nchunks = nr * per_row;
+    int trow[kRegChunks];
 #pragma unroll
-      for (int jj = 0; jj < F::kSPU; ++jj) {
-        uint32_t words[F::kWords];
-        float s0, s1;
-        chunk_scale<FMT>(sraw[b][jj], s0, s1);
-        decode_chunk<FMT>(raw[b][jj], s0, s1, words);
+    for (int j = 0; j < kRegChunks; ++j) {
+      const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
+      trow[j] = a.sorted_tok[c.r0 + cc / per_row];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep the issue order: ids, weights, rows
+    issue_round<FMT, NU>(r, st, u0, u1, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4_t xv[kRegChunks];
 #pragma unroll
-        for (int st = 0; st < ST; ++st)
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              as_bf16x8(av[b][jj][st]),
-              as_bf16x8(words[4 * st], words[4 * st + 1], words[4 * st + 2], words[4 * st + 3]),
-              c, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (tok[b][i] >= 0) acc_s[w][tok[b][i]][lane % 16] += wt[b][i] * (bsc[b] * c[i]);
+    for (int j = 0; j < kRegChunks; ++j) {
+      const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
+      xv[j] = *reinterpret_cast<const u32x4_t*>(a.x + (long)trow[j] * a.H + (cc % per_row) * 8);
+    }
+    finish_stage(xs, xv, nchunks, [&](int cc) {
+      return a.x + (long)a.sorted_tok[c.r0 + cc / per_row] * a.H + (cc % per_row) * 8;
+    });
+    __syncthreads();
+    const uint16_t* xa = xs + (m < nr ? m : 0) * a.H + q * F::kCK;
+    if (c.na <= nr) {   // uniform: every token row is staged
+      consume_round<FMT, NU, true>(r, acc, u0, u1, xa, nullptr);
+      if (u0 + NU < u1) acc = more_rounds<FMT, NU, true>(acc, st, u0 + NU, u1, lane, xa, nullptr);
+    } else {
+      const uint16_t* xg =
+          (m < c.na && m >= nr) ? a.x + (long)a.sorted_tok[c.r0 + m] * a.H + q * F::kCK : nullptr;
+      consume_round<FMT, NU, false>(r, acc, u0, u1, xa, xg);
+      if (u0 + NU < u1) acc = more_rounds<FMT, NU, false>(acc, st, u0 + NU, u1, lane, xa, xg);
     }
   }
+  red[w][lane] = acc;
   __syncthreads();
-  for (int t = threadIdx.x; t < 256; t += 64 * NW) {
-    const int m = t / 16, n = t % 16;
-    if (m < T) {
+  for (int t = threadIdx.x; t < 256; t += blockDim.x) {   // 16 rows x 16 columns
+    const int mm = t / 16, n = t % 16;
+    if (mm < c.na) {
+      const int l = (mm / 4) * 16 + n, i = mm % 4;
+      float g = 0.f, u = 0.f;
+      for (int k = 0; k < ksplit; ++k) {
+        g += red[k][l][i];
+        u += red[ksplit + k][l][i];
+      }
+      if constexpr (FMT == kNVFP4) {
+        const float gsv = a.gs ? a.gs[c.ws] : 1.0f;
+        g *= gsv;
+        u *= gsv;
+      }
+      uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
+      act[(long)(c.r0 + mm) * a.I + 16 * c.sub + n] =
+          f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
+    }
+  }
+}
+
+template <int FMT, bool GENERIC>
+__global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
+  using F = WFmt<FMT>;
+  constexpr int NU = round_units<FMT>();
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // rows x I
+  __shared__ f32x4_t red[4][kWave];
+  const int ppb = a.ppb, ksplit = a.ksplit;
+  const int npb = a.H / 16 / ppb;
+  if ((int)blockIdx.x >= a.n_active[0] * npb) return;
+  const int w = wave_id();
+  const uint32_t lane = threadIdx.x % kWave;
+  const int pp = w / ksplit, ks = w - pp * ksplit;
+  const int nunits = a.I / 128;
+  const int u0 = ks * nunits / ksplit, u1 = (ks + 1) * nunits / ksplit;
+  const int q = lane / 16, m = lane % 16;
+  const Item c = item_at(a, blockIdx.x, npb);
+  const int nr = min(c.na, a.rows);
+  const int nchunks = nr * (a.I / 8);   // the expert's rows are contiguous
+  const uint16_t* xsrc = a.x + (long)c.r0 * a.I;
+
+  u32x4_t xv[kRegChunks];
+#pragma unroll
+  for (int j = 0; j < kRegChunks; ++j) {
+    const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
+    xv[j] = *reinterpret_cast<const u32x4_t*>(xsrc + cc * 8);
+  }
+  const int panel = c.sub * ppb + pp;
+  const Stream<FMT> st = make_stream<FMT>(a, c.ws, panel, a.I);
+  Round<FMT, NU> r;
+  __builtin_amdgcn_sched_barrier(0);   // keep the issue order: rows, weights
+  issue_round<FMT, NU>(r, st, u0, u1, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  finish_stage(xs, xv, nchunks, [&](int cc) { return xsrc + cc * 8; });
+  __syncthreads();
+
+  const uint16_t* xa = xs + (m < nr ? m : 0) * a.I + q * F::kCK;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if (!GENERIC) {
+    consume_round<FMT, NU, true>(r, acc, u0, u1, xa, nullptr);
+  } else if (c.na <= nr) {
+    consume_round<FMT, NU, true>(r, acc, u0, u1, xa, nullptr);
+    if (u0 + NU < u1) acc = more_rounds<FMT, NU, true>(acc, st, u0 + NU, u1, lane, xa, nullptr);
+  } else {
+    const uint16_t* xg = (m < c.na && m >= nr) ? xsrc + (long)m * a.I + q * F::kCK : nullptr;
+    consume_round<FMT, NU, false>(r, acc, u0, u1, xa, xg);
+    if (u0 + NU < u1) acc = more_rounds<FMT, NU, false>(acc, st, u0 + NU, u1, lane, xa, xg);
+  }
+  float gsv = 1.0f;
+  if constexpr (FMT == kNVFP4) gsv = a.gs ? a.gs[c.ws] : 1.0f;
+  float* y = reinterpret_cast<float*>(a.out);
+  if (ksplit == 1) {   // uniform: this wave holds the whole panel
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int mm = 4 * q + i;
+      if (mm < c.na) y[(long)(c.r0 + mm) * a.H + 16 * panel + m] = acc[i] * gsv;
+    }
+    return;
+  }
+  red[w][lane] = acc;
+  __syncthreads();
+  for (int t = threadIdx.x; t < ppb * 256; t += blockDim.x) {
+    const int pq = t / 256, mm = (t % 256) / 16, n = t % 16;
+    if (mm < c.na) {
+      const int l = (mm / 4) * 16 + n, i = mm % 4;
       float v = 0.f;
-#pragma unroll
-      for (int k = 0; k < NW; ++k) v += acc_s[k][m][n];
-      const long o = (long)m * a.H + 16 * panel + n;
-      if (out_bf16) reinterpret_cast<uint16_t*>(a.out)[o] = f32_to_bf16(v);
-      else reinterpret_cast<float*>(a.out)[o] = v;
+      for (int k = 0; k < ksplit; ++k) v += red[pq * ksplit + k][l][i];
+      y[(long)(c.r0 + mm) * a.H + 16 * (c.sub * ppb + pq) + n] = v * gsv;
     }
   }
+}
+
+// Smallest K split (1, 2, 4) that keeps every wave's share within one round.
+int pick_ksplit(int nunits, int nu, int max_split) {
+  int k = 1;
+  while (k < max_split && (nunits + k - 1) / k > nu) k *= 2;
+  return k;
 }
 
 template <int FMT>
 hipError_t launch_decode(int which, DecodeArgs a, int max_active, hipStream_t stream) {
   using F = WFmt<FMT>;
+  constexpr int NU = round_units<FMT>();
   if (which == 0) {
     if (!a.w_estride) a.w_estride = F::w_bytes(2L * a.I, a.H);
     if (!a.s_estride) a.s_estride = F::s_bytes(2L * a.I, a.H);
-    const int items = max_active * (a.I / 16);
-    constexpr int D = FMT == kBF16 ? 2 : (FMT == kFP8 ? XTU_GU_D / 2 : XTU_GU_D);
-    const size_t lds = (size_t)(a.lds_rows + 1) * a.H * sizeof(uint16_t);
-    decode_gate_up_kernel<FMT, XTU_GU_KSPLIT, D>
-        <<<dim3(items < XTU_GU_MAXGRID ? items : XTU_GU_MAXGRID), 128 * XTU_GU_KSPLIT, lds, stream>>>(a);
+    const int row_bytes = a.H * 2;
+    const int cap = kLdsBudget / row_bytes;
+    a.rows = a.T < cap ? a.T : cap;
+    if (a.rows < 1) return hipErrorInvalidValue;
+    a.ksplit = pick_ksplit(a.H / 128, NU, 4);
+    a.ppb = 1;
+    const long items = (long)max_active * (a.I / 16);
+    const int bd = 128 * a.ksplit;
+    const long pieces = (long)a.T * (a.H / 8);   // 16-byte pieces of the batch's rows
+    const bool generic = a.T > a.rows || a.H / 128 > NU * a.ksplit || pieces > 8L * bd;
+    const size_t lds = (size_t)a.rows * row_bytes;
+    if (generic)
+      decode_gate_up_kernel<FMT, true, 1><<<dim3(items), bd, lds, stream>>>(a);
+    else if (pieces <= bd)
+      decode_gate_up_kernel<FMT, false, 1><<<dim3(items), bd, lds, stream>>>(a);
+    else if (pieces <= 2L * bd)
+      decode_gate_up_kernel<FMT, false, 2><<<dim3(items), bd, lds, stream>>>(a);
+    else if (pieces <= 4L * bd)
+      decode_gate_up_kernel<FMT, false, 4><<<dim3(items), bd, lds, stream>>>(a);
+    else
+      decode_gate_up_kernel<FMT, false, 8><<<dim3(items), bd, lds, stream>>>(a);
   } else {
     if (!a.w_estride) a.w_estride = F::w_bytes(a.H, a.I);
     if (!a.s_estride) a.s_estride = F::s_bytes(a.H, a.I);
-    const int items = max_active * (a.H / 16 / XTU_DN_PPB);
-    constexpr int D = FMT == kBF16 ? 2 : (FMT == kFP8 ? XTU_DN_D / 2 : XTU_DN_D);
-    const size_t lds = (size_t)(a.lds_rows + 1) * a.I * sizeof(uint16_t);
-    decode_down_kernel<FMT, XTU_DN_KSPLIT, XTU_DN_PPB, D>
-        <<<dim3(items < XTU_DN_MAXGRID ? items : XTU_DN_MAXGRID), 64 * XTU_DN_KSPLIT * XTU_DN_PPB,
-           lds, stream>>>(a);
+    const int row_bytes = a.I * 2;
+    const int cap = kLdsBudget / row_bytes;
+    const int tmax = a.T < kMaxTok ? a.T : kMaxTok;   // an expert holds at most T pairs
+    a.rows = tmax < cap ? tmax : cap;
+    if (a.rows < 1) return hipErrorInvalidValue;
+    a.ksplit = pick_ksplit(a.I / 128, NU, 4);
+    a.ppb = 4 / a.ksplit;
+    if ((a.H / 16) % a.ppb) a.ppb = 1;
+    const long items = (long)max_active * (a.H / 16 / a.ppb);
+    const bool generic = tmax > a.rows || a.I / 128 > NU * a.ksplit;
+    const size_t lds = (size_t)a.rows * row_bytes;
+    if (generic)
+      decode_down_kernel<FMT, true><<<dim3(items), 64 * a.ksplit * a.ppb, lds, stream>>>(a);
+    else
+      decode_down_kernel<FMT, false><<<dim3(items), 64 * a.ksplit * a.ppb, lds, stream>>>(a);
   }
-  return hipPeekAtLastError();
-}
-
-template <int FMT>
-hipError_t launch_down_combine(DecodeArgs a, int T, int out_bf16, hipStream_t stream) {
-  using F = WFmt<FMT>;
-  if (!a.w_estride) a.w_estride = F::w_bytes(a.H, a.I);
-  if (!a.s_estride) a.s_estride = F::s_bytes(a.H, a.I);
-  constexpr int UNR = FMT == kBF16 ? 2 : 4;
-  decode_down_combine_kernel<FMT, 8, UNR><<<dim3(a.H / 16), 512, 0, stream>>>(a, T, out_bf16);
   return hipPeekAtLastError();
 }
 
@@ -470,16 +527,15 @@ hipError_t xtu_decode_gate_up(int fmt, const void* x, int T, int H, int I, const
                               void* act, float limit, float alpha, float beta,
                               hipStream_t stream) {
   XTU_CHECK_ARG(shape_ok(fmt, H, I) && max_active >= 0 && max_active <= 65535 && T >= 0 &&
-                T <= 16);
+                T <= kMaxTok);
   XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(x && w13 && (fmt == kBF16 || s13) && sorted_tok && seg_start && active &&
                 n_active && act);
-  if (max_active == 0) return hipSuccess;
+  if (max_active == 0 || T == 0) return hipSuccess;
   (void)hipGetLastError();
   DecodeArgs a{(const uint16_t*)x, (const uint8_t*)w13, (const uint8_t*)s13, gs13, sorted_tok,
-               seg_start, active, n_active, slot_map, act, H, I, w_estride, s_estride, limit,
-               alpha, beta};
-  a.lds_rows = T < kLdsRows ? T : kLdsRows;
+               seg_start, active, n_active, slot_map, act, T, H, I, w_estride, s_estride, limit,
+               alpha, beta, 0, 1, 1};
   return dispatch_decode(fmt, 0, a, max_active, stream);
 }
 
@@ -488,42 +544,16 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
                            const int32_t* slot_map, const int32_t* seg_start,
                            const int32_t* active, const int32_t* n_active, int max_active,
                            float* y, hipStream_t stream) {
-  XTU_CHECK_ARG(shape_ok(fmt, H, I) && max_active >= 0 && max_active <= 65535 &&
-                (H / 16) % XTU_DN_PPB == 0 && T >= 0 && T <= 16);
+  XTU_CHECK_ARG(shape_ok(fmt, H, I) && max_active >= 0 && max_active <= 65535 && T >= 0 &&
+                T <= kMaxTok);
   XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(act && w2 && (fmt == kBF16 || s2) && seg_start && active && n_active && y);
-  if (max_active == 0) return hipSuccess;
+  if (max_active == 0 || T == 0) return hipSuccess;
   (void)hipGetLastError();
   DecodeArgs a{(const uint16_t*)act, (const uint8_t*)w2, (const uint8_t*)s2, gs2, nullptr,
-               seg_start, active, n_active, slot_map, y, H, I, w_estride, s_estride, 0.f, 1.f,
-               0.f};
-  a.lds_rows = T < kLdsRows ? T : kLdsRows;
+               seg_start, active, n_active, slot_map, y, T, H, I, w_estride, s_estride, 0.f, 1.f,
+               0.f, 0, 1, 1};
   return dispatch_decode(fmt, 1, a, max_active, stream);
-}
-
-hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int H, int I, const void* w2,
-                                   const void* s2, const float* gs2, long w_estride,
-                                   long s_estride, const int32_t* slot_map,
-                                   const int32_t* sorted_tok, const float* sorted_wts,
-                                   const int32_t* seg_start, const int32_t* active,
-                                   const int32_t* n_active, void* out, int out_bf16,
-                                   hipStream_t stream) {
-  XTU_CHECK_ARG(shape_ok(fmt, H, I) && T >= 0 && T <= 16 && w_estride >= 0 && s_estride >= 0);
-  XTU_CHECK_ARG(act && w2 && (fmt == kBF16 || s2) && sorted_tok && sorted_wts && seg_start &&
-                active && n_active && out);
-  if (T == 0) return hipSuccess;
-  (void)hipGetLastError();
-  DecodeArgs a{(const uint16_t*)act, (const uint8_t*)w2, (const uint8_t*)s2, gs2, sorted_tok,
-               seg_start, active, n_active, slot_map, out, H, I, w_estride, s_estride, 0.f, 1.f,
-               0.f};
-  a.sorted_wts = sorted_wts;
-  switch (fmt) {
-    case kMXFP4: return launch_down_combine<kMXFP4>(a, T, out_bf16, stream);
-    case kNVFP4: return launch_down_combine<kNVFP4>(a, T, out_bf16, stream);
-    case kFP8: return launch_down_combine<kFP8>(a, T, out_bf16, stream);
-    case kBF16: return launch_down_combine<kBF16>(a, T, out_bf16, stream);
-  }
-  return hipErrorInvalidValue;
 }
 
 }  // extern "C"

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a) {
       const uint8_t* region = wexp + (bpanel[i] * nsbk + sb) * 1024 + qbase * 256;
       breg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(region + boff[i] * 16));
       const int lane_eq = qbase * 16 + boff[i];   // (q, r) position inside the super-block
-      bsraw[i] = load_chunk_scale_raw<FMT>(sexp, bpanel[i] * nsbk + sb, lane_eq);
+      bsraw[i] = load_chunk_scale_raw<FMT>(sexp, bpanel[i], sb, lane_eq, K);
     }
   };
   auto lstore = [&]() {

@@ -27,7 +27,7 @@ __device__ __forceinline__ int w4_of(uint32_t nib) {
   return (nib & 8) ? -mag : mag;
 }
 
-// per row n: emin = min over its K/32 e8m0 scale bytes (packed P16 scale layout)
+// per row n: emin = min over its K/32 e8m0 scale bytes (packed scale groups)
 __global__ __launch_bounds__(256) void i8_emin_kernel(const uint8_t* __restrict__ s, int N, int K,
                                                       long s_estride, uint8_t* __restrict__ emin,
                                                       int32_t* __restrict__ dmax) {
@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void i8_emin_kernel(const uint8_t* __restrict_
   int mn = 255, mx = 0;
   for (long sb = 0; sb < nsbk; ++sb)
     for (int q = 0; q < 4; ++q) {
-      const int b = se[((long)p * nsbk + sb) * 64 + q * 16 + r];
+      const int b = se[scale_offset<kMXFP4>(p, sb, q * 16 + r, K)];
       mn = min(mn, b);
       mx = max(mx, b);
     }
@@ -66,7 +66,7 @@ __global__ __launch_bounds__(256) void i8_expand_kernel(const uint8_t* __restric
   const int q4 = (int)(rem % 64) / 16, r = (int)(rem % 16);
   const int n = (int)(p * 16 + r);
   const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(w + (long)e * w_estride + c * 16);
-  const int b = s[(long)e * s_estride + (p * nsb4 + sb4) * 64 + q4 * 16 + r];
+  const int b = s[(long)e * s_estride + scale_offset<kMXFP4>(p, sb4, q4 * 16 + r, K)];
   const int d = b - emin[(long)e * N + n];
   const int k0 = (int)(sb4 * 128 + q4 * 32);
   uint32_t outw[8];
@@ -315,7 +315,8 @@ hipError_t xtu_i8_prepare(const void* w, const void* s, int E, int N, int K, voi
   XTU_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0);
   XTU_CHECK_ARG(w && s && w8 && emin && dmax);
   (void)hipGetLastError();
-  const long w_es = (long)N * K / 2, s_es = (long)N * K / 32, w8_es = (long)N * K;
+  const long w_es = WFmt<kMXFP4>::w_bytes(N, K), s_es = WFmt<kMXFP4>::s_bytes(N, K),
+             w8_es = (long)N * K;
   i8_emin_kernel<<<dim3((N + 255) / 256, E), 256, 0, stream>>>((const uint8_t*)s, N, K, s_es,
                                                                (uint8_t*)emin, dmax);
   const long nch = (long)N * K / 32;

@@ -9,6 +9,12 @@ namespace xtu {
 template <int FMT>
 struct WFmt;
 
+// fp4 scale groups: per panel, the scales of kUG consecutive super-blocks
+// are stored [64 lanes][16 bytes] (lane = 16q + r: chunk q of row r), so one
+// 16-byte load gives a lane the scales of kUG super-blocks.  Groups per panel:
+// ceil((K/128) / kUG); the last group is zero-padded.
+__host__ __device__ constexpr long scale_groups(long K, int ug) { return (K / 128 + ug - 1) / ug; }
+
 // MXFP4: 32 e2m1 codes per chunk, one e8m0 byte per chunk.
 template <>
 struct WFmt<kMXFP4> {
@@ -16,8 +22,12 @@ struct WFmt<kMXFP4> {
   static constexpr int kWords = 16;    // bf16 pairs per chunk
   static constexpr int kSB = 128;      // k per super-block (4 chunks)
   static constexpr int kSPU = 1;       // super-blocks per 128-k unit
+  static constexpr int kSBY = 1;       // scale bytes per chunk
+  static constexpr int kUG = 16;       // super-blocks per scale group
   static __host__ __device__ constexpr long w_bytes(long N, long K) { return N * K / 2; }
-  static __host__ __device__ constexpr long s_bytes(long N, long K) { return N * K / 32; }
+  static __host__ __device__ constexpr long s_bytes(long N, long K) {
+    return N / 16 * scale_groups(K, kUG) * 1024;
+  }
 };
 
 // NVFP4: 32 e2m1 codes per chunk, two e4m3 bytes (one per 16 k) per chunk,
@@ -28,8 +38,12 @@ struct WFmt<kNVFP4> {
   static constexpr int kWords = 16;
   static constexpr int kSB = 128;
   static constexpr int kSPU = 1;
+  static constexpr int kSBY = 2;
+  static constexpr int kUG = 8;
   static __host__ __device__ constexpr long w_bytes(long N, long K) { return N * K / 2; }
-  static __host__ __device__ constexpr long s_bytes(long N, long K) { return N * K / 16; }
+  static __host__ __device__ constexpr long s_bytes(long N, long K) {
+    return N / 16 * scale_groups(K, kUG) * 1024;
+  }
 };
 
 // FP8 e4m3: 16 codes per chunk; one fp32 scale per 128x128 block.
@@ -39,6 +53,8 @@ struct WFmt<kFP8> {
   static constexpr int kWords = 8;
   static constexpr int kSB = 64;
   static constexpr int kSPU = 2;
+  static constexpr int kSBY = 0;
+  static constexpr int kUG = 1;
   static __host__ __device__ constexpr long w_bytes(long N, long K) { return N * K; }
   static __host__ __device__ constexpr long s_bytes(long N, long K) { return (N / 128) * (K / 128) * 4; }
 };
@@ -50,20 +66,31 @@ struct WFmt<kBF16> {
   static constexpr int kWords = 4;
   static constexpr int kSB = 32;
   static constexpr int kSPU = 4;
+  static constexpr int kSBY = 0;
+  static constexpr int kUG = 1;
   static __host__ __device__ constexpr long w_bytes(long N, long K) { return N * K * 2; }
   static __host__ __device__ constexpr long s_bytes(long, long) { return 0; }
 };
 
+// Byte offset of the scale(s) of chunk `lane` (= 16q + r) of super-block sb
+// of a panel inside an expert's fp4 scale array (K = the row length).
+template <int FMT>
+__host__ __device__ __forceinline__ long scale_offset(long panel, long sb, int lane, long K) {
+  using F = WFmt<FMT>;
+  const long g = panel * scale_groups(K, F::kUG) + sb / F::kUG;
+  return (g * 64 + lane) * 16 + (sb % F::kUG) * F::kSBY;
+}
+
 // Raw scale bits of one chunk (no use of the value, so the load does not
 // stall the issue of the loads that follow it).  `sc` points at this expert's
-// fp4 scale array; `sb_index` is the (panel, super-block) index; `lane` = 16q+r.
+// fp4 scale array.
 template <int FMT>
 __device__ __forceinline__ uint32_t load_chunk_scale_raw(const uint8_t* __restrict__ sc,
-                                                         long sb_index, int lane) {
+                                                         long panel, long sb, int lane, long K) {
   if constexpr (FMT == kMXFP4) {
-    return sc[sb_index * 64 + lane];
+    return sc[scale_offset<FMT>(panel, sb, lane, K)];
   } else if constexpr (FMT == kNVFP4) {
-    return *reinterpret_cast<const uint16_t*>(sc + (sb_index * 64 + lane) * 2);
+    return *reinterpret_cast<const uint16_t*>(sc + scale_offset<FMT>(panel, sb, lane, K));
   } else {
     return 0u;
   }
@@ -81,12 +108,6 @@ __device__ __forceinline__ void chunk_scale(uint32_t raw, float& s0, float& s1) 
   } else {
     s0 = s1 = 1.0f;
   }
-}
-
-template <int FMT>
-__device__ __forceinline__ void load_chunk_scale(const uint8_t* __restrict__ sc, long sb_index,
-                                                 int lane, float& s0, float& s1) {
-  chunk_scale<FMT>(load_chunk_scale_raw<FMT>(sc, sb_index, lane), s0, s1);
 }
 
 template <int FMT>

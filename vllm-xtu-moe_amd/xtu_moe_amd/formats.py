@@ -148,42 +148,72 @@ def unpack_weight(fmt: int, p: torch.Tensor, N: int, K: int) -> torch.Tensor:
     return d.view(torch.bfloat16) if fmt == FMT_BF16 else d
 
 
+# fp4 scale groups: per 16-row panel, the scales of UG consecutive 128-k
+# super-blocks are stored [4 chunk q][16 row r][16 bytes] (16 bytes = UG
+# one-byte MXFP4 scales or UG two-byte NVFP4 scale pairs), so one 16-byte load
+# hands the lane that reads chunk (q, r) the scales of UG super-blocks.  The
+# last group of a panel is zero-padded.
+SCALE_GROUP = {FMT_MXFP4: 16, FMT_NVFP4: 8}
+
+
+def scale_groups(fmt: int, K: int) -> int:
+    ug = SCALE_GROUP[fmt]
+    return (K // 128 + ug - 1) // ug
+
+
+def scale_bytes(fmt: int, N: int, K: int) -> int:
+    """Packed scale bytes of one [N, K] matrix (per expert)."""
+    if fmt in SCALE_GROUP:
+        return N // 16 * scale_groups(fmt, K) * 1024
+    if fmt == FMT_FP8:
+        return (N // 128) * (K // 128) * 4
+    return 0
+
+
 def pack_scales(fmt: int, s, N: int, K: int):
-    """Dense scales -> P16 scale layout (fp4) / unchanged (fp8) / None (bf16)."""
+    """Dense scales -> packed scale groups (fp4) / unchanged (fp8) / None (bf16)."""
     if s is None or fmt == FMT_BF16:
         return None
     E = s.shape[0]
-    if fmt == FMT_MXFP4:
-        return s.reshape(E, N // 16, 16, K // 128, 4).permute(0, 1, 3, 4, 2).contiguous().reshape(E, -1)
-    if fmt == FMT_NVFP4:
-        return (s.reshape(E, N // 16, 16, K // 128, 4, 2).permute(0, 1, 3, 4, 2, 5)
-                .contiguous().reshape(E, -1))
-    return s.float().contiguous().reshape(E, -1)
+    if fmt == FMT_FP8:
+        return s.float().contiguous().reshape(E, -1)
+    ug, nsb = SCALE_GROUP[fmt], K // 128
+    G = scale_groups(fmt, K)
+    per = 4 if fmt == FMT_MXFP4 else 8          # scale bytes per (row, super-block)
+    d = s.contiguous().view(torch.uint8).reshape(E, N // 16, 16, nsb, per)
+    if G * ug != nsb:
+        d = torch.nn.functional.pad(d, (0, 0, 0, G * ug - nsb))
+    if fmt == FMT_MXFP4:   # [p][r][g][u][q] -> [p][g][q][r][u]
+        d = d.reshape(E, N // 16, 16, G, ug, 4).permute(0, 1, 3, 5, 2, 4)
+    else:                  # [p][r][g][u][q][h] -> [p][g][q][r][u][h]
+        d = d.reshape(E, N // 16, 16, G, ug, 4, 2).permute(0, 1, 3, 5, 2, 4, 6)
+    return d.contiguous().reshape(E, -1)
 
 
 def unpack_scales(fmt: int, p, N: int, K: int):
     if p is None or fmt == FMT_BF16:
         return None
     E = p.shape[0]
-    if fmt == FMT_MXFP4:
-        return p.reshape(E, N // 16, K // 128, 4, 16).permute(0, 1, 4, 2, 3).contiguous().reshape(E, N, K // 32)
-    if fmt == FMT_NVFP4:
-        return (p.reshape(E, N // 16, K // 128, 4, 16, 2).permute(0, 1, 4, 2, 3, 5)
-                .contiguous().reshape(E, N, K // 16))
-    return p.reshape(E, N // 128, K // 128)
+    if fmt == FMT_FP8:
+        return p.reshape(E, N // 128, K // 128)
+    ug, nsb = SCALE_GROUP[fmt], K // 128
+    G = scale_groups(fmt, K)
+    if fmt == FMT_MXFP4:   # [p][g][q][r][u] -> [p][r][g][u][q]
+        d = p.reshape(E, N // 16, G, 4, 16, ug).permute(0, 1, 4, 2, 5, 3)
+        d = d.reshape(E, N // 16, 16, G * ug, 4)[:, :, :, :nsb]
+        return d.contiguous().reshape(E, N, K // 32)
+    d = p.reshape(E, N // 16, G, 4, 16, ug, 2).permute(0, 1, 4, 2, 5, 3, 6)
+    d = d.reshape(E, N // 16, 16, G * ug, 4, 2)[:, :, :, :nsb]
+    return d.contiguous().reshape(E, N, K // 16)
 
 
 def expert_bytes(fmt: int, H: int, I: int) -> int:
-    """HBM bytes of one expert (w13 + s13 + w2 + s2) in format `fmt`."""
+    """HBM bytes of one expert (w13 + s13 + w2 + s2, plus NVFP4's two global
+    scales) in format `fmt`, as packed."""
     w = 3 * H * I * {FMT_BF16: 2.0, FMT_FP8: 1.0, FMT_MXFP4: 0.5, FMT_NVFP4: 0.5}[fmt]
-    if fmt == FMT_MXFP4:
-        s = 3 * H * I / 32
-    elif fmt == FMT_NVFP4:
-        s = 3 * H * I / 16 + 8
-    elif fmt == FMT_FP8:
-        s = 3 * (H // 128) * (I // 128) * 4
-    else:
-        s = 0
+    s = scale_bytes(fmt, 2 * I, H) + scale_bytes(fmt, H, I)
+    if fmt == FMT_NVFP4:
+        s += 8
     return int(w + s)
 
 

@@ -18,9 +18,6 @@ from .formats import (FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4, pack_scales, pack
 
 DECODE_MAX_TOKENS = 16
 SMALL_MAX_PAIRS = 1024
-# decode: down projection fused with the weighted unpermute (one launch, no y
-# buffer) or split into down (y rows) + combine
-DECODE_FUSED_DOWN = False
 
 
 def _p(t) -> int:
@@ -267,12 +264,6 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0,
                   _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
                   _p(seg.n_active), max_active, _p(act), lim, al, be, st)
-        if DECODE_FUSED_DOWN:
-            _lib.call("xtu_decode_down_combine", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2),
-                      _p(W.gs2), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.sorted_wts),
-                      _p(seg.seg_start), _p(seg.active), _p(seg.n_active), _p(out),
-                      int(odt == torch.bfloat16), st)
-            return (out, seg) if return_seg else out
         _lib.call("xtu_decode_down", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.active), _p(seg.n_active), max_active,
                   _p(y), st)

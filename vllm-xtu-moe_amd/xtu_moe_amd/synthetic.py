@@ -23,10 +23,8 @@ def synth_layer(fmt: int, E: int, n_shared: int, H: int, I: int, *, seed: int = 
     def alloc(N, K):
         rb = F.row_bytes(fmt, K)
         w = torch.empty((n, N * rb), dtype=torch.uint8, device=dev)
-        if fmt == F.FMT_MXFP4:
-            s = torch.empty((n, N * K // 32), dtype=torch.uint8, device=dev)
-        elif fmt == F.FMT_NVFP4:
-            s = torch.empty((n, N * K // 16), dtype=torch.uint8, device=dev)
+        if fmt in (F.FMT_MXFP4, F.FMT_NVFP4):
+            s = torch.empty((n, F.scale_bytes(fmt, N, K)), dtype=torch.uint8, device=dev)
         elif fmt == F.FMT_FP8:
             s = torch.empty((n, (N // 128) * (K // 128)), dtype=torch.float32, device=dev)
         else:
