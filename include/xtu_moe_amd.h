@@ -75,10 +75,10 @@ hipError_t xtu_segment(const int32_t* topk_ids, const float* topk_weights, const
                        int32_t* expert_tile_start, hipStream_t stream);
 
 /* Small batches (A = T*K + T*n_shared <= xtu_route_segment_small_max_pairs()):
- * routing and the whole segmentation in one workgroup, same outputs as
+ * routing and the whole segmentation in one launch, same outputs as
  * xtu_route_* followed by xtu_segment.  mode 0 = softmax routing, 1 = grouped
- * sigmoid routing (topk_ids/topk_weights are written), 2 = ids/weights given
- * (read).  Replaces, for decode, the router call plus _build_segmentation
+ * sigmoid routing (topk_ids/topk_weights are written; up to 16 waves route
+ * one token each at a time), 2 = ids/weights given (read).  One workgroup.  Replaces, for decode, the router call plus _build_segmentation
  * (gpu_prefill.py:849-887) and the in-kernel dispatch scan of
  * moe4_smallm_gu2/dn2 (moe4_smallm.cu:193-206, :266-281). */
 int xtu_route_segment_small_max_pairs(void);

@@ -1,9 +1,12 @@
 // Routing (a1) and token permutation / segmentation (a2) for the MoE expert path.
 //
-// Routing: one wave64 per token.  Each lane owns experts lane, lane+64, ...;
-// top-k is K rounds of a wave argmax under the total order (score desc,
-// index asc), so the result is unique and identical to a sequential scan.
-// Weights are formed by lane 0 in a fixed fp32 sequence (see xtu_expf).
+// Routing: one 256-thread workgroup per token, selection by ranks under the
+// total order (score desc, index asc), so the choice and its order equal a
+// sequential scan's and take a fixed number of barriers: each expert's rank
+// inside its group (grouped routing) or 32-expert chunk (softmax) prunes the
+// candidates to K per group, group scores and group ranks pick the groups,
+// and a candidate's rank among the survivors is its output slot.  Weights
+// are formed by one thread in a fixed fp32 sequence (see xtu_expf).
 //
 // Segmentation: a stable counting sort of the flat (token, expert) pairs by
 // bucket, in three launches (per-block histogram in LDS, one-workgroup scan,
@@ -16,183 +19,215 @@ namespace xtu {
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kMaxPerLane = 16;  // E <= 1024
 
 __device__ __forceinline__ bool better(float sa, int ia, float sb, int ib) {
   return (sa > sb) || (sa == sb && ia < ib);
 }
 
-// One DPP step of the wave argmax: combine with the lane selected by `ctrl`
-// (lanes whose source is masked keep their own value).
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void dpp_argmax_step(float& s, int& i) {
-  const float os = __int_as_float(
-      __builtin_amdgcn_update_dpp(__float_as_int(s), __float_as_int(s), CTRL, ROW_MASK, 0xF, false));
-  const int oi = __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xF, false);
-  if (better(os, oi, s, i)) {
-    s = os;
-    i = oi;
+constexpr int kMaxE = 1024;
+constexpr int kMaxK = 16;
+constexpr int kMaxGroups = 64;
+
+// Routing scratch of one team in LDS, laid out from a base for E experts and
+// nc = groups * K candidate slots (words): sc, ws [E]; csc, ce [ncp];
+// g1, g2, gs, gsel [64]; sel_e, sel_ws, sel_sc [16]; sum.
+__host__ __device__ constexpr int route_team_words(int E, int nc) {
+  return 2 * E + 2 * ((nc + 3) & ~3) + 4 * kMaxGroups + 3 * kMaxK + 4;
+}
+
+struct RouteScratch {
+  float *sc, *ws, *csc, *g1, *g2, *gs, *sel_ws, *sel_sc;
+  int *ce, *gsel, *sel_e;
+  __device__ RouteScratch(float* base, int E, int nc) {
+    const int ncp = (nc + 3) & ~3;
+    sc = base;
+    ws = sc + E;
+    csc = ws + E;
+    ce = reinterpret_cast<int*>(csc + ncp);
+    g1 = reinterpret_cast<float*>(ce + ncp);
+    g2 = g1 + kMaxGroups;
+    gs = g2 + kMaxGroups;
+    gsel = reinterpret_cast<int*>(gs + kMaxGroups);
+    sel_e = gsel + kMaxGroups;
+    sel_ws = reinterpret_cast<float*>(sel_e + kMaxK);
+    sel_sc = sel_ws + kMaxK;
   }
+};
+
+// Make this wave's LDS writes visible to its other lanes.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// wave argmax of (s, i) pairs under `better`; every lane gets the winner.
-// quad xor 1, quad xor 2, half-row mirror, row mirror, row_bcast15, row_bcast31
-// leave the maximum in lane 63, which is then read back as a uniform value.
-__device__ __forceinline__ void wave_argmax(float& s, int& i) {
-  dpp_argmax_step<0xB1, 0xF>(s, i);   // quad_perm [1,0,3,2]
-  dpp_argmax_step<0x4E, 0xF>(s, i);   // quad_perm [2,3,0,1]
-  dpp_argmax_step<0x141, 0xF>(s, i);  // row_half_mirror
-  dpp_argmax_step<0x140, 0xF>(s, i);  // row_mirror
-  dpp_argmax_step<0x142, 0xA>(s, i);  // row_bcast15 into rows 1, 3
-  dpp_argmax_step<0x143, 0xC>(s, i);  // row_bcast31 into rows 2, 3
-  s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
-  i = __builtin_amdgcn_readlane(i, 63);
+// A team of TEAM threads routes one token: TEAM = 64 is one wave (synced as
+// a wave), TEAM = 256 is a quarter of a 1024-thread workgroup whose four
+// teams run in lockstep through workgroup barriers.
+template <int TEAM>
+__device__ __forceinline__ void team_sync() {
+  if constexpr (TEAM == kWave) wave_sync();
+  else __syncthreads();
 }
 
-__device__ __forceinline__ float lane_read(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+// Number of (score, index) pairs in [j0, j1) that beat (v, e): 4-wide LDS
+// reads, independent of each other, so the latencies overlap.
+__device__ __forceinline__ int count_better(const float* sc, const int* idx, int j0, int j1,
+                                            float v, int e) {
+  int r = 0;
+  int j = j0;
+  if ((j0 & 3) == 0) {
+#pragma unroll 4
+    for (; j + 4 <= j1; j += 4) {
+      const f32x4_t s4 = *reinterpret_cast<const f32x4_t*>(sc + j);
+      if (idx) {
+        const i32x4_t i4 = *reinterpret_cast<const i32x4_t*>(idx + j);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r += better(s4[q], i4[q], v, e) ? 1 : 0;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r += better(s4[q], j + q, v, e) ? 1 : 0;
+      }
+    }
+  }
+  for (; j < j1; ++j) r += better(sc[j], idx ? idx[j] : j, v, e) ? 1 : 0;
+  return r;
 }
 
-// Route one token with one wave.  MODE 0: softmax top-k, MODE 1: grouped
-// sigmoid.  NPER = experts per lane (E <= 64 * NPER); sb is this wave's LDS
-// scratch of E floats.  On return lanes k < K hold the k-th choice in
-// (id, weight); the fp32 weight sequence is the one the host oracle restates.
-template <int MODE, int NPER>
-__device__ __forceinline__ void route_one_token(const float* __restrict__ l,
-                                                const float* __restrict__ bias, int E, int K,
-                                                int n_group, int topk_group, float scale,
-                                                int renorm, float* sb, int lane, int& my_id,
-                                                float& my_w) {
+// Route one token with a team (thread `tid` of TEAM; `valid` false: no token,
+// the team only keeps step with the barriers).  MODE 0: softmax top-k over
+// the logits; MODE 1: DeepSeek-V3 grouped sigmoid.  Threads k < K write the
+// k-th choice to ids_out[k] / wts_out[k] (and to the LDS copies if given).
+template <int MODE, int TEAM>
+__device__ void route_token(const float* __restrict__ l, const float* __restrict__ bias, int E,
+                            int K, int n_group, int topk_group, float scale, int renorm,
+                            const RouteScratch& s, int tid, bool valid, int32_t* ids_out,
+                            float* wts_out, int* ids_lds = nullptr, float* wts_lds = nullptr) {
 #pragma clang fp contract(off)
   const float NEG = -__builtin_inff();
-  float sel[NPER], wsc[NPER];
-#pragma unroll
-  for (int j = 0; j < NPER; ++j) {
-    const int e = lane + kWave * j;
-    float v = NEG, w = 0.f;
-    if (e < E) {
+  const int gsz = MODE == 1 ? E / n_group : 32;   // group, or pruning chunk
+  const int ng = MODE == 1 ? n_group : (E + 31) / 32;
+  const int nc = ng * K;
+  const int ncp = (nc + 3) & ~3;
+  if (valid) {
+    for (int e = tid; e < E; e += TEAM) {
       const float x = l[e];
       if (MODE == 0) {
-        v = x;
+        s.sc[e] = x;
+        s.ws[e] = x;
       } else {
-        w = xtu_sigmoid(x);
-        v = w + (bias ? bias[e] : 0.0f);
+        const float w = xtu_sigmoid(x);
+        s.sc[e] = w + (bias ? bias[e] : 0.0f);
+        s.ws[e] = w;
       }
     }
-    sel[j] = v;
-    wsc[j] = w;
   }
-  uint64_t gmask = ~0ull;
-  int gsz = E;
+  for (int c = tid; c < ncp; c += TEAM) {
+    s.csc[c] = NEG;
+    s.ce[c] = 0x7fffffff;
+  }
+  team_sync<TEAM>();
+  // rank inside the group / chunk; the K best of each become candidates
+  if (valid) {
+    for (int e = tid; e < E; e += TEAM) {
+      const int g = e / gsz, j0 = g * gsz;
+      const float v = s.sc[e];
+      const int r = count_better(s.sc, nullptr, j0, min(j0 + gsz, E), v, e);
+      if (r < K) {
+        s.csc[g * K + r] = v;
+        s.ce[g * K + r] = e;
+      }
+      if (MODE == 1) {
+        if (r == 0) s.g1[g] = v;
+        if (r == 1) s.g2[g] = v;
+      }
+    }
+  }
+  team_sync<TEAM>();
   if (MODE == 1) {
-#pragma unroll
-    for (int j = 0; j < NPER; ++j) {
-      const int e = lane + kWave * j;
-      if (e < E) sb[e] = sel[j];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    gsz = E / n_group;
-    float g = NEG;
-    if (lane < n_group) {
-      // two best (score desc, index asc) of the group, kept in registers
-      float v1 = NEG, v2 = NEG;
-      int i1 = -1, i2 = -1;
-      for (int q = 0; q < gsz; ++q) {
-        const int e = lane * gsz + q;
-        const float v = sb[e];
-        if (i1 < 0 || better(v, e, v1, i1)) {
-          v2 = v1; i2 = i1;
-          v1 = v; i1 = e;
-        } else if (i2 < 0 || better(v, e, v2, i2)) {
-          v2 = v; i2 = e;
-        }
+    // group score = best + second best; keep the topk_group best groups
+    if (tid < ng) s.gs[tid] = gsz >= 2 ? s.g1[tid] + s.g2[tid] : s.g1[tid];
+    team_sync<TEAM>();
+    if (tid < ng) s.gsel[tid] = count_better(s.gs, nullptr, 0, ng, s.gs[tid], tid) < topk_group;
+    team_sync<TEAM>();
+    for (int c = tid; c < nc; c += TEAM)   // drop the candidates of the other groups
+      if (!s.gsel[c / K]) {
+        s.csc[c] = NEG;
+        s.ce[c] = 0x7fffffff;
       }
-      g = (gsz >= 2) ? (v1 + v2) : v1;
-    }
-    gmask = 0;
-    bool taken = false;
-    for (int k = 0; k < topk_group; ++k) {
-      float s = (lane < n_group && !taken) ? g : NEG;
-      int i = (lane < n_group && !taken) ? lane : 0x7fffffff;
-      wave_argmax(s, i);
-      if (lane == i) taken = true;
-      gmask |= 1ull << i;
+    team_sync<TEAM>();
+  }
+  // rank among the surviving candidates = output slot
+  for (int c = tid; c < nc; c += TEAM) {
+    const int e = s.ce[c];
+    if (e == 0x7fffffff) continue;
+    const float v = s.csc[c];
+    const int r = count_better(s.csc, s.ce, 0, ncp, v, e);
+    if (r < K) {
+      s.sel_e[r] = e;
+      s.sel_ws[r] = s.ws[e];
+      s.sel_sc[r] = v;
     }
   }
-  uint32_t used = 0;
-  my_id = -1;
-  float my_s = 0.f, my_wsc = 0.f;
-  for (int k = 0; k < K; ++k) {
-    float s = NEG;
-    int i = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < NPER; ++j) {
-      const int e = lane + kWave * j;
-      if (e < E && !((used >> j) & 1u) && ((gmask >> (e / gsz)) & 1ull)) {
-        if (better(sel[j], e, s, i)) {
-          s = sel[j];
-          i = e;
-        }
-      }
-    }
-    wave_argmax(s, i);
-    const int owner = i % kWave, jw = i / kWave;
-    float w = 0.f;
-#pragma unroll
-    for (int j = 0; j < NPER; ++j)
-      if (j == jw) w = wsc[j];
-    if (lane == owner) used |= 1u << jw;
-    w = lane_read(w, owner);
-    if (lane == k) {
-      my_id = i;
-      my_s = s;
-      my_wsc = w;
-    }
-  }
+  team_sync<TEAM>();
+  // weights: lanes k < K of the team's first wave, sums in k order
+  float wk = 0.f;
+  if (tid < K) wk = s.sel_ws[tid];
+  int id = 0;
+  float w = 0.f;
   if (MODE == 0) {
-    const float lmax = lane_read(my_s, 0);
-    const float ev = (lane < K) ? xtu_expf(my_s - lmax) : 0.f;
+    const float lmax = s.sel_sc[0];
+    const float ev = tid < K ? xtu_expf(wk - lmax) : 0.f;   // e^(l_k - lmax)
     float sum = 0.0f;
     if (renorm) {
-      for (int k = 0; k < K; ++k) sum = sum + lane_read(ev, k);
+      for (int k = 0; k < K; ++k) sum = sum + __shfl(ev, k, kWave);
     } else {
-#pragma unroll
-      for (int j = 0; j < NPER; ++j) {
-        const int e = lane + kWave * j;
-        const float x = (e < E) ? xtu_expf(l[e] - lmax) : 0.f;
-        for (int q = 0; q < kWave; ++q)
-          if (q + kWave * j < E) sum = sum + lane_read(x, q);
-      }
+      team_sync<TEAM>();   // sel_* read before ws is rewritten
+      if (valid)
+        for (int e = tid; e < E; e += TEAM) s.ws[e] = xtu_expf(s.sc[e] - lmax);
+      team_sync<TEAM>();
+      if (tid == 0)
+        for (int e = 0; e < E; ++e) sum = sum + s.ws[e];
+      sum = __shfl(sum, 0, kWave);
     }
-    my_w = __fdiv_rn(ev, sum);
+    if (tid < K) {
+      id = s.sel_e[tid];
+      w = __fdiv_rn(ev, sum);
+    }
   } else {
     float sum = 0.0f;
-    for (int k = 0; k < K; ++k) sum = sum + lane_read(my_wsc, k);
-    my_w = renorm ? __fdiv_rn(my_wsc, sum) * scale : my_wsc * scale;
+    for (int k = 0; k < K; ++k) sum = sum + __shfl(wk, k, kWave);
+    if (tid < K) {
+      id = s.sel_e[tid];
+      w = renorm ? __fdiv_rn(wk, sum) * scale : wk * scale;
+    }
   }
+  if (valid && tid < K) {
+    ids_out[tid] = id;
+    wts_out[tid] = w;
+    if (ids_lds) {
+      ids_lds[tid] = id;
+      wts_lds[tid] = w;
+    }
+  }
+  team_sync<TEAM>();   // the scratch may be reused for the next token
 }
 
-template <int MODE, int NPER>
-__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
-                                                    const float* __restrict__ bias, int T, int E,
-                                                    int K, int n_group, int topk_group,
-                                                    float scale, int renorm,
-                                                    int32_t* __restrict__ ids,
-                                                    float* __restrict__ wts) {
-  __shared__ float sb[4][64 * NPER];
-  const int wv = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int t = blockIdx.x * 4 + wv;
-  if (t >= T) return;   // no block-wide barrier below
-  int id;
-  float w;
-  route_one_token<MODE, NPER>(logits + (size_t)t * E, bias, E, K, n_group, topk_group, scale,
-                              renorm, sb[wv], lane, id, w);
-  if (lane < K) {
-    ids[(size_t)t * K + lane] = id;
-    wts[(size_t)t * K + lane] = w;
-  }
+// Four 256-thread teams per workgroup, one token each.
+template <int MODE>
+__global__ __launch_bounds__(1024) void route_kernel(const float* __restrict__ logits,
+                                                     const float* __restrict__ bias, int T, int E,
+                                                     int K, int n_group, int topk_group,
+                                                     float scale, int renorm,
+                                                     int32_t* __restrict__ ids,
+                                                     float* __restrict__ wts) {
+  extern __shared__ float route_lds[];
+  const int team = threadIdx.x / 256, tid = threadIdx.x % 256;
+  const long t = (long)blockIdx.x * 4 + team;
+  const int nc = (MODE == 1 ? n_group : (E + 31) / 32) * K;
+  const RouteScratch s(route_lds + team * route_team_words(E, nc), E, nc);
+  route_token<MODE, 256>(logits + t * E, bias, E, K, n_group, topk_group, scale, renorm, s, tid,
+                         t < T, ids + t * K, wts + t * K);
 }
 
 // ----------------------------------------------------------------------------
@@ -430,38 +465,16 @@ __global__ __launch_bounds__(kSegThreads) void seg_scatter_kernel(
 constexpr int kSmallMaxA = 1024;
 constexpr int kSmallMaxNB = 2048;
 
-// In-place exclusive scan of a[0, n) (n <= 2048) by 256 threads; returns the total.
-__device__ int block_excl_scan_256(int* a, int n, int* wsum) {
-  const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
-  const int per = (n + 255) / 256;
-  int loc[8];
-  int s = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int idx = tid * per + i;
-    const int v = (i < per && idx < n) ? a[idx] : 0;
-    loc[i] = s;
-    s += v;
-  }
-  int incl = s;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int o = __shfl_up(incl, off, kWave);
-    if (lane >= off) incl += o;
-  }
-  if (lane == kWave - 1) wsum[wv] = incl;
-  __syncthreads();
-  int base = 0;
-  for (int q = 0; q < wv; ++q) base += wsum[q];
-  const int total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-  const int ex = base + incl - s;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int idx = tid * per + i;
-    if (i < per && idx < n) a[idx] = ex + loc[i];
-  }
-  __syncthreads();
-  return total;
+// Inclusive prefix sum across the 64 lanes of a wave (DPP row shifts, then
+// row broadcasts); lanes whose source is out of range add 0.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);   // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);   // row_bcast:31
+  return x;
 }
 
 struct SmallArgs {
@@ -477,82 +490,117 @@ struct SmallArgs {
   int32_t *tile_expert, *tile_row0, *n_tiles, *expert_tile_start;
 };
 
-// MODE 0: softmax routing, 1: grouped sigmoid routing, 2: ids/wts given.
-template <int MODE, int NPER>
-__global__ __launch_bounds__(256) void route_seg_small_kernel(SmallArgs a) {
-  __shared__ float sb[4][64 * NPER];
-  __shared__ int s_ids[kSmallMaxA];
-  __shared__ float s_w[kSmallMaxA];
-  __shared__ int s_bk[kSmallMaxA];
-  __shared__ int s_cnt[kSmallMaxNB];
-  __shared__ int s_act[kSmallMaxNB];
-  __shared__ int s_til[kSmallMaxNB];
-  __shared__ int s_wsum[4];
-  const int tid = threadIdx.x, wv = tid / kWave, lane = tid % kWave;
+struct SegSmem {
+  int ids[kSmallMaxA];
+  float w[kSmallMaxA];
+  int bk[kSmallMaxA];
+  int cnt[kSmallMaxNB];
+  int wsum[3][16];
+};
+
+// One workgroup of NT threads.  MODE 0: softmax routing, 1: grouped sigmoid
+// routing (NT/256 teams route that many tokens at a time), 2: ids/wts given.
+// Then the whole segmentation.
+template <int MODE, int NT>
+__global__ __launch_bounds__(NT) void route_seg_small_kernel(SmallArgs a) {
+  __shared__ SegSmem g;
+  extern __shared__ float route_lds[];
+  constexpr int NW = NT / kWave;
+  const int tid = threadIdx.x;
   const int T = a.T, K = a.K, E = a.E, NS = a.NS;
   const int TK = T * K, A = TK + T * NS, NB = E + NS + 1;
   if (MODE < 2) {
-    for (int t = wv; t < T; t += 4) {
-      int id;
-      float w;
-      route_one_token<MODE < 2 ? MODE : 0, NPER>(a.logits + (size_t)t * E, a.bias, E, K,
-                                                  a.n_group, a.topk_group, a.scale, a.renorm,
-                                                  sb[wv], lane, id, w);
-      if (lane < K) {
-        a.ids[t * K + lane] = id;
-        a.wts[t * K + lane] = w;
-        s_ids[t * K + lane] = id;
-        s_w[t * K + lane] = w;
-      }
+    // NT / 256 teams of 256 threads route that many tokens at a time
+    constexpr int NTEAM = NT / 256;
+    const int team = tid / 256, ttid = tid % 256;
+    const int nc = (MODE == 1 ? a.n_group : (E + 31) / 32) * K;
+    const RouteScratch s(route_lds + team * route_team_words(E, nc), E, nc);
+    for (int t0 = 0; t0 < T; t0 += NTEAM) {
+      const int t = t0 + team;
+      const bool valid = t < T;
+      route_token<MODE < 2 ? MODE : 0, 256>(a.logits + (long)t * E, a.bias, E, K, a.n_group,
+                                             a.topk_group, a.scale, a.renorm, s, ttid, valid,
+                                             a.ids + (long)t * K, a.wts + (long)t * K,
+                                             g.ids + t * K, g.w + t * K);
     }
   } else {
-    for (int p = tid; p < TK; p += 256) {
-      s_ids[p] = a.ids[p];
-      s_w[p] = a.wts[p];
+    for (int p = tid; p < TK; p += NT) {
+      g.ids[p] = a.ids[p];
+      g.w[p] = a.wts[p];
     }
   }
-  for (int e = tid; e < NB; e += 256) s_cnt[e] = 0;
+  for (int e = tid; e < NB; e += NT) g.cnt[e] = 0;
   __syncthreads();
-  for (int p = tid; p < A; p += 256) {
+  for (int p = tid; p < A; p += NT) {
     int b;
     if (p < TK) {
-      int e = s_ids[p];
+      int e = g.ids[p];
       if (a.id_map && e >= 0 && e < E) e = a.id_map[e];
       b = (e < 0 || e >= E) ? (E + NS) : e;
-      if (a.drop_zero && s_w[p] == 0.0f) b = E + NS;
+      if (a.drop_zero && g.w[p] == 0.0f) b = E + NS;
     } else {
       b = E + (p - TK) % NS;
     }
-    s_bk[p] = b;
-    atomicAdd(&s_cnt[b], 1);
+    g.bk[p] = b;
+    atomicAdd(&g.cnt[b], 1);
+  }
+  for (int p = A + tid; p < ((A + 3) & ~3); p += NT) g.bk[p] = -1;   // pad for 4-wide reads
+  __syncthreads();
+  // one scan pass over the buckets for (rows, active flag, tiles): each thread
+  // owns `per` consecutive buckets
+  const int per = (NB + NT - 1) / NT;
+  const int lane = tid % kWave, wv = tid / kWave;
+  int c_loc[8], s_rows = 0, s_act = 0, s_til = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = tid * per + i;
+    const int c = (i < per && e < NB) ? g.cnt[e] : 0;
+    c_loc[i] = c;
+    s_rows += c;
+    s_act += (e < NB - 1 && c > 0) ? 1 : 0;
+    s_til += (e < NB - 1) ? (c + a.bm - 1) / a.bm : 0;
+  }
+  const int i_rows = wave_incl_scan(s_rows), i_act = wave_incl_scan(s_act),
+            i_til = wave_incl_scan(s_til);
+  if (lane == kWave - 1) {
+    g.wsum[0][wv] = i_rows;
+    g.wsum[1][wv] = i_act;
+    g.wsum[2][wv] = i_til;
   }
   __syncthreads();
-  for (int e = tid; e < NB; e += 256) {
-    const int c = s_cnt[e];
-    const bool expert = e < NB - 1;
-    s_act[e] = (expert && c > 0) ? 1 : 0;
-    s_til[e] = expert ? (c + a.bm - 1) / a.bm : 0;
-  }
-  __syncthreads();
-  block_excl_scan_256(s_cnt, NB, s_wsum);
-  const int n_act = block_excl_scan_256(s_act, NB, s_wsum);
-  const int n_til = block_excl_scan_256(s_til, NB, s_wsum);
-  for (int e = tid; e < NB; e += 256) {
-    const int st = s_cnt[e];
-    const int en = (e + 1 < NB) ? s_cnt[e + 1] : A;
-    const int c = en - st;
-    a.seg_start[e] = st;
-    a.expert_tile_start[e] = s_til[e];
-    if (e == NB - 1) {
-      a.seg_start[NB] = A;
-      a.expert_tile_start[NB] = n_til;
+  int b_rows = i_rows - s_rows, b_act = i_act - s_act, b_til = i_til - s_til;
+  int n_act = 0, n_til = 0;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) {
+    if (q < wv) {
+      b_rows += g.wsum[0][q];
+      b_act += g.wsum[1][q];
+      b_til += g.wsum[2][q];
     }
-    if (e < NB - 1 && c > 0) {
-      a.active[s_act[e]] = e;
-      const int nt = (c + a.bm - 1) / a.bm;
-      for (int j = 0; j < nt; ++j) {
-        a.tile_expert[s_til[e] + j] = e;
-        a.tile_row0[s_til[e] + j] = st + j * a.bm;
+    n_act += g.wsum[1][q];
+    n_til += g.wsum[2][q];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = tid * per + i;
+    if (i < per && e < NB) {
+      const int c = c_loc[i];
+      a.seg_start[e] = b_rows;
+      a.expert_tile_start[e] = b_til;
+      g.cnt[e] = b_rows;   // bucket start, for the scatter below
+      if (e < NB - 1 && c > 0) {
+        a.active[b_act++] = e;
+        const int nt = (c + a.bm - 1) / a.bm;
+        for (int j = 0; j < nt; ++j) {
+          a.tile_expert[b_til + j] = e;
+          a.tile_row0[b_til + j] = b_rows + j * a.bm;
+        }
+        b_til += nt;
+      }
+      b_rows += c;
+      if (e == NB - 1) {
+        a.seg_start[NB] = A;
+        a.expert_tile_start[NB] = n_til;
       }
     }
   }
@@ -560,16 +608,24 @@ __global__ __launch_bounds__(256) void route_seg_small_kernel(SmallArgs a) {
     a.n_active[0] = n_act;
     a.n_tiles[0] = n_til;
   }
-  for (int p = tid; p < A; p += 256) {
-    const int b = s_bk[p];
+  __syncthreads();
+  // stable scatter: position = bucket start + earlier pairs of the bucket
+  for (int p = tid; p < A; p += NT) {
+    const int b = g.bk[p];
     int r = 0;
-    for (int q = 0; q < p; ++q) r += (s_bk[q] == b) ? 1 : 0;
-    const int pos = s_cnt[b] + r;
+    int q = 0;
+#pragma unroll 4
+    for (; q + 4 <= p; q += 4) {
+      const i32x4_t v = *reinterpret_cast<const i32x4_t*>(g.bk + q);
+      r += (v[0] == b) + (v[1] == b) + (v[2] == b) + (v[3] == b);
+    }
+    for (; q < p; ++q) r += g.bk[q] == b;
+    const int pos = g.cnt[b] + r;
     a.sorted_pair[pos] = p;
     a.inv[p] = pos;
     if (p < TK) {
       a.sorted_tok[pos] = p / K;
-      a.sorted_wts[pos] = s_w[p];
+      a.sorted_wts[pos] = g.w[p];
     } else {
       a.sorted_tok[pos] = (p - TK) / NS;
       a.sorted_wts[pos] = 1.0f;
@@ -578,31 +634,20 @@ __global__ __launch_bounds__(256) void route_seg_small_kernel(SmallArgs a) {
 }
 
 template <int MODE>
-void launch_small(const SmallArgs& a, hipStream_t stream) {
-  if (a.E <= 64) route_seg_small_kernel<MODE, 1><<<1, 256, 0, stream>>>(a);
-  else if (a.E <= 256) route_seg_small_kernel<MODE, 4><<<1, 256, 0, stream>>>(a);
-  else if (a.E <= 512) route_seg_small_kernel<MODE, 8><<<1, 256, 0, stream>>>(a);
-  else route_seg_small_kernel<MODE, 16><<<1, 256, 0, stream>>>(a);
+hipError_t launch_small(const SmallArgs& a, hipStream_t stream) {
+  if constexpr (MODE == 2) {
+    route_seg_small_kernel<MODE, 256><<<1, 256, 0, stream>>>(a);
+  } else {
+    const int nc = (MODE == 1 ? a.n_group : (a.E + 31) / 32) * a.K;
+    const size_t team_lds = route_team_words(a.E, nc) * sizeof(float);
+    if (a.T <= 2)   // one team: fewer waves in lockstep through the barriers
+      route_seg_small_kernel<MODE, 256><<<1, 256, team_lds, stream>>>(a);
+    else
+      route_seg_small_kernel<MODE, 1024><<<1, 1024, 4 * team_lds, stream>>>(a);
+  }
+  return hipSuccess;
 }
 
-template <int MODE>
-void launch_route(const float* logits, const float* bias, int T, int E, int K, int n_group,
-                  int topk_group, float scale, int renorm, int32_t* ids, float* wts,
-                  hipStream_t stream) {
-  const dim3 grid((T + 3) / 4);
-  if (E <= 64)
-    route_kernel<MODE, 1><<<grid, 256, 0, stream>>>(logits, bias, T, E, K, n_group, topk_group,
-                                                    scale, renorm, ids, wts);
-  else if (E <= 256)
-    route_kernel<MODE, 4><<<grid, 256, 0, stream>>>(logits, bias, T, E, K, n_group, topk_group,
-                                                    scale, renorm, ids, wts);
-  else if (E <= 512)
-    route_kernel<MODE, 8><<<grid, 256, 0, stream>>>(logits, bias, T, E, K, n_group, topk_group,
-                                                    scale, renorm, ids, wts);
-  else
-    route_kernel<MODE, 16><<<grid, 256, 0, stream>>>(logits, bias, T, E, K, n_group, topk_group,
-                                                     scale, renorm, ids, wts);
-}
 
 }  // namespace
 }  // namespace xtu
@@ -617,8 +662,9 @@ hipError_t xtu_route_softmax_topk(const float* logits, int T, int E, int K, int 
   XTU_CHECK_ARG(T == 0 || (logits && topk_ids && topk_weights));
   if (T == 0) return hipSuccess;
   (void)hipGetLastError();
-  launch_route<0>(logits, nullptr, T, E, K, 1, 1, 1.0f, renormalize, topk_ids, topk_weights,
-                  stream);
+  const size_t lds = 4 * route_team_words(E, ((E + 31) / 32) * K) * sizeof(float);
+  route_kernel<0><<<(T + 3) / 4, 1024, lds, stream>>>(logits, nullptr, T, E, K, 1, 1, 1.0f,
+                                                      renormalize, topk_ids, topk_weights);
   return hipPeekAtLastError();
 }
 
@@ -632,8 +678,10 @@ hipError_t xtu_route_grouped_sigmoid(const float* logits, const float* bias, int
   XTU_CHECK_ARG(T == 0 || (logits && topk_ids && topk_weights));
   if (T == 0) return hipSuccess;
   (void)hipGetLastError();
-  launch_route<1>(logits, bias, T, E, K, n_group, topk_group, routed_scaling, renormalize,
-                  topk_ids, topk_weights, stream);
+  const size_t lds = 4 * route_team_words(E, n_group * K) * sizeof(float);
+  route_kernel<1><<<(T + 3) / 4, 1024, lds, stream>>>(logits, bias, T, E, K, n_group, topk_group,
+                                                      routed_scaling, renormalize, topk_ids,
+                                                      topk_weights);
   return hipPeekAtLastError();
 }
 
@@ -701,15 +749,17 @@ hipError_t xtu_route_segment_small(int mode, const float* logits, const float* b
   XTU_CHECK_ARG(topk_ids && topk_weights && (mode == 2 || T == 0 || logits));
   XTU_CHECK_ARG(sorted_pair && sorted_tok && sorted_wts && inv && seg_start && active &&
                 n_active && tile_expert && tile_row0 && n_tiles && expert_tile_start);
+  if (mode < 2 && T == 0) mode = 2;   // nothing to route: segment the empty batch
   SmallArgs a{logits, bias, topk_ids, topk_weights, id_map, T, K, E, n_group, topk_group,
               renormalize, n_shared, drop_zero, bm, routed_scaling, sorted_pair, sorted_tok, inv,
               seg_start, active, n_active, sorted_wts, tile_expert, tile_row0, n_tiles,
               expert_tile_start};
   (void)hipGetLastError();
-  if (mode == 0) launch_small<0>(a, stream);
-  else if (mode == 1) launch_small<1>(a, stream);
-  else launch_small<2>(a, stream);
-  return hipPeekAtLastError();
+  hipError_t err;
+  if (mode == 0) err = launch_small<0>(a, stream);
+  else if (mode == 1) err = launch_small<1>(a, stream);
+  else err = launch_small<2>(a, stream);
+  return err != hipSuccess ? err : hipPeekAtLastError();
 }
 
 }  // extern "C"
