@@ -101,8 +101,9 @@ def main():
     if args.workload == "mixtral-tiny-bf16":
         router_w = torch.randn((E, H), generator=gen, device=dev) * 0.02
 
-    e_bytes13 = F.expert_bytes(fmt, H, I) * (2 * I * H) // (3 * H * I)   # w13 + s13 share
-    e_bytes = F.expert_bytes(fmt, H, I)
+    # algorithmic bytes of one expert: gate/up stream, whole expert
+    e_bytes13 = F.algorithmic_bytes(fmt, 2 * I, H)
+    e_bytes = e_bytes13 + F.algorithmic_bytes(fmt, H, I)
     nsteps = args.warmup + args.steps
     results = {}
     for T in cfg["Ts"]:
@@ -218,6 +219,20 @@ def main():
             torch.cuda.synchronize()
             gu_ms.append(a.elapsed_time(b))
 
+        # HIP-event bracket cost on this stream (same flush-then-record pattern,
+        # nothing in between), taken off the single-kernel times
+        empty_ms = []
+        for s in range(max(10, args.steps // 2)):
+            if not args.no_flush:
+                flush.add_(1.0)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            b.record()
+            torch.cuda.synchronize()
+            empty_ms.append(a.elapsed_time(b))
+        ev_overhead = float(np.median(empty_ms))
+        gu_ms = [max(g - ev_overhead, 1e-6) for g in gu_ms]
+
         A = T * K + T * NS
         mean_layer = float(np.mean(layer_ms))
         mean_gu = float(np.mean(gu_ms))
@@ -230,7 +245,8 @@ def main():
                           layer_GBs=layer_bytes / (mean_layer / 1e3) / 1e9,
                           gate_up_ms=mean_gu, gate_up_GBs=gu_bytes / (mean_gu / 1e3) / 1e9,
                           gate_up_TFLOPs=gu_flops / (mean_gu / 1e3) / 1e12,
-                          graph=graph is not None, wall_s=wall)
+                          graph=graph is not None, wall_s=wall,
+                          event_overhead_us=ev_overhead * 1e3)
         log(f"[bench] T={T}: layer {mean_layer * 1e3:.1f} us ({results[T]['layer_GBs']:.0f} GB/s), "
             f"gate_up {mean_gu * 1e3:.1f} us ({results[T]['gate_up_GBs']:.0f} GB/s, "
             f"{results[T]['gate_up_TFLOPs']:.0f} TFLOP/s), |D|={mean_active:.1f}")

@@ -207,6 +207,15 @@ def unpack_scales(fmt: int, p, N: int, K: int):
     return d.contiguous().reshape(E, N, K // 16)
 
 
+def algorithmic_bytes(fmt: int, N: int, K: int) -> int:
+    """Bytes a weight stream of one [N, K] matrix must read: codes plus one
+    scale per scaling block (no layout padding)."""
+    w = N * K * {FMT_BF16: 2.0, FMT_FP8: 1.0, FMT_MXFP4: 0.5, FMT_NVFP4: 0.5}[fmt]
+    s = {FMT_BF16: 0, FMT_FP8: (N // 128) * (K // 128) * 4, FMT_MXFP4: N * K // 32,
+         FMT_NVFP4: N * K // 16 + 4}[fmt]
+    return int(w + s)
+
+
 def expert_bytes(fmt: int, H: int, I: int) -> int:
     """HBM bytes of one expert (w13 + s13 + w2 + s2, plus NVFP4's two global
     scales) in format `fmt`, as packed."""
