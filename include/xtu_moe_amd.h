@@ -176,6 +176,16 @@ hipError_t xtu_i8_gemm_down(const int8_t* a8, const int32_t* crow, int H, int I,
                             const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
                             float* y, int32_t* acc_out, hipStream_t stream);
 
+/* ------------------------------------------------ expert staging (ring / pool)
+ * dst[i*dst_stride, +bytes) <- src[experts[i]*src_stride, +bytes), i < n, as
+ * one hipMemcpyAsync per expert on `stream` (experts: host array; src/dst:
+ * pinned host or device memory).  Replaces the engine's per-expert shard DMA
+ * the ring and the resident pool consume (copy_hostbuf_to_device /
+ * copy_hostbuf_to_device_2d, xiaotu_moe/csrc/binding.cpp:1368-1437;
+ * _dma_hostbuf_range, vllm_xiaotu_moe/gpu_prefill.py:1897). */
+hipError_t xtu_copy_experts(int n, const int32_t* experts, const void* src, long src_stride,
+                            void* dst, long dst_stride, long bytes, hipStream_t stream);
+
 /* -------------------------------------------------------------- probes
  * No reference counterpart: in-bounds checks of the device builtins this
  * library relies on (scaled fp4/fp8 converters, MFMA lane layouts, the

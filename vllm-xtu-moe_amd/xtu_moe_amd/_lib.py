@@ -39,6 +39,7 @@ SIGNATURES = {
     "xtu_gemm_down": (_i, [_i, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp, _vp,
                            _i, _vp, _vp]),
     "xtu_combine": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
+    "xtu_copy_experts": (_i, [_i, _vp, _vp, _l, _vp, _l, _l, _vp]),
     "xtu_i8_weight_bytes": (_sz, [_i, _i]),
     "xtu_i8_prepare": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "xtu_i8_quant_rows": (_i, [_vp, _i, _i, _vp, _vp, _vp]),

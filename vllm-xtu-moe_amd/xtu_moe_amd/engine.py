@@ -1,0 +1,129 @@
+"""Engine surface: the configuration record and the per-format engine
+classes the plugin constructs once per layer, with a ``cpu_prefill``-style
+forward over the flat routing of a batch.
+
+Mirrors the reference engine's Python binding
+(xiaotu_moe/csrc/python_binding/binding.cpp:760-808 class constructor,
+:1438-1450 ``cpu_prefill`` -> ``MOE_V2::forward_many`` (moe_v2.hpp:651-957),
+:1478-1501 ``MOEConfigV2``; config fields moe_v2.hpp:125-147) and its host
+buffer ABI (:1368-1437 ``shard_geometry`` / ``pin_hostbufs`` /
+``copy_hostbuf_to_device``).  The reference engine computes on the CPU; here
+the same call runs the HIP kernels on the weights' device copy, and the
+pinned host copy serves the ring stage and the resident pool.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import formats as F
+from .host_store import HostExpertStore
+from .layer import ExpertWeights, moe_forward
+
+
+@dataclass
+class MOEConfigV2:
+    num_processes: int = 1
+    process_id: int = 0
+    gpu_id: int = 0
+    has_gate_proj: bool = True
+    expert_num: int = 0
+    top_k: int = 0
+    hidden_size: int = 0
+    intermediate_size: int = 0
+    max_batch_size: int = 0
+    max_num_seqs: int = 0
+    stride: int = 32
+    group_min_len: int = 10
+    group_max_len: int = 4096
+    groupN: int = 0
+    groupK: int = 0
+    swiglu_alpha: float = 1.0    # sigmoid scale inside the gated activation
+    swiglu_beta: float = 0.0     # added to `up` before the multiply
+    swiglu_limit: float = 0.0    # gate clamped above, up on both sides; 0 = off
+    activation_type: int = 0     # 0 plain gated SiLU, 1 clamped SwiGLU
+    use_gpu_prefill: bool = False
+    int8_activation: int = 0     # 1 = INT8-activation x FP4-code ALIGN path (MXFP4)
+
+
+class _Engine:
+    FMT = None
+    GROUP = (1, 1)   # (groupN, groupK) the checkpoint scales use
+
+    def __init__(self, cfg: MOEConfigV2, w13_weight, w2_weight, w13_scale=0, w2_scale=0,
+                 w13_global_scale=0, w2_global_scale=0, device=None):
+        if cfg.expert_num <= 0 or cfg.hidden_size <= 0 or cfg.intermediate_size <= 0:
+            raise ValueError("MOEConfigV2: expert_num, hidden_size, intermediate_size must be set")
+        gn, gk = self.GROUP
+        if cfg.groupN and (cfg.groupN, cfg.groupK) != (gn, gk):
+            raise ValueError(f"{type(self).__name__}: groupN/groupK must be {gn}/{gk}")
+        if cfg.int8_activation and self.FMT != F.FMT_MXFP4:
+            raise ValueError("int8_activation needs MXFP4 (e8m0) weights")
+        self.cfg = cfg
+        opt = lambda v: None if (v is None or isinstance(v, int)) else v
+        dev = torch.device(device) if device is not None else torch.device("cuda")
+        self.weights = ExpertWeights.from_dense(self.FMT, w13_weight, opt(w13_scale), w2_weight,
+                                                opt(w2_scale), opt(w13_global_scale),
+                                                opt(w2_global_scale), device=dev)
+        self._store = None
+
+    # ------------------------------------------------------------ forward
+    def forward_many(self, qlen: int, top_k: int, expert_ids, weights, x, out):
+        """out[qlen, H] fp32 = sum_k weights * expert(ids)(x) (ids >= expert_num
+        and zero weights contribute nothing)."""
+        c = self.cfg
+        ids = expert_ids.reshape(qlen, top_k).to(torch.int32)
+        ids = torch.where(ids < 0, torch.full_like(ids, -1), ids)
+        lim = c.swiglu_limit if c.activation_type == 1 else 0.0
+        res = moe_forward(x.reshape(qlen, c.hidden_size).to(torch.bfloat16).contiguous(), ids,
+                          weights.reshape(qlen, top_k).float(), self.weights, swiglu_limit=lim,
+                          swiglu_alpha=c.swiglu_alpha, swiglu_beta=c.swiglu_beta,
+                          out_dtype=torch.float32, int8=bool(c.int8_activation), path="auto")
+        out.view(qlen, c.hidden_size).copy_(res)
+        return out
+
+    def cpu_prefill(self, qlen, top_k, expert_ids, weights, input, output):
+        """Same call and meaning as the reference engine's cpu_prefill (the
+        work runs on the GPU here)."""
+        return self.forward_many(qlen, top_k, expert_ids, weights, input, output)
+
+    # ------------------------------------------------------ host buffers
+    def host_store(self) -> HostExpertStore:
+        if self._store is None:
+            self._store = HostExpertStore.from_weights(self.weights)
+        return self._store
+
+    def shard_geometry(self) -> dict:
+        return self.host_store().shard_geometry()
+
+    def pin_hostbufs(self) -> int:
+        return self.host_store().pin_hostbufs()
+
+    def copy_hostbuf_to_device(self, which: int, node: int, dst_ptr: int, stream=None) -> int:
+        """Plane `which` (0 w13, 1 w2, 2 s13, 3 s2) of expert `node` -> dst."""
+        return self.host_store().copy_hostbuf_to_device(which, node, dst_ptr, stream)
+
+
+class MOE_BF16(_Engine):
+    FMT = F.FMT_BF16
+    GROUP = (1, 1)
+
+
+class MOE_FP8(_Engine):
+    FMT = F.FMT_FP8
+    GROUP = (128, 128)
+
+
+class MOE_MXFP4(_Engine):
+    FMT = F.FMT_MXFP4
+    GROUP = (1, 32)
+
+
+class MOE_NVFP4(_Engine):
+    FMT = F.FMT_NVFP4
+    GROUP = (1, 16)
+
+
+ENGINES = {"MOE_BF16": MOE_BF16, "MOE_FP8": MOE_FP8, "MOE_MXFP4": MOE_MXFP4,
+           "MOE_NVFP4": MOE_NVFP4}

@@ -177,12 +177,23 @@ def _buf(name, shape, dtype, device):
     return t
 
 
+def _same_device(dev, **tensors):
+    """Every given tensor lives on CUDA device `dev` (the kernels take raw
+    device pointers: a host or other-device pointer must never reach them)."""
+    for name, t in tensors.items():
+        if t is not None and (not t.is_cuda or t.device != dev):
+            raise ValueError(f"{name} is on {t.device}, expected {dev}")
+
+
 def route(logits, *, top_k, scoring="softmax", renormalize=True, bias=None, n_group=1,
           topk_group=1, routed_scaling_factor=1.0, ids_out=None, wts_out=None, stream=None):
     """Top-k routing on the GPU.  Returns (topk_weights fp32 [T,K], topk_ids int32 [T,K])."""
     lg = logits.float().contiguous() if logits.dtype != torch.float32 or not logits.is_contiguous() else logits
     T, E = lg.shape
     dev = lg.device
+    if not lg.is_cuda:
+        raise ValueError("logits must be a CUDA tensor")
+    _same_device(dev, bias=bias, ids_out=ids_out, wts_out=wts_out)
     ids = ids_out if ids_out is not None else torch.empty((T, top_k), dtype=torch.int32, device=dev)
     wts = wts_out if wts_out is not None else torch.empty((T, top_k), dtype=torch.float32, device=dev)
     st = _stream(stream)
@@ -217,6 +228,13 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     if x.shape != (T, H):
         raise ValueError(f"x shape {tuple(x.shape)} != ({T}, {H})")
     dev = x.device
+    if not x.is_cuda:
+        raise ValueError("x must be a CUDA tensor")
+    _same_device(dev, topk_ids=topk_ids, topk_weights=topk_weights, w13=W.w13, w2=W.w2,
+                 s13=W.s13, s2=W.s2, gs13=W.gs13, gs2=W.gs2, id_map=id_map, slot_map=slot_map,
+                 out=out)
+    if router is not None:
+        _same_device(dev, logits=router.get("logits"), bias=router.get("bias"))
     if router is not None and not (topk_ids.dtype == torch.int32 and topk_ids.is_contiguous()
                                    and topk_weights.dtype == torch.float32
                                    and topk_weights.is_contiguous()):
@@ -256,10 +274,10 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         out = torch.empty((T, H), dtype=odt, device=dev)
     if T == 0:
         return (out, seg) if return_seg else out
-    act = _buf("act", (max(A, 1), I), torch.bfloat16, dev)
     y = _buf("y", (max(A, 1), H), torch.float32, dev)
-    lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
     if path == "decode":
+        act = _buf("act", (max(A, 1), I), torch.bfloat16, dev)
+        lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
         max_active = min(E, T * K) + NS
         _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0,
                   _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
@@ -267,13 +285,35 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         _lib.call("xtu_decode_down", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.active), _p(seg.n_active), max_active,
                   _p(y), st)
-    elif int8:
+    else:
+        expert_pass(x, seg, W, 0, E + NS, y, slot_map=slot_map, int8=int8,
+                    swiglu_limit=swiglu_limit, swiglu_alpha=swiglu_alpha,
+                    swiglu_beta=swiglu_beta, stream=st)
+    combine(seg, y, wts, out, stream=st)
+    return (out, seg) if return_seg else out
+
+
+def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None, int8=False,
+                swiglu_limit=0.0, swiglu_alpha=1.0, swiglu_beta=0.0, stream=None):
+    """Grouped gate/up (+ SwiGLU-clamp) and down GEMMs for the sorted pairs of
+    buckets [b0, b1), weights of bucket b at slot slot_map[b] of W (identity
+    without a map); writes their fp32 rows of y [A, H]."""
+    T, H = x.shape
+    I = W.I
+    A = seg.A
+    if A == 0 or b1 <= b0:
+        return
+    dev = x.device
+    st = _stream(stream)
+    lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
+    act = _buf("act", (max(A, 1), I), torch.bfloat16, dev)
+    lo, hi = seg.tile_range_ptrs(b0, b1)
+    if int8:
         w13_8, emin13, w2_8, emin2 = W.int8_planes()
         a8x = _buf("a8x", (T, H), torch.int8, dev)
         crx = _buf("crx", (T,), torch.int32, dev)
         a8a = _buf("a8a", (max(A, 1), I), torch.int8, dev)
         cra = _buf("cra", (max(A, 1),), torch.int32, dev)
-        lo, hi = seg.tile_range_ptrs(0, E + NS)
         _lib.call("xtu_i8_quant_rows", _p(x), T, H, _p(a8x), _p(crx), st)
         _lib.call("xtu_i8_gemm_gate_up", _p(a8x), _p(crx), _p(seg.sorted_tok), H, I, _p(w13_8),
                   _p(emin13), _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
@@ -282,14 +322,20 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         _lib.call("xtu_i8_gemm_down", _p(a8a), _p(cra), H, I, _p(w2_8), _p(emin2), _p(slot_map),
                   _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo, hi,
                   seg.max_tiles, _p(y), 0, st)
-    else:
-        lo, hi = seg.tile_range_ptrs(0, E + NS)
-        _lib.call("xtu_gemm_gate_up", fmt, _p(x), _p(seg.sorted_tok), H, I, _p(W.w13), _p(W.s13),
-                  _p(W.gs13), 0, 0, _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
-                  _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), lim, al, be, st)
-        _lib.call("xtu_gemm_down", fmt, _p(act), H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
-                  _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo, hi,
-                  seg.max_tiles, _p(y), st)
-    _lib.call("xtu_combine", _p(y), _p(seg.inv), _p(wts), _p(seg.seg_start) + 4 * (E + NS), T, K,
-              NS, H, _p(out), int(odt == torch.bfloat16), st)
-    return (out, seg) if return_seg else out
+        return
+    fmt = W.fmt
+    _lib.call("xtu_gemm_gate_up", fmt, _p(x), _p(seg.sorted_tok), H, I, _p(W.w13), _p(W.s13),
+              _p(W.gs13), 0, 0, _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
+              _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), lim, al, be, st)
+    _lib.call("xtu_gemm_down", fmt, _p(act), H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
+              _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo, hi,
+              seg.max_tiles, _p(y), st)
+
+
+def combine(seg, y, topk_weights, out, *, stream=None):
+    """out[t] = sum_k w[t,k] * y[pos(t,k)] (+ shared rows), pairs in the trash
+    bucket or of weight 0 skipped; bf16 or fp32 out."""
+    T, K = seg.T, seg.K
+    _lib.call("xtu_combine", _p(y), _p(seg.inv), _p(topk_weights),
+              _p(seg.seg_start) + 4 * (seg.E + seg.NS), T, K, seg.NS, out.shape[1], _p(out),
+              int(out.dtype == torch.bfloat16), _stream(stream))
