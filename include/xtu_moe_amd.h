@@ -13,8 +13,11 @@
  * per-expert global scale).  Weights are in the P16 panel layout: per
  * expert, a [N][K] matrix is stored as
  * [N/16][K/SB][4][16][16 B] with SB = 128 (fp4), 64 (fp8), 32 (bf16) k per
- * super-block; fp4 scales as [N/16][K/128][4][16] (MXFP4, 1 B) or
- * [N/16][K/128][4][16][2] (NVFP4); fp8 block scales as [N/128][K/128] fp32.
+ * super-block; fp4 scales in groups of UG super-blocks per 16-row panel,
+ * [N/16][ceil((K/128)/UG)][64 lanes][16 B], lane 16q+r holding the scales of
+ * row r, k-chunk q for UG consecutive super-blocks (MXFP4: UG = 16, 1 B
+ * each; NVFP4: UG = 8, 2 B each; the last group zero-padded); fp8 block
+ * scales as [N/128][K/128] fp32.
  * w13 rows [0, I) are the gate projection, [I, 2I) the up projection.
  *
  * Citations are to the reference (yeungtuzi/vllm-xtu-moe) interface each
@@ -38,8 +41,8 @@ const char* xtu_error_string(int err);
 /* ---------------------------------------------------------------- routing
  * Replaces the router the hook obtains from vLLM's router factory
  * (vllm_xiaotu_moe/mixed_experts.py:991-1078 _get_router/_select_topk;
- * hybrid_model.py:1877 fused_topk_bias).  One wave per token; ties broken
- * toward the lower expert index.  logits [T][E] fp32; outputs [T][K].
+ * hybrid_model.py:1877 fused_topk_bias).  A 256-thread team per token (four
+ * per workgroup); ties broken toward the lower expert index.  logits [T][E] fp32; outputs [T][K].
  *   softmax:  w = exp(l - lmax) / sum over the K chosen (renormalize=1)
  *   grouped:  s = sigmoid(l), selection by s + bias, group score = sum of the
  *             two best in the group, topk_group groups kept, then
