@@ -73,4 +73,5 @@ def test_library_loads_and_reports_version():
     # argument validation runs on the host: a bad shape is rejected without a launch
     rc = lib.xtu_route_softmax_topk(None, 4, 0, 2, 1, None, None, None)
     assert rc == 1   # hipErrorInvalidValue
-    assert _lib.load().xtu_gemm_tile_m(1) == 64 and _lib.load().xtu_gemm_tile_m(2) == 128
+    assert all(_lib.load().xtu_gemm_tile_m(f) == 128 for f in range(4))
+    assert _lib.load().xtu_gemm_tile_m(4) == 0

@@ -1,35 +1,57 @@
 // Grouped expert GEMMs for prefill-sized batches, and the weighted combine.
 //
-// Tile list: seg_scan_kernel cuts each expert's contiguous segment of sorted
-// pairs into M tiles of BM rows; blockIdx.x walks that list (entries past
-// n_tiles exit at once), blockIdx.y walks 256-row blocks of the weight.
+// Work items are (M tile, N block) pairs.  seg_scan_kernel cuts each expert's
+// contiguous segment of sorted pairs into M tiles of 128 rows; gate/up N
+// blocks hold 128 gate rows and the matching 128 up rows of w13, down N blocks
+// 256 rows of w2.  Items are numbered tile-major (N block fastest) and dealt
+// to the eight XCDs in contiguous ranges (workgroup i runs on XCD i % 8), so
+// the workgroups resident on one XCD at a time share the A rows of a tile
+// and the weight panels of an expert through that XCD's L2.
 //
-// Per K step (BK = 64) a workgroup of four waves stages
-//   A: BM activation rows (gathered through sorted_tok for gate/up, the
-//      contiguous act rows for down) as bf16, and
-//   B: 256 weight rows read from the P16 panel layout (each panel's K slice is
-//      one contiguous run of bytes), dequantised exactly to bf16 while being
-//      written to LDS,
-// then each wave runs v_mfma_f32_32x32x16_bf16 over its BM x 64 sub-tile.
-// Global loads of step k+1 are issued before the MFMAs of step k.
+// A workgroup of four waves runs the K loop in steps of one super-block
+// (128 k for fp4, 64 for fp8, 32 for bf16):
+//   A: the tile's rows (gathered through sorted_tok for gate/up, contiguous
+//      act rows for down) are loaded as bf16 into registers one step ahead
+//      and stored to a double-buffered LDS stage (one barrier per step);
+//   B: each wave owns four 16-row weight panels (64 output columns).  In the
+//      P16 layout one 16-byte load per lane is exactly the B operand of
+//      v_mfma_f32_16x16x32_bf16 for a panel, so the weights go from HBM to
+//      registers (one step ahead), are dequantised there and never touch LDS.
+// Per step a wave issues 8 row tiles x 4 panels x (chunk k / 8) MFMAs; row
+// tiles past the tile's rows are skipped.
 //
-// Scale handling, all exact: MXFP4 e8m0 and NVFP4 e4m3 scales are folded into
-// the bf16 operand (products are representable); NVFP4's per-expert global
-// scale multiplies the fp32 result; FP8's 128x128 fp32 block scales multiply
-// a per-128-k partial accumulator (fp32 promotion, no operand rounding).
+// Dequantisation: MXFP4 (e2m1 x e8m0) and NVFP4 (e2m1 x e4m3) products are
+// exact in bf16; NVFP4's per-expert global scale multiplies the fp32 result.
+// FP8 operands are bf16(e4m3 * block scale), rounded to nearest even -- the
+// reference's GPU FP8 kernels form the same operand (gpu_prefill_fp8.py:
+// 148-149, 195-196).
 //
-// gate/up blocks hold 128 gate rows and the matching 128 up rows, so each
-// lane owns (g, u) of the same output element and the epilogue writes the
-// clamped-SwiGLU activation as bf16.  down writes fp32 y rows; the combine
-// kernel adds them per token in top-k order.
+// gate/up: panels 0,1 of a wave are gate rows and panels 2,3 the up rows of
+// the same output columns, so each lane holds (g, u) of the same element and
+// the epilogue writes the clamped-SwiGLU activation as bf16.  down writes
+// fp32 y rows; the combine kernel adds them per token in top-k order.
+#include <type_traits>
+
 #include "weight_format.hpp"
 
 namespace xtu {
 namespace {
 
-constexpr int kBK = 64;
-constexpr int kBN = 256;
-constexpr int kLDK = kBK + 8;   // LDS row pitch in bf16 (16-byte pad)
+constexpr int kBM = 128;            // rows per M tile
+constexpr int kRT = kBM / 16;       // 16-row MFMA tiles per M tile
+constexpr int kPW = 4;              // 16-row weight panels per wave
+constexpr int kGemmThreads = 256;
+constexpr int kBufFlags = 0x00020000;   // raw buffer resource, dword 3
+
+template <int FMT>
+struct GemmShape {
+  using F = WFmt<FMT>;
+  static constexpr int kBK = F::kSB;                          // k per step
+  static constexpr int kLD = kBK + 8;                         // LDS row pitch (bf16)
+  static constexpr int kAL = kBM * kBK / 8 / kGemmThreads;    // 16-byte A pieces per thread
+  static constexpr int kG = F::kCK / 8;                       // MFMA k groups per step
+  static constexpr int kABuf = kBM * kLD;                     // bf16 per A stage buffer
+};
 
 struct GemmArgs {
   const uint16_t* a;          // gate/up: x [T][K]; down: act [A][K]
@@ -49,200 +71,237 @@ struct GemmArgs {
   float limit, alpha, beta;
 };
 
-template <int FMT, int BM, bool GU>
-__global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a) {
-  using F = WFmt<FMT>;
-  constexpr int MT = BM / 32;                     // 32-row MFMA tiles per wave
-  constexpr int A_CH = BM * kBK / 8 / 256;        // 16-byte A chunks per thread
-  constexpr int CPP = (kBK / F::kCK) * 16;        // B chunks per panel per K step
-  constexpr int B_CH = 16 * CPP / 256;            // B chunks per thread
-  constexpr bool kIsFP8 = (FMT == kFP8);
-  __shared__ __attribute__((aligned(16))) uint16_t As[BM * kLDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[kBN * kLDK];
+// One wave's weights of one step: a 16-byte chunk per panel, the chunk's raw
+// fp4 scale bits, and (fp8) the block scales of panels 0,1 and 2,3.
+template <int FMT>
+struct BStep {
+  u32x4_t w[kPW];
+  uint32_t sc[kPW];
+  float bs0, bs1;
+};
 
-  const int tile = a.tile_lo[0] + blockIdx.x;
-  if (tile >= a.tile_hi[0]) return;
+// bf16 operand of MFMA group g of a chunk (k = q*kCK + 8g .. +7 of the lane's row).
+template <int FMT>
+__device__ __forceinline__ bf16x8_t dequant_group(const BStep<FMT>& b, int p, int g) {
+  uint32_t o[4];
+  if constexpr (FMT == kMXFP4) {
+    fp4x8_to_bf16(b.w[p][g], e8m0_to_f32(b.sc[p]), o);
+  } else if constexpr (FMT == kNVFP4) {
+    const uint32_t raw = b.sc[p] >> (g < 2 ? 0 : 8);
+    fp4x8_to_bf16_mul(b.w[p][g], e4m3_to_f32(raw & 0xffu), o);
+  } else if constexpr (FMT == kFP8) {
+    const float bs = p < 2 ? b.bs0 : b.bs1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t d = b.w[p][2 * g + h];
+      f32x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(d, 1.0f, false);
+      f32x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(d, 1.0f, true);
+      lo = lo * bs;
+      hi = hi * bs;
+      o[2 * h] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2_t));
+      o[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2_t));
+    }
+  } else {
+    return as_bf16x8(b.w[p]);
+  }
+  return as_bf16x8(o[0], o[1], o[2], o[3]);
+}
+
+// Waves per SIMD the register budget is sized for: NVFP4's scale multiply
+// needs more than half of the register file.
+template <int FMT>
+constexpr int gemm_waves_per_simd() { return FMT == kNVFP4 ? 1 : 2; }
+
+template <int FMT, bool GU>
+__global__ __launch_bounds__(kGemmThreads, gemm_waves_per_simd<FMT>()) void moe_gemm_kernel(
+    GemmArgs a) {
+  using F = WFmt<FMT>;
+  using S = GemmShape<FMT>;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2 * S::kABuf];
+
+  // ---- work item
+  const int nbn = GU ? a.I / 128 : a.H / 256;
+  const int lo = a.tile_lo[0];
+  const int total = (a.tile_hi[0] - lo) * nbn;
+  const int per = (total + 7) / 8;
+  const int idx = blockIdx.x / 8;
+  if (idx >= per) return;
+  const int item = (blockIdx.x % 8) * per + idx;
+  if (item >= total) return;
+  const int tile = lo + item / nbn, nb = item % nbn;
   const int e = a.tile_expert[tile];
   const int ws = a.slot_map ? a.slot_map[e] : e;
   const int row0 = a.tile_row0[tile];
-  const int rows = min(BM, a.seg_start[e + 1] - row0);
-  const int nb = blockIdx.y;
+  const int rows = min(kBM, a.seg_start[e + 1] - row0);
   const int K = GU ? a.H : a.I;
-  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
-  const long nsbk = K / F::kSB;
-  const uint8_t* wexp = a.w + (long)ws * a.w_estride;
-  const uint8_t* sexp = a.s ? a.s + (long)ws * a.s_estride : nullptr;
+  const int nsteps = K / S::kBK;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int lane = tid % 64;
 
-  // A source row of each chunk this thread loads (constant over K)
-  const uint16_t* asrc[A_CH];
+  // ---- A pieces of this thread: source byte offset at k = 0, LDS offset
+  constexpr int ppr = S::kBK / 8;   // 16-byte pieces per row per step
+  uint32_t aoff[S::kAL];
+  int alds[S::kAL];
 #pragma unroll
-  for (int i = 0; i < A_CH; ++i) {
-    const int c = i * 256 + tid, r = c / 8;
-    if (r < rows) {
-      const long src = GU ? (long)a.sorted_tok[row0 + r] : (long)(row0 + r);
-      asrc[i] = a.a + src * K + (c % 8) * 8;
-    } else {
-      asrc[i] = nullptr;
-    }
+  for (int i = 0; i < S::kAL; ++i) {
+    const int c = i * kGemmThreads + tid, r = c / ppr, col = c % ppr;
+    const int rr = min(r, rows - 1);
+    const uint32_t src = GU ? (uint32_t)a.sorted_tok[row0 + rr] : (uint32_t)rr;
+    aoff[i] = src * (uint32_t)K * 2u + (uint32_t)col * 16u;
+    alds[i] = r * S::kLD + col * 8;
   }
-  // B: weight panel and in-region offset of each chunk this thread loads
-  long bpanel[B_CH];
-  int boff[B_CH];
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(GU ? a.a : a.a + (long)row0 * K), 0, -1, kBufFlags);
+
+  // ---- B: this wave's panels
+  int pan[kPW];
 #pragma unroll
-  for (int i = 0; i < B_CH; ++i) {
-    const int c = i * 256 + tid, pl = c / CPP;
-    boff[i] = c % CPP;
-    if (GU) bpanel[i] = pl < 8 ? (long)nb * 8 + pl : (long)(a.I / 16) + nb * 8 + (pl - 8);
-    else bpanel[i] = (long)nb * 16 + pl;
+  for (int p = 0; p < kPW; ++p) {
+    if (GU) pan[p] = (p < 2 ? 0 : a.I / 16) + nb * 8 + 2 * w + (p & 1);
+    else pan[p] = nb * 16 + 4 * w + p;
   }
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.w + (long)ws * a.w_estride), 0, (int)a.w_estride, kBufFlags);
+  const uint8_t* sexp = a.s ? a.s + (long)ws * a.s_estride : a.w;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)sexp, 0, (int)a.s_estride, kBufFlags);
+  const int sgroups = (int)scale_groups(K, F::kUG);
+  // fp8 block-scale rows of panels 0,1 and 2,3
+  const float* bsc = reinterpret_cast<const float*>(sexp);
+  const int kb128 = K / 128;
+  const int rb0 = GU ? nb : 2 * nb + w / 2;
+  const int rb1 = GU ? a.I / 128 + nb : rb0;
 
-  u32x4_t areg[A_CH];
-  u32x4_t breg[B_CH];
-  uint32_t bsraw[B_CH];
-
-  auto gload = [&](int kk) {
+  auto load_a = [&](int s, u32x4_t (&ar)[S::kAL]) {
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (asrc[i]) v = *reinterpret_cast<const u32x4_t*>(asrc[i] + kk);
-      areg[i] = v;
-    }
-    const long sb = kk / F::kSB;
-    const int qbase = (kk % F::kSB) / F::kCK;
-#pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-      const uint8_t* region = wexp + (bpanel[i] * nsbk + sb) * 1024 + qbase * 256;
-      breg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(region + boff[i] * 16));
-      const int lane_eq = qbase * 16 + boff[i];   // (q, r) position inside the super-block
-      bsraw[i] = load_chunk_scale_raw<FMT>(sexp, bpanel[i], sb, lane_eq, K);
-    }
+    for (int i = 0; i < S::kAL; ++i)
+      ar[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              ra, aoff[i], s * S::kBK * 2, 0));
   };
-  auto lstore = [&]() {
+  auto store_a = [&](uint16_t* buf, const u32x4_t (&ar)[S::kAL]) {
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-      const int c = i * 256 + tid;
-      *reinterpret_cast<u32x4_t*>(&As[(c / 8) * kLDK + (c % 8) * 8]) = areg[i];
-    }
+    for (int i = 0; i < S::kAL; ++i) *reinterpret_cast<u32x4_t*>(buf + alds[i]) = ar[i];
+  };
+  auto load_b = [&](int s, BStep<FMT>& b) {
 #pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-      const int c = i * 256 + tid, pl = c / CPP;
-      const int r = boff[i] % 16, qr = boff[i] / 16;
-      uint32_t words[F::kWords];
-      float s0, s1;
-      chunk_scale<FMT>(bsraw[i], s0, s1);
-      decode_chunk<FMT>(breg[i], s0, s1, words);
-      uint16_t* dst = &Bs[(pl * 16 + r) * kLDK + qr * F::kCK];
+    for (int p = 0; p < kPW; ++p)
+      b.w[p] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rw, lane * 16, (pan[p] * nsteps + s) * 1024, 0));
+    if constexpr (F::kSBY > 0) {
+      const int g = s / F::kUG, ob = (s % F::kUG) * F::kSBY;
 #pragma unroll
-      for (int j = 0; j < F::kWords / 4; ++j) {
-        u32x4_t v = {words[4 * j], words[4 * j + 1], words[4 * j + 2], words[4 * j + 3]};
-        *reinterpret_cast<u32x4_t*>(dst + 8 * j) = v;
+      for (int p = 0; p < kPW; ++p) {
+        const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(
+            rs, lane * 16, (pan[p] * sgroups + g) * 1024 + (ob & ~3), 0);
+        b.sc[p] = v >> (8 * (ob & 3));
       }
+    } else if constexpr (FMT == kFP8) {
+      const int kb = s * S::kBK / 128;
+      b.bs0 = bsc[rb0 * kb128 + kb];
+      b.bs1 = bsc[rb1 * kb128 + kb];
     }
   };
 
-  // wave's two 32-column tiles inside the 256-row B block
-  const int jt0 = GU ? 32 * w : 64 * w;
-  const int jt1 = GU ? 128 + 32 * w : 64 * w + 32;
+  // LDS element offset of this lane's A operand (row lane%16, k = q*kCK)
+  const int afrag = (lane % 16) * S::kLD + (lane / 16) * F::kCK;
 
-  f32x16_t acc[MT][2];
-  f32x16_t part[kIsFP8 ? MT : 1][2];
+  // K loop and epilogue for NR 16-row tiles (the tile's rows rounded up), so
+  // the inner loop carries no per-row-tile branches.
+  auto run = [&](auto nr_tag) {
+    constexpr int NR = decltype(nr_tag)::value;
+    f32x4_t acc[NR][kPW];
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < NR; ++m)
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[m][n][i] = 0.f;
-    }
-  if constexpr (kIsFP8) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) part[m][n][i] = 0.f;
-  }
+      for (int p = 0; p < kPW; ++p) acc[m][p] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = K / kBK;
-  gload(0);
-  for (int kt = 0; kt < nk; ++kt) {
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (kt + 1 < nk) gload((kt + 1) * kBK);
+    auto compute = [&](const BStep<FMT>& b, const uint16_t* buf) {
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int kofs = ks * 16 + (lane / 32) * 8;
-      const bf16x8_t b0 = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&Bs[(jt0 + lane % 32) * kLDK + kofs]));
-      const bf16x8_t b1 = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&Bs[(jt1 + lane % 32) * kLDK + kofs]));
+      for (int g = 0; g < S::kG; ++g) {
+        bf16x8_t bv[kPW];
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const bf16x8_t av = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&As[(m * 32 + lane % 32) * kLDK + kofs]));
-        if constexpr (kIsFP8) {
-          part[m][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b0, part[m][0], 0, 0, 0);
-          part[m][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b1, part[m][1], 0, 0, 0);
-        } else {
-          acc[m][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b0, acc[m][0], 0, 0, 0);
-          acc[m][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b1, acc[m][1], 0, 0, 0);
+        for (int p = 0; p < kPW; ++p) bv[p] = dequant_group<FMT>(b, p, g);
+#pragma unroll
+        for (int m = 0; m < NR; ++m) {
+          const bf16x8_t av = as_bf16x8(
+              *reinterpret_cast<const u32x4_t*>(buf + afrag + m * 16 * S::kLD + 8 * g));
+#pragma unroll
+          for (int p = 0; p < kPW; ++p)
+            acc[m][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv[p], acc[m][p], 0, 0, 0);
         }
       }
+    };
+
+    // one barrier per step; the loads of step s+1 overlap the MFMAs of step s
+    u32x4_t ar[S::kAL];
+    BStep<FMT> b0, b1;
+    load_a(0, ar);
+    load_b(0, b0);
+    store_a(As, ar);
+    __syncthreads();
+    // (scheduling barriers keep the next step's loads ahead of this step's
+    // MFMAs; left alone, the compiler sinks them next to their first use)
+    for (int s = 0; s < nsteps; s += 2) {
+      const int s1 = min(s + 1, nsteps - 1);
+      load_a(s1, ar);
+      load_b(s1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(b0, As);
+      __builtin_amdgcn_sched_barrier(0);
+      store_a(As + S::kABuf, ar);
+      __syncthreads();
+      if (s + 1 < nsteps) {
+        const int s2 = min(s + 2, nsteps - 1);
+        load_a(s2, ar);
+        load_b(s2, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(b1, As + S::kABuf);
+        __builtin_amdgcn_sched_barrier(0);
+        store_a(As, ar);
+        __syncthreads();
+      }
     }
-    if constexpr (kIsFP8) {
-      if ((kt & 1) == 1) {   // a 128-k block is complete: fold its fp32 scale
-        const float* bsc = reinterpret_cast<const float*>(sexp);
-        const long kb = (long)(kt / 2);
-        long rb0, rb1;
-        if (GU) {
-          rb0 = (long)nb;                      // gate rows nb*128 + ...
-          rb1 = (long)(a.I / 128) + nb;        // up rows I + nb*128 + ...
-        } else {
-          rb0 = ((long)nb * 256 + jt0) / 128;
-          rb1 = ((long)nb * 256 + jt1) / 128;
-        }
-        const float s0 = bsc[rb0 * (K / 128) + kb];
-        const float s1 = bsc[rb1 * (K / 128) + kb];
+
+    float gsv = 1.0f;
+    if constexpr (FMT == kNVFP4) gsv = a.gs ? a.gs[ws] : 1.0f;
+    const int r16 = lane % 16, q = lane / 16;
+    if constexpr (GU) {
+      uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+      for (int m = 0; m < NR; ++m)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            acc[m][0][i] = __builtin_fmaf(s0, part[m][0][i], acc[m][0][i]);
-            acc[m][1][i] = __builtin_fmaf(s1, part[m][1][i], acc[m][1][i]);
-            part[m][0][i] = 0.f;
-            part[m][1][i] = 0.f;
+        for (int p = 0; p < 2; ++p) {
+          const long col = (long)pan[p] * 16 + r16;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = m * 16 + 4 * q + i;
+            if (r < rows) {
+              const float g = acc[m][p][i] * gsv, u = acc[m][p + 2][i] * gsv;
+              act[(long)(row0 + r) * a.I + col] =
+                  f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
+            }
           }
-      }
+        }
+    } else {
+      float* y = reinterpret_cast<float*>(a.out);
+#pragma unroll
+      for (int m = 0; m < NR; ++m)
+#pragma unroll
+        for (int p = 0; p < kPW; ++p) {
+          const long col = (long)pan[p] * 16 + r16;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = m * 16 + 4 * q + i;
+            if (r < rows) y[(long)(row0 + r) * a.H + col] = acc[m][p][i] * gsv;
+          }
+        }
     }
-  }
-
-  float gsv = 1.0f;
-  if constexpr (FMT == kNVFP4) gsv = a.gs ? a.gs[ws] : 1.0f;
-  const int ncol = lane % 32;
-  if constexpr (GU) {
-    uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
-    const long col = (long)nb * 128 + 32 * w + ncol;
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = m * 32 + (i / 4) * 8 + (lane / 32) * 4 + (i % 4);
-        if (r < rows) {
-          const float g = acc[m][0][i] * gsv, u = acc[m][1][i] * gsv;
-          act[(long)(row0 + r) * a.I + col] = f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
-        }
-      }
-  } else {
-    float* y = reinterpret_cast<float*>(a.out);
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = m * 32 + (i / 4) * 8 + (lane / 32) * 4 + (i % 4);
-        if (r < rows) {
-          float* yr = y + (long)(row0 + r) * a.H + (long)nb * 256;
-          yr[jt0 + ncol] = acc[m][0][i] * gsv;
-          yr[jt1 + ncol] = acc[m][1][i] * gsv;
-        }
-      }
-  }
+  };
+  if (rows > 64) run(std::integral_constant<int, kRT>{});
+  else if (rows > 32) run(std::integral_constant<int, 4>{});
+  else if (rows > 16) run(std::integral_constant<int, 2>{});
+  else run(std::integral_constant<int, 1>{});
 }
 
 // out[t][h] = sum_k w[t,k] * y[inv[t*K+k]][h] over the pairs that were not
@@ -280,20 +339,18 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   }
 }
 
-template <int FMT, int BM>
+template <int FMT>
 hipError_t launch_gemm(bool gu, GemmArgs a, int max_tiles, hipStream_t stream) {
   using F = WFmt<FMT>;
-  if (gu) {
-    if (!a.w_estride) a.w_estride = F::w_bytes(2L * a.I, a.H);
-    if (!a.s_estride) a.s_estride = F::s_bytes(2L * a.I, a.H);
-    dim3 grid(max_tiles, a.I / 128);
-    moe_gemm_kernel<FMT, BM, true><<<grid, 256, 0, stream>>>(a);
-  } else {
-    if (!a.w_estride) a.w_estride = F::w_bytes(a.H, a.I);
-    if (!a.s_estride) a.s_estride = F::s_bytes(a.H, a.I);
-    dim3 grid(max_tiles, a.H / 256);
-    moe_gemm_kernel<FMT, BM, false><<<grid, 256, 0, stream>>>(a);
-  }
+  const long N = gu ? 2L * a.I : a.H, K = gu ? a.H : a.I;
+  if (!a.w_estride) a.w_estride = F::w_bytes(N, K);
+  if (!a.s_estride) a.s_estride = F::s_bytes(N, K);
+  if (a.w_estride >= (1L << 31) || a.s_estride >= (1L << 31)) return hipErrorInvalidValue;
+  const long items = (long)max_tiles * (gu ? a.I / 128 : a.H / 256);
+  const long grid = (items + 7) / 8 * 8;
+  if (grid >= (1L << 31)) return hipErrorInvalidValue;
+  if (gu) moe_gemm_kernel<FMT, true><<<dim3((unsigned)grid), kGemmThreads, 0, stream>>>(a);
+  else moe_gemm_kernel<FMT, false><<<dim3((unsigned)grid), kGemmThreads, 0, stream>>>(a);
   return hipPeekAtLastError();
 }
 
@@ -304,7 +361,7 @@ using namespace xtu;
 
 extern "C" {
 
-int xtu_gemm_tile_m(int fmt) { return fmt == kFP8 ? 64 : 128; }
+int xtu_gemm_tile_m(int fmt) { return fmt >= 0 && fmt <= 3 ? kBM : 0; }
 
 hipError_t xtu_gemm_gate_up(int fmt, const void* x, const int32_t* sorted_tok, int H, int I,
                             const void* w13, const void* s13, const float* gs13,
@@ -323,10 +380,10 @@ hipError_t xtu_gemm_gate_up(int fmt, const void* x, const int32_t* sorted_tok, i
              seg_start, tile_expert, tile_row0, tile_lo, tile_hi, slot_map, act, H, I,
              w_estride, s_estride, limit, alpha, beta};
   switch (fmt) {
-    case kMXFP4: return launch_gemm<kMXFP4, 128>(true, a, max_tiles, stream);
-    case kNVFP4: return launch_gemm<kNVFP4, 128>(true, a, max_tiles, stream);
-    case kFP8: return launch_gemm<kFP8, 64>(true, a, max_tiles, stream);
-    case kBF16: return launch_gemm<kBF16, 128>(true, a, max_tiles, stream);
+    case kMXFP4: return launch_gemm<kMXFP4>(true, a, max_tiles, stream);
+    case kNVFP4: return launch_gemm<kNVFP4>(true, a, max_tiles, stream);
+    case kFP8: return launch_gemm<kFP8>(true, a, max_tiles, stream);
+    case kBF16: return launch_gemm<kBF16>(true, a, max_tiles, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -347,10 +404,10 @@ hipError_t xtu_gemm_down(int fmt, const void* act, int H, int I, const void* w2,
              seg_start, tile_expert, tile_row0, tile_lo, tile_hi, slot_map, y, H, I, w_estride,
              s_estride, 0.f, 1.f, 0.f};
   switch (fmt) {
-    case kMXFP4: return launch_gemm<kMXFP4, 128>(false, a, max_tiles, stream);
-    case kNVFP4: return launch_gemm<kNVFP4, 128>(false, a, max_tiles, stream);
-    case kFP8: return launch_gemm<kFP8, 64>(false, a, max_tiles, stream);
-    case kBF16: return launch_gemm<kBF16, 128>(false, a, max_tiles, stream);
+    case kMXFP4: return launch_gemm<kMXFP4>(false, a, max_tiles, stream);
+    case kNVFP4: return launch_gemm<kNVFP4>(false, a, max_tiles, stream);
+    case kFP8: return launch_gemm<kFP8>(false, a, max_tiles, stream);
+    case kBF16: return launch_gemm<kBF16>(false, a, max_tiles, stream);
   }
   return hipErrorInvalidValue;
 }
