@@ -39,7 +39,6 @@ namespace {
 
 constexpr int kBM = 128;            // rows per M tile
 constexpr int kRT = kBM / 16;       // 16-row MFMA tiles per M tile
-constexpr int kPW = 4;              // 16-row weight panels per wave
 constexpr int kGemmThreads = 256;
 constexpr int kBufFlags = 0x00020000;   // raw buffer resource, dword 3
 
@@ -73,16 +72,16 @@ struct GemmArgs {
 
 // One wave's weights of one step: a 16-byte chunk per panel, the chunk's raw
 // fp4 scale bits, and (fp8) the block scales of panels 0,1 and 2,3.
-template <int FMT>
+template <int FMT, int PW>
 struct BStep {
-  u32x4_t w[kPW];
-  uint32_t sc[kPW];
+  u32x4_t w[PW];
+  uint32_t sc[PW];
   float bs0, bs1;
 };
 
 // bf16 operand of MFMA group g of a chunk (k = q*kCK + 8g .. +7 of the lane's row).
-template <int FMT>
-__device__ __forceinline__ bf16x8_t dequant_group(const BStep<FMT>& b, int p, int g) {
+template <int FMT, int PW>
+__device__ __forceinline__ bf16x8_t dequant_group(const BStep<FMT, PW>& b, int p, int g) {
   uint32_t o[4];
   if constexpr (FMT == kMXFP4) {
     fp4x8_to_bf16(b.w[p][g], e8m0_to_f32(b.sc[p]), o);
@@ -90,7 +89,7 @@ __device__ __forceinline__ bf16x8_t dequant_group(const BStep<FMT>& b, int p, in
     const uint32_t raw = b.sc[p] >> (g < 2 ? 0 : 8);
     fp4x8_to_bf16_mul(b.w[p][g], e4m3_to_f32(raw & 0xffu), o);
   } else if constexpr (FMT == kFP8) {
-    const float bs = p < 2 ? b.bs0 : b.bs1;
+    const float bs = p < PW / 2 ? b.bs0 : b.bs1;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t d = b.w[p][2 * g + h];
@@ -107,20 +106,17 @@ __device__ __forceinline__ bf16x8_t dequant_group(const BStep<FMT>& b, int p, in
   return as_bf16x8(o[0], o[1], o[2], o[3]);
 }
 
-// Waves per SIMD the register budget is sized for: NVFP4's scale multiply
-// needs more than half of the register file.
-template <int FMT>
-constexpr int gemm_waves_per_simd() { return FMT == kNVFP4 ? 1 : 2; }
-
-template <int FMT, bool GU>
-__global__ __launch_bounds__(kGemmThreads, gemm_waves_per_simd<FMT>()) void moe_gemm_kernel(
-    GemmArgs a) {
+// Kernel shape: PW weight panels per wave (a workgroup covers 64*PW output
+// columns), weights prefetched PD steps ahead in registers, register budget
+// sized for WPS waves per SIMD.
+template <int FMT, bool GU, int PW, int PD, int WPS>
+__global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a) {
   using F = WFmt<FMT>;
   using S = GemmShape<FMT>;
   __shared__ __attribute__((aligned(16))) uint16_t As[2 * S::kABuf];
 
   // ---- work item
-  const int nbn = GU ? a.I / 128 : a.H / 256;
+  const int nbn = GU ? a.I / (32 * PW) : a.H / (64 * PW);
   const int lo = a.tile_lo[0];
   const int total = (a.tile_hi[0] - lo) * nbn;
   const int per = (total + 7) / 8;
@@ -155,11 +151,13 @@ __global__ __launch_bounds__(kGemmThreads, gemm_waves_per_simd<FMT>()) void moe_
       (void*)(GU ? a.a : a.a + (long)row0 * K), 0, -1, kBufFlags);
 
   // ---- B: this wave's panels
-  int pan[kPW];
+  // gate/up: panels [0, PW/2) are gate rows, [PW/2, PW) the up rows of the
+  // same columns; down: PW consecutive panels
+  int pan[PW];
 #pragma unroll
-  for (int p = 0; p < kPW; ++p) {
-    if (GU) pan[p] = (p < 2 ? 0 : a.I / 16) + nb * 8 + 2 * w + (p & 1);
-    else pan[p] = nb * 16 + 4 * w + p;
+  for (int p = 0; p < PW; ++p) {
+    if (GU) pan[p] = (p < PW / 2 ? 0 : a.I / 16) + (nb * 4 + w) * (PW / 2) + p % (PW / 2);
+    else pan[p] = (nb * 4 + w) * PW + p;
   }
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.w + (long)ws * a.w_estride), 0, (int)a.w_estride, kBufFlags);
@@ -167,11 +165,12 @@ __global__ __launch_bounds__(kGemmThreads, gemm_waves_per_simd<FMT>()) void moe_
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)sexp, 0, (int)a.s_estride, kBufFlags);
   const int sgroups = (int)scale_groups(K, F::kUG);
-  // fp8 block-scale rows of panels 0,1 and 2,3
+  // fp8 block-scale rows of panels [0, PW/2) and [PW/2, PW) (each run of
+  // panels lies inside one 128-row block)
   const float* bsc = reinterpret_cast<const float*>(sexp);
   const int kb128 = K / 128;
-  const int rb0 = GU ? nb : 2 * nb + w / 2;
-  const int rb1 = GU ? a.I / 128 + nb : rb0;
+  const int rb0 = pan[0] / 8;
+  const int rb1 = pan[PW / 2] / 8;
 
   auto load_a = [&](int s, u32x4_t (&ar)[S::kAL]) {
 #pragma unroll
@@ -183,15 +182,15 @@ __global__ __launch_bounds__(kGemmThreads, gemm_waves_per_simd<FMT>()) void moe_
 #pragma unroll
     for (int i = 0; i < S::kAL; ++i) *reinterpret_cast<u32x4_t*>(buf + alds[i]) = ar[i];
   };
-  auto load_b = [&](int s, BStep<FMT>& b) {
+  auto load_b = [&](int s, BStep<FMT, PW>& b) {
 #pragma unroll
-    for (int p = 0; p < kPW; ++p)
+    for (int p = 0; p < PW; ++p)
       b.w[p] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                rw, lane * 16, (pan[p] * nsteps + s) * 1024, 0));
     if constexpr (F::kSBY > 0) {
       const int g = s / F::kUG, ob = (s % F::kUG) * F::kSBY;
 #pragma unroll
-      for (int p = 0; p < kPW; ++p) {
+      for (int p = 0; p < PW; ++p) {
         const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(
             rs, lane * 16, (pan[p] * sgroups + g) * 1024 + (ob & ~3), 0);
         b.sc[p] = v >> (8 * (ob & 3));
@@ -210,56 +209,56 @@ __global__ __launch_bounds__(kGemmThreads, gemm_waves_per_simd<FMT>()) void moe_
   // the inner loop carries no per-row-tile branches.
   auto run = [&](auto nr_tag) {
     constexpr int NR = decltype(nr_tag)::value;
-    f32x4_t acc[NR][kPW];
+    f32x4_t acc[NR][PW];
 #pragma unroll
     for (int m = 0; m < NR; ++m)
 #pragma unroll
-      for (int p = 0; p < kPW; ++p) acc[m][p] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int p = 0; p < PW; ++p) acc[m][p] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](const BStep<FMT>& b, const uint16_t* buf) {
+    auto compute = [&](const BStep<FMT, PW>& b, const uint16_t* buf) {
 #pragma unroll
       for (int g = 0; g < S::kG; ++g) {
-        bf16x8_t bv[kPW];
+        bf16x8_t bv[PW];
 #pragma unroll
-        for (int p = 0; p < kPW; ++p) bv[p] = dequant_group<FMT>(b, p, g);
+        for (int p = 0; p < PW; ++p) bv[p] = dequant_group<FMT, PW>(b, p, g);
 #pragma unroll
         for (int m = 0; m < NR; ++m) {
           const bf16x8_t av = as_bf16x8(
               *reinterpret_cast<const u32x4_t*>(buf + afrag + m * 16 * S::kLD + 8 * g));
 #pragma unroll
-          for (int p = 0; p < kPW; ++p)
+          for (int p = 0; p < PW; ++p)
             acc[m][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv[p], acc[m][p], 0, 0, 0);
         }
       }
     };
 
-    // one barrier per step; the loads of step s+1 overlap the MFMAs of step s
+    // Step s: issue the A rows of step s+1 and the weights of step s+PD,
+    // run the MFMAs of step s, store the A rows to the other LDS buffer,
+    // barrier.  Weight buffers rotate through PD+1 register sets (the step
+    // loop is unrolled PD+1 times so every set is statically indexed).
+    // Scheduling barriers keep the loads ahead of the MFMAs; left alone, the
+    // compiler sinks them next to their first use.
+    constexpr int U = PD + 1;
     u32x4_t ar[S::kAL];
-    BStep<FMT> b0, b1;
+    BStep<FMT, PW> bb[U];
     load_a(0, ar);
-    load_b(0, b0);
+#pragma unroll
+    for (int j = 0; j < PD; ++j) load_b(min(j, nsteps - 1), bb[j]);
     store_a(As, ar);
     __syncthreads();
-    // (scheduling barriers keep the next step's loads ahead of this step's
-    // MFMAs; left alone, the compiler sinks them next to their first use)
-    for (int s = 0; s < nsteps; s += 2) {
-      const int s1 = min(s + 1, nsteps - 1);
-      load_a(s1, ar);
-      load_b(s1, b1);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(b0, As);
-      __builtin_amdgcn_sched_barrier(0);
-      store_a(As + S::kABuf, ar);
-      __syncthreads();
-      if (s + 1 < nsteps) {
-        const int s2 = min(s + 2, nsteps - 1);
-        load_a(s2, ar);
-        load_b(s2, b0);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(b1, As + S::kABuf);
-        __builtin_amdgcn_sched_barrier(0);
-        store_a(As, ar);
-        __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += U) {
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        const int s = s0 + j;
+        if (j == 0 || s < nsteps) {
+          load_a(min(s + 1, nsteps - 1), ar);
+          load_b(min(s + PD, nsteps - 1), bb[(j + PD) % U]);
+          __builtin_amdgcn_sched_barrier(0);
+          compute(bb[j], As + (s & 1) * S::kABuf);
+          __builtin_amdgcn_sched_barrier(0);
+          store_a(As + ((s + 1) & 1) * S::kABuf, ar);
+          __syncthreads();
+        }
       }
     }
 
@@ -271,13 +270,13 @@ __global__ __launch_bounds__(kGemmThreads, gemm_waves_per_simd<FMT>()) void moe_
 #pragma unroll
       for (int m = 0; m < NR; ++m)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
+        for (int p = 0; p < PW / 2; ++p) {
           const long col = (long)pan[p] * 16 + r16;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = m * 16 + 4 * q + i;
             if (r < rows) {
-              const float g = acc[m][p][i] * gsv, u = acc[m][p + 2][i] * gsv;
+              const float g = acc[m][p][i] * gsv, u = acc[m][p + PW / 2][i] * gsv;
               act[(long)(row0 + r) * a.I + col] =
                   f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
             }
@@ -288,7 +287,7 @@ __global__ __launch_bounds__(kGemmThreads, gemm_waves_per_simd<FMT>()) void moe_
 #pragma unroll
       for (int m = 0; m < NR; ++m)
 #pragma unroll
-        for (int p = 0; p < kPW; ++p) {
+        for (int p = 0; p < PW; ++p) {
           const long col = (long)pan[p] * 16 + r16;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -339,6 +338,31 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   }
 }
 
+// Kernel shape.  Measured on the DeepSeek-V3 FP8 layer (T = 8192): four
+// panels per wave, weights one step ahead and two waves per SIMD beat eight
+// panels per wave with two or three steps of prefetch at one wave per SIMD
+// (the second wave hides the first one's load and LDS waits).  XTU_GEMM_PW
+// = 8 selects the larger tile where N divides 512.
+#ifndef XTU_GEMM_PW
+#define XTU_GEMM_PW 4
+#endif
+#ifndef XTU_GEMM_PD
+#define XTU_GEMM_PD 1
+#endif
+#ifndef XTU_GEMM_WPS
+#define XTU_GEMM_WPS 2
+#endif
+
+template <int FMT, int PW, int PD, int WPS>
+hipError_t launch_shape(bool gu, const GemmArgs& a, int max_tiles, hipStream_t stream) {
+  const long items = (long)max_tiles * (gu ? a.I / (32 * PW) : a.H / (64 * PW));
+  const long grid = (items + 7) / 8 * 8;
+  if (grid >= (1L << 31)) return hipErrorInvalidValue;
+  if (gu) moe_gemm_kernel<FMT, true, PW, PD, WPS><<<dim3((unsigned)grid), kGemmThreads, 0, stream>>>(a);
+  else moe_gemm_kernel<FMT, false, PW, PD, WPS><<<dim3((unsigned)grid), kGemmThreads, 0, stream>>>(a);
+  return hipPeekAtLastError();
+}
+
 template <int FMT>
 hipError_t launch_gemm(bool gu, GemmArgs a, int max_tiles, hipStream_t stream) {
   using F = WFmt<FMT>;
@@ -346,12 +370,14 @@ hipError_t launch_gemm(bool gu, GemmArgs a, int max_tiles, hipStream_t stream) {
   if (!a.w_estride) a.w_estride = F::w_bytes(N, K);
   if (!a.s_estride) a.s_estride = F::s_bytes(N, K);
   if (a.w_estride >= (1L << 31) || a.s_estride >= (1L << 31)) return hipErrorInvalidValue;
-  const long items = (long)max_tiles * (gu ? a.I / 128 : a.H / 256);
-  const long grid = (items + 7) / 8 * 8;
-  if (grid >= (1L << 31)) return hipErrorInvalidValue;
-  if (gu) moe_gemm_kernel<FMT, true><<<dim3((unsigned)grid), kGemmThreads, 0, stream>>>(a);
-  else moe_gemm_kernel<FMT, false><<<dim3((unsigned)grid), kGemmThreads, 0, stream>>>(a);
-  return hipPeekAtLastError();
+  constexpr int PW = XTU_GEMM_PW;
+  if constexpr (PW > 4) {
+    if ((gu ? a.I % (32 * PW) : a.H % (64 * PW)) == 0)
+      return launch_shape<FMT, PW, XTU_GEMM_PD, XTU_GEMM_WPS>(gu, a, max_tiles, stream);
+  }
+  // NVFP4's scale multiply needs more than half of the register file
+  constexpr int kWps = FMT == kNVFP4 ? 1 : 2;
+  return launch_shape<FMT, 4, 1, kWps>(gu, a, max_tiles, stream);
 }
 
 }  // namespace
