@@ -195,6 +195,17 @@ def gpu_moe_layer_from_engine_tiled(engine: HostExpertStore, x, topk_ids, topk_w
     for t in range(min(ntile, ring.nslots)):
         issue(t)
     kw = dict(swiglu_limit=swiglu_limit, stream=st)
+    # resident and shared experts first, from the pool's planes: they need no
+    # copy, so their GEMMs run while the first tiles are in flight
+    if res_list or NS:
+        if pool is None:
+            return None   # shared experts need a resident home
+        bmap = pool.bucket_slot_map(streamed + res_list, E, NS)
+        b_lo = len(streamed)
+        if res_list:
+            expert_pass(x, seg, pool.planes, b_lo, b_lo + len(res_list), y, slot_map=bmap, **kw)
+        if NS:
+            expert_pass(x, seg, pool.planes, E, E + NS, y, slot_map=bmap, **kw)
     for t in range(ntile):
         s = t % ring.nslots
         st.wait_event(ring.ready[s])
@@ -205,15 +216,6 @@ def gpu_moe_layer_from_engine_tiled(engine: HostExpertStore, x, topk_ids, topk_w
         ring.free[s] = ev
         if t + ring.nslots < ntile:
             issue(t + ring.nslots)
-    # resident experts and shared experts from the pool's planes
-    if res_list or NS:
-        if pool is None:
-            return None   # shared experts need a resident home
-        bmap = pool.bucket_slot_map(streamed + res_list, E, NS)
-        b_lo = len(streamed)
-        expert_pass(x, seg, pool.planes, b_lo, b_lo + len(res_list), y, slot_map=bmap, **kw)
-        if NS:
-            expert_pass(x, seg, pool.planes, E, E + NS, y, slot_map=bmap, **kw)
     combine(seg, y, wts, out, stream=st)
     if stats is not None:
         stats.bytes, stats.tiles = moved, ntile
