@@ -72,6 +72,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-flush", action="store_true", help="keep caches warm between steps")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter runs behind roofline.traffic")
+    ap.add_argument("--pmc-child", type=int, default=0, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -90,6 +93,8 @@ def main():
     cfg = WORKLOADS[args.workload]
     if "resident" in cfg:
         return streamed(args, cfg)
+    if args.pmc_child:
+        return pmc_child(args, cfg, args.pmc_child)
     fmt = F.fmt_of(cfg["fmt"])
     E, NS, H, I, K = cfg["E"], cfg["NS"], cfg["H"], cfg["I"], cfg["K"]
     dev = torch.device("cuda:0")
@@ -257,7 +262,7 @@ def main():
                           gate_up_ms=mean_gu, gate_up_GBs=gu_bytes / (mean_gu / 1e3) / 1e9,
                           gate_up_TFLOPs=gu_flops / (mean_gu / 1e3) / 1e12,
                           graph=graph is not None, wall_s=wall,
-                          event_overhead_us=ev_overhead * 1e3)
+                          event_overhead_us=ev_overhead * 1e3, gate_up_bytes=gu_bytes)
         log(f"[bench] T={T}: layer {mean_layer * 1e3:.1f} us ({results[T]['layer_GBs']:.0f} GB/s), "
             f"gate_up {mean_gu * 1e3:.1f} us ({results[T]['gate_up_GBs']:.0f} GB/s, "
             f"{results[T]['gate_up_TFLOPs']:.0f} TFLOP/s), |D|={mean_active:.1f}")
@@ -269,6 +274,14 @@ def main():
         roof = dict(bound="hbm", achieved=r["gate_up_GBs"], peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=r["gate_up_GBs"] / HBM_PEAK_GBS, traffic=None,
                     kernel="decode_gate_up_kernel")
+        if not args.no_traffic:
+            tr = measure_traffic(args.workload, Th)
+            if tr is not None:
+                roof["traffic"] = tr["bytes"]
+                roof["traffic_detail"] = tr
+                if tr.get("distinct_experts"):   # the counter run's own routing
+                    tr["algorithmic_bytes"] = (tr["distinct_experts"] * e_bytes13 + Th * H * 2
+                                               + (Th * K + Th * NS) * I * 2)
     else:
         dt = "int8" if cfg["int8"] else "bf16"
         roof = dict(bound="mfma", achieved=r["gate_up_TFLOPs"], peak=PEAK_TFLOPS[dt],
@@ -308,6 +321,109 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+COPY_BYTES = 256 << 20   # calibration copy for the memory counters
+
+
+def pmc_child(args, cfg, T):
+    """Run under rocprofv3 --pmc by measure_traffic: three cold-cache launches
+    of the decode gate/up kernel at T tokens, then one device-to-device copy
+    of COPY_BYTES (the counter calibration)."""
+    import torch
+
+    from xtu_moe_amd import _lib
+    from xtu_moe_amd import formats as F
+    from xtu_moe_amd.layer import _p, _stream, route, segmentation
+    from xtu_moe_amd.synthetic import synth_layer
+
+    fmt = F.fmt_of(cfg["fmt"])
+    E, NS, H, I, K = cfg["E"], cfg["NS"], cfg["H"], cfg["I"], cfg["K"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.load()
+    W = synth_layer(fmt, E, NS, H, I, seed=0, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    x = torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16)
+    lg = torch.randn((T, E), generator=gen, device=dev)
+    rkw = dict(top_k=K, scoring="sigmoid", n_group=8, topk_group=4, routed_scaling_factor=2.5)
+    w_, i_ = route(lg, **rkw)
+    seg = segmentation(T, K, E, NS, 128, dev).run(i_, w_)
+    act = torch.empty((T * K + T * NS, I), dtype=torch.bfloat16, device=dev)
+    flush = torch.empty(256 << 20, dtype=torch.float32, device=dev)
+    st = _stream()
+    for _ in range(3):
+        flush.add_(1.0)
+        _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13),
+                  0, 0, 0, _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
+                  _p(seg.n_active), min(E, T * K) + NS, _p(act), cfg["limit"], 1.0, 0.0, st)
+    torch.cuda.synchronize()
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    flush.add_(1.0)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[pmc-child] distinct experts {len(torch.unique(i_)) + NS}", flush=True)
+
+
+def measure_traffic(workload, T, timeout=150):
+    """HBM bytes per launch of the decode gate/up kernel from two rocprofv3
+    counter runs of pmc_child (FETCH_SIZE, then WRITE_SIZE, in KiB per
+    dispatch), each scaled by the same counter's reading for a device copy of
+    known size.  None when rocprofv3 is unavailable or a run fails."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None
+    res = {}
+    tmp = tempfile.mkdtemp(prefix="xtu_pmc_")
+    try:
+        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+            d = os.path.join(tmp, ctr)
+            cmd = [prof, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", "p", "--",
+                   sys.executable, os.path.abspath(__file__), "--workload", workload,
+                   "--pmc-child", str(int(T))]
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout,
+                               cwd=tempfile.gettempdir(), env=dict(os.environ, TMPDIR=tempfile.gettempdir()))
+            if r.returncode != 0:
+                log(f"[bench] {ctr} counter run failed (rc={r.returncode})")
+                return None
+            for ln in r.stdout.splitlines():
+                if ln.startswith("[pmc-child] distinct experts "):
+                    res["distinct"] = int(ln.split()[-1])
+            path = None
+            for root, _, files in os.walk(d):
+                for f in files:
+                    if f.endswith("counter_collection.csv"):
+                        path = os.path.join(root, f)
+            if path is None:
+                return None
+            kern, copy = [], []
+            for row in csv.DictReader(open(path)):
+                name, v = row["Kernel_Name"], float(row["Counter_Value"]) * 1024.0
+                if "decode_gate_up" in name:
+                    kern.append(v)
+                elif "copyBuffer" in name or "copy" in name.lower():
+                    copy.append(v)
+            if not kern or not copy or max(copy) <= 0:
+                return None
+            factor = COPY_BYTES / max(copy)
+            res[ctr] = dict(raw=sum(kern) / len(kern), factor=factor,
+                            bytes=sum(kern) / len(kern) * factor)
+    except (OSError, subprocess.SubprocessError, ValueError, KeyError) as exc:
+        log(f"[bench] traffic counters unavailable: {type(exc).__name__}: {exc}")
+        return None
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return dict(bytes=res["FETCH_SIZE"]["bytes"] + res["WRITE_SIZE"]["bytes"],
+                distinct_experts=res.get("distinct"),
+                fetch_bytes=res["FETCH_SIZE"]["bytes"], write_bytes=res["WRITE_SIZE"]["bytes"],
+                fetch_factor=res["FETCH_SIZE"]["factor"], write_factor=res["WRITE_SIZE"]["factor"],
+                calibration=f"device copy of {COPY_BYTES} bytes under the same counter")
 
 
 def streamed(args, cfg):
