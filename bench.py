@@ -8,7 +8,11 @@ gate/up+SwiGLU -> down -> combine) over a fresh batch of synthetic tokens
 (x ~ N(0,1) bf16, logits ~ N(0,1)), weights N(0,0.02) quantised and resident in
 HBM.  Every timed step starts with the 256 MB last-level cache flushed (a
 1 GiB read-modify-write of a scratch buffer outside the timed events), so
-weights stream from HBM as they do when 61 layers take turns.
+weights stream from HBM as they do when 61 layers take turns.  Decode layers
+are timed inside a HIP graph of 8 such layers with distinct weights (each
+layer's output the next one's input, as in a model's forward graph): the
+layer time is the graph's time / 8, and the time of a graph of one layer
+(which adds one graph launch per layer) is reported beside it.
 
 The JSON line reports tokens/s at the largest T (value), the layer time, and:
   roofline      the dominant kernel (gate/up) against HBM (decode) or MFMA
@@ -57,6 +61,7 @@ WORKLOADS = {
                                tile_e=16, nslots=4, zipf=1.1),
 }
 PCIE_GEN5_X16_GBS = 64.0   # per direction, before protocol overhead
+CHAIN = 8                  # layers per decode graph
 
 
 def log(*a):
@@ -106,6 +111,14 @@ def main():
         W.int8_planes()
     torch.cuda.synchronize()
     log(f"[bench] built {E}+{NS} experts fmt={cfg['fmt']} in {time.time() - t0:.1f}s")
+    # decode: a graph of CHAIN layers with distinct weights, each layer's output
+    # the next one's input, as a model's forward graph runs them
+    chain_Ws = [W]
+    if cfg["graph"]:
+        for l in range(1, CHAIN):
+            chain_Ws.append(synth_layer(fmt, E, NS, H, I, seed=l, device=dev))
+        torch.cuda.synchronize()
+        log(f"[bench] built {CHAIN} layers for the layer-chain graph")
     flush = torch.empty(256 << 20, dtype=torch.float32, device=dev)   # 1 GiB
     gen = torch.Generator(device=dev).manual_seed(1234)
 
@@ -188,6 +201,60 @@ def main():
         torch.cuda.synchronize()
         wall = time.time() - wall0
         layer_ms = [a.elapsed_time(b) for a, b in ev]
+
+        # ---- layer chain: CHAIN distinct layers in one graph, time / CHAIN
+        chain_ms = []
+        chain_active = []
+        if graph is not None:
+            c_lg = [torch.empty((T, E), dtype=torch.float32, device=dev) for _ in chain_Ws]
+            c_out = [torch.empty((T, H), dtype=torch.bfloat16, device=dev) for _ in chain_Ws]
+            c_ids = [torch.empty((T, K), dtype=torch.int32, device=dev) for _ in chain_Ws]
+            c_wts = [torch.empty((T, K), dtype=torch.float32, device=dev) for _ in chain_Ws]
+
+            def chain_step():
+                xin = x_st
+                for l, Wl in enumerate(chain_Ws):
+                    rt_l = dict(rt, logits=c_lg[l])
+                    moe_forward(xin, c_ids[l], c_wts[l], Wl, swiglu_limit=cfg["limit"],
+                                out=c_out[l], int8=cfg["int8"], router=rt_l)
+                    xin = c_out[l]
+
+            def chain_load(s):
+                x_st.copy_(xs[s % len(xs)])
+                for l in range(len(chain_Ws)):
+                    c_lg[l].copy_(lgs[(s + l) % len(lgs)])
+
+            chain_load(0)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(2):
+                    chain_step()
+            torch.cuda.current_stream().wait_stream(side)
+            cgraph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(cgraph):
+                chain_step()
+            torch.cuda.synchronize()
+            for s in range(args.warmup):
+                chain_load(s)
+                cgraph.replay()
+            torch.cuda.synchronize()
+            cev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(args.steps)]
+            for s in range(args.steps):
+                chain_load(args.warmup + s)
+                if not args.no_flush:
+                    flush.add_(1.0)
+                cev[s][0].record()
+                cgraph.replay()
+                cev[s][1].record()
+            torch.cuda.synchronize()
+            chain_ms = [a.elapsed_time(b) / len(chain_Ws) for a, b in cev]
+            for s in range(args.steps):
+                for l in range(len(chain_Ws)):
+                    w_, i_ = route(lgs[(args.warmup + s + l) % len(lgs)], **rkw)
+                    chain_active.append(len(torch.unique(i_)) + NS)
+            del cgraph
         # distinct experts per step (algorithmic bytes), re-derived outside timing
         for s in range(args.steps):
             load(args.warmup + s)
@@ -250,6 +317,9 @@ def main():
         gu_ms = [max(g - ev_overhead, 1e-6) for g in gu_ms]
 
         A = T * K + T * NS
+        single_ms = float(np.mean(layer_ms))
+        if chain_ms:   # per-layer time inside the layer-chain graph
+            layer_ms, n_active = chain_ms, chain_active
         mean_layer = float(np.mean(layer_ms))
         mean_gu = float(np.mean(gu_ms))
         mean_active = float(np.mean(n_active))
@@ -262,8 +332,11 @@ def main():
                           gate_up_ms=mean_gu, gate_up_GBs=gu_bytes / (mean_gu / 1e3) / 1e9,
                           gate_up_TFLOPs=gu_flops / (mean_gu / 1e3) / 1e12,
                           graph=graph is not None, wall_s=wall,
-                          event_overhead_us=ev_overhead * 1e3, gate_up_bytes=gu_bytes)
-        log(f"[bench] T={T}: layer {mean_layer * 1e3:.1f} us ({results[T]['layer_GBs']:.0f} GB/s), "
+                          event_overhead_us=ev_overhead * 1e3, gate_up_bytes=gu_bytes,
+                          single_layer_graph_ms=single_ms,
+                          layer_chain=len(chain_Ws) if chain_ms else 1)
+        log(f"[bench] T={T}: layer {mean_layer * 1e3:.1f} us ({results[T]['layer_GBs']:.0f} GB/s; "
+            f"single-layer graph {single_ms * 1e3:.1f} us), "
             f"gate_up {mean_gu * 1e3:.1f} us ({results[T]['gate_up_GBs']:.0f} GB/s, "
             f"{results[T]['gate_up_TFLOPs']:.0f} TFLOP/s), |D|={mean_active:.1f}")
 
