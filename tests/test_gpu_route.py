@@ -151,3 +151,67 @@ def test_fused_small_route_segment_bit_exact(T, E, K, NS, mode):
     ets = np.concatenate([[0], np.cumsum((counts + 127) // 128)])
     np.testing.assert_array_equal(seg.expert_tile_start.cpu().numpy()[: E + NS + 1], ets)
     assert int(seg.n_tiles.item()) == ets[-1]
+
+
+@pytest.mark.parametrize("case", ["grouped_ties_bias", "softmax_ties", "given_ids_idmap",
+                                  "grouped_bm4"])
+def test_tiny_route_segment_edge_cases(case):
+    """The one-wave-per-token path (<= 64 pairs): exact ties, bias, id_map,
+    given ids with invalid / zero-weight pairs, several tiles per bucket."""
+    dev = torch.device("cuda")
+    rng = np.random.default_rng(len(case))
+    T, E, K, NS, bm = 4, 256, 8, 1, 128
+    id_map = None
+    if case == "softmax_ties":
+        E, K = 512, 10
+    if case == "grouped_bm4":
+        bm = 4
+    # few distinct values: many exact ties in scores and group scores
+    logits = (rng.integers(-2, 3, size=(T, E)) * 0.5).astype(np.float32)
+    bias = (rng.integers(-1, 2, size=E) * 0.125).astype(np.float32) if case == "grouped_ties_bias" else None
+    seg = L.segmentation(T, K, E, NS, bm, dev)
+    if case == "given_ids_idmap":
+        ids_np, wts_np = random_routing(T, K, E, seed=3, invalid_frac=0.15, zero_frac=0.15)
+        id_map = rng.permutation(E).astype(np.int32)
+        id_map[int(ids_np[0, 0]) % E] = -1
+        ids = torch.from_numpy(ids_np).to(dev)
+        wts = torch.from_numpy(wts_np).to(dev)
+        seg.run_small(2, ids, wts, id_map=torch.from_numpy(id_map).to(dev), drop_zero=True)
+        mapped = np.where((ids_np >= 0) & (ids_np < E), id_map[np.clip(ids_np, 0, E - 1)],
+                          ids_np).astype(np.int32)
+        ref = oracle.segment(mapped, wts_np, E, NS, True)
+    else:
+        ids = torch.empty((T, K), dtype=torch.int32, device=dev)
+        wts = torch.empty((T, K), dtype=torch.float32, device=dev)
+        lg = torch.from_numpy(logits).to(dev)
+        if case == "softmax_ties":
+            seg.run_small(0, ids, wts, logits=lg)
+            ids_np, wts_np = oracle.route_softmax_topk(logits, K)
+        else:
+            b = None if bias is None else torch.from_numpy(bias).to(dev)
+            seg.run_small(1, ids, wts, logits=lg, bias=b, n_group=8, topk_group=4,
+                          routed_scaling=2.5)
+            ids_np, wts_np = oracle.route_grouped_sigmoid(logits, bias, 8, 4, K, 2.5)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ids.cpu().numpy(), ids_np)
+        np.testing.assert_array_equal(wts.cpu().numpy().view(np.uint32), wts_np.view(np.uint32))
+        ref = oracle.segment(ids_np, wts_np, E, NS, True)
+    torch.cuda.synchronize()
+    A = seg.A
+    np.testing.assert_array_equal(seg.seg_start.cpu().numpy(), ref["seg_start"])
+    for k in ("sorted_pair", "sorted_tok", "inv"):
+        np.testing.assert_array_equal(getattr(seg, k).cpu().numpy()[:A], ref[k])
+    np.testing.assert_array_equal(seg.sorted_wts.cpu().numpy()[:A].view(np.uint32),
+                                  ref["sorted_wts"].view(np.uint32))
+    counts = np.diff(ref["seg_start"])[: E + NS]
+    nz = np.nonzero(counts)[0]
+    assert int(seg.n_active.item()) == len(nz)
+    np.testing.assert_array_equal(seg.active.cpu().numpy()[: len(nz)], nz)
+    nt = (counts + bm - 1) // bm
+    ets = np.concatenate([[0], np.cumsum(nt)])
+    np.testing.assert_array_equal(seg.expert_tile_start.cpu().numpy()[: E + NS + 1], ets)
+    assert int(seg.n_tiles.item()) == ets[-1]
+    te = np.repeat(np.arange(E + NS), nt)
+    tr = np.concatenate([ref["seg_start"][e] + bm * np.arange(nt[e]) for e in range(E + NS)])
+    np.testing.assert_array_equal(seg.tile_expert.cpu().numpy()[: ets[-1]], te)
+    np.testing.assert_array_equal(seg.tile_row0.cpu().numpy()[: ets[-1]], tr)
