@@ -51,7 +51,7 @@ WORKLOADS = {
     "ds-v3-fp8-prefill": dict(fmt="fp8", E=256, NS=1, H=7168, I=2048, K=8, router="grouped",
                               Ts=[8192], limit=0.0, int8=False, graph=False),
     "qwen3-next-int8": dict(fmt="mxfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
-                            Ts=[1, 4, 8192], limit=7.0, int8=True, graph=False),
+                            Ts=[1, 4, 8192], limit=7.0, int8=True, graph=True),
     "qwen3-next-nvfp4": dict(fmt="nvfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
                              Ts=[1, 4, 8192], limit=7.0, int8=False, graph=True),
     "mixtral-tiny-bf16": dict(fmt="bf16", E=8, NS=0, H=1024, I=2048, K=2, router="softmax",
@@ -92,7 +92,7 @@ def main():
 
     from xtu_moe_amd import _lib
     from xtu_moe_amd import formats as F
-    from xtu_moe_amd.layer import _p, _stream, moe_forward, route, segmentation
+    from xtu_moe_amd.layer import _p, _stream, int8_align_on, moe_forward, route, segmentation
     from xtu_moe_amd.synthetic import synth_layer
 
     cfg = WORKLOADS[args.workload]
@@ -136,6 +136,8 @@ def main():
     nsteps = args.warmup + args.steps
     results = {}
     for T in cfg["Ts"]:
+        # INT8 activations where the reference engine's token-count gate takes them
+        i8 = cfg["int8"] and int8_align_on(T, True)
         xs = [torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16) for _ in range(min(nsteps, 8))]
         if router_w is not None:
             lgs = [(x.float() @ router_w.t()).contiguous() for x in xs]
@@ -153,7 +155,7 @@ def main():
 
         def step():
             moe_forward(x_st, ids_st, wts_st, W, swiglu_limit=cfg["limit"], out=out_st,
-                        int8=cfg["int8"], router=rt)
+                        int8=i8, router=rt)
 
         def load(s):
             x_st.copy_(xs[s % len(xs)])
@@ -218,7 +220,7 @@ def main():
                 for l, Wl in enumerate(chain_Ws):
                     rt_l = dict(rt, logits=c_lg[l])
                     moe_forward(xin, c_ids[l], c_wts[l], Wl, swiglu_limit=cfg["limit"],
-                                out=c_out[l], int8=cfg["int8"], router=rt_l)
+                                out=c_out[l], int8=i8, router=rt_l)
                     xin = c_out[l]
 
             def chain_load(s):
@@ -266,15 +268,15 @@ def main():
         # ---- dominant kernel alone (gate/up), cold cache, same stream
         seg = None
         gu_ms = []
-        bm = 128 if cfg["int8"] else int(_lib.call("xtu_gemm_tile_m", fmt))
-        decode = T <= 16 and not cfg["int8"]
+        bm = 128 if i8 else int(_lib.call("xtu_gemm_tile_m", fmt))
+        decode = T <= 16 and not i8
         act = torch.empty((T * K + T * NS, I), dtype=torch.bfloat16, device=dev)
         for s in range(args.steps):
             load(args.warmup + s)
             w_, i_ = route(lg_st, **rkw)
             seg = segmentation(T, K, E, NS, bm, dev).run(i_, w_)
             st = _stream()
-            if cfg["int8"]:
+            if i8:
                 w13_8, emin13, _, _ = W.int8_planes()
                 a8x = torch.empty((T, H), dtype=torch.int8, device=dev)
                 crx = torch.empty(T, dtype=torch.int32, device=dev)
@@ -288,7 +290,7 @@ def main():
                           _p(W.gs13), 0, 0, 0, _p(seg.sorted_tok), _p(seg.seg_start),
                           _p(seg.active), _p(seg.n_active), min(E, T * K) + NS, _p(act),
                           cfg["limit"], 1.0, 0.0, st)
-            elif cfg["int8"]:
+            elif i8:
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
                 _lib.call("xtu_i8_gemm_gate_up", _p(a8x), _p(crx), _p(seg.sorted_tok), H, I,
                           _p(w13_8), _p(emin13), 0, _p(seg.seg_start), _p(seg.tile_expert),
@@ -335,7 +337,7 @@ def main():
                           gate_up_TFLOPs=gu_flops / (mean_gu / 1e3) / 1e12,
                           graph=graph is not None, wall_s=wall,
                           event_overhead_us=ev_overhead * 1e3, gate_up_bytes=gu_bytes,
-                          single_layer_graph_ms=single_ms,
+                          single_layer_graph_ms=single_ms, int8_activation=bool(i8),
                           layer_chain=len(chain_Ws) if chain_ms else 1)
         log(f"[bench] T={T}: layer {mean_layer * 1e3:.1f} us ({results[T]['layer_GBs']:.0f} GB/s; "
             f"single-layer graph {single_ms * 1e3:.1f} us), "

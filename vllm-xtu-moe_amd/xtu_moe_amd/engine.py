@@ -79,7 +79,7 @@ class _Engine:
         res = moe_forward(x.reshape(qlen, c.hidden_size).to(torch.bfloat16).contiguous(), ids,
                           weights.reshape(qlen, top_k).float(), self.weights, swiglu_limit=lim,
                           swiglu_alpha=c.swiglu_alpha, swiglu_beta=c.swiglu_beta,
-                          out_dtype=torch.float32, int8=bool(c.int8_activation), path="auto")
+                          out_dtype=torch.float32, int8="auto" if c.int8_activation else False, path="auto")
         out.view(qlen, c.hidden_size).copy_(res)
         return out
 

@@ -11,6 +11,8 @@ shape for the life of the process (as the reference does with its
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _lib
@@ -208,6 +210,32 @@ def route(logits, *, top_k, scoring="softmax", renormalize=True, bias=None, n_gr
     return wts, ids
 
 
+INT8_MIN_TOKENS_ENV = "XIAOTU_MOE_INT8_VNNI_MIN_TOKENS"
+INT8_FORCE_ENV = "XIAOTU_MOE_INT8_ALIGN"
+
+
+def int8_align_on(T: int, allowed: bool = True) -> bool:
+    """Whether a call of T tokens takes the INT8 ALIGN path, as the reference
+    engine gates it (xiaotu_moe/csrc/moe/moe_v2_packed4_w4a8.inc:409-433,
+    xiaotu_int8_mode.h): XIAOTU_MOE_INT8_ALIGN=1 forces it; otherwise the
+    format must allow it (`allowed`) and T must reach
+    XIAOTU_MOE_INT8_VNNI_MIN_TOKENS (default 160; <= 0 turns it off).  Below
+    the threshold the layer runs with bf16 activations (at decode sizes the
+    int8 quantisation buys nothing: the layer streams weights)."""
+    try:
+        if int(os.environ.get(INT8_FORCE_ENV, "0") or 0) != 0:
+            return True
+    except ValueError:
+        pass
+    if not allowed:
+        return False
+    try:
+        m = int(os.environ.get(INT8_MIN_TOKENS_ENV, "160") or 160)
+    except ValueError:
+        m = 160
+    return m > 0 and int(T) >= m
+
+
 def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0, swiglu_alpha=1.0,
                 swiglu_beta=0.0, out=None, out_dtype=torch.bfloat16, path="auto", int8=False,
                 drop_zero=True, id_map=None, slot_map=None, stream=None, return_seg=False,
@@ -215,7 +243,9 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     """Routed (+shared) experts of one layer; returns out [T, H].
 
     path: "auto" (decode kernels for T <= 16, grouped GEMMs otherwise),
-    "decode" or "gemm".  int8: INT8-activation x FP4-code ALIGN path (MXFP4).
+    "decode" or "gemm".  int8: INT8-activation x FP4-code ALIGN path (MXFP4):
+    True forces it, "auto" applies the reference's token-count gate
+    (int8_align_on).
     id_map: int32 [E] applied to topk_ids before bucketing; slot_map: int32
     [E+NS] bucket -> weight slot.  router: dict(logits=, scoring=, bias=,
     n_group=, topk_group=, routed_scaling_factor=, renormalize=) routes from
@@ -243,6 +273,9 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     wts = topk_weights if (topk_weights.dtype == torch.float32 and topk_weights.is_contiguous()) else topk_weights.float().contiguous()
     st = _stream(stream)
     fmt = W.fmt
+    if int8 == "auto":
+        int8 = int8_align_on(T, True)
+    int8 = bool(int8)
     if path == "auto":
         path = "decode" if (T <= DECODE_MAX_TOKENS and not int8) else "gemm"
     if path == "decode" and T > DECODE_MAX_TOKENS:
