@@ -92,7 +92,8 @@ def main():
 
     from xtu_moe_amd import _lib
     from xtu_moe_amd import formats as F
-    from xtu_moe_amd.layer import _p, _stream, int8_align_on, moe_forward, route, segmentation
+    from xtu_moe_amd.layer import (_fp8pair_bufs, _p, _stream, gemm_tile_m, int8_align_on,
+                                   moe_forward, route, segmentation)
     from xtu_moe_amd.synthetic import synth_layer
 
     cfg = WORKLOADS[args.workload]
@@ -268,7 +269,7 @@ def main():
         # ---- dominant kernel alone (gate/up), cold cache, same stream
         seg = None
         gu_ms = []
-        bm = 128 if i8 else int(_lib.call("xtu_gemm_tile_m", fmt))
+        bm = gemm_tile_m(fmt, i8)
         decode = T <= 16 and not i8
         act = torch.empty((T * K + T * NS, I), dtype=torch.bfloat16, device=dev)
         for s in range(args.steps):
@@ -276,6 +277,10 @@ def main():
             w_, i_ = route(lg_st, **rkw)
             seg = segmentation(T, K, E, NS, bm, dev).run(i_, w_)
             st = _stream()
+            fp8x = None
+            if not decode and not i8 and fmt == F.FMT_FP8:
+                fp8x = _fp8pair_bufs("x8", T, H, dev)
+                _lib.call("xtu_fp8pair_quant", _p(x_st), T, H, *[_p(t) for t in fp8x], st)
             if i8:
                 w13_8, emin13, _, _ = W.int8_planes()
                 a8x = torch.empty((T, H), dtype=torch.int8, device=dev)
@@ -296,6 +301,12 @@ def main():
                           _p(w13_8), _p(emin13), 0, _p(seg.seg_start), _p(seg.tile_expert),
                           _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), 0, cfg["limit"],
                           1.0, 0.0, st)
+            elif fp8x is not None:
+                lo, hi = seg.tile_range_ptrs(0, E + NS)
+                _lib.call("xtu_gemm8_gate_up", *[_p(t) for t in fp8x], _p(seg.sorted_tok), H, I,
+                          _p(W.w13), _p(W.s13), 0, 0, 0, _p(seg.seg_start), _p(seg.tile_expert),
+                          _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), cfg["limit"], 1.0,
+                          0.0, st)
             else:
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
                 _lib.call("xtu_gemm_gate_up", fmt, _p(x_st), _p(seg.sorted_tok), H, I, _p(W.w13),
@@ -359,6 +370,14 @@ def main():
                 if tr.get("distinct_experts"):   # the counter run's own routing
                     tr["algorithmic_bytes"] = (tr["distinct_experts"] * e_bytes13 + Th * H * 2
                                                + (Th * K + Th * NS) * I * 2)
+    elif cfg["fmt"] == "fp8" and not cfg["int8"]:
+        # e4m3 x e4m3 MFMA; every algorithmic product is two MFMA products
+        # (the activation's hi and lo halves)
+        ach = r["gate_up_TFLOPs"]
+        roof = dict(bound="mfma", achieved=ach, peak=PEAK_TFLOPS["fp8"], unit="TFLOP/s",
+                    frac=ach / PEAK_TFLOPS["fp8"], traffic=None, kernel="gemm8_kernel",
+                    mfma_issue_frac=2.0 * ach / PEAK_TFLOPS["fp8"],
+                    frac_of_bf16_peak=ach / PEAK_TFLOPS["bf16"])
     else:
         dt = "int8" if cfg["int8"] else "bf16"
         roof = dict(bound="mfma", achieved=r["gate_up_TFLOPs"], peak=PEAK_TFLOPS[dt],
@@ -385,7 +404,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"mxfp4": "bf16-mfma/e2m1+e8m0", "fp8": "bf16-mfma/e4m3+f32-block",
+        "dtype": {"mxfp4": "bf16-mfma/e2m1+e8m0",
+                  "fp8": ("bf16-mfma/e4m3+f32-block" if decode_head
+                          else "fp8-mfma/e4m3-pair x e4m3+f32-block"),
                   "nvfp4": "bf16-mfma/e2m1+e4m3", "bf16": "bf16"}[cfg["fmt"]]
                  if not cfg["int8"] else "int8-mfma/int32-acc",
         "data": "synthetic (seeded N(0,1) tokens and logits, N(0,0.02) weights quantised)",
@@ -619,7 +640,7 @@ def streamed(args, cfg):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16-mfma/e4m3+f32-block",
+        "dtype": "fp8-mfma/e4m3-pair x e4m3+f32-block",
         "data": "synthetic (seeded N(0,1) tokens, Zipf(1.1)+Gumbel logits, N(0,0.02) weights quantised)",
         "config": {"workload": args.workload, "T": T, "hidden": H, "intermediate": I,
                    "routed_experts": E, "shared_experts": NS, "top_k": K, "weights": cfg["fmt"],

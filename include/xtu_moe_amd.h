@@ -151,6 +151,37 @@ hipError_t xtu_combine(const float* y, const int32_t* inv, const float* topk_wei
                        const int32_t* trash_start, int T, int K, int n_shared, int H, void* out,
                        int out_bf16, hipStream_t stream);
 
+/* ------------------------------------------------- exact FP8 prefill GEMMs
+ * FP8-weight grouped GEMMs on the scaled fp8 MFMA (16x16x128 e4m3 x e4m3),
+ * the dequantised-fp32 product up to fp32 summation order.  Replace the
+ * reference's Triton FP8 prefill kernels (gpu_prefill_fp8.py:101-205,
+ * gate_up_kernel_fp8 / down_kernel_fp8), which round e4m3 * block scale to a
+ * bf16 operand.  Activation rows are first split by xtu_fp8pair_quant into
+ * e4m3 pairs (hi, lo) with per-32-k e8m0 scales (shi, slo) such that
+ * x = hi * 2^(shi-127) + lo * 2^(slo-127) exactly (bf16 x); planes hi, lo
+ * [M][K] bytes, shi, slo [M][K/32] bytes.  The GEMMs take the pairs of x
+ * (gate/up, rows gathered through sorted_tok) or of act (down), the e4m3
+ * P16 weights and their [N/128][K/128] fp32 block scales, and M tiles of
+ * xtu_gemm8_tile_m() rows from xtu_segment(bm = that); outputs as
+ * xtu_gemm_gate_up / xtu_gemm_down. */
+int xtu_gemm8_tile_m(void);
+hipError_t xtu_fp8pair_quant(const void* x, int M, int K, uint8_t* hi, uint8_t* lo, uint8_t* shi,
+                             uint8_t* slo, hipStream_t stream);
+hipError_t xtu_gemm8_gate_up(const uint8_t* hi, const uint8_t* lo, const uint8_t* shi,
+                             const uint8_t* slo, const int32_t* sorted_tok, int H, int I,
+                             const void* w13, const float* s13, long w_estride, long s_estride,
+                             const int32_t* slot_map, const int32_t* seg_start,
+                             const int32_t* tile_expert, const int32_t* tile_row0,
+                             const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                             void* act, float limit, float alpha, float beta, hipStream_t stream);
+hipError_t xtu_gemm8_down(const uint8_t* hi, const uint8_t* lo, const uint8_t* shi,
+                          const uint8_t* slo, int H, int I, const void* w2, const float* s2,
+                          long w_estride, long s_estride, const int32_t* slot_map,
+                          const int32_t* seg_start, const int32_t* tile_expert,
+                          const int32_t* tile_row0, const int32_t* tile_lo,
+                          const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream);
+
+
 /* -------------------------------------- INT8-activation x FP4-code (ALIGN) path
  * Replaces the engine's ALIGN integer path (xiaotu_moe/csrc/moe/
  * moe_v2_packed4_w4a8.inc:478-586 xiaotu_predecode_block, :661-715

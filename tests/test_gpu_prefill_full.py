@@ -1,0 +1,69 @@
+"""DeepSeek-V3 FP8 layer at its full prefill size (H=7168, I=2048, 256 routed
++ 1 shared experts, T=8192 tokens, grouped sigmoid top-8): properties that
+hold at any size, and sampled tokens against the oracle.
+
+* Token permutation: each output row is reduced in a fixed order that does
+  not depend on the row's position in its M tile or on the other tokens, so
+  permuting the batch permutes the output bit for bit.
+* Sampled tokens: the oracle's dequantised-fp32 layer for three tokens of
+  the batch (only their experts, at full H and I); the layer's bf16 output
+  within max-abs 2e-2 (plus half a bf16 ulp of the value) and rel-L2 5e-3.
+  FP8 prefill operands are bf16(e4m3 * block scale), the reference GPU
+  kernels' rounding, so fp32 outputs of magnitude ~10 differ from the exact
+  dequantisation by a few 1e-2: the comparison is made on the bf16 outputs
+  the layer returns, and the fp32 rel-L2 is held to the same 5e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import REL_L2, bf16_tensor_to_bits, check_close, oracle_layer, rel_l2
+from xtu_moe_amd import formats as F
+from xtu_moe_amd.layer import moe_forward, route
+from xtu_moe_amd.synthetic import dense_experts, synth_layer
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, NS, K, T = 7168, 2048, 256, 1, 8, 8192
+
+
+@pytest.fixture(scope="module")
+def layer():
+    dev = torch.device("cuda")
+    W = synth_layer(F.FMT_FP8, E, NS, H, I, seed=3, device=dev)
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+    logits = torch.randn((T, E), generator=g, device=dev)
+    wts, ids = route(logits, top_k=K, scoring="sigmoid", n_group=8, topk_group=4,
+                     routed_scaling_factor=2.5)
+    out = moe_forward(x, ids, wts, W, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    yield W, x, ids, wts, out
+    del W
+    torch.cuda.empty_cache()
+
+
+def test_token_permutation_is_bitwise_equivariant(layer):
+    W, x, ids, wts, out = layer
+    perm = torch.randperm(T, generator=torch.Generator().manual_seed(5)).to(x.device)
+    out_p = moe_forward(x[perm].contiguous(), ids[perm].contiguous(), wts[perm].contiguous(), W,
+                        out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(out_p, out[perm])
+
+
+def test_sampled_tokens_match_oracle(layer):
+    W, x, ids, wts, out = layer
+    toks = [0, T // 2 + 17, T - 1]
+    ids_s = ids[toks].cpu().numpy()
+    used = np.unique(ids_s)
+    remap = {int(e): i for i, e in enumerate(used)}
+    cids = np.vectorize(remap.get)(ids_s).astype(np.int32)
+    U = len(used)
+    dn = dense_experts(W, list(used) + [E + s for s in range(NS)])
+    ref = oracle_layer(F.FMT_FP8, dn, bf16_tensor_to_bits(x[toks]), cids,
+                       wts[toks].cpu().numpy(), U, NS, H, I)
+    got = out[toks]
+    check_close(got.to(torch.bfloat16).float().cpu().numpy(), ref, bf16_out=True,
+                what="ds-v3 fp8 T=8192 sample (bf16 output)")
+    assert rel_l2(got.cpu().numpy(), ref) <= REL_L2

@@ -39,6 +39,12 @@ SIGNATURES = {
     "xtu_gemm_down": (_i, [_i, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp, _vp,
                            _i, _vp, _vp]),
     "xtu_combine": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
+    "xtu_gemm8_tile_m": (_i, []),
+    "xtu_fp8pair_quant": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "xtu_gemm8_gate_up": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp,
+                               _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
+    "xtu_gemm8_down": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp,
+                            _vp, _i, _vp, _vp]),
     "xtu_copy_experts": (_i, [_i, _vp, _vp, _l, _vp, _l, _l, _vp]),
     "xtu_i8_weight_bytes": (_sz, [_i, _i]),
     "xtu_i8_prepare": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
@@ -57,7 +63,8 @@ SIGNATURES = {
 # entry points whose int return value is a size/count, not a status
 _NOT_STATUS = {"xtu_version", "xtu_error_string", "xtu_segment_workspace_bytes",
                "xtu_route_segment_small_max_pairs",
-               "xtu_segment_max_tiles", "xtu_gemm_tile_m", "xtu_i8_weight_bytes"}
+               "xtu_segment_max_tiles", "xtu_gemm_tile_m", "xtu_gemm8_tile_m",
+               "xtu_i8_weight_bytes"}
 
 _LIB = None
 

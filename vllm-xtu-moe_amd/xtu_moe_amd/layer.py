@@ -236,6 +236,24 @@ def int8_align_on(T: int, allowed: bool = True) -> bool:
     return m > 0 and int(T) >= m
 
 
+def gemm_tile_m(fmt: int, int8: bool = False) -> int:
+    """Rows per M tile of the grouped GEMM that runs for this format: INT8
+    ALIGN 128, FP8 weights the exact fp8-MFMA kernels, else the bf16-operand
+    kernels (the segmentation's tiles must match)."""
+    if int8:
+        return 128
+    if int(fmt) == FMT_FP8:
+        return int(_lib.call("xtu_gemm8_tile_m"))
+    return int(_lib.call("xtu_gemm_tile_m", int(fmt)))
+
+
+def _fp8pair_bufs(tag, M, K, dev):
+    return (_buf(tag + "_hi", (max(M, 1), K), torch.uint8, dev),
+            _buf(tag + "_lo", (max(M, 1), K), torch.uint8, dev),
+            _buf(tag + "_shi", (max(M, 1), K // 32), torch.uint8, dev),
+            _buf(tag + "_slo", (max(M, 1), K // 32), torch.uint8, dev))
+
+
 def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0, swiglu_alpha=1.0,
                 swiglu_beta=0.0, out=None, out_dtype=torch.bfloat16, path="auto", int8=False,
                 drop_zero=True, id_map=None, slot_map=None, stream=None, return_seg=False,
@@ -280,7 +298,7 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         path = "decode" if (T <= DECODE_MAX_TOKENS and not int8) else "gemm"
     if path == "decode" and T > DECODE_MAX_TOKENS:
         raise ValueError(f"decode path handles at most {DECODE_MAX_TOKENS} tokens")
-    bm = 128 if int8 else int(_lib.call("xtu_gemm_tile_m", fmt))
+    bm = gemm_tile_m(fmt, int8)
     seg = segmentation(T, K, E, NS, bm, dev)
     if router is not None:
         mode = 1 if router.get("scoring", "softmax") == "sigmoid" else 0
@@ -357,6 +375,21 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
                   seg.max_tiles, _p(y), 0, st)
         return
     fmt = W.fmt
+    if fmt == FMT_FP8:
+        # exact FP8: activations split into e4m3 pairs, fp8 MFMA with the fp32
+        # block scale folded per 128-k block
+        xq = _fp8pair_bufs("x8", T, H, dev)
+        aq = _fp8pair_bufs("a8", A, I, dev)
+        _lib.call("xtu_fp8pair_quant", _p(x), T, H, *[_p(t) for t in xq], st)
+        _lib.call("xtu_gemm8_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
+                  _p(W.w13), _p(W.s13), 0, 0, _p(slot_map), _p(seg.seg_start),
+                  _p(seg.tile_expert), _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), lim,
+                  al, be, st)
+        _lib.call("xtu_fp8pair_quant", _p(act), A, I, *[_p(t) for t in aq], st)
+        _lib.call("xtu_gemm8_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(W.s2), 0, 0,
+                  _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo,
+                  hi, seg.max_tiles, _p(y), st)
+        return
     _lib.call("xtu_gemm_gate_up", fmt, _p(x), _p(seg.sorted_tok), H, I, _p(W.w13), _p(W.s13),
               _p(W.gs13), 0, 0, _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
               _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), lim, al, be, st)

@@ -27,9 +27,8 @@ import os
 
 import torch
 
-from . import _lib
 from .host_store import HostExpertStore, empty_slots
-from .layer import _buf, _p, _stream, combine, expert_pass, segmentation
+from .layer import _buf, _p, _stream, combine, expert_pass, gemm_tile_m, segmentation
 
 DEFAULT_TILE_E = 48
 _RINGS: dict = {}
@@ -165,7 +164,7 @@ def gpu_moe_layer_from_engine_tiled(engine: HostExpertStore, x, topk_ids, topk_w
     for b, e in enumerate(streamed + res_list):
         id_map_h[e] = b
     id_map = id_map_h.to(device, non_blocking=True)
-    bm = int(_lib.call("xtu_gemm_tile_m", fmt))
+    bm = gemm_tile_m(fmt)
     seg = segmentation(T, K, E, NS, bm, device)
     seg.run(ids, wts, id_map, True, st)
     y = _buf("ring_y", (max(seg.A, 1), H), torch.float32, device)
