@@ -305,8 +305,8 @@ def main():
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
                 _lib.call("xtu_gemm8_gate_up", *[_p(t) for t in fp8x], _p(seg.sorted_tok), H, I,
                           _p(W.w13), _p(W.s13), 0, 0, 0, _p(seg.seg_start), _p(seg.tile_expert),
-                          _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), cfg["limit"], 1.0,
-                          0.0, st)
+                          _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi, seg.max_tiles,
+                          _p(act), cfg["limit"], 1.0, 0.0, st)
             else:
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
                 _lib.call("xtu_gemm_gate_up", fmt, _p(x_st), _p(seg.sorted_tok), H, I, _p(W.w13),

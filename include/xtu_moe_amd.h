@@ -162,7 +162,8 @@ hipError_t xtu_combine(const float* y, const int32_t* inv, const float* topk_wei
  * [M][K] bytes, shi, slo [M][K/32] bytes.  The GEMMs take the pairs of x
  * (gate/up, rows gathered through sorted_tok) or of act (down), the e4m3
  * P16 weights and their [N/128][K/128] fp32 block scales, and M tiles of
- * xtu_gemm8_tile_m() rows from xtu_segment(bm = that); outputs as
+ * xtu_gemm8_tile_m() rows from xtu_segment(bm = that) (and its
+ * expert_tile_start, which orders the work items); outputs as
  * xtu_gemm_gate_up / xtu_gemm_down. */
 int xtu_gemm8_tile_m(void);
 hipError_t xtu_fp8pair_quant(const void* x, int M, int K, uint8_t* hi, uint8_t* lo, uint8_t* shi,
@@ -172,14 +173,16 @@ hipError_t xtu_gemm8_gate_up(const uint8_t* hi, const uint8_t* lo, const uint8_t
                              const void* w13, const float* s13, long w_estride, long s_estride,
                              const int32_t* slot_map, const int32_t* seg_start,
                              const int32_t* tile_expert, const int32_t* tile_row0,
-                             const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
-                             void* act, float limit, float alpha, float beta, hipStream_t stream);
+                             const int32_t* expert_tile_start, const int32_t* tile_lo,
+                             const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                             float alpha, float beta, hipStream_t stream);
 hipError_t xtu_gemm8_down(const uint8_t* hi, const uint8_t* lo, const uint8_t* shi,
                           const uint8_t* slo, int H, int I, const void* w2, const float* s2,
                           long w_estride, long s_estride, const int32_t* slot_map,
                           const int32_t* seg_start, const int32_t* tile_expert,
-                          const int32_t* tile_row0, const int32_t* tile_lo,
-                          const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream);
+                          const int32_t* tile_row0, const int32_t* expert_tile_start,
+                          const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                          float* y, hipStream_t stream);
 
 
 /* -------------------------------------- INT8-activation x FP4-code (ALIGN) path

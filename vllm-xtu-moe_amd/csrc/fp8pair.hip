@@ -27,9 +27,11 @@
 // chunks of the block's two 64-k super-blocks -- and the e8m0 scale of the
 // 32-k block b comes from lanes 16b..16b+15.
 //
-// Work items, XCD-contiguous ranges, the double-buffered LDS stage of the
-// gathered rows and the epilogues follow the bf16-operand kernels in
-// gemm.hip; M tiles hold 64 rows (4 row tiles) so the two register sets of
+// Work items are dealt to the XCDs in contiguous ranges as in gemm.hip, but
+// ordered (expert, N block, M tile) with the M tile fastest: the weights are
+// the bytes that matter (an expert's weight slice is 7x its rows), and the
+// workgroups streaming one slice run side by side.  The double-buffered LDS
+// stage of the gathered rows and the epilogues follow gemm.hip; M tiles hold 64 rows (4 row tiles) so the two register sets of
 // weights fit beside the accumulators at two waves per SIMD (96 rows spill).
 #include <type_traits>
 
@@ -134,6 +136,7 @@ struct Gemm8Args {
   const int32_t* seg_start;
   const int32_t* tile_expert;
   const int32_t* tile_row0;
+  const int32_t* expert_tile_start;   // first tile of each bucket
   const int32_t* tile_lo;
   const int32_t* tile_hi;
   const int32_t* slot_map;
@@ -161,8 +164,15 @@ __global__ __launch_bounds__(kThreads8, 2) void gemm8_kernel(Gemm8Args a) {
   if (idx >= per) return;
   const int item = (blockIdx.x % 8) * per + idx;
   if (item >= total) return;
-  const int tile = tlo + item / nbn, nb = item % nbn;
-  const int e = a.tile_expert[tile];
+  // an expert's items are contiguous (its tiles x nbn); inside them the M
+  // tile runs fastest, so the workgroups that stream one weight slice start
+  // together and share it through L2
+  const int j0 = tlo + item / nbn;
+  const int e = a.tile_expert[j0];
+  const int t0 = a.expert_tile_start[e];
+  const int ntl = a.expert_tile_start[e + 1] - t0;
+  const int local = tlo * nbn + item - t0 * nbn;
+  const int nb = local / ntl, tile = t0 + local % ntl;
   const int ws = a.slot_map ? a.slot_map[e] : e;
   const int row0 = a.tile_row0[tile];
   const int rows = min(kBM8, a.seg_start[e + 1] - row0);
@@ -396,19 +406,19 @@ hipError_t xtu_gemm8_gate_up(const uint8_t* hi, const uint8_t* lo, const uint8_t
                              const void* w13, const float* s13, long w_estride, long s_estride,
                              const int32_t* slot_map, const int32_t* seg_start,
                              const int32_t* tile_expert, const int32_t* tile_row0,
-                             const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
-                             void* act, float limit, float alpha, float beta,
-                             hipStream_t stream) {
+                             const int32_t* expert_tile_start, const int32_t* tile_lo,
+                             const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                             float alpha, float beta, hipStream_t stream) {
   XTU_CHECK_ARG(H > 0 && I > 0 && H % 256 == 0 && I % 128 == 0 && H <= 65536);
   XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(w_estride < (1L << 31) && 2L * I * H < (1L << 31));
   XTU_CHECK_ARG(hi && lo && shi && slo && sorted_tok && w13 && s13 && seg_start && tile_expert &&
-                tile_row0 && tile_lo && tile_hi && act);
+                tile_row0 && expert_tile_start && tile_lo && tile_hi && act);
   if (max_tiles == 0) return hipSuccess;
   (void)hipGetLastError();
   Gemm8Args a{hi, lo, shi, slo, sorted_tok, (const uint8_t*)w13, s13, seg_start, tile_expert,
-              tile_row0, tile_lo, tile_hi, slot_map, act, H, I, w_estride, s_estride,
-              limit, alpha, beta};
+              tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, act, H, I, w_estride,
+              s_estride, limit, alpha, beta};
   return launch_gemm8(true, a, max_tiles, stream);
 }
 
@@ -416,18 +426,19 @@ hipError_t xtu_gemm8_down(const uint8_t* hi, const uint8_t* lo, const uint8_t* s
                           const uint8_t* slo, int H, int I, const void* w2, const float* s2,
                           long w_estride, long s_estride, const int32_t* slot_map,
                           const int32_t* seg_start, const int32_t* tile_expert,
-                          const int32_t* tile_row0, const int32_t* tile_lo,
-                          const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream) {
+                          const int32_t* tile_row0, const int32_t* expert_tile_start,
+                          const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                          float* y, hipStream_t stream) {
   XTU_CHECK_ARG(H > 0 && I > 0 && H % 256 == 0 && I % 128 == 0 && I <= 65536);
   XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(w_estride < (1L << 31) && (long)H * I < (1L << 31));
   XTU_CHECK_ARG(hi && lo && shi && slo && w2 && s2 && seg_start && tile_expert && tile_row0 &&
-                tile_lo && tile_hi && y);
+                expert_tile_start && tile_lo && tile_hi && y);
   if (max_tiles == 0) return hipSuccess;
   (void)hipGetLastError();
   Gemm8Args a{hi, lo, shi, slo, nullptr, (const uint8_t*)w2, s2, seg_start, tile_expert,
-              tile_row0, tile_lo, tile_hi, slot_map, y, H, I, w_estride, s_estride,
-              0.f, 1.f, 0.f};
+              tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, y, H, I, w_estride,
+              s_estride, 0.f, 1.f, 0.f};
   return launch_gemm8(false, a, max_tiles, stream);
 }
 

@@ -42,9 +42,9 @@ SIGNATURES = {
     "xtu_gemm8_tile_m": (_i, []),
     "xtu_fp8pair_quant": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "xtu_gemm8_gate_up": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp,
-                               _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
+                               _vp, _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
     "xtu_gemm8_down": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp,
-                            _vp, _i, _vp, _vp]),
+                            _vp, _vp, _i, _vp, _vp]),
     "xtu_copy_experts": (_i, [_i, _vp, _vp, _l, _vp, _l, _l, _vp]),
     "xtu_i8_weight_bytes": (_sz, [_i, _i]),
     "xtu_i8_prepare": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp]),

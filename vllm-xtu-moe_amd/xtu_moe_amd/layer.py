@@ -383,12 +383,12 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
         _lib.call("xtu_fp8pair_quant", _p(x), T, H, *[_p(t) for t in xq], st)
         _lib.call("xtu_gemm8_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
                   _p(W.w13), _p(W.s13), 0, 0, _p(slot_map), _p(seg.seg_start),
-                  _p(seg.tile_expert), _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), lim,
-                  al, be, st)
+                  _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi,
+                  seg.max_tiles, _p(act), lim, al, be, st)
         _lib.call("xtu_fp8pair_quant", _p(act), A, I, *[_p(t) for t in aq], st)
         _lib.call("xtu_gemm8_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(W.s2), 0, 0,
-                  _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo,
-                  hi, seg.max_tiles, _p(y), st)
+                  _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
+                  _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
         return
     _lib.call("xtu_gemm_gate_up", fmt, _p(x), _p(seg.sorted_tok), H, I, _p(W.w13), _p(W.s13),
               _p(W.gs13), 0, 0, _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
