@@ -119,6 +119,25 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
                            const int32_t* active, const int32_t* n_active, int max_active,
                            float* y, hipStream_t stream);
 
+/* Down projection with the weighted combine fused: out[t] = sum over t's live
+ * pairs (t, e) of w * (act_row W2_e^T), bf16 (out_bf16 = 1) or fp32 [T][H],
+ * every row written.  Replaces moe4_smallm_dn2 (moe4_smallm.cu:260-333,
+ * 416-430), which scatters the same sums with atomics; here each token's sum
+ * runs over its experts in active-slot order (deterministic).  sorted_wts:
+ * the segmentation's per-row weights (1 for shared rows); trash = E + NS.
+ * xtu_decode_down_combine_ok reports whether a batch fits (T <= 16, I a
+ * multiple of 128 with I/128 splitting into waves of 1, 2 or 4 units, the
+ * A = T*(K+NS) act rows within the LDS stage); the entry returns
+ * hipErrorInvalidValue otherwise. */
+int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int max_active);
+hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int A, int H, int I,
+                                   const void* w2, const void* s2, const float* gs2,
+                                   long w_estride, long s_estride, const int32_t* slot_map,
+                                   const int32_t* sorted_tok, const float* sorted_wts,
+                                   const int32_t* seg_start, int trash, const int32_t* active,
+                                   const int32_t* n_active, int max_active, void* out,
+                                   int out_bf16, hipStream_t stream);
+
 /* ------------------------------------------------ grouped GEMM (prefill) path
  * Replaces _gate_up_kernel / _down_kernel (vllm_xiaotu_moe/gpu_prefill.py:
  * 232-390) and gate_up_kernel_fp8 / down_kernel_fp8

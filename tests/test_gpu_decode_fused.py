@@ -1,0 +1,133 @@
+"""Decode down projection with the weighted combine fused (xtu_decode_down_combine)
+against the dequantized-fp32 oracle and against the separate down + combine
+kernels, all four weight formats, plus the cases the fused form treats on its
+own: a token listing an expert twice, zero weights kept or dropped, invalid
+ids, every pair dropped, a weight-slot map, bf16 output, and token order."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import (bf16_tensor_to_bits, check_close, dense_to_numpy, make_dense_layer,
+                     oracle_layer, random_routing)
+from xtu_moe_amd import formats as F
+from xtu_moe_amd import layer as L
+from xtu_moe_amd.layer import ExpertWeights, moe_forward
+
+pytestmark = pytest.mark.gpu
+
+FMTS = [F.FMT_MXFP4, F.FMT_NVFP4, F.FMT_FP8, F.FMT_BF16]
+
+
+def _layer(fmt, E, NS, H, I, seed):
+    d = make_dense_layer(fmt, E + NS, H, I, seed=seed)
+    W = ExpertWeights.from_dense(fmt, d["w13"], d["s13"], d["w2"], d["s2"], d["gs13"], d["gs2"],
+                                 n_shared=NS, device="cuda")
+    return d, W
+
+
+def _run(x, ids, wts, W, monkeypatch, fused, **kw):
+    monkeypatch.setenv(L.FUSED_DOWN_ENV, "1" if fused else "0")
+    out = moe_forward(x.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(), W,
+                      path="decode", **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,H,I", [(1, 512, 512), (2, 256, 1024), (4, 512, 256), (16, 512, 256)])
+def test_fused_vs_oracle_and_unfused(fmt, T, H, I, monkeypatch):
+    E, NS, K = 16, 1, 4
+    d, W = _layer(fmt, E, NS, H, I, seed=T + I)
+    ids, wts = random_routing(T, K, E, seed=T)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
+    A = T * (K + NS)
+    assert L.decode_fused_down_ok(fmt, T, A, H, I, min(E, T * K) + NS)
+    fused = _run(x, ids, wts, W, monkeypatch, True, out_dtype=torch.float32)
+    split = _run(x, ids, wts, W, monkeypatch, False, out_dtype=torch.float32)
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I)
+    check_close(fused.cpu().numpy(), ref, bf16_out=False, what=f"fused fmt={fmt} T={T}")
+    check_close(split.cpu().numpy(), ref, bf16_out=False, what=f"split fmt={fmt} T={T}")
+    # same products, summed in another order: a few fp32 ulps of the row scale
+    scale = float(np.abs(ref).max()) + 1e-6
+    assert float((fused - split).abs().max()) <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("drop_zero", [True, False])
+def test_fused_duplicates_zero_weights_invalid_ids(drop_zero, monkeypatch):
+    fmt, E, NS, H, I, T, K = F.FMT_MXFP4, 12, 1, 256, 512, 6, 4
+    d, W = _layer(fmt, E, NS, H, I, seed=21)
+    ids, wts = random_routing(T, K, E, seed=22)
+    ids[0, 1] = ids[0, 0]            # token 0 lists one expert twice
+    ids[1, 2] = ids[1, 3] = ids[1, 0]
+    wts[2, 1] = 0.0                  # zero weights, kept or dropped
+    wts[3, :] = 0.0
+    ids[4, 0], ids[4, 2] = -1, E + 2  # invalid ids go to the trash bucket
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
+    out = _run(x, ids, wts, W, monkeypatch, True, out_dtype=torch.float32, drop_zero=drop_zero)
+    split = _run(x, ids, wts, W, monkeypatch, False, out_dtype=torch.float32,
+                 drop_zero=drop_zero)
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"dup/zero drop_zero={drop_zero}")
+    scale = float(np.abs(ref).max()) + 1e-6
+    assert float((out - split).abs().max()) <= 1e-5 * scale
+
+
+def test_fused_every_pair_dropped_writes_zero_rows(monkeypatch):
+    fmt, E, NS, H, I, T, K = F.FMT_NVFP4, 8, 0, 256, 256, 3, 2
+    _, W = _layer(fmt, E, NS, H, I, seed=31)
+    ids = np.full((T, K), -1, np.int32)
+    wts = np.ones((T, K), np.float32)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(32)).to(torch.bfloat16)
+    for dt in (torch.float32, torch.bfloat16):
+        out = torch.full((T, H), float("nan"), dtype=dt, device="cuda")
+        _run(x, ids, wts, W, monkeypatch, True, out=out)
+        assert torch.equal(out.float(), torch.zeros((T, H), device="cuda"))
+
+
+def test_fused_slot_map_and_bf16_out(monkeypatch):
+    fmt, E, NS, H, I, T, K = F.FMT_FP8, 16, 1, 512, 512, 3, 4
+    d, _ = _layer(fmt, E, NS, H, I, seed=41)
+    # store the experts in reverse order; slot_map[b] = where bucket b's weights live
+    order = np.arange(E + NS)[::-1].copy()
+    idx = torch.from_numpy(order)
+    rev = {k: (v[idx].contiguous() if v is not None else None) for k, v in d.items()}
+    W = ExpertWeights.from_dense(fmt, rev["w13"], rev["s13"], rev["w2"], rev["s2"], rev["gs13"],
+                                 rev["gs2"], n_shared=NS, device="cuda")
+    slot_map = torch.from_numpy(np.argsort(order).astype(np.int32)).cuda()
+    ids, wts = random_routing(T, K, E, seed=42)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(43)).to(torch.bfloat16)
+    out = _run(x, ids, wts, W, monkeypatch, True, out_dtype=torch.bfloat16, slot_map=slot_map)
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I)
+    check_close(out.float().cpu().numpy(), ref, bf16_out=True, what="slot map, bf16 out")
+
+
+def test_fused_token_permutation_is_bitwise(monkeypatch):
+    fmt, E, NS, H, I, T, K = F.FMT_MXFP4, 32, 1, 512, 1024, 8, 4
+    _, W = _layer(fmt, E, NS, H, I, seed=51)
+    ids, wts = random_routing(T, K, E, seed=52)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(53)).to(torch.bfloat16)
+    out = _run(x, ids, wts, W, monkeypatch, True, out_dtype=torch.float32)
+    perm = np.random.default_rng(54).permutation(T)
+    out_p = _run(x[perm], ids[perm].copy(), wts[perm].copy(), W, monkeypatch, True,
+                 out_dtype=torch.float32)
+    assert torch.equal(out_p, out[torch.from_numpy(perm).cuda()])
+
+
+def test_fused_ds_v3_mxfp4_t2(monkeypatch):
+    """DeepSeek-V3 shape (H=7168, I=2048, top-8 + 1 shared) at T=2, where the
+    18 act rows still fit the stage; experts compacted to those routed."""
+    H, I, E, K, T = 7168, 2048, 256, 8, 2
+    rng = np.random.default_rng(61)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    wts = (rng.random((T, K)) * 0.3 + 0.05).astype(np.float32)
+    used = np.unique(ids)
+    cids = np.vectorize({int(e): i for i, e in enumerate(used)}.get)(ids).astype(np.int32)
+    U = len(used)
+    d, W = _layer(F.FMT_MXFP4, U, 1, H, I, seed=62)
+    assert L.decode_fused_down_ok(F.FMT_MXFP4, T, T * (K + 1), H, I, min(E, T * K) + 1)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(63)).to(torch.bfloat16)
+    out = _run(x, cids, wts, W, monkeypatch, True, out_dtype=torch.float32)
+    ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d), bf16_tensor_to_bits(x), cids,
+                       wts, U, 1, H, I)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what="ds-v3 fused T=2")
+

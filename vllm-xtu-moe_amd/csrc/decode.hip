@@ -264,6 +264,35 @@ __device__ __forceinline__ void finish_stage(uint16_t* xs, const u32x4_t (&xv)[k
     *reinterpret_cast<u32x4_t*>(xs + c * 8) = *reinterpret_cast<const u32x4_t*>(src(c));
 }
 
+// Reduce the gate (waves [0, ksplit)) and up (waves [ksplit, 2 ksplit)) K
+// splits in a fixed order and write the expert's na SwiGLU rows of panel sub.
+template <int FMT>
+__device__ __forceinline__ void gate_up_epilogue(const DecodeArgs& a, f32x4_t (*red)[kWave],
+                                                 f32x4_t acc, int w, uint32_t lane, int r0,
+                                                 int na, int ws, int sub) {
+  red[w][lane] = acc;
+  __syncthreads();
+  for (int t = threadIdx.x; t < 256; t += blockDim.x) {   // 16 rows x 16 columns
+    const int mm = t / 16, n = t % 16;
+    if (mm < na) {
+      const int l = (mm / 4) * 16 + n, i = mm % 4;
+      float g = 0.f, u = 0.f;
+      for (int k = 0; k < a.ksplit; ++k) {
+        g += red[k][l][i];
+        u += red[a.ksplit + k][l][i];
+      }
+      if constexpr (FMT == kNVFP4) {
+        const float gsv = a.gs ? a.gs[ws] : 1.0f;
+        g *= gsv;
+        u *= gsv;
+      }
+      uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
+      act[(long)(r0 + mm) * a.I + 16 * sub + n] =
+          f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
+    }
+  }
+}
+
 // GENERIC: more than one round per wave, or token rows beyond the stage; the
 // fast instantiation holds neither (the host checks the shape) and stages the
 // batch's T rows through XC register pieces per thread.
@@ -345,27 +374,7 @@ __global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
       if (u0 + NU < u1) acc = more_rounds<FMT, NU, false>(acc, st, u0 + NU, u1, lane, xa, xg);
     }
   }
-  red[w][lane] = acc;
-  __syncthreads();
-  for (int t = threadIdx.x; t < 256; t += blockDim.x) {   // 16 rows x 16 columns
-    const int mm = t / 16, n = t % 16;
-    if (mm < c.na) {
-      const int l = (mm / 4) * 16 + n, i = mm % 4;
-      float g = 0.f, u = 0.f;
-      for (int k = 0; k < ksplit; ++k) {
-        g += red[k][l][i];
-        u += red[ksplit + k][l][i];
-      }
-      if constexpr (FMT == kNVFP4) {
-        const float gsv = a.gs ? a.gs[c.ws] : 1.0f;
-        g *= gsv;
-        u *= gsv;
-      }
-      uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
-      act[(long)(c.r0 + mm) * a.I + 16 * c.sub + n] =
-          f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
-    }
-  }
+  gate_up_epilogue<FMT>(a, red, acc, w, lane, c.r0, c.na, c.ws, c.sub);
 }
 
 template <int FMT, bool GENERIC>
@@ -437,6 +446,286 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
       y[(long)(c.r0 + mm) * a.H + 16 * (c.sub * ppb + pq) + n] = v * gsv;
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Down projection with the weighted combine fused (moe4_smallm_dn2's
+// Y[t] += w * (act_e W2_e^T)[t], computed without atomics).  The MFMA's 16 A
+// rows are the batch's tokens (T <= 16): for active expert j, row t is the act
+// row of pair (t, j) or any staged row when t did not route to j, and the
+// result row t is added to token t's accumulator with the pair's weight (no
+// addition when the weight is 0 or t has no pair on j; a token listing j
+// twice has the weights summed, its two act rows being the same).  Token t's
+// sum runs over its experts in active-slot order, so it does not depend on
+// the other tokens.
+//
+// Workgroup: PPB panels of 16 output columns x KS waves; wave (p, ks) owns
+// the units [ks*NPER, (ks+1)*NPER) of panel p for every active expert, with
+// the loads of D experts in flight (a ring of registers; the slots past the
+// active count get zero-length buffers, so the loads stay unconditional and
+// the waits exact without touching memory).  All active act rows are staged
+// in LDS once per workgroup; the KS partial sums are added in a fixed order.
+struct DownCombineArgs {
+  const uint16_t* act;        // [rows][I] bf16, sorted pair rows
+  const uint8_t* w;
+  const uint8_t* s;
+  const float* gs;
+  const int32_t* sorted_tok;
+  const float* sorted_wts;
+  const int32_t* seg_start;
+  const int32_t* active;
+  const int32_t* n_active;
+  const int32_t* slot_map;
+  void* out;                  // [T][H] bf16 or fp32
+  int out_bf16;
+  int T, H, I;
+  int trash;                  // bucket after the last expert: seg_start[trash] = live rows
+  int max_active;             // table capacity (>= n_active)
+  int row_cap;                // rows the LDS stage holds (>= seg_start[trash])
+  long w_estride, s_estride;
+  int ks, ppb;
+};
+
+constexpr int kDcTok = 16;    // tokens = MFMA rows
+constexpr size_t kDcLds = 80 * 1024;   // two workgroups per CU
+
+// Waves the fused down's grid aims at (K split grows until reached).
+#ifndef XTU_DC_WAVES
+#define XTU_DC_WAVES 1024
+#endif
+
+template <int FMT, int NPER>
+struct ExpLoad {
+  u32x4_t w[NPER][WFmt<FMT>::kSPU];
+  uint32_t sc0, sc1;          // fp4: the scale bytes of units u0.. (low byte first)
+  float bsv;                  // fp8: lane l holds the block scale of unit u0 + l
+};
+
+template <int FMT, int NPER>
+__device__ __forceinline__ void issue_expert(ExpLoad<FMT, NPER>& r, const DownCombineArgs& a,
+                                             int ws, bool live, int panel, int u0,
+                                             uint32_t lane) {
+  using F = WFmt<FMT>;
+  const long nsb = a.I / F::kSB;
+  const uint8_t* sx = a.s + (long)ws * a.s_estride;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.w + (long)ws * a.w_estride + (long)panel * nsb * 1024), 0,
+      live ? (int)(nsb * 1024) : 0, kRawBufferFlags);
+  if constexpr (FMT == kMXFP4 || FMT == kNVFP4) {
+    const long gbytes = scale_groups(a.I, F::kUG) * 1024;
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(sx + (long)panel * gbytes), 0, live ? (int)gbytes : 0, kRawBufferFlags);
+    // the NPER units' bytes sit in one 8-byte-aligned word of the lane's group
+    const int off = (u0 % F::kUG) * F::kSBY;
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(
+        sr, (int)lane * 16 + (off & 8), (u0 / F::kUG) * 1024, kAuxNontemporal);
+    const uint64_t q = ((uint64_t)v[1] << 32 | v[0]) >> (8 * (off & 7));
+    r.sc0 = (uint32_t)q;
+    r.sc1 = (uint32_t)(q >> 32);
+  } else if constexpr (FMT == kFP8) {
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(sx + (long)(panel / 8) * (a.I / 128) * 4), 0, live ? (a.I / 128) * 4 : 0,
+        kRawBufferFlags);
+    r.bsv = __builtin_bit_cast(float,
+                               __builtin_amdgcn_raw_buffer_load_b32(sr, (int)lane * 4, u0 * 4, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < NPER; ++i)
+#pragma unroll
+    for (int j = 0; j < F::kSPU; ++j)
+      r.w[i][j] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)lane * 16,
+                                                         ((u0 + i) * F::kSPU + j) * 1024,
+                                                         kAuxNontemporal));
+}
+
+template <int FMT, int NPER>
+__device__ __forceinline__ f32x4_t consume_expert(const ExpLoad<FMT, NPER>& r, int u0,
+                                                  const uint16_t* xa) {
+  f32x4_t pe = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NPER; ++i) {
+    uint32_t sraw = 0u;
+    float bs = 1.0f;
+    if constexpr (FMT == kMXFP4) {
+      sraw = (i < 4 ? r.sc0 : r.sc1) >> (8 * (i % 4));
+    } else if constexpr (FMT == kNVFP4) {
+      sraw = (i < 2 ? r.sc0 : r.sc1) >> (16 * (i % 2));
+    } else if constexpr (FMT == kFP8) {
+      bs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r.bsv), i));
+    }
+    mma_unit<FMT, true>(r.w[i], sraw, bs, pe, u0 + i, xa, nullptr);
+  }
+  return pe;
+}
+
+// Ring depth in experts: about NU/2 units of weights in flight per wave
+// (at most 128 VGPRs, so two 8-wave workgroups fit a CU).
+#ifndef XTU_DC_RING_DIV
+#define XTU_DC_RING_DIV 2
+#endif
+template <int FMT, int NPER>
+constexpr int dc_depth() {
+  constexpr int d = round_units<FMT>() / XTU_DC_RING_DIV / NPER;
+  return d > 2 ? d : 2;
+}
+
+template <int FMT, int NPER>
+__global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArgs a) {
+  using F = WFmt<FMT>;
+  constexpr int D = dc_depth<FMT, NPER>();
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+  const int ldx = a.I + 8;                       // staged row stride (bf16), 16 B of padding
+  uint16_t* xs = reinterpret_cast<uint16_t*>(dyn);
+  int* rowof = reinterpret_cast<int*>(dyn + (size_t)a.row_cap * ldx * 2);   // [max_active][16]
+  float* wof = reinterpret_cast<float*>(rowof + a.max_active * kDcTok);      // [max_active][16]
+  int* eslot = reinterpret_cast<int*>(wof + a.max_active * kDcTok);          // [max_active]
+  int* r0s = eslot + a.max_active;                                           // [max_active]
+  int* r1s = r0s + a.max_active;                                             // [max_active]
+  int* rtok = r1s + a.max_active;                                            // [row_cap]
+  float* rw = reinterpret_cast<float*>(rtok + a.row_cap);                    // [row_cap]
+  const int tid = threadIdx.x, bd = blockDim.x;
+  const int w = wave_id();
+  const uint32_t lane = tid % kWave;
+  const int q = lane / 16, m = lane % 16;
+  const int pp = w / a.ks, ks = w - pp * a.ks;
+  const int panel = blockIdx.x * a.ppb + pp;
+  const int u0 = ks * NPER;
+  const int nact = min(a.n_active[0], a.max_active);
+
+  // first D experts' loads go out before anything else
+  ExpLoad<FMT, NPER> ring[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int jc = min(d, nact - 1);
+    const int e = jc >= 0 ? a.active[jc] : 0;
+    const int ws = a.slot_map ? a.slot_map[e] : e;
+    issue_expert<FMT, NPER>(ring[d], a, ws, d < nact, panel, u0, lane);
+  }
+  // Prologue, two dependent loads deep: every thread stages act pieces (all
+  // row_cap rows: rows past the live ones are never selected) and the rows'
+  // token / weight, while threads j < nact fetch expert j's slot and row range.
+  const int per_row = a.I / 8;
+  const int pieces = a.row_cap * per_row;
+  for (int i = tid; i < nact * kDcTok; i += bd) {
+    rowof[i] = 0;
+    wof[i] = 0.f;
+  }
+  for (int r = tid; r < a.row_cap; r += bd) {
+    rtok[r] = a.sorted_tok[r];
+    rw[r] = a.sorted_wts[r];
+  }
+  for (int j = tid; j < nact; j += bd) {
+    const int e = a.active[j];
+    eslot[j] = a.slot_map ? a.slot_map[e] : e;
+    r0s[j] = a.seg_start[e];
+    r1s[j] = a.seg_start[e + 1];
+  }
+  for (int c0 = tid; c0 < pieces; c0 += 4 * bd) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = min(c0 + k * bd, pieces - 1);
+      v[k] = *reinterpret_cast<const u32x4_t*>(a.act + (long)c * 8);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = c0 + k * bd;
+      if (c < pieces)
+        *reinterpret_cast<u32x4_t*>(xs + (c / per_row) * ldx + (c % per_row) * 8) = v[k];
+    }
+  }
+  __syncthreads();
+  // token -> act row and summed weight per active expert (from LDS)
+  for (int j = tid; j < nact; j += bd) {
+    const int r1 = min(r1s[j], a.row_cap);
+    for (int r = max(r0s[j], 0); r < r1; ++r) {
+      const int t = rtok[r];
+      if (t >= 0 && t < kDcTok) {
+        rowof[j * kDcTok + t] = r;
+        wof[j * kDcTok + t] += rw[r];
+      }
+    }
+  }
+  __syncthreads();
+
+  f32x4_t tacc = {0.f, 0.f, 0.f, 0.f};   // tokens 4q + i, column m of the panel
+  const int nit = (nact + D - 1) / D;
+  for (int it = 0; it < nit; ++it) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int j = it * D + d;
+      const bool live = j < nact;
+      const int jt = live ? j : 0;
+      const uint16_t* xa = xs + rowof[jt * kDcTok + m] * ldx + q * F::kCK;
+      f32x4_t pe = consume_expert<FMT, NPER>(ring[d], u0, xa);
+      if constexpr (FMT == kNVFP4) {
+        const float g = a.gs ? a.gs[eslot[jt]] : 1.0f;
+        pe = pe * g;
+      }
+      const f32x4_t wv = live ? *reinterpret_cast<const f32x4_t*>(wof + jt * kDcTok + 4 * q)
+                              : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        tacc[i] = wv[i] != 0.f ? __builtin_fmaf(wv[i], pe[i], tacc[i]) : tacc[i];
+      const int jn = j + D;
+      const int wsn = __builtin_amdgcn_readfirstlane(eslot[jn < nact ? jn : 0]);
+      issue_expert<FMT, NPER>(ring[d], a, wsn, jn < nact, panel, u0, lane);
+    }
+  }
+  // the KS partial sums, through the stage's memory once every wave is done with it
+  __syncthreads();
+  f32x4_t(*red)[kWave] = reinterpret_cast<f32x4_t(*)[kWave]>(dyn);
+  red[w][lane] = tacc;
+  __syncthreads();
+  for (int t = tid; t < a.ppb * 256; t += bd) {   // tokens x 16 columns per panel
+    const int pq = t / 256, tok = (t % 256) / 16, n = t % 16;
+    if (tok < a.T) {
+      const int l = (tok / 4) * 16 + n, i = tok % 4;
+      float v = 0.f;
+      for (int k = 0; k < a.ks; ++k) v += red[pq * a.ks + k][l][i];
+      const long o = (long)tok * a.H + 16 * (blockIdx.x * a.ppb + pq) + n;
+      if (a.out_bf16) reinterpret_cast<uint16_t*>(a.out)[o] = f32_to_bf16(v);
+      else reinterpret_cast<float*>(a.out)[o] = v;
+    }
+  }
+}
+
+// Launch shape of the fused down: (KS, NPER) with KS * NPER = I / 128 and
+// NPER in {1, 2, 4}, KS <= 8; KS grows until the grid holds about 2048 waves.
+// Returns false when the shape or the LDS stage does not fit.
+bool dc_shape(int fmt, int T, int rows, int H, int I, int max_active, int& ks, int& nper,
+              int& ppb, size_t& lds) {
+  if (T < 1 || T > kDcTok || fmt < 0 || fmt > 3) return false;
+  const int nunits = I / 128, npan = H / 16;
+  ks = 1;
+  while (ks < 8 && nunits % (2 * ks) == 0 && (long)npan * ks < XTU_DC_WAVES) ks *= 2;
+  while (nunits / ks > 4 && ks < 8 && nunits % (2 * ks) == 0) ks *= 2;
+  nper = nunits / ks;
+  if (nunits % ks || (nper != 1 && nper != 2 && nper != 4)) return false;
+  ppb = 1;
+  while (ks * ppb * 2 <= 4 && npan % (ppb * 2) == 0) ppb *= 2;
+  lds = (size_t)rows * (I + 8) * 2 + (size_t)max_active * (2 * kDcTok + 3) * 4 +
+        (size_t)rows * 8;
+  const size_t red = (size_t)ks * ppb * kWave * 16;
+  if (lds < red) lds = red;
+  return lds <= kDcLds;
+}
+
+template <int FMT>
+hipError_t launch_down_combine(DownCombineArgs a, int nper, size_t lds, hipStream_t stream) {
+  using F = WFmt<FMT>;
+  if (!a.w_estride) a.w_estride = F::w_bytes(a.H, a.I);
+  if (!a.s_estride) a.s_estride = F::s_bytes(a.H, a.I);
+  const dim3 grid(a.H / 16 / a.ppb);
+  const int bd = kWave * a.ks * a.ppb;
+  switch (nper) {
+    case 1: decode_down_combine_kernel<FMT, 1><<<grid, bd, lds, stream>>>(a); break;
+    case 2: decode_down_combine_kernel<FMT, 2><<<grid, bd, lds, stream>>>(a); break;
+    case 4: decode_down_combine_kernel<FMT, 4><<<grid, bd, lds, stream>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipPeekAtLastError();
 }
 
 // Smallest K split (1, 2, 4) that keeps every wave's share within one round.
@@ -554,6 +843,41 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
                seg_start, active, n_active, slot_map, y, T, H, I, w_estride, s_estride, 0.f, 1.f,
                0.f, 0, 1, 1};
   return dispatch_decode(fmt, 1, a, max_active, stream);
+}
+
+int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int max_active) {
+  int ks, nper, ppb;
+  size_t lds;
+  return shape_ok(fmt, H, I) && A >= 0 && max_active >= 0 && max_active <= 65535 &&
+         dc_shape(fmt, T, A, H, I, max_active, ks, nper, ppb, lds);
+}
+
+hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int A, int H, int I,
+                                   const void* w2, const void* s2, const float* gs2,
+                                   long w_estride, long s_estride, const int32_t* slot_map,
+                                   const int32_t* sorted_tok, const float* sorted_wts,
+                                   const int32_t* seg_start, int trash, const int32_t* active,
+                                   const int32_t* n_active, int max_active, void* out,
+                                   int out_bf16, hipStream_t stream) {
+  int ks = 0, nper = 0, ppb = 0;
+  size_t lds = 0;
+  XTU_CHECK_ARG(shape_ok(fmt, H, I) && A >= 0 && max_active >= 0 && max_active <= 65535 &&
+                trash >= 0 && dc_shape(fmt, T, A, H, I, max_active, ks, nper, ppb, lds));
+  XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
+  XTU_CHECK_ARG(act && w2 && (fmt == kBF16 || s2) && sorted_tok && sorted_wts && seg_start &&
+                active && n_active && out);
+  (void)hipGetLastError();
+  DownCombineArgs a{(const uint16_t*)act, (const uint8_t*)w2, (const uint8_t*)s2, gs2,
+                    sorted_tok, sorted_wts, seg_start, active, n_active, slot_map, out,
+                    out_bf16 ? 1 : 0, T, H, I, trash, max_active, A, w_estride, s_estride, ks,
+                    ppb};
+  switch (fmt) {
+    case kMXFP4: return launch_down_combine<kMXFP4>(a, nper, lds, stream);
+    case kNVFP4: return launch_down_combine<kNVFP4>(a, nper, lds, stream);
+    case kFP8: return launch_down_combine<kFP8>(a, nper, lds, stream);
+    case kBF16: return launch_down_combine<kBF16>(a, nper, lds, stream);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // extern "C"

@@ -247,6 +247,19 @@ def gemm_tile_m(fmt: int, int8: bool = False) -> int:
     return int(_lib.call("xtu_gemm_tile_m", int(fmt)))
 
 
+FUSED_DOWN_ENV = "XTU_DECODE_FUSED_DOWN"
+
+
+def decode_fused_down_ok(fmt: int, T: int, A: int, H: int, I: int, max_active: int) -> bool:
+    """Whether the decode path runs the down projection and the weighted
+    combine as one kernel (the batch's act rows fit the kernel's LDS stage);
+    XTU_DECODE_FUSED_DOWN=0 keeps the separate down + combine."""
+    if os.environ.get(FUSED_DOWN_ENV, "1") == "0":
+        return False
+    return bool(_lib.call("xtu_decode_down_combine_ok", int(fmt), int(T), int(A), int(H), int(I),
+                          int(max_active)))
+
+
 def _fp8pair_bufs(tag, M, K, dev):
     return (_buf(tag + "_hi", (max(M, 1), K), torch.uint8, dev),
             _buf(tag + "_lo", (max(M, 1), K), torch.uint8, dev),
@@ -325,18 +338,27 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         out = torch.empty((T, H), dtype=odt, device=dev)
     if T == 0:
         return (out, seg) if return_seg else out
-    y = _buf("y", (max(A, 1), H), torch.float32, dev)
     if path == "decode":
         act = _buf("act", (max(A, 1), I), torch.bfloat16, dev)
         lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
         max_active = min(E, T * K) + NS
-        _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0,
-                  _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
+        _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13),
+                  0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
                   _p(seg.n_active), max_active, _p(act), lim, al, be, st)
+        if odt in (torch.bfloat16, torch.float32) and decode_fused_down_ok(fmt, T, A, H, I,
+                                                                          max_active):
+            # down projection and weighted combine in one pass, out written whole
+            _lib.call("xtu_decode_down_combine", fmt, _p(act), T, A, H, I, _p(W.w2), _p(W.s2),
+                      _p(W.gs2), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.sorted_wts),
+                      _p(seg.seg_start), E + NS, _p(seg.active), _p(seg.n_active), max_active,
+                      _p(out), int(out.dtype == torch.bfloat16), st)
+            return (out, seg) if return_seg else out
+        y = _buf("y", (max(A, 1), H), torch.float32, dev)
         _lib.call("xtu_decode_down", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.active), _p(seg.n_active), max_active,
                   _p(y), st)
     else:
+        y = _buf("y", (max(A, 1), H), torch.float32, dev)
         expert_pass(x, seg, W, 0, E + NS, y, slot_map=slot_map, int8=int8,
                     swiglu_limit=swiglu_limit, swiglu_alpha=swiglu_alpha,
                     swiglu_beta=swiglu_beta, stream=st)
