@@ -131,3 +131,27 @@ def test_fused_ds_v3_mxfp4_t2(monkeypatch):
                        wts, U, 1, H, I)
     check_close(out.cpu().numpy(), ref, bf16_out=False, what="ds-v3 fused T=2")
 
+
+
+@pytest.mark.parametrize("fmt", [F.FMT_MXFP4, F.FMT_NVFP4])
+@pytest.mark.parametrize("T,H", [(1, 2048), (3, 2048), (5, 4096), (2, 7168)])
+def test_decode_hidden_sizes_and_single_expert(fmt, T, H, monkeypatch):
+    """Decode layers at hidden sizes 2048 / 4096 / 7168 (16, 32 and 56 units
+    of 128 k per gate/up row) against the oracle, and a batch whose tokens all
+    route to one expert with no shared expert (most work items idle)."""
+    E, NS, I, K = 24, 1, 256, 4
+    d, W = _layer(fmt, E, NS, H, I, seed=T + H)
+    ids, wts = random_routing(T, K, E, seed=T + 1)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(T + 2)).to(torch.bfloat16)
+    out = _run(x, ids, wts, W, monkeypatch, True, out_dtype=torch.float32)
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"decode fmt={fmt} T={T} H={H}")
+    # a single routed expert for every token and no shared expert
+    _, W1 = _layer(fmt, E, 0, H, I, seed=T + H + 1)
+    ids1 = np.full((T, 1), 5, np.int32)
+    wts1 = np.ones((T, 1), np.float32)
+    out1 = _run(x, ids1, wts1, W1, monkeypatch, True, out_dtype=torch.float32)
+    d1 = make_dense_layer(fmt, E, H, I, seed=T + H + 1)
+    ref1 = oracle_layer(fmt, dense_to_numpy(fmt, d1), bf16_tensor_to_bits(x), ids1, wts1, E, 0, H,
+                        I)
+    check_close(out1.cpu().numpy(), ref1, bf16_out=False, what=f"single expert T={T}")

@@ -816,9 +816,8 @@ __device__ void route_token_wave(const float* __restrict__ l, const float* __res
 struct TinySmem {
   int ids[kTinyMaxA];
   float w[kTinyMaxA];
-  int bk[kTinyMaxA];          // bucket of pair p (INT_MAX past A)
+  int bk[kTinyMaxA];          // sort key of pair p: bucket * 64 + p (INT_MAX past A)
   int sb[kTinyMaxA];          // bucket at sorted position j (INT_MAX past A)
-  int scnt[kTinyMaxA];        // its bucket's pair count
   int act_b[kTinyMaxA + 4];   // active buckets, ascending (INT_MAX past n_act)
   int act_r[kTinyMaxA + 1];   // first row of active bucket i; [n_act] = trash start
   int act_t[kTinyMaxA + 1];   // first tile of active bucket i; [n_act] = all tiles
@@ -826,7 +825,7 @@ struct TinySmem {
 };
 
 // MODE 0/1: wave t routes token t (E = 64 * EPL), then the segmentation;
-// MODE 2: ids/wts given.  blockDim.x = 64 * max(T, 4).
+// MODE 2: ids/wts given.  blockDim.x = 64 * max(T, 4, (NB + 1) / 64 rounded up, to 16).
 template <int MODE, int EPL>
 __global__ __launch_bounds__(1024) void route_seg_tiny_kernel(SmallArgs a) {
   __shared__ __attribute__((aligned(16))) TinySmem g;
@@ -859,22 +858,18 @@ __global__ __launch_bounds__(1024) void route_seg_tiny_kernel(SmallArgs a) {
     } else if (lane < A) {
       b = E + (lane - TK) % NS;
     }
-    g.bk[lane] = b;
+    // stable position: rank of the unique key (bucket, pair) among the pairs
+    const int key = lane < A ? b * kTinyMaxA + lane : BIG;
+    g.bk[lane] = key;
     lds_wave_order();
-    // stable position and bucket size
-    int pos = 0, cnt = 0;
+    int pos = 0;
 #pragma unroll
     for (int q = 0; q < kTinyMaxA; q += 4) {
       const i32x4_t v = *reinterpret_cast<const i32x4_t*>(g.bk + q);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        pos += (v[u] < b || (v[u] == b && q + u < lane)) ? 1 : 0;
-        cnt += v[u] == b ? 1 : 0;
-      }
+      pos += (v[0] < key) + (v[1] < key) + (v[2] < key) + (v[3] < key);
     }
     if (lane < A) {
       g.sb[pos] = b;
-      g.scnt[pos] = cnt;
       a.sorted_pair[pos] = lane;
       a.inv[lane] = pos;
       a.sorted_tok[pos] = lane < TK ? lane / K : (lane - TK) / NS;
@@ -883,15 +878,20 @@ __global__ __launch_bounds__(1024) void route_seg_tiny_kernel(SmallArgs a) {
       g.sb[lane] = BIG;
     }
     lds_wave_order();
-    // sorted position `lane`: the first of its bucket opens an active entry
+    // sorted position `lane`: the first of its bucket opens an active entry;
+    // the bucket's size runs to the next bucket's first row (or A)
     const int sbj = g.sb[lane];
     const int prev = lane > 0 ? g.sb[lane - 1] : -1;
-    const bool first = lane < A && sbj != trash && sbj != prev;
+    const bool start = lane < A && sbj != prev;
+    const unsigned long long bnd = __ballot(start);
+    const unsigned long long above = lane == 63 ? 0ull : bnd & (~0ull << (lane + 1));
+    const int cnt = (above ? __builtin_ctzll(above) : A) - lane;
+    const bool first = start && sbj != trash;
     const unsigned long long fm = __ballot(first);
     const int ai = __builtin_amdgcn_mbcnt_hi((uint32_t)(fm >> 32),
                                              __builtin_amdgcn_mbcnt_lo((uint32_t)fm, 0u));
     const int na = __popcll(fm);
-    const int nt = first ? (g.scnt[lane] + a.bm - 1) / a.bm : 0;
+    const int nt = first ? (cnt + a.bm - 1) / a.bm : 0;
     const int incl = wave_incl_scan(nt);
     const int t0 = incl - nt;
     if (first) {
@@ -953,7 +953,11 @@ __host__ int tiny_epl(const SmallArgs& a, int mode) {
 template <int MODE>
 hipError_t launch_small(const SmallArgs& a, hipStream_t stream) {
   const int epl = tiny_epl(a, MODE);
-  const int tiny_threads = kWave * (a.T > 4 ? a.T : 4);
+  // one wave per token, and one thread per bucket start for the last pass
+  const int nb_waves = (a.E + a.NS + 2 + kWave - 1) / kWave;
+  int tiny_waves = a.T > 4 ? a.T : 4;
+  if (tiny_waves < nb_waves) tiny_waves = nb_waves < 16 ? nb_waves : 16;
+  const int tiny_threads = kWave * tiny_waves;
   if (epl != 0) {
     if constexpr (MODE == 2) {
       route_seg_tiny_kernel<2, 1><<<1, tiny_threads, 0, stream>>>(a);
