@@ -129,7 +129,7 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
  * multiple of 128 with I/128 splitting into waves of 1, 2 or 4 units, the
  * A = T*(K+NS) act rows within the LDS stage); the entry returns
  * hipErrorInvalidValue otherwise. */
-int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int max_active);
+int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int trash, int max_active);
 hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int A, int H, int I,
                                    const void* w2, const void* s2, const float* gs2,
                                    long w_estride, long s_estride, const int32_t* slot_map,

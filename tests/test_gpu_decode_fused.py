@@ -41,7 +41,7 @@ def test_fused_vs_oracle_and_unfused(fmt, T, H, I, monkeypatch):
     ids, wts = random_routing(T, K, E, seed=T)
     x = torch.randn((T, H), generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
     A = T * (K + NS)
-    assert L.decode_fused_down_ok(fmt, T, A, H, I, min(E, T * K) + NS)
+    assert L.decode_fused_down_ok(fmt, T, A, H, I, min(E, T * K) + NS, E + NS)
     fused = _run(x, ids, wts, W, monkeypatch, True, out_dtype=torch.float32)
     split = _run(x, ids, wts, W, monkeypatch, False, out_dtype=torch.float32)
     ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I)
@@ -124,7 +124,7 @@ def test_fused_ds_v3_mxfp4_t2(monkeypatch):
     cids = np.vectorize({int(e): i for i, e in enumerate(used)}.get)(ids).astype(np.int32)
     U = len(used)
     d, W = _layer(F.FMT_MXFP4, U, 1, H, I, seed=62)
-    assert L.decode_fused_down_ok(F.FMT_MXFP4, T, T * (K + 1), H, I, min(E, T * K) + 1)
+    assert L.decode_fused_down_ok(F.FMT_MXFP4, T, T * (K + 1), H, I, min(E, T * K) + 1, U + 1)
     x = torch.randn((T, H), generator=torch.Generator().manual_seed(63)).to(torch.bfloat16)
     out = _run(x, cids, wts, W, monkeypatch, True, out_dtype=torch.float32)
     ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d), bf16_tensor_to_bits(x), cids,

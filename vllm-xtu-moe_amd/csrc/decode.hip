@@ -487,6 +487,8 @@ struct DownCombineArgs {
 };
 
 constexpr int kDcTok = 16;    // tokens = MFMA rows
+constexpr int kDcSB = 12;     // act pieces per thread in flight while staging
+constexpr int kDcSegW = 4;    // bucket starts per thread in the first batch
 constexpr size_t kDcLds = 80 * 1024;   // two workgroups per CU
 
 // Waves the fused down's grid aims at (K split grows until reached).
@@ -576,13 +578,14 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
   constexpr int D = dc_depth<FMT, NPER>();
   extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
   const int ldx = a.I + 8;                       // staged row stride (bf16), 16 B of padding
+  const int nseg = a.trash + 2;                  // seg_start entries
   uint16_t* xs = reinterpret_cast<uint16_t*>(dyn);
   int* rowof = reinterpret_cast<int*>(dyn + (size_t)a.row_cap * ldx * 2);   // [max_active][16]
   float* wof = reinterpret_cast<float*>(rowof + a.max_active * kDcTok);      // [max_active][16]
   int* eslot = reinterpret_cast<int*>(wof + a.max_active * kDcTok);          // [max_active]
-  int* r0s = eslot + a.max_active;                                           // [max_active]
-  int* r1s = r0s + a.max_active;                                             // [max_active]
-  int* rtok = r1s + a.max_active;                                            // [row_cap]
+  int* l_act = eslot + a.max_active;                                         // [max_active]
+  int* l_seg = l_act + a.max_active;                                         // [nseg]
+  int* rtok = l_seg + nseg;                                                  // [row_cap]
   float* rw = reinterpret_cast<float*>(rtok + a.row_cap);                    // [row_cap]
   const int tid = threadIdx.x, bd = blockDim.x;
   const int w = wave_id();
@@ -591,55 +594,82 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
   const int pp = w / a.ks, ks = w - pp * a.ks;
   const int panel = blockIdx.x * a.ppb + pp;
   const int u0 = ks * NPER;
-  const int nact = min(a.n_active[0], a.max_active);
 
-  // first D experts' loads go out before anything else
+  // Prologue.  Issue order: the active count and the first D active buckets
+  // (scalar), the first batch of act pieces and table words (one level deep,
+  // into registers), the first D experts' weights, then the LDS stores --
+  // which wait for the batch only, not for the weights.  Rows past the live
+  // ones are staged too (never selected).  Remainders (large batches) go
+  // after the weights.
+  const int per_row = a.I / 8;
+  const int pieces = a.row_cap * per_row;
+  const int nact_g = a.n_active[0];
+  int e_first[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) e_first[d] = a.active[min(d, a.max_active - 1)];
+  u32x4_t v[kDcSB];
+#pragma unroll
+  for (int k = 0; k < kDcSB; ++k)
+    v[k] = *reinterpret_cast<const u32x4_t*>(a.act + (long)min(tid + k * bd, pieces - 1) * 8);
+  const int act_v = a.active[min(tid, a.max_active - 1)];
+  int seg_v[kDcSegW];
+#pragma unroll
+  for (int k = 0; k < kDcSegW; ++k) seg_v[k] = a.seg_start[min(tid + k * bd, nseg - 1)];
+  const int tok_v = a.sorted_tok[min(tid, a.row_cap - 1)];
+  const float w_v = a.sorted_wts[min(tid, a.row_cap - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  const int nact = min(nact_g, a.max_active);
   ExpLoad<FMT, NPER> ring[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    const int jc = min(d, nact - 1);
-    const int e = jc >= 0 ? a.active[jc] : 0;
+    const int e = d < nact ? min(max(e_first[d], 0), a.trash - 1) : 0;
     const int ws = a.slot_map ? a.slot_map[e] : e;
     issue_expert<FMT, NPER>(ring[d], a, ws, d < nact, panel, u0, lane);
   }
-  // Prologue, two dependent loads deep: every thread stages act pieces (all
-  // row_cap rows: rows past the live ones are never selected) and the rows'
-  // token / weight, while threads j < nact fetch expert j's slot and row range.
-  const int per_row = a.I / 8;
-  const int pieces = a.row_cap * per_row;
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < kDcSB; ++k) {
+    const int c = tid + k * bd;
+    if (c < pieces)
+      *reinterpret_cast<u32x4_t*>(xs + (c / per_row) * ldx + (c % per_row) * 8) = v[k];
+  }
+  if (tid < a.max_active) l_act[tid] = act_v;
+#pragma unroll
+  for (int k = 0; k < kDcSegW; ++k)
+    if (tid + k * bd < nseg) l_seg[tid + k * bd] = seg_v[k];
+  if (tid < a.row_cap) {
+    rtok[tid] = tok_v;
+    rw[tid] = w_v;
+  }
+  for (int c0 = tid + kDcSB * bd; c0 < pieces; c0 += kDcSB * bd) {
+    u32x4_t vr[kDcSB];
+#pragma unroll
+    for (int k = 0; k < kDcSB; ++k)
+      vr[k] = *reinterpret_cast<const u32x4_t*>(a.act + (long)min(c0 + k * bd, pieces - 1) * 8);
+#pragma unroll
+    for (int k = 0; k < kDcSB; ++k) {
+      const int c = c0 + k * bd;
+      if (c < pieces)
+        *reinterpret_cast<u32x4_t*>(xs + (c / per_row) * ldx + (c % per_row) * 8) = vr[k];
+    }
+  }
+  for (int j = tid + bd; j < a.max_active; j += bd) l_act[j] = a.active[j];
+  for (int e = tid + kDcSegW * bd; e < nseg; e += bd) l_seg[e] = a.seg_start[e];
+  for (int r = tid + bd; r < a.row_cap; r += bd) {
+    rtok[r] = a.sorted_tok[r];
+    rw[r] = a.sorted_wts[r];
+  }
+  // token -> act row and summed weight per active expert
   for (int i = tid; i < nact * kDcTok; i += bd) {
     rowof[i] = 0;
     wof[i] = 0.f;
   }
-  for (int r = tid; r < a.row_cap; r += bd) {
-    rtok[r] = a.sorted_tok[r];
-    rw[r] = a.sorted_wts[r];
-  }
-  for (int j = tid; j < nact; j += bd) {
-    const int e = a.active[j];
-    eslot[j] = a.slot_map ? a.slot_map[e] : e;
-    r0s[j] = a.seg_start[e];
-    r1s[j] = a.seg_start[e + 1];
-  }
-  for (int c0 = tid; c0 < pieces; c0 += 4 * bd) {
-    u32x4_t v[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int c = min(c0 + k * bd, pieces - 1);
-      v[k] = *reinterpret_cast<const u32x4_t*>(a.act + (long)c * 8);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int c = c0 + k * bd;
-      if (c < pieces)
-        *reinterpret_cast<u32x4_t*>(xs + (c / per_row) * ldx + (c % per_row) * 8) = v[k];
-    }
-  }
   __syncthreads();
-  // token -> act row and summed weight per active expert (from LDS)
   for (int j = tid; j < nact; j += bd) {
-    const int r1 = min(r1s[j], a.row_cap);
-    for (int r = max(r0s[j], 0); r < r1; ++r) {
+    const int e = l_act[j];
+    eslot[j] = a.slot_map ? a.slot_map[e] : e;
+    const int r1 = min(l_seg[e + 1], a.row_cap);
+    for (int r = max(l_seg[e], 0); r < r1; ++r) {
       const int t = rtok[r];
       if (t >= 0 && t < kDcTok) {
         rowof[j * kDcTok + t] = r;
@@ -694,9 +724,11 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
 // Launch shape of the fused down: (KS, NPER) with KS * NPER = I / 128 and
 // NPER in {1, 2, 4}, KS <= 8; KS grows until the grid holds about 2048 waves.
 // Returns false when the shape or the LDS stage does not fit.
-bool dc_shape(int fmt, int T, int rows, int H, int I, int max_active, int& ks, int& nper,
-              int& ppb, size_t& lds) {
-  if (T < 1 || T > kDcTok || fmt < 0 || fmt > 3) return false;
+bool dc_shape(int fmt, int T, int rows, int H, int I, int trash, int max_active, int& ks,
+              int& nper, int& ppb, size_t& lds) {
+  if (T < 1 || T > kDcTok || fmt < 0 || fmt > 3 || trash < 0 || trash > 4096 || rows < 1 ||
+      max_active < 1)
+    return false;
   const int nunits = I / 128, npan = H / 16;
   ks = 1;
   while (ks < 8 && nunits % (2 * ks) == 0 && (long)npan * ks < XTU_DC_WAVES) ks *= 2;
@@ -705,8 +737,8 @@ bool dc_shape(int fmt, int T, int rows, int H, int I, int max_active, int& ks, i
   if (nunits % ks || (nper != 1 && nper != 2 && nper != 4)) return false;
   ppb = 1;
   while (ks * ppb * 2 <= 4 && npan % (ppb * 2) == 0) ppb *= 2;
-  lds = (size_t)rows * (I + 8) * 2 + (size_t)max_active * (2 * kDcTok + 3) * 4 +
-        (size_t)rows * 8;
+  lds = (size_t)rows * (I + 8) * 2 + (size_t)max_active * (2 * kDcTok + 2) * 4 +
+        (size_t)(trash + 2) * 4 + (size_t)rows * 8;
   const size_t red = (size_t)ks * ppb * kWave * 16;
   if (lds < red) lds = red;
   return lds <= kDcLds;
@@ -845,11 +877,11 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
   return dispatch_decode(fmt, 1, a, max_active, stream);
 }
 
-int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int max_active) {
+int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int trash, int max_active) {
   int ks, nper, ppb;
   size_t lds;
   return shape_ok(fmt, H, I) && A >= 0 && max_active >= 0 && max_active <= 65535 &&
-         dc_shape(fmt, T, A, H, I, max_active, ks, nper, ppb, lds);
+         dc_shape(fmt, T, A, H, I, trash, max_active, ks, nper, ppb, lds);
 }
 
 hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int A, int H, int I,
@@ -862,7 +894,7 @@ hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int A, int H
   int ks = 0, nper = 0, ppb = 0;
   size_t lds = 0;
   XTU_CHECK_ARG(shape_ok(fmt, H, I) && A >= 0 && max_active >= 0 && max_active <= 65535 &&
-                trash >= 0 && dc_shape(fmt, T, A, H, I, max_active, ks, nper, ppb, lds));
+                trash >= 0 && dc_shape(fmt, T, A, H, I, trash, max_active, ks, nper, ppb, lds));
   XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(act && w2 && (fmt == kBF16 || s2) && sorted_tok && sorted_wts && seg_start &&
                 active && n_active && out);

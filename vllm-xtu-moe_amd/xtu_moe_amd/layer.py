@@ -250,14 +250,15 @@ def gemm_tile_m(fmt: int, int8: bool = False) -> int:
 FUSED_DOWN_ENV = "XTU_DECODE_FUSED_DOWN"
 
 
-def decode_fused_down_ok(fmt: int, T: int, A: int, H: int, I: int, max_active: int) -> bool:
+def decode_fused_down_ok(fmt: int, T: int, A: int, H: int, I: int, max_active: int,
+                         trash: int) -> bool:
     """Whether the decode path runs the down projection and the weighted
     combine as one kernel (the batch's act rows fit the kernel's LDS stage);
     XTU_DECODE_FUSED_DOWN=0 keeps the separate down + combine."""
     if os.environ.get(FUSED_DOWN_ENV, "1") == "0":
         return False
     return bool(_lib.call("xtu_decode_down_combine_ok", int(fmt), int(T), int(A), int(H), int(I),
-                          int(max_active)))
+                          int(trash), int(max_active)))
 
 
 def _fp8pair_bufs(tag, M, K, dev):
@@ -346,7 +347,7 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
                   0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
                   _p(seg.n_active), max_active, _p(act), lim, al, be, st)
         if odt in (torch.bfloat16, torch.float32) and decode_fused_down_ok(fmt, T, A, H, I,
-                                                                          max_active):
+                                                                          max_active, E + NS):
             # down projection and weighted combine in one pass, out written whole
             _lib.call("xtu_decode_down_combine", fmt, _p(act), T, A, H, I, _p(W.w2), _p(W.s2),
                       _p(W.gs2), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.sorted_wts),
