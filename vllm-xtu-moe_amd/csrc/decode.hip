@@ -70,22 +70,24 @@ struct Stream {
   __amdgpu_buffer_rsrc_t s;   // fp4: the panel's scale groups; fp8: its block-scale row
 };
 
+// live = false: zero-length ranges (loads return 0 without touching memory).
 template <int FMT>
-__device__ __forceinline__ Stream<FMT> make_stream(const DecodeArgs& a, int ws, int panel, int K) {
+__device__ __forceinline__ Stream<FMT> make_stream(const DecodeArgs& a, int ws, int panel, int K,
+                                                   bool live = true) {
   using F = WFmt<FMT>;
   const long nsb = K / F::kSB;
   const uint8_t* sx = a.s + (long)ws * a.s_estride;
   Stream<FMT> st;
   st.w = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.w + (long)ws * a.w_estride + (long)panel * nsb * 1024), 0, (int)(nsb * 1024),
-      kRawBufferFlags);
+      (void*)(a.w + (long)ws * a.w_estride + (long)panel * nsb * 1024), 0,
+      live ? (int)(nsb * 1024) : 0, kRawBufferFlags);
   if constexpr (FMT == kMXFP4 || FMT == kNVFP4) {
     const long gbytes = scale_groups(K, F::kUG) * 1024;
-    st.s = __builtin_amdgcn_make_buffer_rsrc((void*)(sx + (long)panel * gbytes), 0, (int)gbytes,
-                                             kRawBufferFlags);
+    st.s = __builtin_amdgcn_make_buffer_rsrc((void*)(sx + (long)panel * gbytes), 0,
+                                             live ? (int)gbytes : 0, kRawBufferFlags);
   } else if constexpr (FMT == kFP8) {
     st.s = __builtin_amdgcn_make_buffer_rsrc((void*)(sx + (long)(panel / 8) * (K / 128) * 4), 0,
-                                             (K / 128) * 4, kRawBufferFlags);
+                                             live ? (K / 128) * 4 : 0, kRawBufferFlags);
   } else {
     st.s = st.w;
   }
@@ -303,7 +305,6 @@ __global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // rows x H
   __shared__ f32x4_t red[8][kWave];
   const int npan = a.I / 16;
-  if ((int)blockIdx.x >= a.n_active[0] * npan) return;   // whole workgroup
   const int ksplit = a.ksplit;
   const int w = wave_id();
   const uint32_t lane = threadIdx.x % kWave;
@@ -311,17 +312,19 @@ __global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
   const int nunits = a.H / 128;
   const int u0 = ks * nunits / ksplit, u1 = (ks + 1) * nunits / ksplit;
   const int q = lane / 16, m = lane % 16;
-  const Item c = item_at(a, blockIdx.x, npan);
   const int per_row = a.H / 8;        // 16-byte pieces per row
-  const Stream<FMT> st = make_stream<FMT>(a, c.ws, half ? npan + c.sub : c.sub, a.H);
   Round<FMT, NU> r;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  if (!GENERIC) {
-    // every token row of the batch is staged (x rows 0..T-1 are contiguous):
-    // lane m reads the row of its expert's m-th token.  Issue order: token
-    // ids, rows, weights, so the row stores wait for the rows only and the
-    // units are consumed as they arrive.
-    const int tok = a.sorted_tok[c.r0 + min(m, c.na - 1)];
+  if constexpr (!GENERIC) {
+    // Every token row of the batch is staged (x rows 0..T-1 are contiguous).
+    // Issue order: the active count and the slot's expert (scalar, one
+    // level), the rows, the weights (zero-length ranges for a slot past the
+    // active count, which then exits), then the expert's row range and lane
+    // m's token; the row stores wait for the rows only and the units are
+    // consumed as they arrive.
+    const int slot = blockIdx.x / npan, sub = blockIdx.x - slot * npan;
+    const int nact = a.n_active[0];
+    const int e_raw = a.active[slot];
     const int nchunks = a.T * per_row;
     u32x4_t xv[XC];
 #pragma unroll
@@ -329,9 +332,17 @@ __global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
       const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
       xv[j] = *reinterpret_cast<const u32x4_t*>(a.x + (long)cc * 8);
     }
+    const bool live = slot < nact;
+    const int e = live ? e_raw : 0;
+    const int ws = live && a.slot_map ? a.slot_map[e] : e;
+    const Stream<FMT> st = make_stream<FMT>(a, ws, half ? npan + sub : sub, a.H, live);
     __builtin_amdgcn_sched_barrier(0);
     issue_round<FMT, NU>(r, st, u0, u1, lane);
     __builtin_amdgcn_sched_barrier(0);
+    if (!live) return;   // whole workgroup
+    const int r0 = a.seg_start[e];
+    const int na = min(a.seg_start[e + 1] - r0, kMaxTok);
+    const int tok = a.sorted_tok[r0 + min(m, na - 1)];
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
       const int cc = threadIdx.x + j * blockDim.x;
@@ -339,7 +350,12 @@ __global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
     }
     __syncthreads();
     consume_round<FMT, NU, true>(r, acc, u0, u1, xs + tok * a.H + q * F::kCK, nullptr);
+    gate_up_epilogue<FMT>(a, red, acc, w, lane, r0, na, ws, sub);
+    return;
   } else {
+    if ((int)blockIdx.x >= a.n_active[0] * npan) return;   // whole workgroup
+    const Item c = item_at(a, blockIdx.x, npan);
+    const Stream<FMT> st = make_stream<FMT>(a, c.ws, half ? npan + c.sub : c.sub, a.H);
     // the expert's first `rows` token rows are staged, the rest read from
     // global memory; more than one round per wave when K needs it
     const int nr = min(c.na, a.rows);
@@ -373,8 +389,8 @@ __global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
       consume_round<FMT, NU, false>(r, acc, u0, u1, xa, xg);
       if (u0 + NU < u1) acc = more_rounds<FMT, NU, false>(acc, st, u0 + NU, u1, lane, xa, xg);
     }
+    gate_up_epilogue<FMT>(a, red, acc, w, lane, c.r0, c.na, c.ws, c.sub);
   }
-  gate_up_epilogue<FMT>(a, red, acc, w, lane, c.r0, c.na, c.ws, c.sub);
 }
 
 template <int FMT, bool GENERIC>
