@@ -182,33 +182,36 @@ __global__ __launch_bounds__(kThreads8, 2) void gemm8_kernel(Gemm8Args a) {
   const int w = __builtin_amdgcn_readfirstlane(tid / 64);
   const int lane = tid % 64;
 
-  // ---- row pieces of this thread: piece j = tid % 16 of rows (i*256 + tid) / 16
-  // (j < 8: hi bytes 16j..; j >= 8: lo bytes 16(j-8)..), and one scale word
-  const int pj = tid % 16;
+  // ---- row pieces of this thread.  Waves 0-1 stage the hi plane, waves 2-3
+  // the lo plane (so each wave's buffer descriptor is uniform: no per-lane
+  // descriptor loop); piece i of thread t covers plane bytes 16 * (f % 8) of
+  // row f / 8, f = i * 128 + t % 128.  Scale words: wave 0 the hi scales,
+  // wave 1 the lo scales, row = lane.
+  const int aplane = __builtin_amdgcn_readfirstlane(tid / 128);
   uint32_t aoff[kAP8];
   int alds[kAP8];
 #pragma unroll
   for (int i = 0; i < kAP8; ++i) {
-    const int r = (i * kThreads8 + tid) / 16;
+    const int f = i * 128 + tid % 128;
+    const int r = f / 8;
     const int rr = min(r, rows - 1);
     const uint32_t src = GU ? (uint32_t)a.sorted_tok[row0 + rr] : (uint32_t)(row0 + rr);
-    aoff[i] = src * (uint32_t)K + (uint32_t)(pj % 8) * 16u;
-    alds[i] = r * kLD8 + pj * 16;
+    aoff[i] = src * (uint32_t)K + (uint32_t)(f % 8) * 16u;
+    alds[i] = r * kLD8 + aplane * 128 + (f % 8) * 16;
   }
-  const uint8_t* plane = pj < 8 ? a.hi : a.lo;
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)plane, 0, -1, kFlags8);
-  // scale words: threads < 2*kBM8, row tid/2, hi (even) or lo (odd)
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(aplane ? a.lo : a.hi), 0, -1, kFlags8);
   const bool sthr = tid < 2 * kBM8;
-  const int srow = sthr ? tid / 2 : 0;
+  const int splane = __builtin_amdgcn_readfirstlane(tid / 64);   // wave 0 / 1
+  const int srow = sthr ? tid % 64 : 0;
   const uint32_t ssrc = GU ? (uint32_t)a.sorted_tok[row0 + min(srow, rows - 1)]
                            : (uint32_t)(row0 + min(srow, rows - 1));
   const uint32_t soff = ssrc * (uint32_t)(K / 32);
-  const int slds = srow * kLD8 + 256 + 4 * (tid % 2);
+  // waves 2-3 store their (unused) word into the row padding: the store stays
+  // unconditional, so the step has no branch the MFMAs could be sunk past
+  const int slds = sthr ? srow * kLD8 + 256 + 4 * (splane & 1) : (tid % 64) * kLD8 + 264;
   const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((tid % 2) ? a.slo : a.shi), 0, -1, kFlags8);
-  if (!GU) {
-    (void)0;   // act rows are contiguous: src = row0 + r above
-  }
+      (void*)((splane & 1) ? a.slo : a.shi), 0, -1, kFlags8);
 
   // ---- weights: this wave's panels, block-scale rows
   int pan[kPW8];
@@ -238,7 +241,7 @@ __global__ __launch_bounds__(kThreads8, 2) void gemm8_kernel(Gemm8Args a) {
   auto store_a = [&](uint8_t* buf, const u32x4_t (&ar)[kAP8], uint32_t sw) {
 #pragma unroll
     for (int i = 0; i < kAP8; ++i) *reinterpret_cast<u32x4_t*>(buf + alds[i]) = ar[i];
-    if (sthr) *reinterpret_cast<uint32_t*>(buf + slds) = sw;
+    *reinterpret_cast<uint32_t*>(buf + slds) = sw;
   };
   auto load_b = [&](int s, B8Step& b) {
 #pragma unroll
@@ -313,26 +316,28 @@ __global__ __launch_bounds__(kThreads8, 2) void gemm8_kernel(Gemm8Args a) {
     load_b(0, b0);
     store_a(As, ar, sw);
     __syncthreads();
-    for (int s = 0; s < nsteps; s += 2) {
-      const int s1 = min(s + 1, nsteps - 1);
-      load_a(s1, ar, sw);
-      load_b(s1, b1);
+    // two steps per trip with no branch inside, so the MFMAs stay between
+    // the next step's loads and the LDS stores that wait for them; an odd
+    // last step runs after the loop (the step past the end is a re-read)
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+      load_a(s + 1, ar, sw);
+      load_b(s + 1, b1);
       __builtin_amdgcn_sched_barrier(0);
       compute(b0, As);
       __builtin_amdgcn_sched_barrier(0);
       store_a(As + kBuf8, ar, sw);
       __syncthreads();
-      if (s + 1 < nsteps) {
-        const int s2 = min(s + 2, nsteps - 1);
-        load_a(s2, ar, sw);
-        load_b(s2, b0);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(b1, As + kBuf8);
-        __builtin_amdgcn_sched_barrier(0);
-        store_a(As, ar, sw);
-        __syncthreads();
-      }
+      const int s2 = min(s + 2, nsteps - 1);
+      load_a(s2, ar, sw);
+      load_b(s2, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(b1, As + kBuf8);
+      __builtin_amdgcn_sched_barrier(0);
+      store_a(As, ar, sw);
+      __syncthreads();
     }
+    if (s < nsteps) compute(b0, As);
 
     if constexpr (GU) {
       uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
