@@ -250,15 +250,34 @@ def gemm_tile_m(fmt: int, int8: bool = False) -> int:
 FUSED_DOWN_ENV = "XTU_DECODE_FUSED_DOWN"
 
 
+FUSED_DOWN_MAX_EXPERTS = 24
+
+
 def decode_fused_down_ok(fmt: int, T: int, A: int, H: int, I: int, max_active: int,
                          trash: int) -> bool:
-    """Whether the decode path runs the down projection and the weighted
-    combine as one kernel (the batch's act rows fit the kernel's LDS stage);
-    XTU_DECODE_FUSED_DOWN=0 keeps the separate down + combine."""
-    if os.environ.get(FUSED_DOWN_ENV, "1") == "0":
-        return False
+    """Whether the down projection with the weighted combine fused can run
+    this batch (its act rows fit the kernel's LDS stage)."""
     return bool(_lib.call("xtu_decode_down_combine_ok", int(fmt), int(T), int(A), int(H), int(I),
                           int(trash), int(max_active)))
+
+
+def decode_fused_down_use(fmt: int, T: int, A: int, H: int, I: int, max_active: int,
+                          trash: int) -> bool:
+    """Whether the decode path takes the fused down + combine.  Each of its
+    waves walks every active expert, so it pays where few experts meet wide
+    panels; measured (MI355X): faster for DeepSeek-V3 MXFP4 at T = 1, 2 (9 / 17
+    experts) and Qwen3-Next MXFP4 at T = 1 (11), slower with 40 experts and
+    for NVFP4 at I = 512.  XTU_DECODE_FUSED_DOWN=1 takes it whenever it fits,
+    =0 never."""
+    mode = os.environ.get(FUSED_DOWN_ENV, "auto")
+    if mode == "0":
+        return False
+    if mode != "1":
+        if max_active > FUSED_DOWN_MAX_EXPERTS:
+            return False
+        if int(fmt) == FMT_NVFP4 and I < 1024:
+            return False
+    return decode_fused_down_ok(fmt, T, A, H, I, max_active, trash)
 
 
 def _fp8pair_bufs(tag, M, K, dev):
@@ -346,8 +365,8 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13),
                   0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
                   _p(seg.n_active), max_active, _p(act), lim, al, be, st)
-        if odt in (torch.bfloat16, torch.float32) and decode_fused_down_ok(fmt, T, A, H, I,
-                                                                          max_active, E + NS):
+        if odt in (torch.bfloat16, torch.float32) and decode_fused_down_use(fmt, T, A, H, I,
+                                                                           max_active, E + NS):
             # down projection and weighted combine in one pass, out written whole
             _lib.call("xtu_decode_down_combine", fmt, _p(act), T, A, H, I, _p(W.w2), _p(W.s2),
                       _p(W.gs2), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.sorted_wts),
