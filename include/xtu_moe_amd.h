@@ -119,18 +119,61 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
                            const int32_t* active, const int32_t* n_active, int max_active,
                            float* y, hipStream_t stream);
 
+/* Routing + segmentation and the shared experts' gate/up in one launch
+ * (tiny batches, n_shared >= 1): workgroup 0 does exactly what
+ * xtu_route_segment_small does (same outputs, same order; mode 0 softmax /
+ * 1 grouped sigmoid from fp32 logits, 2 ids given), workgroups 1.. run the
+ * shared experts' gate/up for all T tokens -- they need no routing -- and
+ * write act_shared bf16 [n_shared][T][I] in token order.  The argument list
+ * is xtu_route_segment_small's followed by the gate/up weights.  Then
+ * xtu_decode_gate_up_routed runs the routed experts (the last n_shared
+ * active slots, the shared buckets, left out) and xtu_decode_down_combine
+ * takes the shared rows from act_shared.  Replaces, for decode, the router
+ * call plus _build_segmentation (gpu_prefill.py:849-887) and the shared
+ * expert's share of moe4_smallm_gu2 (moe4_smallm.cu:395-413).
+ * xtu_decode_route_shared_ok: the shape fits (the tiny router's envelope,
+ * one wave per token in the gate/up workgroup, the gate/up fast path: every
+ * token row staged in LDS, one round per wave); logits / bias rows must
+ * also be 16-byte aligned (hipErrorInvalidValue otherwise). */
+int xtu_decode_route_shared_ok(int fmt, int mode, int T, int E, int K, int n_group,
+                               int n_shared, int H, int I);
+hipError_t xtu_decode_route_shared(
+    int mode, const float* logits, const float* bias, int32_t* topk_ids, float* topk_weights,
+    int T, int E, int K, int n_group, int topk_group, float routed_scaling, int renormalize,
+    const int32_t* id_map, int n_shared, int drop_zero, int bm, int32_t* sorted_pair,
+    int32_t* sorted_tok, float* sorted_wts, int32_t* inv, int32_t* seg_start, int32_t* active,
+    int32_t* n_active, int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
+    int32_t* expert_tile_start, int fmt, const void* x, int H, int I, const void* w13,
+    const void* s13, const float* gs13, long w_estride, long s_estride, const int32_t* slot_map,
+    void* act_shared, float limit, float alpha, float beta, hipStream_t stream);
+/* xtu_decode_gate_up for the routed experts only: the last n_shared active
+ * slots (the shared buckets) are left out; the gate/up fast-path shape is
+ * required. */
+hipError_t xtu_decode_gate_up_routed(int fmt, const void* x, int T, int H, int I,
+                                     const void* w13, const void* s13, const float* gs13,
+                                     long w_estride, long s_estride, const int32_t* slot_map,
+                                     const int32_t* sorted_tok, const int32_t* seg_start,
+                                     const int32_t* active, const int32_t* n_active,
+                                     int max_active, int n_shared, void* act, float limit,
+                                     float alpha, float beta, hipStream_t stream);
+
 /* Down projection with the weighted combine fused: out[t] = sum over t's live
  * pairs (t, e) of w * (act_row W2_e^T), bf16 (out_bf16 = 1) or fp32 [T][H],
  * every row written.  Replaces moe4_smallm_dn2 (moe4_smallm.cu:260-333,
  * 416-430), which scatters the same sums with atomics; here each token's sum
  * runs over its experts in active-slot order (deterministic).  sorted_wts:
  * the segmentation's per-row weights (1 for shared rows); trash = E + NS.
- * xtu_decode_down_combine_ok reports whether a batch fits (T <= 16, I a
- * multiple of 128 with I/128 splitting into waves of 1, 2 or 4 units, the
- * A = T*(K+NS) act rows within the LDS stage); the entry returns
- * hipErrorInvalidValue otherwise. */
-int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int trash, int max_active);
-hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int A, int H, int I,
+ * act_shared (nullable): the shared experts' rows [n_shared][T][I] written
+ * by xtu_decode_route_shared, used for buckets trash - n_shared .. trash - 1
+ * instead of their rows in act.  xtu_decode_down_combine_ok reports whether
+ * a batch fits (T <= 16, I a multiple of 128 with I/128 splitting into waves
+ * of 1, 2 or 4 units, the A = T*(K+NS) act rows plus shared_rows =
+ * n_shared*T (when act_shared is given) within the LDS stage); the entry
+ * returns hipErrorInvalidValue otherwise. */
+int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int trash, int max_active,
+                               int shared_rows);
+hipError_t xtu_decode_down_combine(int fmt, const void* act, const void* act_shared, int n_shared,
+                                   int T, int A, int H, int I,
                                    const void* w2, const void* s2, const float* gs2,
                                    long w_estride, long s_estride, const int32_t* slot_map,
                                    const int32_t* sorted_tok, const float* sorted_wts,

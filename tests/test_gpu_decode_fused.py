@@ -155,3 +155,131 @@ def test_decode_hidden_sizes_and_single_expert(fmt, T, H, monkeypatch):
     ref1 = oracle_layer(fmt, dense_to_numpy(fmt, d1), bf16_tensor_to_bits(x), ids1, wts1, E, 0, H,
                         I)
     check_close(out1.cpu().numpy(), ref1, bf16_out=False, what=f"single expert T={T}")
+
+
+# ---------------------------------------------------------------------------
+# shared experts' gate/up inside the routing launch (xtu_decode_route_shared)
+
+_SEG_FIELDS = ("sorted_pair", "sorted_tok", "sorted_wts", "inv", "seg_start", "active",
+               "n_active", "tile_expert", "tile_row0", "n_tiles", "expert_tile_start")
+
+
+def _seg_state(seg):
+    n_act = int(seg.n_active.item())
+    n_til = int(seg.n_tiles.item())
+    out = {}
+    for f in _SEG_FIELDS:
+        t = getattr(seg, f)
+        if f in ("sorted_pair", "sorted_tok", "sorted_wts", "inv"):
+            t = t[:seg.A]
+        elif f == "active":
+            t = t[:n_act]
+        elif f in ("tile_expert", "tile_row0"):
+            t = t[:n_til]
+        out[f] = t.clone()
+    return out
+
+
+def _split_run(monkeypatch, split, x, W, K, router=None, ids=None, wts=None, **kw):
+    monkeypatch.setenv(L.SHARED_SPLIT_ENV, "1" if split else "0")
+    monkeypatch.setenv(L.FUSED_DOWN_ENV, "1")
+    T = x.shape[0]
+    if router is not None:
+        ids = torch.full((T, K), -7, dtype=torch.int32, device="cuda")
+        wts = torch.full((T, K), float("nan"), dtype=torch.float32, device="cuda")
+    for t in L._BUF_CACHE.values():   # unwritten rows would show up as NaN
+        if t.is_floating_point():
+            t.fill_(float("nan"))
+    out, seg = moe_forward(x, ids, wts, W, path="decode", router=router, return_seg=True,
+                           out_dtype=torch.float32, **kw)
+    torch.cuda.synchronize()
+    return out, ids.clone(), wts.clone(), _seg_state(seg)
+
+
+def _same(a, b, what):
+    oa, ia, wa, sa = a
+    ob, ib, wb, sb = b
+    assert torch.equal(ia, ib), f"{what}: ids"
+    assert torch.equal(wa.view(torch.int32), wb.view(torch.int32)), f"{what}: weights"
+    for f in _SEG_FIELDS:
+        ta, tb = sa[f], sb[f]
+        if ta.dtype == torch.float32:
+            ta, tb = ta.view(torch.int32), tb.view(torch.int32)
+        assert torch.equal(ta, tb), f"{what}: {f}"
+    assert torch.equal(oa, ob), f"{what}: output"
+
+
+@pytest.mark.parametrize("T,H", [(1, 512), (2, 512), (4, 4096)])
+def test_shared_split_grouped_sigmoid(T, H, monkeypatch):
+    # one routing wave per token: H = 512 gives 2-wave workgroups, 4096 four
+    fmt, E, NS, I, K = F.FMT_MXFP4, 256, 1, 256, 8
+    d, W = _layer(fmt, E, NS, H, I, seed=70 + T)
+    g = torch.Generator(device="cuda").manual_seed(71 + T)
+    logits = torch.randn((T, E), generator=g, device="cuda")
+    bias = torch.randn((E,), generator=g, device="cuda") * 0.1
+    x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    router = dict(logits=logits, scoring="sigmoid", bias=bias, n_group=8, topk_group=4,
+                  routed_scaling_factor=2.5, renormalize=True)
+    assert L._route_shared_ok(fmt, 1, T, E, K, router, H, I, NS)
+    a = _split_run(monkeypatch, True, x, W, K, router=router)
+    b = _split_run(monkeypatch, False, x, W, K, router=router)
+    _same(a, b, f"grouped sigmoid T={T}")
+    out, ids, wts, _ = a
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids.cpu().numpy(),
+                       wts.cpu().numpy(), E, NS, H, I)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"split T={T} vs oracle")
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_shared_split_softmax_512(T, monkeypatch):
+    fmt, E, NS, H, I, K = F.FMT_NVFP4, 512, 1, 512, 256, 10
+    _, W = _layer(fmt, E, NS, H, I, seed=80 + T)
+    g = torch.Generator(device="cuda").manual_seed(81 + T)
+    logits = torch.randn((T, E), generator=g, device="cuda")
+    x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    router = dict(logits=logits, scoring="softmax", renormalize=True)
+    assert L._route_shared_ok(fmt, 0, T, E, K, router, H, I, NS)
+    _same(_split_run(monkeypatch, True, x, W, K, router=router),
+          _split_run(monkeypatch, False, x, W, K, router=router), f"softmax T={T}")
+
+
+@pytest.mark.parametrize("drop_zero", [True, False])
+def test_shared_split_given_ids_two_shared(drop_zero, monkeypatch):
+    fmt, E, NS, H, I, T, K = F.FMT_FP8, 16, 2, 512, 256, 2, 4
+    d, _ = _layer(fmt, E, NS, H, I, seed=91)
+    # experts stored in reverse order behind a slot map, ids through an id map
+    order = np.arange(E + NS)[::-1].copy()
+    idx = torch.from_numpy(order)
+    rev = {k: (v[idx].contiguous() if v is not None else None) for k, v in d.items()}
+    W = ExpertWeights.from_dense(fmt, rev["w13"], rev["s13"], rev["w2"], rev["s2"], rev["gs13"],
+                                 rev["gs2"], n_shared=NS, device="cuda")
+    slot_map = torch.from_numpy(np.argsort(order).astype(np.int32)).cuda()
+    ids_np, wts_np = random_routing(T, K, E, seed=92)
+    ids_np[0, 1] = -1
+    ids_np[1, 2] = ids_np[1, 0]
+    wts_np[1, 3] = 0.0
+    ids = torch.from_numpy(ids_np).cuda()
+    wts = torch.from_numpy(wts_np).cuda()
+    id_map = torch.from_numpy(np.roll(np.arange(E), 3).astype(np.int32)).cuda()
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(93)).to(torch.bfloat16).cuda()
+    assert L._route_shared_ok(fmt, 2, T, E, K, None, H, I, NS)
+    kw = dict(ids=ids, wts=wts, drop_zero=drop_zero, id_map=id_map, slot_map=slot_map)
+    a = _split_run(monkeypatch, True, x, W, K, **kw)
+    _same(a, _split_run(monkeypatch, False, x, W, K, **kw), f"given ids drop_zero={drop_zero}")
+    mapped = np.where((ids_np >= 0) & (ids_np < E), np.roll(np.arange(E), 3)[ids_np % E], -1)
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x.cpu()),
+                       mapped.astype(np.int32), wts_np, E, NS, H, I)
+    check_close(a[0].cpu().numpy(), ref, bf16_out=False, what="split given ids vs oracle")
+
+
+def test_shared_split_misaligned_logits_fall_back(monkeypatch):
+    fmt, E, NS, H, I, T, K = F.FMT_MXFP4, 256, 1, 512, 256, 1, 8
+    _, W = _layer(fmt, E, NS, H, I, seed=95)
+    base = torch.randn((T * E + 1,), device="cuda")
+    logits = base[1:].view(T, E)          # 4-byte offset: not 16-byte aligned
+    router = dict(logits=logits, scoring="sigmoid", n_group=8, topk_group=4,
+                  routed_scaling_factor=2.5)
+    assert not L._route_shared_ok(fmt, 1, T, E, K, router, H, I, NS)
+    x = torch.randn((T, H), device="cuda").to(torch.bfloat16)
+    _same(_split_run(monkeypatch, True, x, W, K, router=router),
+          _split_run(monkeypatch, False, x, W, K, router=router), "misaligned logits")

@@ -19,6 +19,7 @@
 //   the matching up rows I+16p.., so the SwiGLU of row n is formed in the
 //   reduction step and only the bf16 activation row is written.
 // down: y is fp32; with KSPLIT = 1 each wave writes its panel directly.
+#include "route_tiny.hpp"
 #include "weight_format.hpp"
 
 namespace xtu {
@@ -45,6 +46,7 @@ struct DecodeArgs {
   float limit, alpha, beta;
   int rows;                  // rows the LDS stage holds
   int ksplit, ppb;           // waves per panel K range; panels per workgroup (down)
+  int skip;                  // gate/up fast path: trailing active slots left out
 };
 
 // Units issued per round: about 80 VGPRs of weights in flight per wave, and
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
       const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
       xv[j] = *reinterpret_cast<const u32x4_t*>(a.x + (long)cc * 8);
     }
-    const bool live = slot < nact;
+    const bool live = slot < nact - a.skip;
     const int e = live ? e_raw : 0;
     const int ws = live && a.slot_map ? a.slot_map[e] : e;
     const Stream<FMT> st = make_stream<FMT>(a, ws, half ? npan + sub : sub, a.H, live);
@@ -391,6 +393,63 @@ __global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
     }
     gate_up_epilogue<FMT>(a, red, acc, w, lane, c.r0, c.na, c.ws, c.sub);
   }
+}
+
+// Routing + segmentation (workgroup 0, tiny::route_segment_block) and the
+// shared experts' gate/up (workgroups 1.., one per (shared expert, gate
+// panel)) in one launch: a shared expert needs no routing, so its weight
+// stream runs beside the router instead of after it.  Its act rows go to
+// act_sh [n_shared][T][I] (token order), since their sorted positions are
+// known only once the batch is routed; the routed gate/up then leaves the
+// shared slots out (DecodeArgs::skip) and the fused down reads them from
+// act_sh.  The gate/up part is decode_gate_up_kernel's fast path with all T
+// rows of the batch as the expert's rows.
+template <int FMT, int MODE, int EPL, int XC>
+__global__ __launch_bounds__(512) void decode_route_shared_kernel(tiny::SmallArgs ra,
+                                                                  DecodeArgs a) {
+  using F = WFmt<FMT>;
+  constexpr int NU = round_units<FMT>();
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // T rows x H
+  __shared__ f32x4_t red[8][kWave];
+  __shared__ __attribute__((aligned(16))) tiny::TinySmem g;
+  if (blockIdx.x == 0) {
+    tiny::route_segment_block<MODE, EPL>(ra, g);
+    return;
+  }
+  const int npan = a.I / 16;
+  const int item = blockIdx.x - 1;
+  const int sh = item / npan, sub = item - sh * npan;
+  const int e = ra.E + sh;
+  const int ws = a.slot_map ? a.slot_map[e] : e;
+  const int ksplit = a.ksplit;
+  const int w = wave_id();
+  const uint32_t lane = threadIdx.x % kWave;
+  const int half = w / ksplit, ks = w - half * ksplit;
+  const int nunits = a.H / 128;
+  const int u0 = ks * nunits / ksplit, u1 = (ks + 1) * nunits / ksplit;
+  const int q = lane / 16, m = lane % 16;
+  const int nchunks = a.T * (a.H / 8);
+  u32x4_t xv[XC];
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
+    xv[j] = *reinterpret_cast<const u32x4_t*>(a.x + (long)cc * 8);
+  }
+  const Stream<FMT> st = make_stream<FMT>(a, ws, half ? npan + sub : sub, a.H);
+  Round<FMT, NU> r;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_sched_barrier(0);
+  issue_round<FMT, NU>(r, st, u0, u1, lane);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int cc = threadIdx.x + j * blockDim.x;
+    if (cc < nchunks) *reinterpret_cast<u32x4_t*>(xs + cc * 8) = xv[j];
+  }
+  __syncthreads();
+  const int tok = min(m, a.T - 1);
+  consume_round<FMT, NU, true>(r, acc, u0, u1, xs + tok * a.H + q * F::kCK, nullptr);
+  gate_up_epilogue<FMT>(a, red, acc, w, lane, sh * a.T, a.T, ws, sub);
 }
 
 template <int FMT, bool GENERIC>
@@ -500,6 +559,8 @@ struct DownCombineArgs {
   int row_cap;                // rows the LDS stage holds (>= seg_start[trash])
   long w_estride, s_estride;
   int ks, ppb;
+  const uint16_t* act_sh;     // shared experts' act rows [n_shared][T][I] (or null)
+  int n_shared;               // buckets trash - n_shared .. trash - 1 are shared
 };
 
 constexpr int kDcTok = 16;    // tokens = MFMA rows
@@ -595,8 +656,9 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
   extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
   const int ldx = a.I + 8;                       // staged row stride (bf16), 16 B of padding
   const int nseg = a.trash + 2;                  // seg_start entries
+  const int sh_rows = a.act_sh ? a.n_shared * a.T : 0;   // staged after the sorted rows
   uint16_t* xs = reinterpret_cast<uint16_t*>(dyn);
-  int* rowof = reinterpret_cast<int*>(dyn + (size_t)a.row_cap * ldx * 2);   // [max_active][16]
+  int* rowof = reinterpret_cast<int*>(dyn + (size_t)(a.row_cap + sh_rows) * ldx * 2);   // [max_active][16]
   float* wof = reinterpret_cast<float*>(rowof + a.max_active * kDcTok);      // [max_active][16]
   int* eslot = reinterpret_cast<int*>(wof + a.max_active * kDcTok);          // [max_active]
   int* l_act = eslot + a.max_active;                                         // [max_active]
@@ -618,15 +680,19 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
   // ones are staged too (never selected).  Remainders (large batches) go
   // after the weights.
   const int per_row = a.I / 8;
-  const int pieces = a.row_cap * per_row;
+  const int pieces = (a.row_cap + sh_rows) * per_row;
+  const int nreg = a.row_cap * per_row;   // pieces of the sorted rows; then the shared rows
   const int nact_g = a.n_active[0];
   int e_first[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) e_first[d] = a.active[min(d, a.max_active - 1)];
   u32x4_t v[kDcSB];
 #pragma unroll
-  for (int k = 0; k < kDcSB; ++k)
-    v[k] = *reinterpret_cast<const u32x4_t*>(a.act + (long)min(tid + k * bd, pieces - 1) * 8);
+  for (int k = 0; k < kDcSB; ++k) {
+    const int c = min(tid + k * bd, pieces - 1);
+    v[k] = *reinterpret_cast<const u32x4_t*>(c < nreg ? a.act + (long)c * 8
+                                                       : a.act_sh + (long)(c - nreg) * 8);
+  }
   const int act_v = a.active[min(tid, a.max_active - 1)];
   int seg_v[kDcSegW];
 #pragma unroll
@@ -660,8 +726,11 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
   for (int c0 = tid + kDcSB * bd; c0 < pieces; c0 += kDcSB * bd) {
     u32x4_t vr[kDcSB];
 #pragma unroll
-    for (int k = 0; k < kDcSB; ++k)
-      vr[k] = *reinterpret_cast<const u32x4_t*>(a.act + (long)min(c0 + k * bd, pieces - 1) * 8);
+    for (int k = 0; k < kDcSB; ++k) {
+      const int c = min(c0 + k * bd, pieces - 1);
+      vr[k] = *reinterpret_cast<const u32x4_t*>(c < nreg ? a.act + (long)c * 8
+                                                         : a.act_sh + (long)(c - nreg) * 8);
+    }
 #pragma unroll
     for (int k = 0; k < kDcSB; ++k) {
       const int c = c0 + k * bd;
@@ -681,14 +750,17 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
     wof[i] = 0.f;
   }
   __syncthreads();
+  const int e_sh = a.trash - a.n_shared;   // first shared bucket
   for (int j = tid; j < nact; j += bd) {
     const int e = l_act[j];
     eslot[j] = a.slot_map ? a.slot_map[e] : e;
+    // a shared expert's rows come from act_sh when given: token t at row_cap + s*T + t
+    const int shb = (a.act_sh && e >= e_sh) ? a.row_cap + (e - e_sh) * a.T : -1;
     const int r1 = min(l_seg[e + 1], a.row_cap);
     for (int r = max(l_seg[e], 0); r < r1; ++r) {
       const int t = rtok[r];
       if (t >= 0 && t < kDcTok) {
-        rowof[j * kDcTok + t] = r;
+        rowof[j * kDcTok + t] = shb >= 0 ? shb + min(t, a.T - 1) : r;
         wof[j * kDcTok + t] += rw[r];
       }
     }
@@ -740,8 +812,8 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
 // Launch shape of the fused down: (KS, NPER) with KS * NPER = I / 128 and
 // NPER in {1, 2, 4}, KS <= 8; KS grows until the grid holds about 2048 waves.
 // Returns false when the shape or the LDS stage does not fit.
-bool dc_shape(int fmt, int T, int rows, int H, int I, int trash, int max_active, int& ks,
-              int& nper, int& ppb, size_t& lds) {
+bool dc_shape(int fmt, int T, int rows, int sh_rows, int H, int I, int trash, int max_active,
+              int& ks, int& nper, int& ppb, size_t& lds) {
   if (T < 1 || T > kDcTok || fmt < 0 || fmt > 3 || trash < 0 || trash > 4096 || rows < 1 ||
       max_active < 1)
     return false;
@@ -753,7 +825,7 @@ bool dc_shape(int fmt, int T, int rows, int H, int I, int trash, int max_active,
   if (nunits % ks || (nper != 1 && nper != 2 && nper != 4)) return false;
   ppb = 1;
   while (ks * ppb * 2 <= 4 && npan % (ppb * 2) == 0) ppb *= 2;
-  lds = (size_t)rows * (I + 8) * 2 + (size_t)max_active * (2 * kDcTok + 2) * 4 +
+  lds = (size_t)(rows + sh_rows) * (I + 8) * 2 + (size_t)max_active * (2 * kDcTok + 2) * 4 +
         (size_t)(trash + 2) * 4 + (size_t)rows * 8;
   const size_t red = (size_t)ks * ppb * kWave * 16;
   if (lds < red) lds = red;
@@ -833,6 +905,66 @@ hipError_t launch_decode(int which, DecodeArgs a, int max_active, hipStream_t st
   return hipPeekAtLastError();
 }
 
+// The gate/up fast path's shape (every token row staged, one round per wave,
+// at most 8 row pieces per thread); ksplit and the row-piece count out.
+template <int FMT>
+bool gate_up_fast_shape(int T, int H, int& ksplit, int& xc) {
+  constexpr int NU = round_units<FMT>();
+  const int cap = kLdsBudget / (H * 2);
+  ksplit = pick_ksplit(H / 128, NU, 4);
+  const int bd = 128 * ksplit;
+  const long pieces = (long)T * (H / 8);
+  xc = pieces <= bd ? 1 : pieces <= 2L * bd ? 2 : pieces <= 4L * bd ? 4 : 8;
+  return T >= 1 && T <= cap && H / 128 <= NU * ksplit && pieces <= 8L * bd;
+}
+
+bool gate_up_fast_shape_fmt(int fmt, int T, int H, int& ksplit, int& xc) {
+  switch (fmt) {
+    case kMXFP4: return gate_up_fast_shape<kMXFP4>(T, H, ksplit, xc);
+    case kNVFP4: return gate_up_fast_shape<kNVFP4>(T, H, ksplit, xc);
+    case kFP8: return gate_up_fast_shape<kFP8>(T, H, ksplit, xc);
+    case kBF16: return gate_up_fast_shape<kBF16>(T, H, ksplit, xc);
+  }
+  return false;
+}
+
+template <int FMT, int XC>
+void launch_route_shared_xc(int mode, int epl, dim3 grid, int bd, size_t lds,
+                            const tiny::SmallArgs& ra, const DecodeArgs& a, hipStream_t stream) {
+  if (mode == 2) {
+    decode_route_shared_kernel<FMT, 2, 1, XC><<<grid, bd, lds, stream>>>(ra, a);
+  } else if (mode == 1) {
+    if (epl == 4) decode_route_shared_kernel<FMT, 1, 4, XC><<<grid, bd, lds, stream>>>(ra, a);
+    else decode_route_shared_kernel<FMT, 1, 8, XC><<<grid, bd, lds, stream>>>(ra, a);
+  } else {
+    if (epl == 4) decode_route_shared_kernel<FMT, 0, 4, XC><<<grid, bd, lds, stream>>>(ra, a);
+    else decode_route_shared_kernel<FMT, 0, 8, XC><<<grid, bd, lds, stream>>>(ra, a);
+  }
+}
+
+template <int FMT>
+hipError_t launch_route_shared(int mode, int epl, const tiny::SmallArgs& ra, DecodeArgs a,
+                               hipStream_t stream) {
+  using F = WFmt<FMT>;
+  if (!a.w_estride) a.w_estride = F::w_bytes(2L * a.I, a.H);
+  if (!a.s_estride) a.s_estride = F::s_bytes(2L * a.I, a.H);
+  int ksplit = 0, xc = 0;
+  if (!gate_up_fast_shape<FMT>(a.T, a.H, ksplit, xc)) return hipErrorInvalidValue;
+  a.ksplit = ksplit;
+  a.rows = a.T;
+  const int bd = 128 * ksplit;
+  if (a.T * kWave > bd) return hipErrorInvalidValue;   // one routing wave per token
+  const dim3 grid(1 + ra.NS * (a.I / 16));
+  const size_t lds = (size_t)a.T * a.H * 2;
+  switch (xc) {
+    case 1: launch_route_shared_xc<FMT, 1>(mode, epl, grid, bd, lds, ra, a, stream); break;
+    case 2: launch_route_shared_xc<FMT, 2>(mode, epl, grid, bd, lds, ra, a, stream); break;
+    case 4: launch_route_shared_xc<FMT, 4>(mode, epl, grid, bd, lds, ra, a, stream); break;
+    default: launch_route_shared_xc<FMT, 8>(mode, epl, grid, bd, lds, ra, a, stream); break;
+  }
+  return hipPeekAtLastError();
+}
+
 hipError_t dispatch_decode(int fmt, int which, DecodeArgs a, int max_active, hipStream_t stream) {
   switch (fmt) {
     case kMXFP4: return launch_decode<kMXFP4>(which, a, max_active, stream);
@@ -893,14 +1025,95 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
   return dispatch_decode(fmt, 1, a, max_active, stream);
 }
 
-int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int trash, int max_active) {
+int xtu_decode_route_shared_ok(int fmt, int mode, int T, int E, int K, int n_group,
+                               int n_shared, int H, int I) {
+  int ksplit = 0, xc = 0;
+  if (!shape_ok(fmt, H, I) || mode < 0 || mode > 2 || K < 1 || K > 16 || K > E || E < 1 ||
+      E > 1024 || n_shared < 1 || n_shared > 16 ||
+      !gate_up_fast_shape_fmt(fmt, T, H, ksplit, xc) || T * kWave > 128 * ksplit)
+    return 0;
+  if (mode == 1 && (n_group <= 0 || n_group > 64 || E % n_group)) return 0;
+  tiny::SmallArgs r{};
+  r.T = T;
+  r.K = K;
+  r.E = E;
+  r.NS = n_shared;
+  r.n_group = n_group > 0 ? n_group : 1;
+  r.renorm = 1;
+  static const float probe[4] = {0.f, 0.f, 0.f, 0.f};   // a 16-byte-aligned row stands in
+  r.logits = probe;
+  return tiny::tiny_epl(r, mode) != 0;
+}
+
+hipError_t xtu_decode_route_shared(
+    int mode, const float* logits, const float* bias, int32_t* topk_ids, float* topk_weights,
+    int T, int E, int K, int n_group, int topk_group, float routed_scaling, int renormalize,
+    const int32_t* id_map, int n_shared, int drop_zero, int bm, int32_t* sorted_pair,
+    int32_t* sorted_tok, float* sorted_wts, int32_t* inv, int32_t* seg_start, int32_t* active,
+    int32_t* n_active, int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
+    int32_t* expert_tile_start, int fmt, const void* x, int H, int I, const void* w13,
+    const void* s13, const float* gs13, long w_estride, long s_estride, const int32_t* slot_map,
+    void* act_shared, float limit, float alpha, float beta, hipStream_t stream) {
+  XTU_CHECK_ARG(xtu_decode_route_shared_ok(fmt, mode, T, E, K, n_group, n_shared, H, I));
+  XTU_CHECK_ARG(bm > 0 && w_estride >= 0 && s_estride >= 0);
+  if (mode == 1)
+    XTU_CHECK_ARG(topk_group > 0 && topk_group <= n_group && K <= topk_group * (E / n_group));
+  XTU_CHECK_ARG(topk_ids && topk_weights && (mode == 2 || logits));
+  XTU_CHECK_ARG(sorted_pair && sorted_tok && sorted_wts && inv && seg_start && active &&
+                n_active && tile_expert && tile_row0 && n_tiles && expert_tile_start);
+  XTU_CHECK_ARG(x && w13 && (fmt == kBF16 || s13) && act_shared);
+  tiny::SmallArgs ra{logits, bias, topk_ids, topk_weights, id_map, T, K, E, n_group,
+                     topk_group, renormalize, n_shared, drop_zero, bm, routed_scaling,
+                     sorted_pair, sorted_tok, inv, seg_start, active, n_active, sorted_wts,
+                     tile_expert, tile_row0, n_tiles, expert_tile_start};
+  const int epl = tiny::tiny_epl(ra, mode);   // also checks the logit / bias alignment
+  XTU_CHECK_ARG(epl != 0);
+  (void)hipGetLastError();
+  DecodeArgs a{(const uint16_t*)x, (const uint8_t*)w13, (const uint8_t*)s13, gs13, nullptr,
+               nullptr, nullptr, nullptr, slot_map, act_shared, T, H, I, w_estride, s_estride,
+               limit, alpha, beta, 0, 1, 1, 0};
+  switch (fmt) {
+    case kMXFP4: return launch_route_shared<kMXFP4>(mode, epl, ra, a, stream);
+    case kNVFP4: return launch_route_shared<kNVFP4>(mode, epl, ra, a, stream);
+    case kFP8: return launch_route_shared<kFP8>(mode, epl, ra, a, stream);
+    case kBF16: return launch_route_shared<kBF16>(mode, epl, ra, a, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t xtu_decode_gate_up_routed(int fmt, const void* x, int T, int H, int I,
+                                     const void* w13, const void* s13, const float* gs13,
+                                     long w_estride, long s_estride, const int32_t* slot_map,
+                                     const int32_t* sorted_tok, const int32_t* seg_start,
+                                     const int32_t* active, const int32_t* n_active,
+                                     int max_active, int n_shared, void* act, float limit,
+                                     float alpha, float beta, hipStream_t stream) {
+  int ksplit = 0, xc = 0;
+  XTU_CHECK_ARG(shape_ok(fmt, H, I) && max_active >= 0 && max_active <= 65535 && T >= 0 &&
+                T <= kMaxTok && n_shared >= 0 && n_shared <= max_active);
+  XTU_CHECK_ARG(T == 0 || gate_up_fast_shape_fmt(fmt, T, H, ksplit, xc));
+  XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
+  XTU_CHECK_ARG(x && w13 && (fmt == kBF16 || s13) && sorted_tok && seg_start && active &&
+                n_active && act);
+  if (max_active == n_shared || T == 0) return hipSuccess;
+  (void)hipGetLastError();
+  DecodeArgs a{(const uint16_t*)x, (const uint8_t*)w13, (const uint8_t*)s13, gs13, sorted_tok,
+               seg_start, active, n_active, slot_map, act, T, H, I, w_estride, s_estride, limit,
+               alpha, beta, 0, 1, 1, n_shared};
+  return dispatch_decode(fmt, 0, a, max_active - n_shared, stream);
+}
+
+int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int trash, int max_active,
+                               int shared_rows) {
   int ks, nper, ppb;
   size_t lds;
   return shape_ok(fmt, H, I) && A >= 0 && max_active >= 0 && max_active <= 65535 &&
-         dc_shape(fmt, T, A, H, I, trash, max_active, ks, nper, ppb, lds);
+         shared_rows >= 0 && shared_rows <= kDcTok * 16 &&
+         dc_shape(fmt, T, A, shared_rows, H, I, trash, max_active, ks, nper, ppb, lds);
 }
 
-hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int A, int H, int I,
+hipError_t xtu_decode_down_combine(int fmt, const void* act, const void* act_shared, int n_shared,
+                                   int T, int A, int H, int I,
                                    const void* w2, const void* s2, const float* gs2,
                                    long w_estride, long s_estride, const int32_t* slot_map,
                                    const int32_t* sorted_tok, const float* sorted_wts,
@@ -909,8 +1122,11 @@ hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int A, int H
                                    int out_bf16, hipStream_t stream) {
   int ks = 0, nper = 0, ppb = 0;
   size_t lds = 0;
+  XTU_CHECK_ARG(n_shared >= 0 && n_shared <= 16 && n_shared <= trash);
+  const int sh_rows = act_shared ? n_shared * T : 0;
   XTU_CHECK_ARG(shape_ok(fmt, H, I) && A >= 0 && max_active >= 0 && max_active <= 65535 &&
-                trash >= 0 && dc_shape(fmt, T, A, H, I, trash, max_active, ks, nper, ppb, lds));
+                trash >= 0 &&
+                dc_shape(fmt, T, A, sh_rows, H, I, trash, max_active, ks, nper, ppb, lds));
   XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(act && w2 && (fmt == kBF16 || s2) && sorted_tok && sorted_wts && seg_start &&
                 active && n_active && out);
@@ -918,7 +1134,7 @@ hipError_t xtu_decode_down_combine(int fmt, const void* act, int T, int A, int H
   DownCombineArgs a{(const uint16_t*)act, (const uint8_t*)w2, (const uint8_t*)s2, gs2,
                     sorted_tok, sorted_wts, seg_start, active, n_active, slot_map, out,
                     out_bf16 ? 1 : 0, T, H, I, trash, max_active, A, w_estride, s_estride, ks,
-                    ppb};
+                    ppb, (const uint16_t*)act_shared, n_shared};
   switch (fmt) {
     case kMXFP4: return launch_down_combine<kMXFP4>(a, nper, lds, stream);
     case kNVFP4: return launch_down_combine<kNVFP4>(a, nper, lds, stream);

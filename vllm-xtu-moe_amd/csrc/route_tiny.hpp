@@ -1,0 +1,363 @@
+// Routing and segmentation of tiny batches (at most 64 (token, expert)
+// pairs) by one workgroup: the one-launch router (route.hip) and the decode
+// launch that routes while other workgroups run the shared experts'
+// gate/up (decode.hip).
+#pragma once
+
+#include "xtu_common.hpp"
+
+namespace xtu {
+namespace tiny {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ bool better(float sa, int ia, float sb, int ib) {
+  return (sa > sb) || (sa == sb && ia < ib);
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave (DPP row shifts, then
+// row broadcasts); lanes whose source is out of range add 0.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);   // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);   // row_bcast:31
+  return x;
+}
+
+// Arguments of the one-launch routing + segmentation (xtu_route_segment_small).
+struct SmallArgs {
+  const float* logits;
+  const float* bias;
+  int32_t* ids;
+  float* wts;
+  const int32_t* id_map;
+  int T, K, E, n_group, topk_group, renorm, NS, drop_zero, bm;
+  float scale;
+  int32_t *sorted_pair, *sorted_tok, *inv, *seg_start, *active, *n_active;
+  float* sorted_wts;
+  int32_t *tile_expert, *tile_row0, *n_tiles, *expert_tile_start;
+};
+
+// ---------------------------------------------------------------------------
+// Tiny batches (at most 64 pairs; routing for E = 64 * EPL, EPL = 4 or 8): one
+// wave routes one token with no workgroup barrier.  Lane l holds experts
+// [l*EPL, (l+1)*EPL).  The K choices are taken in K rounds of a wave-wide
+// maximum of order-preserving score keys; equal scores go to the lowest
+// lane, whose local choice is its lowest index, so the order is (score desc,
+// index asc) as in route_token.  Group scores (top two over a group's lanes)
+// and group ranks follow route_token's definitions; the weights use its fp32
+// sequences.  The segmentation of the <= 64 pairs works on the pair buckets
+// staged in LDS with fixed-length loops.
+// ---------------------------------------------------------------------------
+constexpr int kTinyMaxA = 64;
+
+// Larger score -> larger key; -0 and +0 share a key.
+__device__ __forceinline__ uint32_t score_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) == 0u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Maximum over the wave (DPP row shifts and broadcasts; lane 63 ends with
+// the maximum of all lanes), returned to every lane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xA, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xC, 0xF, false));
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// Order this wave's LDS writes before its later LDS reads by other lanes:
+// a wave's LDS instructions execute in issue order, so only the compiler
+// must not move them (no wait for outstanding global stores).
+__device__ __forceinline__ void lds_wave_order() {
+  __builtin_amdgcn_wave_barrier();
+  __asm__ __volatile__("" ::: "memory");
+}
+
+// Top two of (v1 >= v2) pairs over aligned groups of lpg lanes (1..64).
+__device__ __forceinline__ void top2_merge(float& v1, float& v2, float b1, float b2) {
+  const float n1 = fmaxf(v1, b1), n2 = fmaxf(fminf(v1, b1), fmaxf(v2, b2));
+  v1 = n1;
+  v2 = n2;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ void group_top2(float& v1, float& v2, int lpg) {
+  // partner lanes within a quad (xor 1, xor 2), then the mirrored quad of the
+  // 8-lane half row, then the mirrored half of the 16-lane row, then across rows
+  if (lpg >= 2) top2_merge(v1, v2, dpp_f<0xB1>(v1), dpp_f<0xB1>(v2));     // quad_perm [1,0,3,2]
+  if (lpg >= 4) top2_merge(v1, v2, dpp_f<0x4E>(v1), dpp_f<0x4E>(v2));     // quad_perm [2,3,0,1]
+  if (lpg >= 8) top2_merge(v1, v2, dpp_f<0x141>(v1), dpp_f<0x141>(v2));   // row_half_mirror
+  if (lpg >= 16) top2_merge(v1, v2, dpp_f<0x140>(v1), dpp_f<0x140>(v2));  // row_mirror
+  for (int o = 16; o < lpg; o <<= 1) top2_merge(v1, v2, __shfl_xor(v1, o, 64), __shfl_xor(v2, o, 64));
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+template <int MODE, int EPL>
+__device__ void route_token_wave(const float* __restrict__ l, const float* __restrict__ bias,
+                                 int K, int n_group, int topk_group, float scale, int renorm,
+                                 int lane, int32_t* ids_out, float* wts_out, int* ids_lds,
+                                 float* wts_lds) {
+#pragma clang fp contract(off)
+  constexpr int E = kWave * EPL;
+  const int e0 = lane * EPL;
+  float x[EPL], bi[EPL], ws[EPL], sc[EPL];
+  uint32_t key[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; j += 4) {
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(l + e0 + j);
+    f32x4_t bv = {0.f, 0.f, 0.f, 0.f};
+    if (MODE == 1 && bias) bv = *reinterpret_cast<const f32x4_t*>(bias + e0 + j);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x[j + q] = v[q];
+      bi[j + q] = bv[q];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    if (MODE == 0) {
+      ws[j] = x[j];
+      sc[j] = x[j];
+    } else {
+      ws[j] = xtu_sigmoid(x[j]);
+      sc[j] = ws[j] + bi[j];
+    }
+    key[j] = score_key(sc[j]);
+  }
+  if (MODE == 1) {
+    // group score: best + second best over the group's lanes; keep the
+    // topk_group best groups (rank under (score desc, group asc))
+    const float NEG = -__builtin_inff();
+    const int gsz = E / n_group, lpg = gsz / EPL;
+    float v1 = NEG, v2 = NEG;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      if (sc[j] > v1) {
+        v2 = v1;
+        v1 = sc[j];
+      } else if (sc[j] > v2) {
+        v2 = sc[j];
+      }
+    }
+    group_top2(v1, v2, lpg);
+    const float gs = gsz >= 2 ? v1 + v2 : v1;
+    const int my_g = lane / lpg;
+    int r = 0;
+    for (int j = 0; j < n_group; ++j) r += better(readlane_f(gs, j * lpg), j, gs, my_g) ? 1 : 0;
+    if (r >= topk_group) {
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) key[j] = 0u;
+    }
+  }
+  // local best (lowest index among equal keys)
+  uint32_t bkey = 0u;
+  int bj = 0;
+  float bws = 0.f;
+  auto local_best = [&]() {
+    bkey = 0u;
+    bj = 0;
+    bws = 0.f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      if (key[j] > bkey) {
+        bkey = key[j];
+        bj = j;
+        bws = ws[j];
+      }
+    }
+  };
+  local_best();
+  int my_e = 0;
+  float my_ws = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const uint32_t gmax = wave_max_u32(bkey);
+    const unsigned long long m = __ballot(bkey == gmax);
+    const int wl = __builtin_ctzll(m);
+    const int ek = wl * EPL + __builtin_amdgcn_readlane(bj, wl);
+    const float wk = readlane_f(bws, wl);
+    if (lane == k) {
+      my_e = ek;
+      my_ws = wk;
+    }
+    if (lane == wl) {
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (j == bj) key[j] = 0u;
+      local_best();
+    }
+  }
+  float w = 0.f;
+  if (MODE == 0) {
+    const float lmax = readlane_f(my_ws, 0);
+    const float ev = lane < K ? xtu_expf(my_ws - lmax) : 0.f;
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) sum = sum + readlane_f(ev, k);
+    w = __fdiv_rn(ev, sum);
+  } else {
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) sum = sum + readlane_f(my_ws, k);
+    w = renorm ? __fdiv_rn(my_ws, sum) * scale : my_ws * scale;
+  }
+  if (lane < K) {
+    ids_out[lane] = my_e;
+    wts_out[lane] = w;
+    ids_lds[lane] = my_e;
+    wts_lds[lane] = w;
+  }
+}
+
+struct TinySmem {
+  int ids[kTinyMaxA];
+  float w[kTinyMaxA];
+  int bk[kTinyMaxA];          // sort key of pair p: bucket * 64 + p (INT_MAX past A)
+  int sb[kTinyMaxA];          // bucket at sorted position j (INT_MAX past A)
+  int act_b[kTinyMaxA + 4];   // active buckets, ascending (INT_MAX past n_act)
+  int act_r[kTinyMaxA + 1];   // first row of active bucket i; [n_act] = trash start
+  int act_t[kTinyMaxA + 1];   // first tile of active bucket i; [n_act] = all tiles
+  int n_act;
+};
+
+// MODE 0/1: wave t routes token t (E = 64 * EPL), then the segmentation;
+// MODE 2: ids/wts given.  One workgroup with blockDim.x >= 64 * T; the last
+// pass writes one bucket start per thread (any block size is correct).
+template <int MODE, int EPL>
+__device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
+  const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
+  const int T = a.T, K = a.K, E = a.E, NS = a.NS;
+  const int TK = T * K, A = TK + T * NS, NB = E + NS + 1, trash = E + NS;
+  constexpr int BIG = 0x7fffffff;
+  if (MODE < 2) {
+    if (wv < T)
+      route_token_wave<MODE, EPL>(a.logits + (long)wv * E, a.bias, K, a.n_group, a.topk_group,
+                                  a.scale, a.renorm, lane, a.ids + (long)wv * K,
+                                  a.wts + (long)wv * K, g.ids + wv * K, g.w + wv * K);
+  } else {
+    if (tid < TK) {
+      g.ids[tid] = a.ids[tid];
+      g.w[tid] = a.wts[tid];
+    }
+  }
+  __syncthreads();
+  if (wv == 0) {
+    // bucket of pair `lane`
+    int b = BIG;
+    float w = 1.0f;
+    if (lane < TK) {
+      int e = g.ids[lane];
+      w = g.w[lane];
+      if (a.id_map && e >= 0 && e < E) e = a.id_map[e];
+      b = (e < 0 || e >= E) ? trash : e;
+      if (a.drop_zero && w == 0.0f) b = trash;
+    } else if (lane < A) {
+      b = E + (lane - TK) % NS;
+    }
+    // stable position: rank of the unique key (bucket, pair) among the pairs
+    const int key = lane < A ? b * kTinyMaxA + lane : BIG;
+    g.bk[lane] = key;
+    lds_wave_order();
+    int pos = 0;
+#pragma unroll
+    for (int q = 0; q < kTinyMaxA; q += 4) {
+      const i32x4_t v = *reinterpret_cast<const i32x4_t*>(g.bk + q);
+      pos += (v[0] < key) + (v[1] < key) + (v[2] < key) + (v[3] < key);
+    }
+    if (lane < A) {
+      g.sb[pos] = b;
+      a.sorted_pair[pos] = lane;
+      a.inv[lane] = pos;
+      a.sorted_tok[pos] = lane < TK ? lane / K : (lane - TK) / NS;
+      a.sorted_wts[pos] = w;
+    } else {
+      g.sb[lane] = BIG;
+    }
+    lds_wave_order();
+    // sorted position `lane`: the first of its bucket opens an active entry;
+    // the bucket's size runs to the next bucket's first row (or A)
+    const int sbj = g.sb[lane];
+    const int prev = lane > 0 ? g.sb[lane - 1] : -1;
+    const bool start = lane < A && sbj != prev;
+    const unsigned long long bnd = __ballot(start);
+    const unsigned long long above = lane == 63 ? 0ull : bnd & (~0ull << (lane + 1));
+    const int cnt = (above ? __builtin_ctzll(above) : A) - lane;
+    const bool first = start && sbj != trash;
+    const unsigned long long fm = __ballot(first);
+    const int ai = __builtin_amdgcn_mbcnt_hi((uint32_t)(fm >> 32),
+                                             __builtin_amdgcn_mbcnt_lo((uint32_t)fm, 0u));
+    const int na = __popcll(fm);
+    const int nt = first ? (cnt + a.bm - 1) / a.bm : 0;
+    const int incl = wave_incl_scan(nt);
+    const int t0 = incl - nt;
+    if (first) {
+      g.act_b[ai] = sbj;
+      g.act_r[ai] = lane;
+      g.act_t[ai] = t0;
+      a.active[ai] = sbj;
+      for (int j = 0; j < nt; ++j) {
+        a.tile_expert[t0 + j] = sbj;
+        a.tile_row0[t0 + j] = lane + j * a.bm;
+      }
+    }
+    // rows before the trash bucket (= pairs in active buckets)
+    const unsigned long long tm = __ballot(lane < A && sbj != trash);
+    if (lane == 0) {
+      const int tot = __builtin_amdgcn_readlane(incl, 63);
+      g.n_act = na;
+      g.act_r[na] = __popcll(tm);
+      g.act_t[na] = tot;
+      a.n_active[0] = na;
+      a.n_tiles[0] = tot;
+    }
+    if (lane >= na && lane < kTinyMaxA + 4) g.act_b[lane] = BIG;
+    if (lane < 4) g.act_b[kTinyMaxA + lane] = BIG;
+  }
+  __syncthreads();
+  // per-bucket starts: i = active buckets below e; rows and tiles before e
+  for (int e = tid; e <= NB; e += blockDim.x) {
+    int i = 0;
+#pragma unroll
+    for (int q = 0; q < kTinyMaxA; q += 4) {
+      const i32x4_t v = *reinterpret_cast<const i32x4_t*>(g.act_b + q);
+      i += (v[0] < e) + (v[1] < e) + (v[2] < e) + (v[3] < e);
+    }
+    a.seg_start[e] = e == NB ? A : g.act_r[i];
+    a.expert_tile_start[e] = g.act_t[i];
+  }
+}
+
+// The tiny path's envelope: at most 64 pairs and 16 tokens; routing for
+// E = 256 or 512, whole lanes per group, renormalised softmax.
+__host__ inline int tiny_epl(const SmallArgs& a, int mode) {
+  const long A = (long)a.T * a.K + (long)a.T * a.NS;
+  if (A > kTinyMaxA || a.T > 16) return 0;
+  if (mode == 2) return 1;
+  const int epl = a.E / kWave;
+  if (a.T < 1 || a.E % kWave != 0 || (epl != 4 && epl != 8)) return 0;
+  // 16-byte loads of the logit and bias rows
+  if (reinterpret_cast<uintptr_t>(a.logits) % 16 != 0 ||
+      (a.bias && reinterpret_cast<uintptr_t>(a.bias) % 16 != 0))
+    return 0;
+  if (mode == 0) return a.renorm != 0 ? epl : 0;
+  const int gsz = a.E / a.n_group;
+  if (gsz % epl != 0) return 0;
+  const int lpg = gsz / epl;
+  return (lpg >= 1 && lpg <= kWave && (lpg & (lpg - 1)) == 0) ? epl : 0;
+}
+
+
+}  // namespace tiny
+}  // namespace xtu

@@ -33,9 +33,16 @@ SIGNATURES = {
                                 _vp, _i, _vp, _f, _f, _f, _vp]),
     "xtu_decode_down": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _i,
                              _vp, _vp]),
-    "xtu_decode_down_combine_ok": (_i, [_i, _i, _i, _i, _i, _i, _i]),
-    "xtu_decode_down_combine": (_i, [_i, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp,
-                                     _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp]),
+    "xtu_decode_down_combine_ok": (_i, [_i, _i, _i, _i, _i, _i, _i, _i]),
+    "xtu_decode_down_combine": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _l, _l,
+                                     _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp]),
+    "xtu_decode_route_shared_ok": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i]),
+    "xtu_decode_route_shared": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp,
+                                     _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp,
+                                     _vp, _f, _f, _f, _vp]),
+    "xtu_decode_gate_up_routed": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp,
+                                       _vp, _vp, _vp, _i, _i, _vp, _f, _f, _f, _vp]),
     "xtu_gemm_tile_m": (_i, [_i]),
     "xtu_gemm_gate_up": (_i, [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
                               _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
@@ -67,7 +74,7 @@ SIGNATURES = {
 _NOT_STATUS = {"xtu_version", "xtu_error_string", "xtu_segment_workspace_bytes",
                "xtu_route_segment_small_max_pairs",
                "xtu_segment_max_tiles", "xtu_gemm_tile_m", "xtu_gemm8_tile_m",
-               "xtu_decode_down_combine_ok",
+               "xtu_decode_down_combine_ok", "xtu_decode_route_shared_ok",
                "xtu_i8_weight_bytes"}
 
 _LIB = None

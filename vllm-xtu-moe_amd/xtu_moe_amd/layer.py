@@ -254,15 +254,16 @@ FUSED_DOWN_MAX_EXPERTS = 24
 
 
 def decode_fused_down_ok(fmt: int, T: int, A: int, H: int, I: int, max_active: int,
-                         trash: int) -> bool:
+                         trash: int, shared_rows: int = 0) -> bool:
     """Whether the down projection with the weighted combine fused can run
-    this batch (its act rows fit the kernel's LDS stage)."""
+    this batch (its act rows, plus shared_rows staged separately, fit the
+    kernel's LDS stage)."""
     return bool(_lib.call("xtu_decode_down_combine_ok", int(fmt), int(T), int(A), int(H), int(I),
-                          int(trash), int(max_active)))
+                          int(trash), int(max_active), int(shared_rows)))
 
 
 def decode_fused_down_use(fmt: int, T: int, A: int, H: int, I: int, max_active: int,
-                          trash: int) -> bool:
+                          trash: int, shared_rows: int = 0) -> bool:
     """Whether the decode path takes the fused down + combine.  Each of its
     waves walks every active expert, so it pays where few experts meet wide
     panels; measured (MI355X): faster for DeepSeek-V3 MXFP4 at T = 1, 2 (9 / 17
@@ -277,7 +278,32 @@ def decode_fused_down_use(fmt: int, T: int, A: int, H: int, I: int, max_active: 
             return False
         if int(fmt) == FMT_NVFP4 and I < 1024:
             return False
-    return decode_fused_down_ok(fmt, T, A, H, I, max_active, trash)
+    return decode_fused_down_ok(fmt, T, A, H, I, max_active, trash, shared_rows)
+
+
+SHARED_SPLIT_ENV = "XTU_DECODE_SHARED_SPLIT"
+
+
+def _route_shared_ok(fmt, mode, T, E, K, router, H, I, NS) -> bool:
+    """Whether the routing launch can also run the shared experts' gate/up
+    (tiny batch, one wave per token, fp32 logits / bias rows 16-byte
+    aligned); XTU_DECODE_SHARED_SPLIT=0 keeps them with the routed ones."""
+    if os.environ.get(SHARED_SPLIT_ENV, "1") == "0":
+        return False
+    n_group = 1
+    if router is not None:
+        lg, bias = router.get("logits"), router.get("bias")
+        for t in (lg, bias):
+            if t is not None and not (t.is_cuda and t.dtype == torch.float32
+                                      and t.is_contiguous() and t.data_ptr() % 16 == 0):
+                return False
+        if lg is None or tuple(lg.shape) != (T, E):
+            return False
+        if mode == 0 and not router.get("renormalize", True):
+            return False
+        n_group = int(router.get("n_group", 1))
+    return bool(_lib.call("xtu_decode_route_shared_ok", int(fmt), int(mode), int(T), int(E),
+                          int(K), n_group, int(NS), int(H), int(I)))
 
 
 def _fp8pair_bufs(tag, M, K, dev):
@@ -333,8 +359,31 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         raise ValueError(f"decode path handles at most {DECODE_MAX_TOKENS} tokens")
     bm = gemm_tile_m(fmt, int8)
     seg = segmentation(T, K, E, NS, bm, dev)
-    if router is not None:
-        mode = 1 if router.get("scoring", "softmax") == "sigmoid" else 0
+    odt = out_dtype if out is None else out.dtype
+    max_active = min(E, T * K) + NS
+    # decode with shared experts: their gate/up runs in the routing launch
+    # (they need no routing), the routed gate/up leaves them out and the fused
+    # down takes their rows from act_sh
+    rmode = 2 if router is None else (1 if router.get("scoring", "softmax") == "sigmoid" else 0)
+    split = (path == "decode" and T > 0 and NS > 0 and seg.small
+             and odt in (torch.bfloat16, torch.float32)
+             and decode_fused_down_use(fmt, T, seg.A, H, I, max_active, E + NS, NS * T)
+             and _route_shared_ok(fmt, rmode, T, E, K, router, H, I, NS))
+    lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
+    if split:
+        r = router or {}
+        act_sh = _buf("act_sh", (NS * T, I), torch.bfloat16, dev)
+        _lib.call("xtu_decode_route_shared", rmode, _p(r.get("logits")), _p(r.get("bias")),
+                  _p(ids), _p(wts), T, E, K, int(r.get("n_group", 1)),
+                  int(r.get("topk_group", 1)), float(r.get("routed_scaling_factor", 1.0)),
+                  int(r.get("renormalize", True)), _p(id_map), NS, int(drop_zero), seg.bm,
+                  _p(seg.sorted_pair), _p(seg.sorted_tok), _p(seg.sorted_wts), _p(seg.inv),
+                  _p(seg.seg_start), _p(seg.active), _p(seg.n_active), _p(seg.tile_expert),
+                  _p(seg.tile_row0), _p(seg.n_tiles), _p(seg.expert_tile_start), fmt, _p(x), H,
+                  I, _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0, _p(slot_map), _p(act_sh), lim, al,
+                  be, st)
+    elif router is not None:
+        mode = rmode
         if seg.small and T > 0:
             seg.run_small(mode, ids, wts, logits=router["logits"], bias=router.get("bias"),
                           n_group=router.get("n_group", 1), topk_group=router.get("topk_group", 1),
@@ -353,22 +402,25 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     else:
         seg.run(ids, wts, id_map, drop_zero, st)
     A = seg.A
-    odt = out_dtype if out is None else out.dtype
     if out is None:
         out = torch.empty((T, H), dtype=odt, device=dev)
     if T == 0:
         return (out, seg) if return_seg else out
     if path == "decode":
         act = _buf("act", (max(A, 1), I), torch.bfloat16, dev)
-        lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
-        max_active = min(E, T * K) + NS
-        _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13),
-                  0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
-                  _p(seg.n_active), max_active, _p(act), lim, al, be, st)
-        if odt in (torch.bfloat16, torch.float32) and decode_fused_down_use(fmt, T, A, H, I,
-                                                                           max_active, E + NS):
+        if split:
+            _lib.call("xtu_decode_gate_up_routed", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13),
+                      _p(W.gs13), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start),
+                      _p(seg.active), _p(seg.n_active), max_active, NS, _p(act), lim, al, be, st)
+        else:
+            _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13),
+                      _p(W.gs13), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start),
+                      _p(seg.active), _p(seg.n_active), max_active, _p(act), lim, al, be, st)
+        if split or (odt in (torch.bfloat16, torch.float32)
+                     and decode_fused_down_use(fmt, T, A, H, I, max_active, E + NS)):
             # down projection and weighted combine in one pass, out written whole
-            _lib.call("xtu_decode_down_combine", fmt, _p(act), T, A, H, I, _p(W.w2), _p(W.s2),
+            _lib.call("xtu_decode_down_combine", fmt, _p(act),
+                      _p(act_sh) if split else 0, NS, T, A, H, I, _p(W.w2), _p(W.s2),
                       _p(W.gs2), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.sorted_wts),
                       _p(seg.seg_start), E + NS, _p(seg.active), _p(seg.n_active), max_active,
                       _p(out), int(out.dtype == torch.bfloat16), st)
