@@ -352,6 +352,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 #ifndef XTU_GEMM_WPS
 #define XTU_GEMM_WPS 2
 #endif
+constexpr long kGemmSmallItems = 512;   // below this, half-width work items
 
 template <int FMT, int PW, int PD, int WPS>
 hipError_t launch_shape(bool gu, const GemmArgs& a, int max_tiles, hipStream_t stream) {
@@ -377,6 +378,12 @@ hipError_t launch_gemm(bool gu, GemmArgs a, int max_tiles, hipStream_t stream) {
   }
   // NVFP4's scale multiply needs more than half of the register file
   constexpr int kWps = FMT == kNVFP4 ? 1 : 2;
+  // few work items (small batches over few experts, e.g. 128 tokens on 8
+  // experts: 32 down items for 256 CUs): half-width items, twice as many
+  // weight streams in flight
+  const long items4 = (long)max_tiles * (gu ? a.I / 128 : a.H / 256);
+  if (items4 < kGemmSmallItems && (gu ? a.I % 64 : a.H % 128) == 0)
+    return launch_shape<FMT, 2, 1, kWps>(gu, a, max_tiles, stream);
   return launch_shape<FMT, 4, 1, kWps>(gu, a, max_tiles, stream);
 }
 
