@@ -55,7 +55,7 @@ WORKLOADS = {
     "qwen3-next-nvfp4": dict(fmt="nvfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
                              Ts=[1, 4, 8192], limit=7.0, int8=False, graph=True),
     "mixtral-tiny-bf16": dict(fmt="bf16", E=8, NS=0, H=1024, I=2048, K=2, router="softmax",
-                              Ts=[128], limit=0.0, int8=False, graph=False),
+                              Ts=[128], limit=0.0, int8=False, graph=True, graph_max_T=128),
     "ds-v3-fp8-streamed": dict(fmt="fp8", E=256, NS=1, H=7168, I=2048, K=8, router="grouped",
                                Ts=[8192], limit=0.0, int8=False, graph=False, resident=64,
                                tile_e=16, nslots=4, zipf=1.1),
@@ -165,7 +165,7 @@ def main():
         load(0)
         step()
         torch.cuda.synchronize()
-        use_graph = cfg["graph"] and T <= 16
+        use_graph = cfg["graph"] and T <= cfg.get("graph_max_T", 16)
         graph = None
         if use_graph:
             side = torch.cuda.Stream()

@@ -57,3 +57,58 @@ def test_decode_graph_replays_match_eager(fmt):
         np.testing.assert_array_equal(out_st.view(torch.int16).cpu().numpy(),
                                       eager.view(torch.int16).cpu().numpy())
         del junk
+
+
+@pytest.mark.parametrize("case", ["decode-split", "gemm-128"])
+def test_routed_layer_graph_replays_match_eager(case):
+    """moe_forward routing from logits inside the graph: the decode layer whose
+    routing launch also runs the shared expert (T = 1), and a 128-token batch
+    on the multi-workgroup router and the grouped GEMMs."""
+    dev = torch.device("cuda")
+    if case == "decode-split":
+        fmt, H, I, E, NS, K, T = F.FMT_MXFP4, 1024, 256, 256, 1, 8, 1
+        rt = dict(scoring="sigmoid", n_group=8, topk_group=4, routed_scaling_factor=2.5)
+    else:
+        fmt, H, I, E, NS, K, T = F.FMT_BF16, 1024, 512, 8, 0, 2, 128
+        rt = dict(scoring="softmax", renormalize=True)
+    W = synth_layer(fmt, E, NS, H, I, seed=5, device=dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    xs = [torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    lgs = [torch.randn((T, E), generator=g, device=dev) for _ in range(4)]
+    x_st = torch.empty_like(xs[0])
+    lg_st = torch.empty_like(lgs[0])
+    ids_st = torch.empty((T, K), dtype=torch.int32, device=dev)
+    wts_st = torch.empty((T, K), dtype=torch.float32, device=dev)
+    out_st = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        moe_forward(x_st, ids_st, wts_st, W, out=out_st, router=dict(rt, logits=lg_st))
+
+    x_st.copy_(xs[0])
+    lg_st.copy_(lgs[0])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for r in range(1, 4):
+        x_st.copy_(xs[r])
+        lg_st.copy_(lgs[r])
+        step()
+        torch.cuda.synchronize()
+        eager = out_st.clone()
+        eager_ids = ids_st.clone()
+        junk = torch.randn(1 << 20, device=dev).sum()   # eager work between replays
+        out_st.zero_()
+        ids_st.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ids_st, eager_ids)
+        np.testing.assert_array_equal(out_st.view(torch.int16).cpu().numpy(),
+                                      eager.view(torch.int16).cpu().numpy())
+        del junk
