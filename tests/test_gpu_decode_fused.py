@@ -126,10 +126,18 @@ def test_fused_ds_v3_mxfp4_t2(monkeypatch):
     d, W = _layer(F.FMT_MXFP4, U, 1, H, I, seed=62)
     assert L.decode_fused_down_ok(F.FMT_MXFP4, T, T * (K + 1), H, I, min(E, T * K) + 1, U + 1)
     x = torch.randn((T, H), generator=torch.Generator().manual_seed(63)).to(torch.bfloat16)
+    # the shared expert beside the router: its act rows staged from act_sh,
+    # only the 16 routed sorted rows from act (the stage then fits)
+    assert L.decode_fused_down_ok(F.FMT_MXFP4, T, T * (K + 1), H, I, min(E, T * K) + 1, U + 1,
+                                  T)
+    assert L._route_shared_ok(F.FMT_MXFP4, 2, T, U, K, None, H, I, 1)
     out = _run(x, cids, wts, W, monkeypatch, True, out_dtype=torch.float32)
     ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d), bf16_tensor_to_bits(x), cids,
                        wts, U, 1, H, I)
     check_close(out.cpu().numpy(), ref, bf16_out=False, what="ds-v3 fused T=2")
+    monkeypatch.setenv(L.SHARED_SPLIT_ENV, "0")
+    out0 = _run(x, cids, wts, W, monkeypatch, True, out_dtype=torch.float32)
+    assert torch.equal(out, out0), "shared expert beside the router vs with the routed ones"
 
 
 

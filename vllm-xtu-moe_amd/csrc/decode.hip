@@ -556,7 +556,7 @@ struct DownCombineArgs {
   int T, H, I;
   int trash;                  // bucket after the last expert: seg_start[trash] = live rows
   int max_active;             // table capacity (>= n_active)
-  int row_cap;                // rows the LDS stage holds (>= seg_start[trash])
+  int row_cap;                // sorted rows staged (>= the rows of every staged bucket)
   long w_estride, s_estride;
   int ks, ppb;
   const uint16_t* act_sh;     // shared experts' act rows [n_shared][T][I] (or null)
@@ -754,13 +754,20 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
   for (int j = tid; j < nact; j += bd) {
     const int e = l_act[j];
     eslot[j] = a.slot_map ? a.slot_map[e] : e;
-    // a shared expert's rows come from act_sh when given: token t at row_cap + s*T + t
-    const int shb = (a.act_sh && e >= e_sh) ? a.row_cap + (e - e_sh) * a.T : -1;
+    if (a.act_sh && e >= e_sh) {
+      // a shared expert's rows come from act_sh: token t at row_cap + s*T + t,
+      // weight 1 (its bucket holds every token once, weight 1, never dropped)
+      for (int t = 0; t < a.T; ++t) {
+        rowof[j * kDcTok + t] = a.row_cap + (e - e_sh) * a.T + t;
+        wof[j * kDcTok + t] = 1.0f;
+      }
+      continue;
+    }
     const int r1 = min(l_seg[e + 1], a.row_cap);
     for (int r = max(l_seg[e], 0); r < r1; ++r) {
       const int t = rtok[r];
       if (t >= 0 && t < kDcTok) {
-        rowof[j * kDcTok + t] = shb >= 0 ? shb + min(t, a.T - 1) : r;
+        rowof[j * kDcTok + t] = r;
         wof[j * kDcTok + t] += rw[r];
       }
     }
@@ -807,6 +814,13 @@ __global__ __launch_bounds__(512) void decode_down_combine_kernel(DownCombineArg
       else reinterpret_cast<float*>(a.out)[o] = v;
     }
   }
+}
+
+// Sorted act rows the fused down stages: all A, or, when the shared experts'
+// rows come from act_sh, the A - shared_rows routed ones (the segmentation
+// puts the T * n_shared shared pairs after every routed pair).
+int dc_sorted_rows(int A, int shared_rows) {
+  return shared_rows > 0 ? (A - shared_rows > 1 ? A - shared_rows : 1) : A;
 }
 
 // Launch shape of the fused down: (KS, NPER) with KS * NPER = I / 128 and
@@ -1109,7 +1123,8 @@ int xtu_decode_down_combine_ok(int fmt, int T, int A, int H, int I, int trash, i
   size_t lds;
   return shape_ok(fmt, H, I) && A >= 0 && max_active >= 0 && max_active <= 65535 &&
          shared_rows >= 0 && shared_rows <= kDcTok * 16 &&
-         dc_shape(fmt, T, A, shared_rows, H, I, trash, max_active, ks, nper, ppb, lds);
+         dc_shape(fmt, T, dc_sorted_rows(A, shared_rows), shared_rows, H, I, trash, max_active,
+                  ks, nper, ppb, lds);
 }
 
 hipError_t xtu_decode_down_combine(int fmt, const void* act, const void* act_shared, int n_shared,
@@ -1124,17 +1139,18 @@ hipError_t xtu_decode_down_combine(int fmt, const void* act, const void* act_sha
   size_t lds = 0;
   XTU_CHECK_ARG(n_shared >= 0 && n_shared <= 16 && n_shared <= trash);
   const int sh_rows = act_shared ? n_shared * T : 0;
+  const int rows = dc_sorted_rows(A, sh_rows);
   XTU_CHECK_ARG(shape_ok(fmt, H, I) && A >= 0 && max_active >= 0 && max_active <= 65535 &&
                 trash >= 0 &&
-                dc_shape(fmt, T, A, sh_rows, H, I, trash, max_active, ks, nper, ppb, lds));
+                dc_shape(fmt, T, rows, sh_rows, H, I, trash, max_active, ks, nper, ppb, lds));
   XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(act && w2 && (fmt == kBF16 || s2) && sorted_tok && sorted_wts && seg_start &&
                 active && n_active && out);
   (void)hipGetLastError();
   DownCombineArgs a{(const uint16_t*)act, (const uint8_t*)w2, (const uint8_t*)s2, gs2,
                     sorted_tok, sorted_wts, seg_start, active, n_active, slot_map, out,
-                    out_bf16 ? 1 : 0, T, H, I, trash, max_active, A, w_estride, s_estride, ks,
-                    ppb, (const uint16_t*)act_shared, n_shared};
+                    out_bf16 ? 1 : 0, T, H, I, trash, max_active, rows, w_estride, s_estride,
+                    ks, ppb, (const uint16_t*)act_shared, n_shared};
   switch (fmt) {
     case kMXFP4: return launch_down_combine<kMXFP4>(a, nper, lds, stream);
     case kNVFP4: return launch_down_combine<kNVFP4>(a, nper, lds, stream);
