@@ -70,7 +70,7 @@ def _gpu_segment(ids, wts, E, NS, drop_zero, id_map=None, bm=128):
 
 @pytest.mark.parametrize("T,K,E,NS", [(1, 8, 256, 1), (4, 8, 256, 1), (128, 2, 8, 0),
                                       (8192, 8, 256, 1), (8192, 10, 512, 1), (5000, 3, 40, 2),
-                                      (0, 4, 16, 1)])
+                                      (0, 4, 16, 1), (3000, 6, 1024, 3), (4096, 4, 5, 0)])
 @pytest.mark.parametrize("drop_zero", [False, True])
 def test_segmentation_bit_exact(T, K, E, NS, drop_zero):
     ids, wts = random_routing(T, K, E, seed=T + K, invalid_frac=0.05, zero_frac=0.05)

@@ -409,27 +409,24 @@ __global__ __launch_bounds__(kSegThreads) void seg_scatter_kernel(
   __syncthreads();
   const int base = blockIdx.x * kSegChunk;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int nbits = 32 - __builtin_clz(a.NB - 1);   // bits of the largest bucket id (NB >= 2)
   for (int r = 0; r < kSegRounds; ++r) {
     const int p = base + r * kSegThreads + threadIdx.x;
     const bool valid = p < a.A;
     float w = 0.f;
     int tok = 0;
     const int bk = valid ? bucket_of(a, p, &w, &tok) : -1;
-    // lanes of this wave that share my bucket
-    uint64_t remaining = __ballot(valid);
-    int rank = 0, wcount = 0;
-    bool leader = false;
-    while (remaining) {
-      const int ld = __builtin_ctzll(remaining);
-      const int lb = __shfl(bk, ld, kWave);
-      const uint64_t m = __ballot(valid && bk == lb);
-      if (valid && bk == lb) {
-        rank = __builtin_popcountll(m & lt_mask);
-        wcount = __builtin_popcountll(m);
-        leader = (lane == ld);
-      }
-      remaining &= ~m;
+    // lanes of this wave that share my bucket: the valid lanes that agree
+    // with mine on every bit of the bucket id (one ballot per bit)
+    uint64_t m = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (bk >> bit) & 1;
+      const uint64_t b1 = __ballot(valid && on);
+      m &= on ? b1 : ~b1;
     }
+    const int rank = __builtin_popcountll(m & lt_mask);
+    const int wcount = __builtin_popcountll(m);
+    const bool leader = valid && lane == __builtin_ctzll(m);
     if (leader) wcnt[wv * a.NB + bk] = wcount;
     __syncthreads();
     if (valid) {
