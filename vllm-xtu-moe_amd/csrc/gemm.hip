@@ -376,15 +376,21 @@ hipError_t launch_gemm(bool gu, GemmArgs a, int max_tiles, hipStream_t stream) {
     if ((gu ? a.I % (32 * PW) : a.H % (64 * PW)) == 0)
       return launch_shape<FMT, PW, XTU_GEMM_PD, XTU_GEMM_WPS>(gu, a, max_tiles, stream);
   }
-  // NVFP4's scale multiply needs more than half of the register file
-  constexpr int kWps = FMT == kNVFP4 ? 1 : 2;
-  // few work items (small batches over few experts, e.g. 128 tokens on 8
-  // experts: 32 down items for 256 CUs): half-width items, twice as many
-  // weight streams in flight
-  const long items4 = (long)max_tiles * (gu ? a.I / 128 : a.H / 256);
-  if (items4 < kGemmSmallItems && (gu ? a.I % 64 : a.H % 128) == 0)
-    return launch_shape<FMT, 2, 1, kWps>(gu, a, max_tiles, stream);
-  return launch_shape<FMT, 4, 1, kWps>(gu, a, max_tiles, stream);
+  // NVFP4's exact scale multiply keeps fp32 products live: four panels per
+  // wave need more than half of the register file (one wave per SIMD), two
+  // fit at two waves per SIMD -- measured 32% faster (Qwen3-Next T = 8192
+  // gate/up 999 -> 678 us).  H % 128 == 0 and I % 64 == 0 always hold here.
+  if constexpr (FMT == kNVFP4) {
+    return launch_shape<FMT, 2, 1, 2>(gu, a, max_tiles, stream);
+  } else {
+    // few work items (small batches over few experts, e.g. 128 tokens on 8
+    // experts: 32 down items for 256 CUs): half-width items, twice as many
+    // weight streams in flight
+    const long items4 = (long)max_tiles * (gu ? a.I / 128 : a.H / 256);
+    if (items4 < kGemmSmallItems && (gu ? a.I % 64 : a.H % 128) == 0)
+      return launch_shape<FMT, 2, 1, 2>(gu, a, max_tiles, stream);
+    return launch_shape<FMT, 4, 1, 2>(gu, a, max_tiles, stream);
+  }
 }
 
 }  // namespace

@@ -161,8 +161,10 @@ struct I8GemmArgs {
   float limit, alpha, beta;
 };
 
+// Two waves per SIMD (at most 256 registers; 272 unbounded, one wave per
+// SIMD): measured 32% faster on Qwen3-Next T = 8192 (gate/up 851 -> 577 us).
 template <int BM, bool GU>
-__global__ __launch_bounds__(256) void i8_gemm_kernel(I8GemmArgs a) {
+__global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8GemmArgs a) {
   constexpr int MT = BM / 32;
   constexpr int A_CH = BM * kBK / 16 / 256;   // 16-byte A chunks per thread
   constexpr int CPP = (kBK / 16) * 16;        // B chunks per panel per K step
