@@ -172,13 +172,22 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8GemmArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t As[BM * kLDB];
   __shared__ __attribute__((aligned(16))) int8_t Bs[kBN * kLDB];
 
-  const int tile = a.tile_lo[0] + blockIdx.x;
-  if (tile >= a.tile_hi[0]) return;
+  // work item (M tile, N block), N block fastest, dealt to the eight XCDs in
+  // contiguous ranges (workgroup i runs on XCD i % 8): the workgroups
+  // resident on one XCD share a tile's rows and an expert's weights in L2
+  const int nbn = GU ? a.I / 128 : a.H / 256;
+  const int lo = a.tile_lo[0];
+  const int total = (a.tile_hi[0] - lo) * nbn;
+  const int per = (total + 7) / 8;
+  const int idx = blockIdx.x / 8;
+  if (idx >= per) return;
+  const int item = (blockIdx.x % 8) * per + idx;
+  if (item >= total) return;
+  const int tile = lo + item / nbn, nb = item % nbn;
   const int e = a.tile_expert[tile];
   const int ws = a.slot_map ? a.slot_map[e] : e;
   const int row0 = a.tile_row0[tile];
   const int rows = min(BM, a.seg_start[e + 1] - row0);
-  const int nb = blockIdx.y;
   const int K = GU ? a.H : a.I;
   const int N = GU ? 2 * a.I : a.H;
   const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
@@ -339,12 +348,16 @@ hipError_t xtu_i8_quant_rows(const void* rows_bf16, int M, int K, int8_t* a8, in
 }
 
 static hipError_t i8_gemm(bool gu, I8GemmArgs a, int max_tiles, hipStream_t stream) {
+  const long items = (long)max_tiles * (gu ? a.I / 128 : a.H / 256);
+  const long grid = (items + 7) / 8 * 8;
+  if (grid >= (1L << 31)) return hipErrorInvalidValue;
+  if (grid == 0) return hipSuccess;
   if (gu) {
     a.w_estride = 2L * a.I * a.H;
-    i8_gemm_kernel<128, true><<<dim3(max_tiles, a.I / 128), 256, 0, stream>>>(a);
+    i8_gemm_kernel<128, true><<<dim3((unsigned)grid), 256, 0, stream>>>(a);
   } else {
     a.w_estride = (long)a.H * a.I;
-    i8_gemm_kernel<128, false><<<dim3(max_tiles, a.H / 256), 256, 0, stream>>>(a);
+    i8_gemm_kernel<128, false><<<dim3((unsigned)grid), 256, 0, stream>>>(a);
   }
   return hipPeekAtLastError();
 }
