@@ -12,6 +12,8 @@
 // the P16 panel layout with 16 int8 per chunk, next to a per-row emin; the
 // GEMM then runs v_mfma_i32_32x32x32_i8 on LDS tiles with the same tile list
 // and epilogues as the bf16 grouped GEMM.
+#include <type_traits>
+
 #include "weight_format.hpp"
 
 namespace xtu {
@@ -243,72 +245,85 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8GemmArgs a) {
   };
   const int jt0 = GU ? 32 * w : 64 * w;
   const int jt1 = GU ? 128 + 32 * w : 64 * w + 32;
-  i32x16_t acc[MT][2];
+  // K loop and epilogue for NT 32-row tiles (the tile's rows rounded up):
+  // a partial tile does no MFMAs for rows it does not hold
+  auto run = [&](auto nt_tag) {
+    constexpr int NT = decltype(nt_tag)::value;
+    i32x16_t acc[NT][2];
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < NT; ++m)
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
+      for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[m][n][i] = 0;
+        for (int i = 0; i < 16; ++i) acc[m][n][i] = 0;
 
-  const int nk = K / kBK;
-  gload(0);
-  for (int kt = 0; kt < nk; ++kt) {
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (kt + 1 < nk) gload((kt + 1) * kBK);
+    // single LDS stage (a double-buffered one, one barrier per step, measured
+    // 8% slower): the next step's loads are in flight during the MFMAs
+    const int nk = K / kBK;
+    gload(0);
+    for (int kt = 0; kt < nk; ++kt) {
+      __syncthreads();
+      lstore();
+      __syncthreads();
+      if (kt + 1 < nk) gload((kt + 1) * kBK);
 #pragma unroll
-    for (int ks = 0; ks < kBK / 32; ++ks) {
-      const int kofs = ks * 32 + (lane / 32) * 16;
-      const i32x4_t b0 = *reinterpret_cast<const i32x4_t*>(&Bs[(jt0 + lane % 32) * kLDB + kofs]);
-      const i32x4_t b1 = *reinterpret_cast<const i32x4_t*>(&Bs[(jt1 + lane % 32) * kLDB + kofs]);
+      for (int ks = 0; ks < kBK / 32; ++ks) {
+        const int kofs = ks * 32 + (lane / 32) * 16;
+        const i32x4_t b0 =
+            *reinterpret_cast<const i32x4_t*>(&Bs[(jt0 + lane % 32) * kLDB + kofs]);
+        const i32x4_t b1 =
+            *reinterpret_cast<const i32x4_t*>(&Bs[(jt1 + lane % 32) * kLDB + kofs]);
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const i32x4_t av = *reinterpret_cast<const i32x4_t*>(&As[(m * 32 + lane % 32) * kLDB + kofs]);
-        acc[m][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, acc[m][0], 0, 0, 0);
-        acc[m][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, acc[m][1], 0, 0, 0);
-      }
-    }
-  }
-
-  const int ncol = lane % 32;
-  long gcol0, gcol1;   // global weight rows of the two column tiles
-  if (GU) {
-    gcol0 = (long)nb * 128 + 32 * w + ncol;
-    gcol1 = (long)a.I + nb * 128 + 32 * w + ncol;
-  } else {
-    gcol0 = (long)nb * 256 + jt0 + ncol;
-    gcol1 = (long)nb * 256 + jt1 + ncol;
-  }
-  const int em0 = a.emin[(long)ws * N + gcol0];
-  const int em1 = a.emin[(long)ws * N + gcol1];
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = m * 32 + (i / 4) * 8 + (lane / 32) * 4 + (i % 4);
-      if (r < rows) {
-        const long prow = row0 + r;
-        const int cr = a.crow[GU ? (long)a.sorted_tok[prow] : prow];
-        const float sc0 = ldexpf(1.0f, em0 - 128 + cr);
-        const float sc1 = ldexpf(1.0f, em1 - 128 + cr);
-        const float c0 = (float)acc[m][0][i] * sc0;
-        const float c1 = (float)acc[m][1][i] * sc1;
-        if (a.acc_out) {
-          a.acc_out[prow * N + gcol0] = acc[m][0][i];
-          a.acc_out[prow * N + gcol1] = acc[m][1][i];
-        }
-        if (GU) {
-          uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
-          act[prow * a.I + gcol0] = f32_to_bf16(silu_gate(c0, c1, a.limit, a.alpha, a.beta));
-        } else {
-          float* y = reinterpret_cast<float*>(a.out);
-          y[prow * a.H + gcol0] = c0;
-          y[prow * a.H + gcol1] = c1;
+        for (int m = 0; m < NT; ++m) {
+          const i32x4_t av =
+              *reinterpret_cast<const i32x4_t*>(&As[(m * 32 + lane % 32) * kLDB + kofs]);
+          acc[m][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, acc[m][0], 0, 0, 0);
+          acc[m][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, acc[m][1], 0, 0, 0);
         }
       }
     }
+    const int ncol = lane % 32;
+    long gcol0, gcol1;   // global weight rows of the two column tiles
+    if (GU) {
+      gcol0 = (long)nb * 128 + 32 * w + ncol;
+      gcol1 = (long)a.I + nb * 128 + 32 * w + ncol;
+    } else {
+      gcol0 = (long)nb * 256 + jt0 + ncol;
+      gcol1 = (long)nb * 256 + jt1 + ncol;
+    }
+    const int em0 = a.emin[(long)ws * N + gcol0];
+    const int em1 = a.emin[(long)ws * N + gcol1];
+#pragma unroll
+    for (int m = 0; m < NT; ++m)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = m * 32 + (i / 4) * 8 + (lane / 32) * 4 + (i % 4);
+        if (r < rows) {
+          const long prow = row0 + r;
+          const int cr = a.crow[GU ? (long)a.sorted_tok[prow] : prow];
+          const float sc0 = ldexpf(1.0f, em0 - 128 + cr);
+          const float sc1 = ldexpf(1.0f, em1 - 128 + cr);
+          const float c0 = (float)acc[m][0][i] * sc0;
+          const float c1 = (float)acc[m][1][i] * sc1;
+          if (a.acc_out) {
+            a.acc_out[prow * N + gcol0] = acc[m][0][i];
+            a.acc_out[prow * N + gcol1] = acc[m][1][i];
+          }
+          if (GU) {
+            uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
+            act[prow * a.I + gcol0] = f32_to_bf16(silu_gate(c0, c1, a.limit, a.alpha, a.beta));
+          } else {
+            float* y = reinterpret_cast<float*>(a.out);
+            y[prow * a.H + gcol0] = c0;
+            y[prow * a.H + gcol1] = c1;
+          }
+        }
+      }
+  };
+  if (rows > 96) run(std::integral_constant<int, MT>{});
+  else if (rows > 64) run(std::integral_constant<int, 3>{});
+  else if (rows > 32) run(std::integral_constant<int, 2>{});
+  else run(std::integral_constant<int, 1>{});
 }
 
 }  // namespace
