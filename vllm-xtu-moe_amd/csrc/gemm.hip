@@ -317,7 +317,27 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   if (h >= H) return;
   const int trash = trash_start[0];
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < K; ++k) {
+  // pairs in k order with four row loads in flight; a skipped pair reads row
+  // 0 and is not added
+  int k = 0;
+  for (; k + 4 <= K; k += 4) {
+    int pos[4];
+    float w[4];
+    bool ok[4];
+    f32x4_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pos[j] = inv[t * K + k + j];
+      w[j] = wts[t * K + k + j];
+      ok[j] = pos[j] < trash && w[j] != 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] = *reinterpret_cast<const f32x4_t*>(y + (long)(ok[j] ? pos[j] : 0) * H + h);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = ok[j] ? acc + w[j] * v[j] : acc;
+  }
+  for (; k < K; ++k) {
     const int pos = inv[t * K + k];
     const float w = wts[t * K + k];
     if (pos >= trash || w == 0.f) continue;
