@@ -233,6 +233,37 @@ __global__ __launch_bounds__(1024) void route_kernel(const float* __restrict__ l
                          t < T, ids + t * K, wts + t * K);
 }
 
+// Batches of any size on E = 256 / 512 (tiny::wave_epl): one wave routes one
+// token with tiny::route_token_wave (no workgroup barrier), four tokens per
+// workgroup.  Same ids, order and fp32 sequences as route_kernel.
+template <int MODE, int EPL>
+__global__ __launch_bounds__(256) void route_wave_kernel(const float* __restrict__ logits,
+                                                         const float* __restrict__ bias, int T,
+                                                         int K, int n_group, int topk_group,
+                                                         float scale, int renorm,
+                                                         int32_t* __restrict__ ids,
+                                                         float* __restrict__ wts) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const long t = (long)blockIdx.x * 4 + w;
+  if (t >= T) return;   // whole wave
+  tiny::route_token_wave<MODE, EPL>(logits + t * (kWave * EPL), bias, K, n_group, topk_group,
+                                    scale, renorm, threadIdx.x % kWave, ids + t * K, wts + t * K,
+                                    nullptr, nullptr);
+}
+
+template <int MODE>
+void launch_route_wave(int epl, const float* logits, const float* bias, int T, int K,
+                       int n_group, int topk_group, float scale, int renorm, int32_t* ids,
+                       float* wts, hipStream_t stream) {
+  const dim3 grid((unsigned)((T + 3) / 4));
+  if (epl == 4)
+    route_wave_kernel<MODE, 4><<<grid, 256, 0, stream>>>(logits, bias, T, K, n_group, topk_group,
+                                                         scale, renorm, ids, wts);
+  else
+    route_wave_kernel<MODE, 8><<<grid, 256, 0, stream>>>(logits, bias, T, K, n_group, topk_group,
+                                                         scale, renorm, ids, wts);
+}
+
 // ----------------------------------------------------------------------------
 // segmentation
 // ----------------------------------------------------------------------------
@@ -672,6 +703,11 @@ hipError_t xtu_route_softmax_topk(const float* logits, int T, int E, int K, int 
   XTU_CHECK_ARG(T == 0 || (logits && topk_ids && topk_weights));
   if (T == 0) return hipSuccess;
   (void)hipGetLastError();
+  if (const int epl = tiny::wave_epl(0, E, 1, renormalize, logits, nullptr)) {
+    launch_route_wave<0>(epl, logits, nullptr, T, K, 1, 1, 1.0f, renormalize, topk_ids,
+                         topk_weights, stream);
+    return hipPeekAtLastError();
+  }
   const size_t lds = 4 * route_team_words(E, ((E + 31) / 32) * K) * sizeof(float);
   route_kernel<0><<<(T + 3) / 4, 1024, lds, stream>>>(logits, nullptr, T, E, K, 1, 1, 1.0f,
                                                       renormalize, topk_ids, topk_weights);
@@ -688,6 +724,11 @@ hipError_t xtu_route_grouped_sigmoid(const float* logits, const float* bias, int
   XTU_CHECK_ARG(T == 0 || (logits && topk_ids && topk_weights));
   if (T == 0) return hipSuccess;
   (void)hipGetLastError();
+  if (const int epl = tiny::wave_epl(1, E, n_group, renormalize, logits, bias)) {
+    launch_route_wave<1>(epl, logits, bias, T, K, n_group, topk_group, routed_scaling,
+                         renormalize, topk_ids, topk_weights, stream);
+    return hipPeekAtLastError();
+  }
   const size_t lds = 4 * route_team_words(E, n_group * K) * sizeof(float);
   route_kernel<1><<<(T + 3) / 4, 1024, lds, stream>>>(logits, bias, T, E, K, n_group, topk_group,
                                                       routed_scaling, renormalize, topk_ids,

@@ -216,8 +216,10 @@ __device__ void route_token_wave(const float* __restrict__ l, const float* __res
   if (lane < K) {
     ids_out[lane] = my_e;
     wts_out[lane] = w;
-    ids_lds[lane] = my_e;
-    wts_lds[lane] = w;
+    if (ids_lds) {
+      ids_lds[lane] = my_e;
+      wts_lds[lane] = w;
+    }
   }
 }
 
@@ -339,23 +341,32 @@ __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
   }
 }
 
-// The tiny path's envelope: at most 64 pairs and 16 tokens; routing for
-// E = 256 or 512, whole lanes per group, renormalised softmax.
+// Experts per lane of route_token_wave for this router (0: outside its
+// envelope): E = 256 or 512, whole lanes per group, renormalised softmax,
+// 16-byte-aligned logit and bias rows.
+__host__ inline int wave_epl(int mode, int E, int n_group, int renorm, const float* logits,
+                             const float* bias) {
+  const int epl = E / kWave;
+  if (E % kWave != 0 || (epl != 4 && epl != 8)) return 0;
+  if (reinterpret_cast<uintptr_t>(logits) % 16 != 0 ||
+      (bias && reinterpret_cast<uintptr_t>(bias) % 16 != 0))
+    return 0;
+  if (mode == 0) return renorm != 0 ? epl : 0;
+  if (n_group <= 0 || E % n_group != 0) return 0;
+  const int gsz = E / n_group;
+  if (gsz % epl != 0) return 0;
+  const int lpg = gsz / epl;
+  return (lpg >= 1 && lpg <= kWave && (lpg & (lpg - 1)) == 0) ? epl : 0;
+}
+
+// The tiny path's envelope: at most 64 pairs and 16 tokens, and the wave
+// router's (mode 2, ids given, routes nothing).
 __host__ inline int tiny_epl(const SmallArgs& a, int mode) {
   const long A = (long)a.T * a.K + (long)a.T * a.NS;
   if (A > kTinyMaxA || a.T > 16) return 0;
   if (mode == 2) return 1;
-  const int epl = a.E / kWave;
-  if (a.T < 1 || a.E % kWave != 0 || (epl != 4 && epl != 8)) return 0;
-  // 16-byte loads of the logit and bias rows
-  if (reinterpret_cast<uintptr_t>(a.logits) % 16 != 0 ||
-      (a.bias && reinterpret_cast<uintptr_t>(a.bias) % 16 != 0))
-    return 0;
-  if (mode == 0) return a.renorm != 0 ? epl : 0;
-  const int gsz = a.E / a.n_group;
-  if (gsz % epl != 0) return 0;
-  const int lpg = gsz / epl;
-  return (lpg >= 1 && lpg <= kWave && (lpg & (lpg - 1)) == 0) ? epl : 0;
+  if (a.T < 1) return 0;
+  return wave_epl(mode, a.E, a.n_group, a.renorm, a.logits, a.bias);
 }
 
 
