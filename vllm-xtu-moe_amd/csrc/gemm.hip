@@ -399,9 +399,12 @@ hipError_t launch_gemm(bool gu, GemmArgs a, int max_tiles, hipStream_t stream) {
   // NVFP4's exact scale multiply keeps fp32 products live: four panels per
   // wave need more than half of the register file (one wave per SIMD), two
   // fit at two waves per SIMD -- measured 32% faster (Qwen3-Next T = 8192
-  // gate/up 999 -> 678 us).  H % 128 == 0 and I % 64 == 0 always hold here.
+  // gate/up 999 -> 678 us).  The down pass (short K: 4 steps at I = 512)
+  // takes its weights three steps ahead (580 -> 490 us; no gain for gate/up).
+  // H % 128 == 0 and I % 64 == 0 always hold here.
   if constexpr (FMT == kNVFP4) {
-    return launch_shape<FMT, 2, 1, 2>(gu, a, max_tiles, stream);
+    if (gu) return launch_shape<FMT, 2, 1, 2>(gu, a, max_tiles, stream);
+    return launch_shape<FMT, 2, 3, 2>(gu, a, max_tiles, stream);
   } else {
     // few work items (small batches over few experts, e.g. 128 tokens on 8
     // experts: 32 down items for 256 CUs): half-width items, twice as many
