@@ -19,7 +19,7 @@
 namespace xtu {
 namespace {
 
-constexpr int kBK = 64;
+constexpr int kBK = 128;   // k per step (64 measured 6% slower: twice the barriers)
 constexpr int kBN = 256;
 constexpr int kLDB = kBK + 16;   // LDS pitch in bytes
 
@@ -199,10 +199,10 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8GemmArgs a) {
   const int8_t* asrc[A_CH];
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) {
-    const int c = i * 256 + tid, r = c / 4;
+    const int c = i * 256 + tid, r = c / (kBK / 16);
     if (r < rows) {
       const long src = GU ? (long)a.sorted_tok[row0 + r] : (long)(row0 + r);
-      asrc[i] = a.a + src * K + (c % 4) * 16;
+      asrc[i] = a.a + src * K + (c % (kBK / 16)) * 16;
     } else {
       asrc[i] = nullptr;
     }
@@ -234,7 +234,8 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int c = i * 256 + tid;
-      *reinterpret_cast<u32x4_t*>(&As[(c / 4) * kLDB + (c % 4) * 16]) = areg[i];
+      const int r = c / (kBK / 16), col = c % (kBK / 16);
+      *reinterpret_cast<u32x4_t*>(&As[r * kLDB + col * 16]) = areg[i];
     }
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
