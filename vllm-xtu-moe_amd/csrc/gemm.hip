@@ -305,7 +305,11 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
 
 // out[t][h] = sum_k w[t,k] * y[inv[t*K+k]][h] over the pairs that were not
 // sent to the trash bucket (sorted position < *trash_start) and have a
-// non-zero weight, in k order, + sum_s y[inv[T*K + t*NS + s]][h]
+// non-zero weight, in k order, + sum_s y[inv[T*K + t*NS + s]][h].
+// KC, NSC > 0: K and NS fixed at compile time -- every row position is
+// loaded first, then every row at once (two load latencies per token
+// instead of one per pair); 0: loops over the run-time K and NS.
+template <int KC, int NSC>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y,
                                                       const int32_t* __restrict__ inv,
                                                       const float* __restrict__ wts,
@@ -317,36 +321,46 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   if (h >= H) return;
   const int trash = trash_start[0];
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  // pairs in k order with four row loads in flight; a skipped pair reads row
-  // 0 and is not added
-  int k = 0;
-  for (; k + 4 <= K; k += 4) {
-    int pos[4];
-    float w[4];
-    bool ok[4];
-    f32x4_t v[4];
+  if constexpr (KC > 0) {
+    K = KC;
+    NS = NSC;
+    int pos[KC + NSC];
+    float w[KC];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      pos[j] = inv[t * K + k + j];
-      w[j] = wts[t * K + k + j];
-      ok[j] = pos[j] < trash && w[j] != 0.f;
+    for (int j = 0; j < KC; ++j) {
+      pos[j] = inv[t * KC + j];
+      w[j] = wts[t * KC + j];
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      v[j] = *reinterpret_cast<const f32x4_t*>(y + (long)(ok[j] ? pos[j] : 0) * H + h);
+    for (int s = 0; s < NSC; ++s) pos[KC + s] = inv[T * KC + t * NSC + s];
+    // a skipped pair reads row 0 and is not added
+    bool ok[KC];
+    f32x4_t v[KC + NSC];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc = ok[j] ? acc + w[j] * v[j] : acc;
-  }
-  for (; k < K; ++k) {
-    const int pos = inv[t * K + k];
-    const float w = wts[t * K + k];
-    if (pos >= trash || w == 0.f) continue;
-    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(y + (long)pos * H + h);
-    acc += w * v;
-  }
-  for (int s = 0; s < NS; ++s) {
-    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(y + (long)inv[T * K + t * NS + s] * H + h);
-    acc += v;
+    for (int j = 0; j < KC; ++j) {
+      ok[j] = pos[j] < trash && w[j] != 0.f;
+      v[j] = *reinterpret_cast<const f32x4_t*>(y + (long)(ok[j] ? pos[j] : 0) * H + h);
+    }
+#pragma unroll
+    for (int s = 0; s < NSC; ++s)
+      v[KC + s] = *reinterpret_cast<const f32x4_t*>(y + (long)pos[KC + s] * H + h);
+#pragma unroll
+    for (int j = 0; j < KC; ++j) acc = ok[j] ? acc + w[j] * v[j] : acc;
+#pragma unroll
+    for (int s = 0; s < NSC; ++s) acc += v[KC + s];
+  } else {
+    for (int k = 0; k < K; ++k) {
+      const int pos = inv[t * K + k];
+      const float w = wts[t * K + k];
+      if (pos >= trash || w == 0.f) continue;
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(y + (long)pos * H + h);
+      acc += w * v;
+    }
+    for (int s = 0; s < NS; ++s) {
+      const f32x4_t v =
+          *reinterpret_cast<const f32x4_t*>(y + (long)inv[T * K + t * NS + s] * H + h);
+      acc += v;
+    }
   }
   if (out_bf16) {
     uint16_t* o = reinterpret_cast<uint16_t*>(out) + (long)t * H + h;
@@ -356,6 +370,37 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   } else {
     *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(out) + (long)t * H + h) = acc;
   }
+}
+
+template <int KC>
+bool launch_combine_k(dim3 grid, hipStream_t stream, const float* y, const int32_t* inv,
+                      const float* w, const int32_t* trash, int T, int NS, int H, void* out,
+                      int out_bf16) {
+  switch (NS) {
+    case 0: combine_kernel<KC, 0><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, KC, 0, H, out,
+                                                            out_bf16); return true;
+    case 1: combine_kernel<KC, 1><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, KC, 1, H, out,
+                                                            out_bf16); return true;
+    case 2: combine_kernel<KC, 2><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, KC, 2, H, out,
+                                                            out_bf16); return true;
+  }
+  return false;
+}
+
+// The compile-time shapes: the routers' top-k of the configurations here
+// (1, 2, 4, 6, 8, 10) with up to two shared experts.
+bool launch_combine_fixed(dim3 grid, hipStream_t stream, const float* y, const int32_t* inv,
+                          const float* w, const int32_t* trash, int T, int K, int NS, int H,
+                          void* out, int out_bf16) {
+  switch (K) {
+    case 1: return launch_combine_k<1>(grid, stream, y, inv, w, trash, T, NS, H, out, out_bf16);
+    case 2: return launch_combine_k<2>(grid, stream, y, inv, w, trash, T, NS, H, out, out_bf16);
+    case 4: return launch_combine_k<4>(grid, stream, y, inv, w, trash, T, NS, H, out, out_bf16);
+    case 6: return launch_combine_k<6>(grid, stream, y, inv, w, trash, T, NS, H, out, out_bf16);
+    case 8: return launch_combine_k<8>(grid, stream, y, inv, w, trash, T, NS, H, out, out_bf16);
+    case 10: return launch_combine_k<10>(grid, stream, y, inv, w, trash, T, NS, H, out, out_bf16);
+  }
+  return false;
 }
 
 // Kernel shape.  Measured on the DeepSeek-V3 FP8 layer (T = 8192): four
@@ -482,8 +527,10 @@ hipError_t xtu_combine(const float* y, const int32_t* inv, const float* topk_wei
   if (T == 0) return hipSuccess;
   (void)hipGetLastError();
   dim3 grid((H / 4 + 255) / 256, T);
-  combine_kernel<<<grid, 256, 0, stream>>>(y, inv, topk_weights, trash_start, T, K, n_shared, H,
-                                           out, out_bf16);
+  if (!launch_combine_fixed(grid, stream, y, inv, topk_weights, trash_start, T, K, n_shared, H,
+                            out, out_bf16))
+    combine_kernel<0, 0><<<grid, 256, 0, stream>>>(y, inv, topk_weights, trash_start, T, K,
+                                                   n_shared, H, out, out_bf16);
   return hipPeekAtLastError();
 }
 
