@@ -166,8 +166,10 @@ _SEG_CACHE: dict = {}
 _BUF_CACHE: dict = {}
 
 
-def segmentation(T, K, E, NS, bm, device) -> _Segmentation:
-    key = (T, K, E, NS, bm, str(device))
+def segmentation(T, K, E, NS, bm, device, stream=None) -> _Segmentation:
+    """The segmentation buffers of this shape for (device, stream): calls on
+    one stream run in order and share them; another stream gets its own."""
+    key = (T, K, E, NS, bm, str(device), _stream(stream))
     s = _SEG_CACHE.get(key)
     if s is None:
         s = _Segmentation(T, K, E, NS, bm, device)
@@ -175,8 +177,10 @@ def segmentation(T, K, E, NS, bm, device) -> _Segmentation:
     return s
 
 
-def _buf(name, shape, dtype, device):
-    key = (name, tuple(shape), dtype, str(device))
+def _buf(name, shape, dtype, device, stream=None):
+    """Scratch buffer `name` of this shape for (device, stream), kept for the
+    process (stream-ordered reuse; concurrent streams get their own)."""
+    key = (name, tuple(shape), dtype, str(device), _stream(stream))
     t = _BUF_CACHE.get(key)
     if t is None:
         t = torch.empty(shape, dtype=dtype, device=device)
@@ -311,11 +315,11 @@ def _route_shared_ok(fmt, mode, T, E, K, router, H, I, NS) -> bool:
                           int(K), n_group, int(NS), int(H), int(I)))
 
 
-def _fp8pair_bufs(tag, M, K, dev):
-    return (_buf(tag + "_hi", (max(M, 1), K), torch.uint8, dev),
-            _buf(tag + "_lo", (max(M, 1), K), torch.uint8, dev),
-            _buf(tag + "_shi", (max(M, 1), K // 32), torch.uint8, dev),
-            _buf(tag + "_slo", (max(M, 1), K // 32), torch.uint8, dev))
+def _fp8pair_bufs(tag, M, K, dev, stream=None):
+    return (_buf(tag + "_hi", (max(M, 1), K), torch.uint8, dev, stream),
+            _buf(tag + "_lo", (max(M, 1), K), torch.uint8, dev, stream),
+            _buf(tag + "_shi", (max(M, 1), K // 32), torch.uint8, dev, stream),
+            _buf(tag + "_slo", (max(M, 1), K // 32), torch.uint8, dev, stream))
 
 
 def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0, swiglu_alpha=1.0,
@@ -363,7 +367,7 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     if path == "decode" and T > DECODE_MAX_TOKENS:
         raise ValueError(f"decode path handles at most {DECODE_MAX_TOKENS} tokens")
     bm = gemm_tile_m(fmt, int8)
-    seg = segmentation(T, K, E, NS, bm, dev)
+    seg = segmentation(T, K, E, NS, bm, dev, st)
     odt = out_dtype if out is None else out.dtype
     max_active = min(E, T * K) + NS
     # decode with shared experts: their gate/up runs in the routing launch
@@ -377,7 +381,7 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
     if split:
         r = router or {}
-        act_sh = _buf("act_sh", (NS * T, I), torch.bfloat16, dev)
+        act_sh = _buf("act_sh", (NS * T, I), torch.bfloat16, dev, st)
         _lib.call("xtu_decode_route_shared", rmode, _p(r.get("logits")), _p(r.get("bias")),
                   _p(ids), _p(wts), T, E, K, int(r.get("n_group", 1)),
                   int(r.get("topk_group", 1)), float(r.get("routed_scaling_factor", 1.0)),
@@ -412,7 +416,7 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     if T == 0:
         return (out, seg) if return_seg else out
     if path == "decode":
-        act = _buf("act", (max(A, 1), I), torch.bfloat16, dev)
+        act = _buf("act", (max(A, 1), I), torch.bfloat16, dev, st)
         if split:
             _lib.call("xtu_decode_gate_up_routed", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13),
                       _p(W.gs13), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start),
@@ -430,12 +434,12 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
                       _p(seg.seg_start), E + NS, _p(seg.active), _p(seg.n_active), max_active,
                       _p(out), int(out.dtype == torch.bfloat16), st)
             return (out, seg) if return_seg else out
-        y = _buf("y", (max(A, 1), H), torch.float32, dev)
+        y = _buf("y", (max(A, 1), H), torch.float32, dev, st)
         _lib.call("xtu_decode_down", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.active), _p(seg.n_active), max_active,
                   _p(y), st)
     else:
-        y = _buf("y", (max(A, 1), H), torch.float32, dev)
+        y = _buf("y", (max(A, 1), H), torch.float32, dev, st)
         expert_pass(x, seg, W, 0, E + NS, y, slot_map=slot_map, int8=int8,
                     swiglu_limit=swiglu_limit, swiglu_alpha=swiglu_alpha,
                     swiglu_beta=swiglu_beta, stream=st)
@@ -456,14 +460,14 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
     dev = x.device
     st = _stream(stream)
     lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
-    act = _buf("act", (max(A, 1), I), torch.bfloat16, dev)
+    act = _buf("act", (max(A, 1), I), torch.bfloat16, dev, st)
     lo, hi = seg.tile_range_ptrs(b0, b1)
     if int8:
         w13_8, emin13, w2_8, emin2 = W.int8_planes()
-        a8x = _buf("a8x", (T, H), torch.int8, dev)
-        crx = _buf("crx", (T,), torch.int32, dev)
-        a8a = _buf("a8a", (max(A, 1), I), torch.int8, dev)
-        cra = _buf("cra", (max(A, 1),), torch.int32, dev)
+        a8x = _buf("a8x", (T, H), torch.int8, dev, st)
+        crx = _buf("crx", (T,), torch.int32, dev, st)
+        a8a = _buf("a8a", (max(A, 1), I), torch.int8, dev, st)
+        cra = _buf("cra", (max(A, 1),), torch.int32, dev, st)
         _lib.call("xtu_i8_quant_rows", _p(x), T, H, _p(a8x), _p(crx), st)
         _lib.call("xtu_i8_gemm_gate_up", _p(a8x), _p(crx), _p(seg.sorted_tok), H, I, _p(w13_8),
                   _p(emin13), _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
@@ -477,8 +481,8 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
     if fmt == FMT_FP8:
         # exact FP8: activations split into e4m3 pairs, fp8 MFMA with the fp32
         # block scale folded per 128-k block
-        xq = _fp8pair_bufs("x8", T, H, dev)
-        aq = _fp8pair_bufs("a8", A, I, dev)
+        xq = _fp8pair_bufs("x8", T, H, dev, st)
+        aq = _fp8pair_bufs("a8", A, I, dev, st)
         _lib.call("xtu_fp8pair_quant", _p(x), T, H, *[_p(t) for t in xq], st)
         _lib.call("xtu_gemm8_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
                   _p(W.w13), _p(W.s13), 0, 0, _p(slot_map), _p(seg.seg_start),

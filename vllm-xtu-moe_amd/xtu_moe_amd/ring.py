@@ -165,9 +165,9 @@ def gpu_moe_layer_from_engine_tiled(engine: HostExpertStore, x, topk_ids, topk_w
         id_map_h[e] = b
     id_map = id_map_h.to(device, non_blocking=True)
     bm = gemm_tile_m(fmt)
-    seg = segmentation(T, K, E, NS, bm, device)
+    seg = segmentation(T, K, E, NS, bm, device, st)
     seg.run(ids, wts, id_map, True, st)
-    y = _buf("ring_y", (max(seg.A, 1), H), torch.float32, device)
+    y = _buf("ring_y", (max(seg.A, 1), H), torch.float32, device, st)
     te = int(tile_e) if tile_e else staging_tile_experts(E)
     ring = _ring_for(engine, te, nslots, device)
     ntile = (len(streamed) + te - 1) // te
