@@ -163,3 +163,32 @@ def test_int8_layer_vs_oracle():
     ref = oracle.moe_layer_i8(bf16_tensor_to_bits(x), ids, wts, E, NS, H, I, dn["w13"], dn["s13"],
                               dn["w2"], dn["s2"])
     check_close(out.cpu().numpy(), ref, bf16_out=False, what="int8 layer")
+
+
+@pytest.mark.parametrize("path", ["decode", "gemm"])
+def test_two_streams_do_not_share_scratch(path):
+    """Layers issued on two streams back to back, without waiting for each
+    other: each stream's scratch buffers and segmentation are its own, so both
+    outputs equal those of the same layers run one after the other."""
+    fmt, E, NS, H, I, K = F.FMT_MXFP4, 32, 1, 512, 256, 4
+    T = 4 if path == "decode" else 96
+    d = make_dense_layer(fmt, E + NS, H, I, seed=41)
+    W = ExpertWeights.from_dense(fmt, d["w13"], d["s13"], d["w2"], d["s2"], d["gs13"], d["gs2"],
+                                 n_shared=NS, device="cuda")
+    ins = []
+    for seed in (42, 43):
+        ids, wts = random_routing(T, K, E, seed=seed)
+        x = torch.randn((T, H), generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16)
+        ins.append((x.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda()))
+    ref = [moe_forward(x, i, w, W, path=path, out_dtype=torch.float32) for x, i, w in ins]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for s, (x, i, w) in zip((s1, s2), ins):
+        with torch.cuda.stream(s):
+            outs.append(moe_forward(x, i, w, W, path=path, out_dtype=torch.float32, stream=s))
+    torch.cuda.synchronize()
+    for a, b in zip(outs, ref):
+        assert torch.equal(a, b)
