@@ -42,13 +42,16 @@ constexpr int kRT = kBM / 16;       // 16-row MFMA tiles per M tile
 constexpr int kGemmThreads = 256;
 constexpr int kBufFlags = 0x00020000;   // raw buffer resource, dword 3
 
-template <int FMT>
+// SPS super-blocks per K step (BF16 only: its 32-k super-blocks make short
+// steps, one barrier each).
+template <int FMT, int SPS = 1>
 struct GemmShape {
   using F = WFmt<FMT>;
-  static constexpr int kBK = F::kSB;                          // k per step
+  static_assert(SPS == 1 || FMT == kBF16, "several super-blocks per step: BF16 only");
+  static constexpr int kBK = F::kSB * SPS;                    // k per step
   static constexpr int kLD = kBK + 8;                         // LDS row pitch (bf16)
   static constexpr int kAL = kBM * kBK / 8 / kGemmThreads;    // 16-byte A pieces per thread
-  static constexpr int kG = F::kCK / 8;                       // MFMA k groups per step
+  static constexpr int kG = F::kCK / 8;                       // MFMA k groups per super-block
   static constexpr int kABuf = kBM * kLD;                     // bf16 per A stage buffer
 };
 
@@ -72,16 +75,18 @@ struct GemmArgs {
 
 // One wave's weights of one step: a 16-byte chunk per panel, the chunk's raw
 // fp4 scale bits, and (fp8) the block scales of panels 0,1 and 2,3.
-template <int FMT, int PW>
+template <int FMT, int PW, int SPS = 1>
 struct BStep {
-  u32x4_t w[PW];
+  u32x4_t w[PW * SPS];        // panel p, super-block j of the step: w[p * SPS + j]
   uint32_t sc[PW];
   float bs0, bs1;
 };
 
-// bf16 operand of MFMA group g of a chunk (k = q*kCK + 8g .. +7 of the lane's row).
-template <int FMT, int PW>
-__device__ __forceinline__ bf16x8_t dequant_group(const BStep<FMT, PW>& b, int p, int g) {
+// bf16 operand of MFMA group g of a chunk (k = q*kCK + 8g .. +7 of the lane's row),
+// super-block j of the step.
+template <int FMT, int PW, int SPS>
+__device__ __forceinline__ bf16x8_t dequant_group(const BStep<FMT, PW, SPS>& b, int p, int g,
+                                                  int j) {
   uint32_t o[4];
   if constexpr (FMT == kMXFP4) {
     fp4x8_to_bf16(b.w[p][g], e8m0_to_f32(b.sc[p]), o);
@@ -101,7 +106,7 @@ __device__ __forceinline__ bf16x8_t dequant_group(const BStep<FMT, PW>& b, int p
       o[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2_t));
     }
   } else {
-    return as_bf16x8(b.w[p]);
+    return as_bf16x8(b.w[p * SPS + j]);
   }
   return as_bf16x8(o[0], o[1], o[2], o[3]);
 }
@@ -109,10 +114,10 @@ __device__ __forceinline__ bf16x8_t dequant_group(const BStep<FMT, PW>& b, int p
 // Kernel shape: PW weight panels per wave (a workgroup covers 64*PW output
 // columns), weights prefetched PD steps ahead in registers, register budget
 // sized for WPS waves per SIMD.
-template <int FMT, bool GU, int PW, int PD, int WPS>
+template <int FMT, bool GU, int PW, int PD, int WPS, int SPS = 1>
 __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a) {
   using F = WFmt<FMT>;
-  using S = GemmShape<FMT>;
+  using S = GemmShape<FMT, SPS>;
   __shared__ __attribute__((aligned(16))) uint16_t As[2 * S::kABuf];
 
   // ---- work item
@@ -131,6 +136,7 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
   const int rows = min(kBM, a.seg_start[e + 1] - row0);
   const int K = GU ? a.H : a.I;
   const int nsteps = K / S::kBK;
+  const int nsb = K / F::kSB;   // super-blocks per panel row
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid / 64);
   const int lane = tid % 64;
@@ -182,11 +188,14 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
 #pragma unroll
     for (int i = 0; i < S::kAL; ++i) *reinterpret_cast<u32x4_t*>(buf + alds[i]) = ar[i];
   };
-  auto load_b = [&](int s, BStep<FMT, PW>& b) {
+  auto load_b = [&](int s, BStep<FMT, PW, SPS>& b) {
 #pragma unroll
     for (int p = 0; p < PW; ++p)
-      b.w[p] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rw, lane * 16, (pan[p] * nsteps + s) * 1024, 0));
+#pragma unroll
+      for (int j = 0; j < SPS; ++j)
+        b.w[p * SPS + j] = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                         rw, lane * 16, (pan[p] * nsb + s * SPS + j) * 1024, 0));
     if constexpr (F::kSBY > 0) {
       const int g = s / F::kUG, ob = (s % F::kUG) * F::kSBY;
 #pragma unroll
@@ -215,16 +224,18 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
 #pragma unroll
       for (int p = 0; p < PW; ++p) acc[m][p] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](const BStep<FMT, PW>& b, const uint16_t* buf) {
+    auto compute = [&](const BStep<FMT, PW, SPS>& b, const uint16_t* buf) {
+#pragma unroll
+      for (int j = 0; j < SPS; ++j)
 #pragma unroll
       for (int g = 0; g < S::kG; ++g) {
         bf16x8_t bv[PW];
 #pragma unroll
-        for (int p = 0; p < PW; ++p) bv[p] = dequant_group<FMT, PW>(b, p, g);
+        for (int p = 0; p < PW; ++p) bv[p] = dequant_group<FMT, PW, SPS>(b, p, g, j);
 #pragma unroll
         for (int m = 0; m < NR; ++m) {
-          const bf16x8_t av = as_bf16x8(
-              *reinterpret_cast<const u32x4_t*>(buf + afrag + m * 16 * S::kLD + 8 * g));
+          const bf16x8_t av = as_bf16x8(*reinterpret_cast<const u32x4_t*>(
+              buf + afrag + m * 16 * S::kLD + j * F::kSB + 8 * g));
 #pragma unroll
           for (int p = 0; p < PW; ++p)
             acc[m][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv[p], acc[m][p], 0, 0, 0);
@@ -240,7 +251,7 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
     // compiler sinks them next to their first use.
     constexpr int U = PD + 1;
     u32x4_t ar[S::kAL];
-    BStep<FMT, PW> bb[U];
+    BStep<FMT, PW, SPS> bb[U];
     load_a(0, ar);
 #pragma unroll
     for (int j = 0; j < PD; ++j) load_b(min(j, nsteps - 1), bb[j]);
@@ -419,13 +430,14 @@ bool launch_combine_fixed(dim3 grid, hipStream_t stream, const float* y, const i
 #endif
 constexpr long kGemmSmallItems = 512;   // below this, half-width work items
 
-template <int FMT, int PW, int PD, int WPS>
+template <int FMT, int PW, int PD, int WPS, int SPS = 1>
 hipError_t launch_shape(bool gu, const GemmArgs& a, int max_tiles, hipStream_t stream) {
   const long items = (long)max_tiles * (gu ? a.I / (32 * PW) : a.H / (64 * PW));
   const long grid = (items + 7) / 8 * 8;
   if (grid >= (1L << 31)) return hipErrorInvalidValue;
-  if (gu) moe_gemm_kernel<FMT, true, PW, PD, WPS><<<dim3((unsigned)grid), kGemmThreads, 0, stream>>>(a);
-  else moe_gemm_kernel<FMT, false, PW, PD, WPS><<<dim3((unsigned)grid), kGemmThreads, 0, stream>>>(a);
+  const dim3 g((unsigned)grid);
+  if (gu) moe_gemm_kernel<FMT, true, PW, PD, WPS, SPS><<<g, kGemmThreads, 0, stream>>>(a);
+  else moe_gemm_kernel<FMT, false, PW, PD, WPS, SPS><<<g, kGemmThreads, 0, stream>>>(a);
   return hipPeekAtLastError();
 }
 
@@ -455,8 +467,12 @@ hipError_t launch_gemm(bool gu, GemmArgs a, int max_tiles, hipStream_t stream) {
     // experts: 32 down items for 256 CUs): half-width items, twice as many
     // weight streams in flight
     const long items4 = (long)max_tiles * (gu ? a.I / 128 : a.H / 256);
+#ifndef XTU_SMALL_SPS
+#define XTU_SMALL_SPS 4
+#endif
     if (items4 < kGemmSmallItems && (gu ? a.I % 64 : a.H % 128) == 0)
-      return launch_shape<FMT, 2, 1, 2>(gu, a, max_tiles, stream);
+      return launch_shape<FMT, 2, 1, 2, FMT == kBF16 ? XTU_SMALL_SPS : 1>(gu, a, max_tiles,
+                                                                          stream);
     return launch_shape<FMT, 4, 1, 2>(gu, a, max_tiles, stream);
   }
 }
