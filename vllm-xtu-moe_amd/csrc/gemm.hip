@@ -178,15 +178,18 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
   const int rb0 = pan[0] / 8;
   const int rb1 = pan[PW / 2] / 8;
 
-  auto load_a = [&](int s, u32x4_t (&ar)[S::kAL]) {
+  // piece i holds rows [i, i + 1) * (kGemmThreads / ppr); np_tag: the pieces
+  // that hold the rows the MFMAs read (the rest are never staged)
+  auto load_a = [&](int s, u32x4_t (&ar)[S::kAL], auto np_tag) {
 #pragma unroll
-    for (int i = 0; i < S::kAL; ++i)
+    for (int i = 0; i < decltype(np_tag)::value; ++i)
       ar[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                               ra, aoff[i], s * S::kBK * 2, 0));
   };
-  auto store_a = [&](uint16_t* buf, const u32x4_t (&ar)[S::kAL]) {
+  auto store_a = [&](uint16_t* buf, const u32x4_t (&ar)[S::kAL], auto np_tag) {
 #pragma unroll
-    for (int i = 0; i < S::kAL; ++i) *reinterpret_cast<u32x4_t*>(buf + alds[i]) = ar[i];
+    for (int i = 0; i < decltype(np_tag)::value; ++i)
+      *reinterpret_cast<u32x4_t*>(buf + alds[i]) = ar[i];
   };
   auto load_b = [&](int s, BStep<FMT, PW, SPS>& b) {
 #pragma unroll
@@ -250,24 +253,31 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
     // Scheduling barriers keep the loads ahead of the MFMAs; left alone, the
     // compiler sinks them next to their first use.
     constexpr int U = PD + 1;
+    // small-batch BF16 items (several super-blocks per step) stage only the
+    // pieces holding the NR*16 rows the MFMAs read (tiny Mixtral 62.0 -> 59.0
+    // us); the other shapes measured slower that way (Qwen3-Next NVFP4 T=8192
+    // +6%) and stage every piece
+    constexpr int kRowsPerPiece = kGemmThreads / ppr;
+    constexpr int kNeed = (NR * 16 + kRowsPerPiece - 1) / kRowsPerPiece;
+    constexpr std::integral_constant<int, (SPS > 1 && kNeed < S::kAL ? kNeed : S::kAL)> NP{};
     u32x4_t ar[S::kAL];
     BStep<FMT, PW, SPS> bb[U];
-    load_a(0, ar);
+    load_a(0, ar, NP);
 #pragma unroll
     for (int j = 0; j < PD; ++j) load_b(min(j, nsteps - 1), bb[j]);
-    store_a(As, ar);
+    store_a(As, ar, NP);
     __syncthreads();
     for (int s0 = 0; s0 < nsteps; s0 += U) {
 #pragma unroll
       for (int j = 0; j < U; ++j) {
         const int s = s0 + j;
         if (j == 0 || s < nsteps) {
-          load_a(min(s + 1, nsteps - 1), ar);
+          load_a(min(s + 1, nsteps - 1), ar, NP);
           load_b(min(s + PD, nsteps - 1), bb[(j + PD) % U]);
           __builtin_amdgcn_sched_barrier(0);
           compute(bb[j], As + (s & 1) * S::kABuf);
           __builtin_amdgcn_sched_barrier(0);
-          store_a(As + ((s + 1) & 1) * S::kABuf, ar);
+          store_a(As + ((s + 1) & 1) * S::kABuf, ar, NP);
           __syncthreads();
         }
       }
