@@ -302,7 +302,8 @@ __global__ __launch_bounds__(kSegThreads) void seg_hist_kernel(SegArgs a,
   for (int e = threadIdx.x; e < a.NB; e += kSegThreads) cnt[e] = 0;
   __syncthreads();
   const int base = blockIdx.x * kSegChunk;
-  for (int r = 0; r < kSegRounds; ++r) {
+  const int nrounds = min(kSegRounds, (a.A - base + kSegThreads - 1) / kSegThreads);
+  for (int r = 0; r < nrounds; ++r) {
     const int p = base + r * kSegThreads + threadIdx.x;
     if (p < a.A) {
       float w;
@@ -441,7 +442,9 @@ __global__ __launch_bounds__(kSegThreads) void seg_scatter_kernel(
   const int base = blockIdx.x * kSegChunk;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int nbits = 32 - __builtin_clz(a.NB - 1);   // bits of the largest bucket id (NB >= 2)
-  for (int r = 0; r < kSegRounds; ++r) {
+  // rounds holding pairs only (uniform: a short batch skips the empty ones)
+  const int nrounds = min(kSegRounds, (a.A - base + kSegThreads - 1) / kSegThreads);
+  for (int r = 0; r < nrounds; ++r) {
     const int p = base + r * kSegThreads + threadIdx.x;
     const bool valid = p < a.A;
     float w = 0.f;
