@@ -405,7 +405,10 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
                   n_group=router.get("n_group", 1), topk_group=router.get("topk_group", 1),
                   routed_scaling_factor=router.get("routed_scaling_factor", 1.0), ids_out=ids,
                   wts_out=wts, stream=st)
-            seg.run(ids, wts, id_map, drop_zero, st)
+            if seg.small:   # the whole segmentation in one launch
+                seg.run_small(2, ids, wts, id_map=id_map, drop_zero=drop_zero, stream=st)
+            else:
+                seg.run(ids, wts, id_map, drop_zero, st)
     elif seg.small and T > 0:
         seg.run_small(2, ids, wts, id_map=id_map, drop_zero=drop_zero, stream=st)
     else:
