@@ -215,3 +215,33 @@ def test_tiny_route_segment_edge_cases(case):
     tr = np.concatenate([ref["seg_start"][e] + bm * np.arange(nt[e]) for e in range(E + NS)])
     np.testing.assert_array_equal(seg.tile_expert.cpu().numpy()[: ets[-1]], te)
     np.testing.assert_array_equal(seg.tile_row0.cpu().numpy()[: ets[-1]], tr)
+
+
+@pytest.mark.parametrize("case", ["misaligned", "not-renormalized", "other-E"])
+def test_large_batch_router_fallbacks_bit_exact(case):
+    """Batches outside the one-wave-per-token router's envelope (logit rows
+    not 16-byte aligned, softmax without renormalisation, E other than 256 or
+    512) take the 256-thread-team router: same bit-exact results."""
+    rng = np.random.default_rng(77)
+    T = 300
+    if case == "other-E":
+        E, G, TG, K = 320, 16, 4, 8
+        logits = rng.standard_normal((T, E)).astype(np.float32)
+        ids, wts = _gpu_route(logits, top_k=K, scoring="sigmoid", n_group=G, topk_group=TG,
+                              routed_scaling_factor=2.5)
+        rids, rwts = oracle.route_grouped_sigmoid(logits, None, G, TG, K, 2.5)
+    else:
+        E, K = 512, 10
+        logits = rng.standard_normal((T, E)).astype(np.float32)
+        renorm = case != "not-renormalized"
+        if case == "misaligned":
+            base = torch.from_numpy(np.concatenate([[0.0], logits.ravel()]).astype(np.float32))
+            lg = base.cuda()[1:].view(T, E)     # 4-byte offset
+            w, i = L.route(lg, top_k=K, scoring="softmax")
+            torch.cuda.synchronize()
+            ids, wts = i.cpu().numpy(), w.cpu().numpy()
+        else:
+            ids, wts = _gpu_route(logits, top_k=K, scoring="softmax", renormalize=False)
+        rids, rwts = oracle.route_softmax_topk(logits, K, renormalize=renorm)
+    np.testing.assert_array_equal(ids, rids)
+    np.testing.assert_array_equal(wts.view(np.uint32), rwts.view(np.uint32))
