@@ -82,8 +82,8 @@ def main():
     ap.add_argument("--pmc-child", type=int, default=0, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the expert-parallel design is described in DESIGN.md); run with --gpus 1",
+        print("bench.py measures one GPU only: the expert path here runs on one GPU "
+              "(no collectives or expert-parallel sharding); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
 

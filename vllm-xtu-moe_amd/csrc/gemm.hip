@@ -393,17 +393,23 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   }
 }
 
+template <int KC, int NSC>
+bool launch_combine_kn(dim3 grid, hipStream_t stream, const float* y, const int32_t* inv,
+                       const float* w, const int32_t* trash, int T, int H, void* out,
+                       int out_bf16) {
+  combine_kernel<KC, NSC><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, KC, NSC, H, out,
+                                                    out_bf16);
+  return true;
+}
+
 template <int KC>
 bool launch_combine_k(dim3 grid, hipStream_t stream, const float* y, const int32_t* inv,
                       const float* w, const int32_t* trash, int T, int NS, int H, void* out,
                       int out_bf16) {
   switch (NS) {
-    case 0: combine_kernel<KC, 0><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, KC, 0, H, out,
-                                                            out_bf16); return true;
-    case 1: combine_kernel<KC, 1><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, KC, 1, H, out,
-                                                            out_bf16); return true;
-    case 2: combine_kernel<KC, 2><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, KC, 2, H, out,
-                                                            out_bf16); return true;
+    case 0: return launch_combine_kn<KC, 0>(grid, stream, y, inv, w, trash, T, H, out, out_bf16);
+    case 1: return launch_combine_kn<KC, 1>(grid, stream, y, inv, w, trash, T, H, out, out_bf16);
+    case 2: return launch_combine_kn<KC, 2>(grid, stream, y, inv, w, trash, T, H, out, out_bf16);
   }
   return false;
 }
