@@ -1,7 +1,8 @@
 """Weighted unpermute (xtu_combine) against a float64 restatement of the
 reference's per-token ordered sum (moe_v2.hpp:920-930): pairs in top-k order,
 pairs sent to the trash bucket or with zero weight skipped, shared rows added
-with weight 1.  Top-k widths on both sides of the kernel's four-pair batches."""
+with weight 1.  Top-k widths with and without a compile-time shape, small and
+larger batches."""
 import numpy as np
 import pytest
 import torch
@@ -14,7 +15,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("T,K,E,NS,H", [(7, 1, 8, 0, 256), (33, 3, 16, 1, 512), (64, 4, 32, 0, 1024),
                                         (50, 8, 64, 1, 2048), (40, 10, 512, 2, 768),
-                                        (9, 11, 40, 1, 128)])
+                                        (9, 11, 40, 1, 128), (300, 8, 64, 1, 1280),
+                                        (257, 2, 8, 0, 256)])
 @pytest.mark.parametrize("drop_zero", [False, True])
 @pytest.mark.parametrize("out_bf16", [False, True])
 def test_combine_matches_ordered_sum(T, K, E, NS, H, drop_zero, out_bf16):
