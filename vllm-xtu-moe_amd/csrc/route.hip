@@ -216,8 +216,10 @@ __device__ void route_token(const float* __restrict__ l, const float* __restrict
   team_sync<TEAM>();   // the scratch may be reused for the next token
 }
 
-// Four 256-thread teams per workgroup, one token each.
-template <int MODE>
+// 1024 / TEAM teams per workgroup, one token each: four 256-thread teams, or
+// sixteen one-wave teams for at most 64 experts (wave syncs, no workgroup
+// barrier).
+template <int MODE, int TEAM = 256>
 __global__ __launch_bounds__(1024) void route_kernel(const float* __restrict__ logits,
                                                      const float* __restrict__ bias, int T, int E,
                                                      int K, int n_group, int topk_group,
@@ -225,12 +227,27 @@ __global__ __launch_bounds__(1024) void route_kernel(const float* __restrict__ l
                                                      int32_t* __restrict__ ids,
                                                      float* __restrict__ wts) {
   extern __shared__ float route_lds[];
-  const int team = threadIdx.x / 256, tid = threadIdx.x % 256;
-  const long t = (long)blockIdx.x * 4 + team;
+  constexpr int kTeams = 1024 / TEAM;
+  const int team = threadIdx.x / TEAM, tid = threadIdx.x % TEAM;
+  const long t = (long)blockIdx.x * kTeams + team;
   const int nc = (MODE == 1 ? n_group : (E + 31) / 32) * K;
   const RouteScratch s(route_lds + team * route_team_words(E, nc), E, nc);
-  route_token<MODE, 256>(logits + t * E, bias, E, K, n_group, topk_group, scale, renorm, s, tid,
-                         t < T, ids + t * K, wts + t * K);
+  route_token<MODE, TEAM>(logits + t * E, bias, E, K, n_group, topk_group, scale, renorm, s, tid,
+                          t < T, ids + t * K, wts + t * K);
+}
+
+// The team router's launch: one-wave teams for E <= 64.
+template <int MODE>
+void launch_route_teams(const float* logits, const float* bias, int T, int E, int K, int n_group,
+                        int topk_group, float scale, int renorm, int nc, int32_t* ids,
+                        float* wts, hipStream_t stream) {
+  const size_t words = route_team_words(E, nc) * sizeof(float);
+  if (E <= kWave)
+    route_kernel<MODE, kWave><<<(T + 15) / 16, 1024, 16 * words, stream>>>(
+        logits, bias, T, E, K, n_group, topk_group, scale, renorm, ids, wts);
+  else
+    route_kernel<MODE, 256><<<(T + 3) / 4, 1024, 4 * words, stream>>>(
+        logits, bias, T, E, K, n_group, topk_group, scale, renorm, ids, wts);
 }
 
 // Batches of any size on E = 256 / 512 (tiny::wave_epl): one wave routes one
@@ -711,9 +728,8 @@ hipError_t xtu_route_softmax_topk(const float* logits, int T, int E, int K, int 
                          topk_weights, stream);
     return hipPeekAtLastError();
   }
-  const size_t lds = 4 * route_team_words(E, ((E + 31) / 32) * K) * sizeof(float);
-  route_kernel<0><<<(T + 3) / 4, 1024, lds, stream>>>(logits, nullptr, T, E, K, 1, 1, 1.0f,
-                                                      renormalize, topk_ids, topk_weights);
+  launch_route_teams<0>(logits, nullptr, T, E, K, 1, 1, 1.0f, renormalize, ((E + 31) / 32) * K,
+                       topk_ids, topk_weights, stream);
   return hipPeekAtLastError();
 }
 
@@ -732,10 +748,8 @@ hipError_t xtu_route_grouped_sigmoid(const float* logits, const float* bias, int
                          renormalize, topk_ids, topk_weights, stream);
     return hipPeekAtLastError();
   }
-  const size_t lds = 4 * route_team_words(E, n_group * K) * sizeof(float);
-  route_kernel<1><<<(T + 3) / 4, 1024, lds, stream>>>(logits, bias, T, E, K, n_group, topk_group,
-                                                      routed_scaling, renormalize, topk_ids,
-                                                      topk_weights);
+  launch_route_teams<1>(logits, bias, T, E, K, n_group, topk_group, routed_scaling, renormalize,
+                       n_group * K, topk_ids, topk_weights, stream);
   return hipPeekAtLastError();
 }
 
