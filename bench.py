@@ -293,7 +293,7 @@ def main():
             if decode:
                 _lib.call("xtu_decode_gate_up", fmt, _p(x_st), T, H, I, _p(W.w13), _p(W.s13),
                           _p(W.gs13), 0, 0, 0, _p(seg.sorted_tok), _p(seg.seg_start),
-                          _p(seg.active), _p(seg.n_active), min(E, T * K) + NS, _p(act),
+                          _p(seg.active), 0, _p(seg.n_active), min(E, T * K) + NS, _p(act),
                           cfg["limit"], 1.0, 0.0, st)
             elif i8:
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
@@ -453,7 +453,7 @@ def pmc_child(args, cfg, T):
     for _ in range(3):
         flush.add_(1.0)
         _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13),
-                  0, 0, 0, _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active),
+                  0, 0, 0, _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active), 0,
                   _p(seg.n_active), min(E, T * K) + NS, _p(act), cfg["limit"], 1.0, 0.0, st)
     torch.cuda.synchronize()
     src = torch.ones(COPY_BYTES, dtype=torch.uint8, device=dev)

@@ -98,9 +98,15 @@ hipError_t xtu_route_segment_small(int mode, const float* logits, const float* b
 /* --------------------------------------------------- skinny-M (decode) path
  * Replaces moe4_smallm_gu2 / moe4_smallm_dn2 (xiaotu_moe/csrc/moe4_smallm.cu:
  * 395-430) and the FP8 pair kernels _gate_up_pairs_kernel / _act_pairs_kernel
- * / _down_pairs_kernel (vllm_xiaotu_moe/decode_moe_fp8.py:23-101).  At most 16
- * pairs per expert (callers route T <= 16 here).  One workgroup per (active
- * expert, weight panel group); slots beyond *n_active exit at once.
+ * / _down_pairs_kernel (vllm_xiaotu_moe/decode_moe_fp8.py:23-101).  Batches
+ * of T <= 16 tokens.  Work slots are either the active experts (tile_row0 =
+ * NULL: slot j is expert active[j], rows from seg_start, at most 16 of them
+ * computed) or the segmentation's 16-row tiles (xtu_segment with bm = 16:
+ * active = tile_expert, tile_row0, n_active = n_tiles), which cover every
+ * row of every bucket -- an expert listed twice by a token, or zero-weight
+ * pairs kept with drop_zero = 0, may hold more than 16 rows.  One workgroup
+ * per (work slot, weight panel group); slots beyond *n_active exit at once;
+ * max_active bounds the grid.
  * gate_up writes act bf16 [A][I] = SwiGLU-clamp(x W_gate^T, x W_up^T) per
  * sorted pair row; down writes y fp32 [A][H].  T = tokens of the batch (up
  * to 72 KiB of an expert's activation rows are staged in LDS, the rest read
@@ -111,13 +117,15 @@ hipError_t xtu_decode_gate_up(int fmt, const void* x, int T, int H, int I, const
                               const void* s13, const float* gs13, long w_estride, long s_estride,
                               const int32_t* slot_map, const int32_t* sorted_tok,
                               const int32_t* seg_start, const int32_t* active,
-                              const int32_t* n_active, int max_active, void* act, float limit,
-                              float alpha, float beta, hipStream_t stream);
+                              const int32_t* tile_row0, const int32_t* n_active, int max_active,
+                              void* act, float limit, float alpha, float beta,
+                              hipStream_t stream);
 hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const void* w2, const void* s2,
                            const float* gs2, long w_estride, long s_estride,
                            const int32_t* slot_map, const int32_t* seg_start,
-                           const int32_t* active, const int32_t* n_active, int max_active,
-                           float* y, hipStream_t stream);
+                           const int32_t* active, const int32_t* tile_row0,
+                           const int32_t* n_active, int max_active, float* y,
+                           hipStream_t stream);
 
 /* Routing + segmentation and the shared experts' gate/up in one launch
  * (tiny batches, n_shared >= 1): workgroup 0 does exactly what
@@ -146,16 +154,17 @@ hipError_t xtu_decode_route_shared(
     int32_t* expert_tile_start, int fmt, const void* x, int H, int I, const void* w13,
     const void* s13, const float* gs13, long w_estride, long s_estride, const int32_t* slot_map,
     void* act_shared, float limit, float alpha, float beta, hipStream_t stream);
-/* xtu_decode_gate_up for the routed experts only: the last n_shared active
- * slots (the shared buckets) are left out; the gate/up fast-path shape is
- * required. */
+/* xtu_decode_gate_up for the routed experts only: the last n_shared work
+ * slots (the shared buckets, one 16-row tile each) are left out; the gate/up
+ * fast-path shape is required. */
 hipError_t xtu_decode_gate_up_routed(int fmt, const void* x, int T, int H, int I,
                                      const void* w13, const void* s13, const float* gs13,
                                      long w_estride, long s_estride, const int32_t* slot_map,
                                      const int32_t* sorted_tok, const int32_t* seg_start,
-                                     const int32_t* active, const int32_t* n_active,
-                                     int max_active, int n_shared, void* act, float limit,
-                                     float alpha, float beta, hipStream_t stream);
+                                     const int32_t* active, const int32_t* tile_row0,
+                                     const int32_t* n_active, int max_active, int n_shared,
+                                     void* act, float limit, float alpha, float beta,
+                                     hipStream_t stream);
 
 /* Down projection with the weighted combine fused: out[t] = sum over t's live
  * pairs (t, e) of w * (act_row W2_e^T), bf16 (out_bf16 = 1) or fp32 [T][H],
@@ -284,16 +293,13 @@ hipError_t xtu_i8_gemm_down(const int8_t* a8, const int32_t* crow, int H, int I,
  * _dma_hostbuf_range, vllm_xiaotu_moe/gpu_prefill.py:1897). */
 hipError_t xtu_copy_experts(int n, const int32_t* experts, const void* src, long src_stride,
                             void* dst, long dst_stride, long bytes, hipStream_t stream);
-
-/* -------------------------------------------------------------- probes
- * No reference counterpart: in-bounds checks of the device builtins this
- * library relies on (scaled fp4/fp8 converters, MFMA lane layouts, the
- * fixed-sequence exp/sigmoid), compared with host expectations by tests. */
-hipError_t xtu_probe_fp4(const float* scales, int nscale, uint32_t* out, hipStream_t stream);
-hipError_t xtu_probe_fp4_mul(const float* scales, int nscale, uint32_t* out, hipStream_t stream);
-hipError_t xtu_probe_fp8(uint32_t* out, hipStream_t stream);
-hipError_t xtu_probe_mfma(int which, const void* A, const void* B, void* C, hipStream_t stream);
-hipError_t xtu_probe_exp(const float* x, int n, float* e, float* s, hipStream_t stream);
+/* Pitched copy: height rows of width bytes, src rows spitch apart, dst rows
+ * dpitch apart (hipMemcpy2DAsync, any direction).  Replaces the engine's
+ * copy_hostbuf_to_device_2d (xiaotu_moe/csrc/python_binding/binding.cpp:
+ * 1404-1435), which DMAs a NUMA node's shard rows straight into their strided
+ * place in a device slot. */
+hipError_t xtu_copy_2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width,
+                       size_t height, hipStream_t stream);
 
 #ifdef __cplusplus
 }

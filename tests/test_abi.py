@@ -75,3 +75,30 @@ def test_library_loads_and_reports_version():
     assert rc == 1   # hipErrorInvalidValue
     assert all(_lib.load().xtu_gemm_tile_m(f) == 128 for f in range(4))
     assert _lib.load().xtu_gemm_tile_m(4) == 0
+
+
+PROBE_HEADER = os.path.join(os.path.dirname(os.path.abspath(__file__)), "probes", "xtu_probes.h")
+
+
+def _exports(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    return {l.split()[-1] for l in out.splitlines() if " T " in l}
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_product_library_carries_no_test_probes():
+    assert not [s for s in _exports(_lib.LIB_PATH) if s.startswith("xtu_probe")]
+
+
+def test_probe_library_matches_its_header():
+    from probes import probe_lib
+    global HEADER
+    saved, HEADER = HEADER, PROBE_HEADER
+    try:
+        protos = _prototypes()
+    finally:
+        HEADER = saved
+    assert set(protos) == set(probe_lib.SIGNATURES)
+    if os.path.exists(probe_lib.LIB_PATH):
+        assert not set(protos) - _exports(probe_lib.LIB_PATH)

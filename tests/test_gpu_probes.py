@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import oracle
-from xtu_moe_amd import _lib
+from probes import probe_lib as _lib
 from xtu_moe_amd.layer import _p, _stream
 
 pytestmark = pytest.mark.gpu

@@ -2,8 +2,9 @@
 
 The ring-streamed layer (experts copied tile by tile from pinned host memory,
 pool-resident experts read in place) equals the all-resident layer bit for
-bit; the pool's resident part equals the layer restricted to the resident
-experts, before and after swaps; the engine, the quant-method hook and the
+bit and the oracle within tolerance; the pool's resident part equals the
+layer restricted to the resident experts and the oracle restricted the same
+way, before and after swaps; the engine, the quant-method hook and the
 reference-signature layer entries agree with the oracle / the direct call."""
 import os
 import types
@@ -35,6 +36,16 @@ def _layer(fmt, E, NS, H, I, seed):
     return d, W
 
 
+def _oracle(fmt, d, x, ids, wts, E, NS, H, I, keep=None):
+    """The oracle layer; with `keep`, only those routed experts' pairs."""
+    ids = ids.cpu().numpy().copy() if torch.is_tensor(ids) else ids.copy()
+    wts = wts.cpu().numpy() if torch.is_tensor(wts) else wts
+    if keep is not None:
+        ids[~np.isin(ids, list(keep))] = -1
+    return oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS,
+                        H, I)
+
+
 def _inputs(T, K, E, H, seed, invalid=0.0):
     ids, wts = random_routing(T, K, E, seed=seed, invalid_frac=invalid)
     g = torch.Generator().manual_seed(seed)
@@ -46,7 +57,7 @@ def _inputs(T, K, E, H, seed, invalid=0.0):
 @pytest.mark.parametrize("nslots", [2, 3])
 def test_ring_equals_resident_layer_bitwise(fmt, nslots):
     E, NS, H, I, T, K = 32, 1, 512, 256, 300, 4
-    _, W = _layer(fmt, E, NS, H, I, seed=fmt + 30)
+    d, W = _layer(fmt, E, NS, H, I, seed=fmt + 30)
     x, ids, wts = _inputs(T, K, E, H, seed=7, invalid=0.05)
     ref = moe_forward(x, ids, wts, W, path="gemm", out_dtype=torch.float32)
     store = HostExpertStore.from_weights(W)
@@ -62,6 +73,32 @@ def test_ring_equals_resident_layer_bitwise(fmt, nslots):
     assert st.tiles == (len(streamed) + 4) // 5
     assert st.bytes == len(streamed) * store.expert_bytes()
     np.testing.assert_array_equal(out.cpu().numpy(), ref.cpu().numpy())
+    check_close(out.cpu().numpy(), _oracle(fmt, d, x, ids, wts, E, NS, H, I), bf16_out=False,
+                what=f"ring fmt={fmt}")
+
+
+def test_ring_takes_the_engine_object_and_accumulates_into_out():
+    """The reference calls the ring with its engine object and E, and adds
+    the layer into a given `out` (gpu_prefill.py:2984-3095)."""
+    E, H, I, T, K = 24, 512, 256, 200, 4
+    fmt = F.FMT_FP8
+    d = make_dense_layer(fmt, E, H, I, seed=34)
+    cfg = MOEConfigV2(expert_num=E, top_k=K, hidden_size=H, intermediate_size=I, groupN=128,
+                      groupK=128)
+    eng = MOE_FP8(cfg, d["w13"], d["w2"], d["s13"], d["s2"], device=DEV)
+    x, ids, wts = _inputs(T, K, E, H, seed=35, invalid=0.05)
+    wts[::7, 0] = 0.0     # zero-weight pairs: skipped, their experts need not stream
+    base = torch.randn((T, H), generator=torch.Generator().manual_seed(36)).to(DEV)
+    out = base.clone()
+    st = RingStats()
+    got = gpu_moe_layer_from_engine_tiled(eng, x, ids, wts, H, I, E, K, device=DEV,
+                                          group_k=128, nslots=2, out=out, tile_e=4, stats=st)
+    torch.cuda.synchronize()
+    assert got is out
+    ref = _oracle(fmt, d, x, ids, wts, E, 0, H, I)
+    check_close((out - base).cpu().numpy(), ref, bf16_out=False, what="ring via engine")
+    live = ((ids >= 0) & (ids < E) & (wts != 0))
+    assert st.bytes == len(set(ids[live].tolist())) * eng.host_store().expert_bytes()
 
 
 def test_ring_without_shared_home_falls_back():
@@ -86,28 +123,35 @@ def _restricted(W, x, ids, wts, resident):
 
 def test_pool_resident_part_and_swaps():
     E, NS, H, I, T, K = 24, 1, 512, 256, 64, 3
-    _, W = _layer(F.FMT_FP8, E, NS, H, I, seed=5)
+    d, W = _layer(F.FMT_FP8, E, NS, H, I, seed=5)
     x, ids, wts = _inputs(T, K, E, H, seed=6)
     store = HostExpertStore.from_weights(W)
     pool = LayerPool(store, DEV, H, I, 128, E, [1, 4, 7, 10, 13, 16], 0, layout="fp8")
     got = pool.forward(x, ids, wts, path="gemm", out_dtype=torch.float32)
     ref = _restricted(W, x, ids, wts, {1, 4, 7, 10, 13, 16})
     np.testing.assert_array_equal(got.cpu().numpy(), ref.cpu().numpy())
-    # swap expert 7 out and 20 in (slot 2), then 11 into the freed slot of 16
+    check_close(got.cpu().numpy(), _oracle(F.FMT_FP8, d, x, ids, wts, E, NS, H, I,
+                                           keep={1, 4, 7, 10, 13, 16}),
+                bf16_out=False, what="pool before swaps")
+    # swap expert 7 out and 20 in (slot 2), then 11 into the freed slot of 16;
+    # `gp` first, as the reference's adapter calls it
     assert pool.swap_out(2) == 7 and int(pool.slotmap[7]) == 7
-    assert pool.swap_in(20, 2) == 2 and int(pool.slotmap[20]) == E + 2
-    assert pool.swap_in(20, 3) is None   # already resident
+    assert pool.swap_in(GP, 20, 2) == 2 and int(pool.slotmap[20]) == E + 2
+    assert pool.swap_in(GP, 20, 3) is None   # already resident
     pool.swap_out(5)
-    pool.swap_in(11, 5)
+    pool.swap_in(GP, 11, 5)
     got = pool.forward(x, ids, wts, path="gemm", out_dtype=torch.float32)
     ref = _restricted(W, x, ids, wts, {1, 4, 20, 10, 13, 11})
     np.testing.assert_array_equal(got.cpu().numpy(), ref.cpu().numpy())
+    check_close(got.cpu().numpy(), _oracle(F.FMT_FP8, d, x, ids, wts, E, NS, H, I,
+                                           keep={1, 4, 20, 10, 13, 11}),
+                bf16_out=False, what="pool after swaps")
     assert pool.swaps_in == 2 and pool.swaps_out == 2
 
 
 def test_pool_routing_counts_and_adaptation(monkeypatch):
     E, NS, H, I, K = 16, 0, 256, 128, 2
-    _, W = _layer(F.FMT_MXFP4, E, NS, H, I, seed=8)
+    d, W = _layer(F.FMT_MXFP4, E, NS, H, I, seed=8)
     store = HostExpertStore.from_weights(W)
     pool = LayerPool(store, DEV, H, I, 32, E, [0, 1, 2, 3], 0)
     hot = torch.tensor([[9, 12]] * 30 + [[0, 9]] * 5, dtype=torch.int32, device=DEV)
@@ -117,13 +161,16 @@ def test_pool_routing_counts_and_adaptation(monkeypatch):
     assert counts[9] == 35 and counts[12] == 30 and counts[0] == 5 and sum(counts) == 70
     monkeypatch.setenv("XTU_PIN_WINDOW", "2")
     monkeypatch.setenv("XTU_PIN_MAXSWAP", "2")
-    assert pool.maybe_adapt() == 0                    # staging may be active: no-op
-    n = pool.maybe_adapt(staging_active=False)
+    assert pool.maybe_adapt(GP) == 0                  # staging may be active: no-op
+    n = pool.maybe_adapt(GP, staging_active=False)    # the reference's call form
     assert n == 2 and pool.expert_of == [0, 9, 12, 3]
     x, ids, wts = _inputs(20, K, E, H, seed=9)
     got = pool.forward(x, ids, wts, path="gemm", out_dtype=torch.float32)
-    ref = _restricted(W, x, ids, wts, set(e for e in pool.expert_of if e >= 0))
+    res = set(e for e in pool.expert_of if e >= 0)
+    ref = _restricted(W, x, ids, wts, res)
     np.testing.assert_array_equal(got.cpu().numpy(), ref.cpu().numpy())
+    check_close(got.cpu().numpy(), _oracle(F.FMT_MXFP4, d, x, ids, wts, E, NS, H, I, keep=res),
+                bf16_out=False, what="pool after adaptation")
 
 
 def test_engine_forward_many_matches_oracle():
@@ -144,7 +191,8 @@ def test_engine_forward_many_matches_oracle():
                        limit=7.0)
     check_close(out.cpu().numpy(), ref, bf16_out=False, what="engine fp8")
     g = eng.shard_geometry()
-    assert g["w13_bytes"] == 2 * I * H and eng.pin_hostbufs() == 4
+    assert g["w13_node_bytes"] == g["ns"] * 0 + E * 2 * g["w13_cbytes"]
+    assert g["w13_cbytes"] * g["ns"] == I * H and eng.pin_hostbufs() == 2 * g["ns"] + 2
     with pytest.raises(ValueError):
         MOE_MXFP4(MOEConfigV2(expert_num=E, top_k=K, hidden_size=H, intermediate_size=I,
                               groupN=128, groupK=128), d["w13"], d["w2"], device=DEV)

@@ -37,10 +37,11 @@ struct DecodeArgs {
   const float* gs;           // NVFP4 per-expert global scale (may be null)
   const int32_t* sorted_tok;
   const int32_t* seg_start;
-  const int32_t* active;
-  const int32_t* n_active;
+  const int32_t* active;     // work slots: active experts, or the 16-row tiles' experts
+  const int32_t* n_active;   // number of work slots
   const int32_t* slot_map;   // expert -> weight slot (null: identity)
   void* out;                 // gate/up: act bf16 [A][I]; down: y fp32 [A][H]
+  const int32_t* tile_row0;  // null: slot = whole expert from seg_start; else its first row
   int T, H, I;
   long w_estride, s_estride;
   float limit, alpha, beta;
@@ -248,7 +249,7 @@ __device__ __forceinline__ Item item_at(const DecodeArgs& a, int it, int per_exp
   const int slot = it / per_expert;
   c.sub = it - slot * per_expert;
   c.e = a.active[slot];
-  c.r0 = a.seg_start[c.e];
+  c.r0 = a.tile_row0 ? a.tile_row0[slot] : a.seg_start[c.e];
   c.na = min(a.seg_start[c.e + 1] - c.r0, kMaxTok);
   c.ws = a.slot_map ? a.slot_map[c.e] : c.e;
   return c;
@@ -342,7 +343,7 @@ __global__ __launch_bounds__(512) void decode_gate_up_kernel(DecodeArgs a) {
     issue_round<FMT, NU>(r, st, u0, u1, lane);
     __builtin_amdgcn_sched_barrier(0);
     if (!live) return;   // whole workgroup
-    const int r0 = a.seg_start[e];
+    const int r0 = a.tile_row0 ? a.tile_row0[slot] : a.seg_start[e];
     const int na = min(a.seg_start[e + 1] - r0, kMaxTok);
     const int tok = a.sorted_tok[r0 + min(m, na - 1)];
 #pragma unroll
@@ -489,7 +490,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
 
   const uint16_t* xa = xs + (m < nr ? m : 0) * a.I + q * F::kCK;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  if (!GENERIC) {
+  if (!GENERIC && c.na <= nr) {   // one round, every row staged
     consume_round<FMT, NU, true>(r, acc, u0, u1, xa, nullptr);
   } else if (c.na <= nr) {
     consume_round<FMT, NU, true>(r, acc, u0, u1, xa, nullptr);
@@ -1006,9 +1007,9 @@ hipError_t xtu_decode_gate_up(int fmt, const void* x, int T, int H, int I, const
                               const void* s13, const float* gs13, long w_estride,
                               long s_estride, const int32_t* slot_map,
                               const int32_t* sorted_tok, const int32_t* seg_start,
-                              const int32_t* active, const int32_t* n_active, int max_active,
-                              void* act, float limit, float alpha, float beta,
-                              hipStream_t stream) {
+                              const int32_t* active, const int32_t* tile_row0,
+                              const int32_t* n_active, int max_active, void* act, float limit,
+                              float alpha, float beta, hipStream_t stream) {
   XTU_CHECK_ARG(shape_ok(fmt, H, I) && max_active >= 0 && max_active <= 65535 && T >= 0 &&
                 T <= kMaxTok);
   XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
@@ -1017,16 +1018,17 @@ hipError_t xtu_decode_gate_up(int fmt, const void* x, int T, int H, int I, const
   if (max_active == 0 || T == 0) return hipSuccess;
   (void)hipGetLastError();
   DecodeArgs a{(const uint16_t*)x, (const uint8_t*)w13, (const uint8_t*)s13, gs13, sorted_tok,
-               seg_start, active, n_active, slot_map, act, T, H, I, w_estride, s_estride, limit,
-               alpha, beta, 0, 1, 1};
+               seg_start, active, n_active, slot_map, act, tile_row0, T, H, I, w_estride,
+               s_estride, limit, alpha, beta, 0, 1, 1};
   return dispatch_decode(fmt, 0, a, max_active, stream);
 }
 
 hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const void* w2,
                            const void* s2, const float* gs2, long w_estride, long s_estride,
                            const int32_t* slot_map, const int32_t* seg_start,
-                           const int32_t* active, const int32_t* n_active, int max_active,
-                           float* y, hipStream_t stream) {
+                           const int32_t* active, const int32_t* tile_row0,
+                           const int32_t* n_active, int max_active, float* y,
+                           hipStream_t stream) {
   XTU_CHECK_ARG(shape_ok(fmt, H, I) && max_active >= 0 && max_active <= 65535 && T >= 0 &&
                 T <= kMaxTok);
   XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
@@ -1034,8 +1036,8 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
   if (max_active == 0 || T == 0) return hipSuccess;
   (void)hipGetLastError();
   DecodeArgs a{(const uint16_t*)act, (const uint8_t*)w2, (const uint8_t*)s2, gs2, nullptr,
-               seg_start, active, n_active, slot_map, y, T, H, I, w_estride, s_estride, 0.f, 1.f,
-               0.f, 0, 1, 1};
+               seg_start, active, n_active, slot_map, y, tile_row0, T, H, I, w_estride,
+               s_estride, 0.f, 1.f, 0.f, 0, 1, 1};
   return dispatch_decode(fmt, 1, a, max_active, stream);
 }
 
@@ -1084,8 +1086,8 @@ hipError_t xtu_decode_route_shared(
   XTU_CHECK_ARG(epl != 0);
   (void)hipGetLastError();
   DecodeArgs a{(const uint16_t*)x, (const uint8_t*)w13, (const uint8_t*)s13, gs13, nullptr,
-               nullptr, nullptr, nullptr, slot_map, act_shared, T, H, I, w_estride, s_estride,
-               limit, alpha, beta, 0, 1, 1, 0};
+               nullptr, nullptr, nullptr, slot_map, act_shared, nullptr, T, H, I, w_estride,
+               s_estride, limit, alpha, beta, 0, 1, 1, 0};
   switch (fmt) {
     case kMXFP4: return launch_route_shared<kMXFP4>(mode, epl, ra, a, stream);
     case kNVFP4: return launch_route_shared<kNVFP4>(mode, epl, ra, a, stream);
@@ -1099,9 +1101,10 @@ hipError_t xtu_decode_gate_up_routed(int fmt, const void* x, int T, int H, int I
                                      const void* w13, const void* s13, const float* gs13,
                                      long w_estride, long s_estride, const int32_t* slot_map,
                                      const int32_t* sorted_tok, const int32_t* seg_start,
-                                     const int32_t* active, const int32_t* n_active,
-                                     int max_active, int n_shared, void* act, float limit,
-                                     float alpha, float beta, hipStream_t stream) {
+                                     const int32_t* active, const int32_t* tile_row0,
+                                     const int32_t* n_active, int max_active, int n_shared,
+                                     void* act, float limit, float alpha, float beta,
+                                     hipStream_t stream) {
   int ksplit = 0, xc = 0;
   XTU_CHECK_ARG(shape_ok(fmt, H, I) && max_active >= 0 && max_active <= 65535 && T >= 0 &&
                 T <= kMaxTok && n_shared >= 0 && n_shared <= max_active);
@@ -1112,8 +1115,8 @@ hipError_t xtu_decode_gate_up_routed(int fmt, const void* x, int T, int H, int I
   if (max_active == n_shared || T == 0) return hipSuccess;
   (void)hipGetLastError();
   DecodeArgs a{(const uint16_t*)x, (const uint8_t*)w13, (const uint8_t*)s13, gs13, sorted_tok,
-               seg_start, active, n_active, slot_map, act, T, H, I, w_estride, s_estride, limit,
-               alpha, beta, 0, 1, 1, n_shared};
+               seg_start, active, n_active, slot_map, act, tile_row0, T, H, I, w_estride,
+               s_estride, limit, alpha, beta, 0, 1, 1, n_shared};
   return dispatch_decode(fmt, 0, a, max_active - n_shared, stream);
 }
 

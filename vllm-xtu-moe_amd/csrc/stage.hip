@@ -30,4 +30,16 @@ hipError_t xtu_copy_experts(int n, const int32_t* experts, const void* src, long
   return hipSuccess;
 }
 
+// Pitched copy of `height` rows of `width` bytes (hipMemcpy2DAsync, any
+// direction).  Replaces the engine's copy_hostbuf_to_device_2d
+// (xiaotu_moe/csrc/python_binding/binding.cpp:1411-1435), which DMAs one NUMA
+// node's shard rows straight into their strided place in a device slot.
+hipError_t xtu_copy_2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width,
+                       size_t height, hipStream_t stream) {
+  XTU_CHECK_ARG(width <= dpitch && width <= spitch);
+  XTU_CHECK_ARG(width == 0 || height == 0 || (dst && src));
+  if (width == 0 || height == 0) return hipSuccess;
+  return hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyDefault, stream);
+}
+
 }  // extern "C"

@@ -30,9 +30,9 @@ SIGNATURES = {
     "xtu_segment": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp,
                          _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "xtu_decode_gate_up": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
-                                _vp, _i, _vp, _f, _f, _f, _vp]),
-    "xtu_decode_down": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _i,
-                             _vp, _vp]),
+                                _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
+    "xtu_decode_down": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
+                             _vp, _i, _vp, _vp]),
     "xtu_decode_down_combine_ok": (_i, [_i, _i, _i, _i, _i, _i, _i, _i]),
     "xtu_decode_down_combine": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _l, _l,
                                      _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp]),
@@ -42,7 +42,7 @@ SIGNATURES = {
                                      _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp,
                                      _vp, _f, _f, _f, _vp]),
     "xtu_decode_gate_up_routed": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp,
-                                       _vp, _vp, _vp, _i, _i, _vp, _f, _f, _f, _vp]),
+                                       _vp, _vp, _vp, _vp, _i, _i, _vp, _f, _f, _f, _vp]),
     "xtu_gemm_tile_m": (_i, [_i]),
     "xtu_gemm_gate_up": (_i, [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
                               _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
@@ -56,6 +56,7 @@ SIGNATURES = {
     "xtu_gemm8_down": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp,
                             _vp, _vp, _i, _vp, _vp]),
     "xtu_copy_experts": (_i, [_i, _vp, _vp, _l, _vp, _l, _l, _vp]),
+    "xtu_copy_2d": (_i, [_vp, _sz, _vp, _sz, _sz, _sz, _vp]),
     "xtu_i8_weight_bytes": (_sz, [_i, _i]),
     "xtu_i8_prepare": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "xtu_i8_quant_rows": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
@@ -63,11 +64,6 @@ SIGNATURES = {
                                  _i, _vp, _vp, _f, _f, _f, _vp]),
     "xtu_i8_gemm_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                               _vp, _vp]),
-    "xtu_probe_fp4": (_i, [_vp, _i, _vp, _vp]),
-    "xtu_probe_fp4_mul": (_i, [_vp, _i, _vp, _vp]),
-    "xtu_probe_fp8": (_i, [_vp, _vp]),
-    "xtu_probe_mfma": (_i, [_i, _vp, _vp, _vp, _vp]),
-    "xtu_probe_exp": (_i, [_vp, _i, _vp, _vp, _vp]),
 }
 
 # entry points whose int return value is a size/count, not a status

@@ -7,12 +7,14 @@ Mirrors the reference engine's Python binding
 :1438-1450 ``cpu_prefill`` -> ``MOE_V2::forward_many`` (moe_v2.hpp:651-957),
 :1478-1501 ``MOEConfigV2``; config fields moe_v2.hpp:125-147) and its host
 buffer ABI (:1368-1437 ``shard_geometry`` / ``pin_hostbufs`` /
-``copy_hostbuf_to_device``).  The reference engine computes on the CPU; here
+``copy_hostbuf_to_device`` / ``copy_hostbuf_to_device_2d``).  The reference engine computes on the CPU; here
 the same call runs the HIP kernels on the weights' device copy, and the
 pinned host copy serves the ring stage and the resident pool.
 """
 from __future__ import annotations
 
+import glob
+import os
 from dataclasses import dataclass
 
 import torch
@@ -90,9 +92,27 @@ class _Engine:
 
     # ------------------------------------------------------ host buffers
     def host_store(self) -> HostExpertStore:
+        """The pinned host copy of the experts, in shard_count() NUMA-node
+        shards (built on first use)."""
         if self._store is None:
-            self._store = HostExpertStore.from_weights(self.weights)
+            self._store = HostExpertStore.from_weights(self.weights, ns=self.shard_count())
         return self._store
+
+    def shard_count(self) -> int:
+        """Shards of the host copy: XIAOTU_MOE_NSHARD when >= 2, else the
+        host's NUMA node count; 1 when I and H do not split into 16-row
+        panels that many ways (as the reference engine falls back to one
+        copy, moe_v2.hpp:584-604)."""
+        try:
+            ns = int(os.environ.get("XIAOTU_MOE_NSHARD", "0") or 0)
+        except ValueError:
+            ns = 0
+        if ns < 2:
+            ns = max(1, len(glob.glob("/sys/devices/system/node/node[0-9]*")))
+        W = self.weights
+        if ns < 2 or W.I % (16 * ns) or W.H % (16 * ns):
+            return 1
+        return ns
 
     def shard_geometry(self) -> dict:
         return self.host_store().shard_geometry()
@@ -100,9 +120,17 @@ class _Engine:
     def pin_hostbufs(self) -> int:
         return self.host_store().pin_hostbufs()
 
-    def copy_hostbuf_to_device(self, which: int, node: int, dst_ptr: int, stream=None) -> int:
-        """Plane `which` (0 w13, 1 w2, 2 s13, 3 s2) of expert `node` -> dst."""
-        return self.host_store().copy_hostbuf_to_device(which, node, dst_ptr, stream)
+    def copy_hostbuf_to_device(self, which: int, node: int, dst: int, stream=None) -> int:
+        """Buffer `which` (0 w13 shard, 1 w2 shard, 2 s13, 3 s2) of NUMA node
+        `node` -> device address dst on `stream`; returns bytes (0: none)."""
+        return self.host_store().copy_hostbuf_to_device(which, node, dst, stream)
+
+    def copy_hostbuf_to_device_2d(self, which: int, node: int, src_off: int, dst: int,
+                                  dpitch: int, spitch: int, width: int, height: int,
+                                  stream=None) -> int:
+        """Pitched copy out of buffer `which` of `node` (0 on a bad request)."""
+        return self.host_store().copy_hostbuf_to_device_2d(which, node, src_off, dst, dpitch,
+                                                           spitch, width, height, stream)
 
 
 class MOE_BF16(_Engine):

@@ -137,10 +137,16 @@ class ReadySlot:
 class LayerPool:
     """One layer's pool (nslots = number of pinned experts)."""
 
-    def __init__(self, engine: HostExpertStore, device, hidden: int, inter: int, group_k: int,
+    def __init__(self, engine, device, hidden: int, inter: int, group_k: int,
                  n_local: int, pinned_local: list, layer_idx: int, layout: str = "mxfp4",
                  topk: int = 0):
         from .formats import FMT_NAMES
+        from .ring import _as_store
+        store = _as_store(engine)
+        if store is None:
+            raise ValueError("the pool needs an engine with a host store (MOE_* or "
+                             "HostExpertStore)")
+        engine = store
         if FMT_NAMES.get(engine.fmt) != str(layout):
             raise ValueError(f"pool layout {layout!r} does not match the store's "
                              f"{FMT_NAMES.get(engine.fmt)!r} weights")
@@ -238,10 +244,12 @@ class LayerPool:
         self._hits.index_add_(0, safe, w)
         self._win_t += 1
 
-    def swap_in(self, new_expert: int, s: int):
+    def swap_in(self, gp, new_expert: int, s: int):
         """Load new_expert into slot s on a side stream, then flip the map
         (the main stream waits for the copy first).  Returns s, or None if
-        the expert is already resident."""
+        the expert is already resident.  `gp` is the reference's loader
+        module argument (its gpu_prefill module, expert_pool.py:353); the
+        copy here is the host store's own, so it is accepted and unused."""
         if new_expert in self.expert_of:
             return None
         if self._side is None:
@@ -258,7 +266,7 @@ class LayerPool:
         self.swaps_in += 1
         return s
 
-    def maybe_adapt(self, *, staging_active: bool = True, window=None) -> int:
+    def maybe_adapt(self, gp=None, *, staging_active: bool = True, window=None) -> int:
         """Re-plan once per window of forwards (one device-to-host copy of the
         counts); returns the number of experts swapped in.  Does nothing
         unless the caller states that no staging burst is in flight."""
@@ -281,7 +289,7 @@ class LayerPool:
                 continue
             s = self.expert_of.index(victim)
             self.swap_out(s)
-            if self.swap_in(e, s) is not None:
+            if self.swap_in(gp, e, s) is not None:
                 n += 1
         return n
 

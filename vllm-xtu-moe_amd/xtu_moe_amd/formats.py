@@ -176,7 +176,14 @@ def pack_scales(fmt: int, s, N: int, K: int):
         return None
     E = s.shape[0]
     if fmt == FMT_FP8:
-        return s.float().contiguous().reshape(E, -1)
+        if s.dtype != torch.float32 or tuple(s.shape[1:]) != (N // 128, K // 128):
+            raise ValueError(f"FP8 block scales must be fp32 [E, {N // 128}, {K // 128}], "
+                             f"got {s.dtype} {tuple(s.shape)}")
+        return s.contiguous().reshape(E, -1)
+    gk = 32 if fmt == FMT_MXFP4 else 16
+    if s.element_size() != 1 or tuple(s.shape[1:]) != (N, K // gk):
+        raise ValueError(f"{FMT_NAMES[fmt]} scales must be one byte each [E, {N}, {K // gk}], "
+                         f"got {s.dtype} {tuple(s.shape)}")
     ug, nsb = SCALE_GROUP[fmt], K // 128
     G = scale_groups(fmt, K)
     per = 4 if fmt == FMT_MXFP4 else 8          # scale bytes per (row, super-block)

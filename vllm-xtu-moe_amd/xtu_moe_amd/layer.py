@@ -19,6 +19,7 @@ from . import _lib
 from .formats import (FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4, pack_scales, pack_weight)
 
 DECODE_MAX_TOKENS = 16
+DECODE_TILE = 16     # rows per work slot of the decode kernels (one MFMA M tile)
 SMALL_MAX_PAIRS = 1024
 # The one-launch router routes 4 tokens at a time in one workgroup (the tiny
 # path one wave per token); past this many tokens the multi-workgroup router
@@ -35,6 +36,19 @@ def _stream(stream=None) -> int:
     if stream is None:
         return int(torch.cuda.current_stream().cuda_stream)
     return int(stream.cuda_stream) if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _fp8_block_scales(s):
+    """FP8 block scales as fp32: uint8 planes holding fp32 bytes (last dim
+    x4, the reference pool's form) are reinterpreted, other float dtypes
+    converted by value."""
+    if s is None or s.dtype == torch.float32:
+        return s
+    if s.dtype == torch.uint8:
+        return s.contiguous().view(torch.float32)
+    if not s.is_floating_point():
+        raise ValueError(f"FP8 block scales of dtype {s.dtype}")
+    return s.float()
 
 
 class ExpertWeights:
@@ -61,6 +75,12 @@ class ExpertWeights:
     def device(self):
         return self.w13.device
 
+    def __iter__(self):
+        """(w13, s13, w2, s2): callers that star-unpack a pool's planes into a
+        layer entry (``gpu_moe_layer(x, ids, w, *pool.planes, ...)``) pass
+        the device-layout planes, which the entries use in place."""
+        return iter((self.w13, self.s13, self.w2, self.s2))
+
     @classmethod
     def from_dense(cls, fmt, w13, s13, w2, s2, gs13=None, gs2=None, *, E=None, n_shared=0,
                    device=None):
@@ -75,6 +95,8 @@ class ExpertWeights:
         def mv(t):
             return None if t is None else t.to(dev).contiguous()
 
+        if fmt == FMT_FP8:
+            s13, s2 = _fp8_block_scales(s13), _fp8_block_scales(s2)
         w13p = pack_weight(fmt, mv(w13))
         w2p = pack_weight(fmt, mv(w2))
         s13p = pack_scales(fmt, mv(s13), 2 * I, H)
@@ -106,16 +128,23 @@ class ExpertWeights:
         return self._i8
 
 
-class _Segmentation:
-    """Device buffers of one segmentation shape (process-lifetime cache)."""
+def _cap_rows(n: int) -> int:
+    """Row capacity for n rows: the next power of two (at least 16), so a
+    stream of varying token counts settles on a few allocations."""
+    n = max(int(n), 1)
+    return max(16, 1 << (n - 1).bit_length())
 
-    def __init__(self, T, K, E, NS, bm, device):
-        self.T, self.K, self.E, self.NS, self.bm = T, K, E, NS, bm
-        A = T * K + T * NS
+
+class _SegBuffers:
+    """Device buffers of the segmentation for (K, E, NS, bm) and up to
+    `cap_t` tokens (the sizes grow monotonically with T)."""
+
+    def __init__(self, cap_t, K, E, NS, bm, device):
+        self.cap_t = cap_t
+        A = cap_t * K + cap_t * NS
         NB = E + NS + 1
-        self.A, self.NB = A, NB
         i32 = dict(dtype=torch.int32, device=device)
-        self.ws = torch.empty(int(_lib.call("xtu_segment_workspace_bytes", T, K, E, NS)),
+        self.ws = torch.empty(int(_lib.call("xtu_segment_workspace_bytes", cap_t, K, E, NS)),
                               dtype=torch.uint8, device=device)
         Am = max(A, 1)
         self.sorted_pair = torch.empty(Am, **i32)
@@ -125,11 +154,38 @@ class _Segmentation:
         self.seg_start = torch.empty(NB + 1, **i32)
         self.active = torch.empty(NB, **i32)
         self.n_active = torch.empty(1, **i32)
-        self.max_tiles = int(_lib.call("xtu_segment_max_tiles", T, K, E, NS, bm))
-        self.tile_expert = torch.empty(self.max_tiles, **i32)
-        self.tile_row0 = torch.empty(self.max_tiles, **i32)
+        mt = int(_lib.call("xtu_segment_max_tiles", cap_t, K, E, NS, bm))
+        self.tile_expert = torch.empty(mt, **i32)
+        self.tile_row0 = torch.empty(mt, **i32)
         self.n_tiles = torch.empty(1, **i32)
         self.expert_tile_start = torch.empty(NB + 1, **i32)
+
+
+class _Segmentation:
+    """The segmentation of one call of T tokens, over cached buffers sized
+    for at least T tokens (views of their first rows)."""
+
+    def __init__(self, bufs: _SegBuffers, T, K, E, NS, bm):
+        self.T, self.K, self.E, self.NS, self.bm = T, K, E, NS, bm
+        A = T * K + T * NS
+        NB = E + NS + 1
+        self.A, self.NB = A, NB
+        self._bufs = bufs
+        Am = max(A, 1)
+        self.ws = bufs.ws
+        self.sorted_pair = bufs.sorted_pair[:Am]
+        self.sorted_tok = bufs.sorted_tok[:Am]
+        self.sorted_wts = bufs.sorted_wts[:Am]
+        self.inv = bufs.inv[:Am]
+        self.seg_start = bufs.seg_start
+        self.active = bufs.active
+        self.n_active = bufs.n_active
+        # grid bound of the GEMMs for this T (the buffers may hold more)
+        self.max_tiles = int(_lib.call("xtu_segment_max_tiles", T, K, E, NS, bm))
+        self.tile_expert = bufs.tile_expert[:self.max_tiles]
+        self.tile_row0 = bufs.tile_row0[:self.max_tiles]
+        self.n_tiles = bufs.n_tiles
+        self.expert_tile_start = bufs.expert_tile_start
 
     def run(self, ids, wts, id_map=None, drop_zero=True, stream=None):
         _lib.call("xtu_segment", _p(ids), _p(wts), _p(id_map), self.T, self.K, self.E, self.NS,
@@ -164,28 +220,62 @@ class _Segmentation:
 
 _SEG_CACHE: dict = {}
 _BUF_CACHE: dict = {}
+# Buffers replaced by a larger one.  They stay allocated for the life of the
+# process: a captured HIP graph may still hold their addresses.  Growth is
+# geometric (power-of-two rows), so they total less than the live ones.
+_RETIRED: list = []
+# Streams that own scratch per device; past this many, the least recently
+# used stream's buffers are dropped (a stream that comes back reallocates).
+MAX_STREAMS = 8
+_STREAM_LRU: dict = {}
+
+
+def _touch_stream(device, stream: int) -> None:
+    lru = _STREAM_LRU.setdefault(str(device), [])
+    if lru and lru[-1] == stream:
+        return
+    if stream in lru:
+        lru.remove(stream)
+    lru.append(stream)
+    while len(lru) > MAX_STREAMS:
+        old = lru.pop(0)
+        for cache in (_SEG_CACHE, _BUF_CACHE):
+            for k in [k for k in cache if k[-2] == str(device) and k[-1] == old]:
+                del cache[k]
 
 
 def segmentation(T, K, E, NS, bm, device, stream=None) -> _Segmentation:
-    """The segmentation buffers of this shape for (device, stream): calls on
-    one stream run in order and share them; another stream gets its own."""
-    key = (T, K, E, NS, bm, str(device), _stream(stream))
-    s = _SEG_CACHE.get(key)
-    if s is None:
-        s = _Segmentation(T, K, E, NS, bm, device)
-        _SEG_CACHE[key] = s
-    return s
+    """The segmentation of T tokens, over buffers kept per (shape without T,
+    device, stream): calls on one stream run in order and share them;
+    another stream gets its own.  Capacity grows to the next power of two
+    of T, so varying batch sizes allocate O(log T_max) times in total."""
+    st = _stream(stream)
+    _touch_stream(device, st)
+    key = (K, E, NS, bm, str(device), st)
+    b = _SEG_CACHE.get(key)
+    if b is None or b.cap_t < T:
+        if b is not None:
+            _RETIRED.append(b)
+        b = _SegBuffers(_cap_rows(T), K, E, NS, bm, device)
+        _SEG_CACHE[key] = b
+    return _Segmentation(b, T, K, E, NS, bm)
 
 
 def _buf(name, shape, dtype, device, stream=None):
-    """Scratch buffer `name` of this shape for (device, stream), kept for the
-    process (stream-ordered reuse; concurrent streams get their own)."""
-    key = (name, tuple(shape), dtype, str(device), _stream(stream))
+    """Scratch buffer `name` of shape (rows, *tail) for (device, stream): the
+    first `rows` rows of a cached buffer whose row capacity is a power of two
+    (stream-ordered reuse; concurrent streams get their own)."""
+    rows, tail = int(shape[0]), tuple(int(s) for s in shape[1:])
+    st = _stream(stream)
+    _touch_stream(device, st)
+    key = (name, tail, dtype, str(device), st)
     t = _BUF_CACHE.get(key)
-    if t is None:
-        t = torch.empty(shape, dtype=dtype, device=device)
+    if t is None or t.shape[0] < rows:
+        if t is not None:
+            _RETIRED.append(t)
+        t = torch.empty((_cap_rows(rows),) + tail, dtype=dtype, device=device)
         _BUF_CACHE[key] = t
-    return t
+    return t[:rows]
 
 
 def _same_device(dev, **tensors):
@@ -243,6 +333,14 @@ def int8_align_on(T: int, allowed: bool = True) -> bool:
     except ValueError:
         m = 160
     return m > 0 and int(T) >= m
+
+
+def decode_max_tiles(A: int, max_active: int) -> int:
+    """Upper bound on the 16-row tiles of a decode batch of A pairs over at
+    most max_active non-empty expert buckets: a bucket of n rows has
+    ceil(n/16) <= 1 + (n-1)//16 tiles, so the total is at most
+    b + (A - b)//16 for b non-empty buckets, which grows with b."""
+    return int(max_active) + max(int(A) - int(max_active), 0) // DECODE_TILE
 
 
 def gemm_tile_m(fmt: int, int8: bool = False) -> int:
@@ -366,7 +464,9 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         path = "decode" if (T <= DECODE_MAX_TOKENS and not int8) else "gemm"
     if path == "decode" and T > DECODE_MAX_TOKENS:
         raise ValueError(f"decode path handles at most {DECODE_MAX_TOKENS} tokens")
-    bm = gemm_tile_m(fmt, int8)
+    # decode: the gate/up and down kernels take the segmentation's 16-row
+    # tiles as work slots (every row of a bucket, however many)
+    bm = DECODE_TILE if path == "decode" else gemm_tile_m(fmt, int8)
     seg = segmentation(T, K, E, NS, bm, dev, st)
     odt = out_dtype if out is None else out.dtype
     max_active = min(E, T * K) + NS
@@ -420,14 +520,17 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         return (out, seg) if return_seg else out
     if path == "decode":
         act = _buf("act", (max(A, 1), I), torch.bfloat16, dev, st)
+        max_dt = decode_max_tiles(A, max_active)
         if split:
             _lib.call("xtu_decode_gate_up_routed", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13),
                       _p(W.gs13), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start),
-                      _p(seg.active), _p(seg.n_active), max_active, NS, _p(act), lim, al, be, st)
+                      _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.n_tiles), max_dt, NS,
+                      _p(act), lim, al, be, st)
         else:
             _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13),
                       _p(W.gs13), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start),
-                      _p(seg.active), _p(seg.n_active), max_active, _p(act), lim, al, be, st)
+                      _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.n_tiles), max_dt, _p(act),
+                      lim, al, be, st)
         if split or (odt in (torch.bfloat16, torch.float32)
                      and decode_fused_down_use(fmt, T, A, H, I, max_active, E + NS)):
             # down projection and weighted combine in one pass, out written whole
@@ -439,8 +542,8 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
             return (out, seg) if return_seg else out
         y = _buf("y", (max(A, 1), H), torch.float32, dev, st)
         _lib.call("xtu_decode_down", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
-                  _p(slot_map), _p(seg.seg_start), _p(seg.active), _p(seg.n_active), max_active,
-                  _p(y), st)
+                  _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
+                  _p(seg.n_tiles), max_dt, _p(y), st)
     else:
         y = _buf("y", (max(A, 1), H), torch.float32, dev, st)
         expert_pass(x, seg, W, 0, E + NS, y, slot_map=slot_map, int8=int8,

@@ -22,7 +22,7 @@ import enum
 import torch
 
 from . import formats as F
-from .layer import ExpertWeights, moe_forward, route
+from .layer import ExpertWeights, _buf as _scratch, moe_forward, route
 
 _ROUTING_ATTRS = ("use_grouped_topk", "renormalize", "scoring_func", "custom_routing_function",
                   "num_expert_group", "topk_group", "e_score_correction_bias",
@@ -158,24 +158,57 @@ class XiaotuExperts:
             self.e_score_correction_bias = e_score_correction_bias
         if routed_scaling_factor is not None:
             self.routed_scaling_factor = routed_scaling_factor
+        T = hidden_states.shape[0]
+        x = hidden_states
+        if x.dtype != torch.bfloat16 or not x.is_contiguous():
+            x = x.to(torch.bfloat16).contiguous()
+        odt = hidden_states.dtype if hidden_states.dtype in (torch.bfloat16, torch.float32) \
+            else torch.float32
+        direct = (output is not None and output.dtype == odt and output.is_contiguous()
+                  and tuple(output.shape) == (T, self._weights.H) and output.device == x.device)
+        kw = dict(swiglu_limit=float(self.swiglu_limit or 0.0),
+                  swiglu_alpha=float(self.swiglu_alpha if self.swiglu_alpha is not None else 1.0),
+                  swiglu_beta=float(self.swiglu_beta or 0.0),
+                  out=output if direct else None, out_dtype=odt)
         if topk_weights is not None and topk_ids is not None:
-            topk_weights = topk_weights.to(torch.float32)
-            topk_ids = topk_ids.to(torch.int32)
+            res = moe_forward(x, topk_ids.to(torch.int32).contiguous(),
+                              topk_weights.to(torch.float32).contiguous(), self._weights, **kw)
+        elif (expert_map is None and self.custom_routing_function is None
+              and router_logits is not None):
+            # monolithic path: routing (+ segmentation, + the shared experts'
+            # gate/up at decode sizes) inside the layer's own launches
+            ids = _scratch("hook_ids", (T, int(self.top_k)), torch.int32, x.device)
+            wts = _scratch("hook_wts", (T, int(self.top_k)), torch.float32, x.device)
+            res = moe_forward(x, ids, wts, self._weights, router=self._router_args(router_logits),
+                              **kw)
         else:
             topk_weights, topk_ids = self._select_topk(hidden_states, router_logits)
             if expert_map is not None:
                 topk_ids, topk_weights = self._local_ids(expert_map, topk_ids, topk_weights)
-        x = hidden_states.to(torch.bfloat16).contiguous()
-        res = moe_forward(x, topk_ids.contiguous(), topk_weights.contiguous(), self._weights,
-                          swiglu_limit=float(self.swiglu_limit or 0.0),
-                          swiglu_alpha=float(self.swiglu_alpha if self.swiglu_alpha is not None else 1.0),
-                          swiglu_beta=float(self.swiglu_beta or 0.0),
-                          out_dtype=torch.float32)
+            res = moe_forward(x, topk_ids.contiguous(), topk_weights.contiguous(), self._weights,
+                              **kw)
+        if direct:
+            return output
         res = res.to(hidden_states.dtype)
         if output is not None:
             output.copy_(res)
             return output
         return res
+
+    def _router_args(self, router_logits) -> dict:
+        lg = router_logits
+        if lg.dtype != torch.float32 or not lg.is_contiguous():
+            lg = lg.float().contiguous()
+        if self.use_grouped_topk or str(self.scoring_func) == "sigmoid":
+            bias = self.e_score_correction_bias
+            if bias is not None:
+                bias = bias.to(device=lg.device, dtype=torch.float32).contiguous()
+            return dict(logits=lg, scoring=str(self.scoring_func), bias=bias,
+                        n_group=int(self.num_expert_group or 1),
+                        topk_group=int(self.topk_group or 1),
+                        routed_scaling_factor=float(self.routed_scaling_factor or 1.0),
+                        renormalize=bool(self.renormalize))
+        return dict(logits=lg, scoring="softmax", renormalize=bool(self.renormalize))
 
 
 class XiaotuExpertsBF16(XiaotuExperts):

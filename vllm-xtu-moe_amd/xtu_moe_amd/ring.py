@@ -128,32 +128,45 @@ class RingStats:
         self.dma_ms = sum(a.elapsed_time(b) for a, b in self.events)
 
 
-def gpu_moe_layer_from_engine_tiled(engine: HostExpertStore, x, topk_ids, topk_weights, H: int,
-                                    I: int, E: int, K: int, *, device, group_k: int = 32,
-                                    nslots: int = 2, out=None, swiglu_limit: float = 0.0,
-                                    pool=None, tile_e=None, out_dtype=torch.bfloat16,
-                                    stats: RingStats | None = None):
+def _as_store(engine):
+    """The HostExpertStore behind `engine`: the store itself, or an engine
+    object (``MOE_*``) exposing one through ``host_store()``; None else."""
+    if isinstance(engine, HostExpertStore):
+        return engine
+    hs = getattr(engine, "host_store", None)
+    return hs() if callable(hs) else None
+
+
+def gpu_moe_layer_from_engine_tiled(engine, x, topk_ids, topk_weights, H: int, I: int, E: int,
+                                    K: int, *, device, group_k: int = 32, nslots: int = 2,
+                                    out=None, swiglu_limit: float = 0.0, pool=None, tile_e=None,
+                                    out_dtype=torch.bfloat16, stats: RingStats | None = None):
     """One layer's routed (+ shared) experts with the weights streamed from
-    `engine` (a HostExpertStore) through the tile ring; experts resident in
-    `pool` (a LayerPool) are read in place.  Returns out [T, H], or None when
-    the layer cannot be streamed (shape mismatch)."""
+    `engine` (an ``MOE_*`` engine object or its HostExpertStore) through the
+    tile ring; experts resident in `pool` (a LayerPool) are read in place.
+    Returns out [T, H]: a new tensor (out_dtype) holding the layer, or the
+    given `out` with the layer added to it (the reference accumulates into
+    `out`, gpu_prefill.py:3020, gpu_prefill_fp8.py:1478).  None when the
+    layer cannot be streamed (no host store, or a shape mismatch)."""
     device = torch.device(device)
-    if not isinstance(engine, HostExpertStore) or engine.H != int(H) or engine.I != int(I) \
-            or engine.E != int(E):
+    store = _as_store(engine)
+    if store is None or store.H != int(H) or store.I != int(I) or store.E != int(E):
         return None
+    engine = store
     T = x.shape[0]
     NS = engine.n_shared
     fmt = engine.fmt
-    if out is None:
-        out = torch.empty((T, H), dtype=out_dtype, device=device)
+    acc = out
+    out = torch.empty((T, H), dtype=out_dtype if acc is None else acc.dtype, device=device)
     if T == 0 or K == 0:
         out.zero_()
-        return out
+        return out if acc is None else acc
     st = torch.cuda.current_stream(device)
     ids = topk_ids.to(torch.int32).contiguous()
     wts = topk_weights.float().contiguous()
-    # which experts the batch routes to (one device-to-host copy of E counts)
-    valid = (ids >= 0) & (ids < E)
+    # which experts the batch routes to with a non-zero weight (one
+    # device-to-host copy of E counts): zero-weight pairs are skipped
+    valid = (ids >= 0) & (ids < E) & (wts != 0)
     counts = torch.bincount(ids[valid].long(), minlength=E)
     routed = torch.nonzero(counts > 0).flatten().tolist()
     resident = pool.resident_map() if pool is not None else {}
@@ -218,4 +231,7 @@ def gpu_moe_layer_from_engine_tiled(engine: HostExpertStore, x, topk_ids, topk_w
     combine(seg, y, wts, out, stream=st)
     if stats is not None:
         stats.bytes, stats.tiles = moved, ntile
+    if acc is not None:
+        acc.add_(out)
+        return acc
     return out
