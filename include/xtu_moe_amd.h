@@ -77,6 +77,26 @@ hipError_t xtu_segment(const int32_t* topk_ids, const float* topk_weights, const
                        int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
                        int32_t* expert_tile_start, hipStream_t stream);
 
+/* xtu_segment without the workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * workspace is a static device array of 4 MiB per GPU, held until the process
+ * ends, so the call allocates nothing.  Outputs and their meaning are
+ * xtu_segment's.  Shapes whose xtu_segment_workspace_bytes() exceeds 4 MiB
+ * (1M per-block bucket counts, e.g. up to 16.6M pairs at 258 buckets, 2M at
+ * 2048) are rejected with hipErrorInvalidValue and a message on stderr.  The
+ * array is shared by every call on a GPU and holds the last call's counts
+ * (each call rewrites every word it reads, so nothing needs clearing): calls
+ * that overlap on one GPU (different streams) race -- serialise them.  The
+ * stream must belong to the current device. */
+hipError_t xtu_segment_noalloc(const int32_t* topk_ids, const float* topk_weights,
+                               const int32_t* id_map, int T, int K, int E, int n_shared,
+                               int drop_zero, int bm, int32_t* sorted_pair, int32_t* sorted_tok,
+                               float* sorted_wts, int32_t* inv, int32_t* seg_start,
+                               int32_t* active, int32_t* n_active, int32_t* tile_expert,
+                               int32_t* tile_row0, int32_t* n_tiles, int32_t* expert_tile_start,
+                               hipStream_t stream);
+
 /* Small batches (A = T*K + T*n_shared <= xtu_route_segment_small_max_pairs()):
  * routing and the whole segmentation in one launch, same outputs as
  * xtu_route_* followed by xtu_segment.  mode 0 = softmax routing, 1 = grouped

@@ -13,8 +13,18 @@
 // per-block stable scatter).  Ranks inside a block are exact: a wave finds
 // the lanes sharing its bucket with ballots, waves are ordered through LDS
 // counters, and blocks through the scanned histogram.
+#include <mutex>
+#include <stdio.h>
+
 #include "route_tiny.hpp"
 #include "xtu_common.hpp"
+
+// Segmentation workspace of xtu_segment_noalloc: one statically allocated
+// array per GPU (each device holds its own copy until the process ends).
+// Host code must not use this name as an address: it is a host-side stand-in.
+// The device address comes from hipGetSymbolAddress, once per device.
+static constexpr size_t kNoAllocScratchBytes = 4u << 20;
+static __device__ __align__(256) int32_t scratch[kNoAllocScratchBytes / sizeof(int32_t)];
 
 namespace xtu {
 namespace {
@@ -766,12 +776,20 @@ int xtu_segment_max_tiles(int T, int K, int E, int n_shared, int bm) {
   return (int)(A / bm + (A < nb ? A : nb) + 1);
 }
 
-hipError_t xtu_segment(const int32_t* topk_ids, const float* topk_weights,
-                       const int32_t* id_map, int T, int K, int E, int n_shared, int drop_zero,
-                       int bm, void* workspace, int32_t* sorted_pair, int32_t* sorted_tok,
-                       float* sorted_wts, int32_t* inv, int32_t* seg_start, int32_t* active,
-                       int32_t* n_active, int32_t* tile_expert, int32_t* tile_row0,
-                       int32_t* n_tiles, int32_t* expert_tile_start, hipStream_t stream) {
+}  // extern "C"
+
+namespace xtu {
+namespace {
+
+// The three segmentation launches over a caller-supplied workspace of
+// xtu_segment_workspace_bytes() bytes (every word written by seg_hist_kernel
+// before seg_scan_kernel reads it, so it needs no clearing).
+hipError_t segment_impl(const int32_t* topk_ids, const float* topk_weights,
+                        const int32_t* id_map, int T, int K, int E, int n_shared, int drop_zero,
+                        int bm, void* workspace, int32_t* sorted_pair, int32_t* sorted_tok,
+                        float* sorted_wts, int32_t* inv, int32_t* seg_start, int32_t* active,
+                        int32_t* n_active, int32_t* tile_expert, int32_t* tile_row0,
+                        int32_t* n_tiles, int32_t* expert_tile_start, hipStream_t stream) {
   XTU_CHECK_ARG(T >= 0 && K >= 0 && E > 0 && n_shared >= 0 && bm > 0);
   const int NB = E + n_shared + 1;
   XTU_CHECK_ARG(NB <= 2048);
@@ -795,6 +813,68 @@ hipError_t xtu_segment(const int32_t* topk_ids, const float* topk_weights,
         a, bcnt, seg_start, sorted_pair, sorted_tok, sorted_wts, inv);
   }
   return hipPeekAtLastError();
+}
+
+// Device address of `scratch` on the current device, looked up once per
+// device (hipGetSymbolAddress with that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+hipError_t scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+}  // namespace xtu
+
+extern "C" {
+
+hipError_t xtu_segment(const int32_t* topk_ids, const float* topk_weights,
+                       const int32_t* id_map, int T, int K, int E, int n_shared, int drop_zero,
+                       int bm, void* workspace, int32_t* sorted_pair, int32_t* sorted_tok,
+                       float* sorted_wts, int32_t* inv, int32_t* seg_start, int32_t* active,
+                       int32_t* n_active, int32_t* tile_expert, int32_t* tile_row0,
+                       int32_t* n_tiles, int32_t* expert_tile_start, hipStream_t stream) {
+  return segment_impl(topk_ids, topk_weights, id_map, T, K, E, n_shared, drop_zero, bm,
+                      workspace, sorted_pair, sorted_tok, sorted_wts, inv, seg_start, active,
+                      n_active, tile_expert, tile_row0, n_tiles, expert_tile_start, stream);
+}
+
+hipError_t xtu_segment_noalloc(const int32_t* topk_ids, const float* topk_weights,
+                               const int32_t* id_map, int T, int K, int E, int n_shared,
+                               int drop_zero, int bm, int32_t* sorted_pair, int32_t* sorted_tok,
+                               float* sorted_wts, int32_t* inv, int32_t* seg_start,
+                               int32_t* active, int32_t* n_active, int32_t* tile_expert,
+                               int32_t* tile_row0, int32_t* n_tiles, int32_t* expert_tile_start,
+                               hipStream_t stream) {
+  XTU_CHECK_ARG(T >= 0 && K >= 0 && E > 0 && n_shared >= 0);
+  const size_t need = xtu_segment_workspace_bytes(T, K, E, n_shared);
+  if (need > kNoAllocScratchBytes) {
+    fprintf(stderr,
+            "xtu_segment_noalloc: T=%d K=%d E=%d n_shared=%d needs %zu bytes of workspace, more "
+            "than the %zu-byte static scratch; use xtu_segment with a workspace\n",
+            T, K, E, n_shared, need, kNoAllocScratchBytes);
+    return hipErrorInvalidValue;
+  }
+  void* ws = nullptr;
+  const hipError_t e = scratch_address(&ws);
+  if (e != hipSuccess) return e;
+  return segment_impl(topk_ids, topk_weights, id_map, T, K, E, n_shared, drop_zero, bm, ws,
+                      sorted_pair, sorted_tok, sorted_wts, inv, seg_start, active, n_active,
+                      tile_expert, tile_row0, n_tiles, expert_tile_start, stream);
 }
 
 int xtu_route_segment_small_max_pairs(void) { return kSmallMaxA; }

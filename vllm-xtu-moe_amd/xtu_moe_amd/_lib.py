@@ -29,6 +29,8 @@ SIGNATURES = {
     "xtu_segment_max_tiles": (_i, [_i, _i, _i, _i, _i]),
     "xtu_segment": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp,
                          _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "xtu_segment_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp,
+                                 _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "xtu_decode_gate_up": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
                                 _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
     "xtu_decode_down": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
