@@ -282,7 +282,11 @@ hipError_t xtu_gemm8_down(const uint8_t* hi, const uint8_t* lo, const uint8_t* s
  * xiaotu_quant_row_align_into, :811-858 xiaotu_i8_align_tile).
  * xtu_i8_prepare expands MXFP4 weights (P16) of E experts into shifted int8
  * w8' (P16 with 16 int8 per chunk, N*K bytes per expert) and emin [E][N];
- * *dmax (zero on entry) receives the largest shift (the path needs <= 3).
+ * *dmax (zero on entry) receives the largest shift.  A row whose shift
+ * exceeds 3 is marked (emin 0xFF, int8 weights 0): the integer GEMMs leave
+ * its output column unwritten (gate/up: act column n when gate row n or up
+ * row n is marked) and xtu_i8_fallback computes it in fp32 -- the reference
+ * sends such tiles to its fp32 path (moe_v2_packed4_w4a8.inc:1344-1366).
  * xtu_i8_quant_rows: per-row power-of-two int8 quantisation of bf16 rows.
  * The GEMMs accumulate in int32 (optionally stored to acc_out [A][N]) and
  * apply 2^(emin-128+crow) in fp32; epilogues as the bf16 GEMMs. */
@@ -303,6 +307,20 @@ hipError_t xtu_i8_gemm_down(const int8_t* a8, const int32_t* crow, int H, int I,
                             const int32_t* tile_expert, const int32_t* tile_row0,
                             const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
                             float* y, int32_t* acc_out, hipStream_t stream);
+/* fp32 path for the marked columns: gate_up = 1 writes act[m][n] =
+ * bf16(SwiGLU(x.w_gate_n, x.w_up_n)) for the column pairs n listed per weight
+ * slot (CSR col_start [slots + 1] / cols), x rows gathered through
+ * sorted_tok; gate_up = 0 writes y[m][h] = act_m . w2_h for the listed rows
+ * h.  Operands: bf16 activations (x / act) and the MXFP4 weights (P16 codes
+ * and packed e8m0 scales) dequantised exactly; fp32 sums.  Tiles of bm <= 128
+ * rows from the same tile list as the integer GEMMs. */
+hipError_t xtu_i8_fallback(int gate_up, const void* x, const int32_t* sorted_tok, int H, int I,
+                           const void* w, const void* s, const int32_t* slot_map,
+                           const int32_t* seg_start, const int32_t* tile_expert,
+                           const int32_t* tile_row0, const int32_t* tile_lo,
+                           const int32_t* tile_hi, int max_tiles, int bm,
+                           const int32_t* col_start, const int32_t* cols, void* out, float limit,
+                           float alpha, float beta, hipStream_t stream);
 
 /* ------------------------------------------------ expert staging (ring / pool)
  * dst[i*dst_stride, +bytes) <- src[experts[i]*src_stride, +bytes), i < n, as

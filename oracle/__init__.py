@@ -109,7 +109,9 @@ def route_softmax_topk(logits: np.ndarray, K: int, renormalize: bool = True):
     T, E = logits.shape
     ids = np.zeros((T, K), np.int32)
     wts = np.zeros((T, K), np.float32)
-    lib().xo_route_softmax_topk(_p(logits), T, E, K, int(renormalize), _p(ids), _p(wts))
+    rc = lib().xo_route_softmax_topk(_p(logits), T, E, K, int(renormalize), _p(ids), _p(wts))
+    if rc != 0:
+        raise ValueError(f"oracle softmax router: unsupported E={E} K={K}")
     return ids, wts
 
 
@@ -120,8 +122,10 @@ def route_grouped_sigmoid(logits, bias, n_group, topk_group, K, routed_scaling=1
     b = None if bias is None else np.ascontiguousarray(bias, np.float32)
     ids = np.zeros((T, K), np.int32)
     wts = np.zeros((T, K), np.float32)
-    lib().xo_route_grouped_sigmoid(_p(logits), _p(b), T, E, n_group, topk_group, K,
-                                   float(routed_scaling), int(renormalize), _p(ids), _p(wts))
+    rc = lib().xo_route_grouped_sigmoid(_p(logits), _p(b), T, E, n_group, topk_group, K,
+                                        float(routed_scaling), int(renormalize), _p(ids), _p(wts))
+    if rc != 0:
+        raise ValueError(f"oracle grouped router: unsupported E={E} n_group={n_group} K={K}")
     return ids, wts
 
 

@@ -16,8 +16,14 @@
  *   xo_segment                       numpy stable argsort restatement + brute force
  *   xo_moe_layer (bf16/fp8/mxfp4/nvfp4) vs the compiled reference engine
  *                                    (oracle/_ref) forward_many, rel err ~1e-6
- *   xo_i8_* (INT8 ALIGN)             vs the compiled reference engine's MXFP4
- *                                    traits with the ALIGN gate on (bit-exact C)
+ *   xo_i8_* (INT8 ALIGN)             int32 accumulators bit-exact against an
+ *                                    int64 closed form built from the codec
+ *                                    tables (brute force); the layer (marked
+ *                                    rows' fp32 fallback included) against the
+ *                                    compiled reference engine with the ALIGN
+ *                                    gate on, within the layer tolerance (the
+ *                                    engine's lane-sum order differs, so C is
+ *                                    not bit-exact)
  */
 #include <math.h>
 #include <stdint.h>
@@ -74,7 +80,8 @@ static float bf16_round(float f) { return xo_bf16_to_f32(xo_f32_to_bf16(f)); }
 
 /* ------------------------------------------------------------------------ */
 /* exp / sigmoid: the build's own fp32 formula, restated operation by        */
-/* operation from the device code (vllm-xtu-moe_amd/csrc/xtu_math.hpp).      */
+/* operation from the device code (vllm-xtu-moe_amd/csrc/xtu_common.hpp,    */
+/* xtu_expf / xtu_sigmoid).                                                  */
 /* Cody-Waite reduction x = k ln2 + r, |r| <= ln2/2, degree-7 Taylor in r,   */
 /* Horner with fused multiply-add, scale by 2^k through the exponent field.  */
 /* ------------------------------------------------------------------------ */
@@ -125,8 +132,9 @@ static int better(float sa, int ia, float sb, int ib) {
  *   e_i = exp(l_i - l_max),  w_i = e_i / (e_0 + e_1 + ... + e_{K-1})
  * summed in selection order.  renormalize == 0: w_i = e_i / sum_all where
  * sum_all adds e_0..e_{E-1} in index order. */
-void xo_route_softmax_topk(const float* logits, int T, int E, int K, int renormalize,
-                           int32_t* ids, float* wts) {
+int xo_route_softmax_topk(const float* logits, int T, int E, int K, int renormalize,
+                          int32_t* ids, float* wts) {
+  if (E < 1 || K < 1 || K > 64 || K > E) return -1;
   int sel[64];
   for (int t = 0; t < T; ++t) {
     const float* l = logits + (size_t)t * E;
@@ -156,6 +164,7 @@ void xo_route_softmax_topk(const float* logits, int T, int E, int K, int renorma
       wts[(size_t)t * K + k] = ev[k] / s;
     }
   }
+  return 0;
 }
 
 /* DeepSeek-V3 grouped sigmoid routing:
@@ -164,9 +173,12 @@ void xo_route_softmax_topk(const float* logits, int T, int E, int K, int renorma
  *   keep the topk_group best groups, then the K best b_i inside them
  *   w_i = s_i / (s_0 + ... + s_{K-1}) * routed_scaling   (renormalize)
  *   w_i = s_i * routed_scaling                          (renormalize == 0) */
-void xo_route_grouped_sigmoid(const float* logits, const float* bias, int T, int E,
-                              int n_group, int topk_group, int K, float routed_scaling,
-                              int renormalize, int32_t* ids, float* wts) {
+int xo_route_grouped_sigmoid(const float* logits, const float* bias, int T, int E,
+                             int n_group, int topk_group, int K, float routed_scaling,
+                             int renormalize, int32_t* ids, float* wts) {
+  if (E < 1 || E > 1024 || n_group < 1 || n_group > 64 || E % n_group || K < 1 || K > 64 ||
+      topk_group < 1 || topk_group > n_group || K > topk_group * (E / n_group))
+    return -1;
   const int gsz = E / n_group;
   float s[1024], b[1024], g[64];
   int gsel[64], sel[64];
@@ -219,6 +231,7 @@ void xo_route_grouped_sigmoid(const float* logits, const float* bias, int T, int
           renormalize ? (s[sel[k]] / sum) * routed_scaling : s[sel[k]] * routed_scaling;
     }
   }
+  return 0;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -483,9 +496,34 @@ int xo_i8_gemm(const float* a, int M, const uint8_t* w, const uint8_t* s, int N,
   return dmax;
 }
 
+/* e8m0 spread of one MXFP4 weight row (its K/32 scale bytes): max - min. */
+int xo_i8_row_spread(const uint8_t* srow, int K) {
+  int mn = 255, mx = 0;
+  for (int g = 0; g < K / 32; ++g) {
+    if (srow[g] < mn) mn = srow[g];
+    if (srow[g] > mx) mx = srow[g];
+  }
+  return mx - mn;
+}
+
+/* fp32-path dot of a[K] with dequantized MXFP4 weight row n of [N][K] */
+static float i8_fallback_dot(const float* a, const uint8_t* w, const uint8_t* s, int N, int K,
+                             int n, float* wrow) {
+  double d = 0.0;
+  deq_row(XO_MXFP4, w, s, NULL, 0, N, K, n, wrow);
+  for (int k = 0; k < K; ++k) d += (double)a[k] * wrow[k];
+  return (float)d;
+}
+
 /* Full MXFP4 layer with INT8 activations for both GEMMs (the engine with
  * int8_activation ALIGN on, moe_v2_packed4_w4a8.inc:1341-1362): gate/up from
- * int8(x), act fp32 -> bf16, down from int8(bf16(act)). */
+ * int8(x), act fp32 -> bf16, down from int8(bf16(act)).
+ * Fallback (the reference's per-tile guard wtmax <= 3, :1344-1366, sends a
+ * tile whose weight rows spread more than 3 e8m0 steps to its fp32 path): a
+ * gate/up column pair i whose gate row i or up row i spreads more than 3, and
+ * a down column h whose row spreads more than 3, are computed from the bf16
+ * activation and the dequantized weights in fp32 instead.  (The reference
+ * decides per CPU tile of output columns; this build decides per column.) */
 int xo_moe_layer_i8(int T, int K, int E, int n_shared, int H, int I, const uint16_t* x,
                     const int32_t* ids, const float* wts, const uint8_t* w13,
                     const uint8_t* s13, const uint8_t* w2, const uint8_t* s2, float limit,
@@ -495,8 +533,9 @@ int xo_moe_layer_i8(int T, int K, int E, int n_shared, int H, int I, const uint1
   int32_t* accb = (int32_t*)malloc(sizeof(int32_t) * (size_t)(2 * I > H ? 2 * I : H));
   float* actf = (float*)malloc(sizeof(float) * (size_t)I);
   float* y = (float*)malloc(sizeof(float) * (size_t)H);
-  if (!xf || !gu || !accb || !actf || !y) {
-    free(xf); free(gu); free(accb); free(actf); free(y);
+  float* wrow = (float*)malloc(sizeof(float) * (size_t)(H > I ? H : I));
+  if (!xf || !gu || !accb || !actf || !y || !wrow) {
+    free(xf); free(gu); free(accb); free(actf); free(y); free(wrow);
     return -1;
   }
   for (int t = 0; t < T; ++t) {
@@ -514,15 +553,26 @@ int xo_moe_layer_i8(int T, int K, int E, int n_shared, int H, int I, const uint1
         e = E + (r - K);
         w = 1.0f;
       }
-      xo_i8_gemm(xf, 1, w13 + (size_t)e * 2 * I * (H / 2), s13 + (size_t)e * 2 * I * (H / 32),
-                 2 * I, H, 1.0f, accb, gu);
-      for (int i = 0; i < I; ++i)
+      const uint8_t* w13e = w13 + (size_t)e * 2 * I * (H / 2);
+      const uint8_t* s13e = s13 + (size_t)e * 2 * I * (H / 32);
+      const uint8_t* w2e = w2 + (size_t)e * H * (I / 2);
+      const uint8_t* s2e = s2 + (size_t)e * H * (I / 32);
+      xo_i8_gemm(xf, 1, w13e, s13e, 2 * I, H, 1.0f, accb, gu);
+      for (int i = 0; i < I; ++i) {
+        if (xo_i8_row_spread(s13e + (size_t)i * (H / 32), H) > 3 ||
+            xo_i8_row_spread(s13e + (size_t)(I + i) * (H / 32), H) > 3) {
+          gu[i] = i8_fallback_dot(xf, w13e, s13e, 2 * I, H, i, wrow);
+          gu[I + i] = i8_fallback_dot(xf, w13e, s13e, 2 * I, H, I + i, wrow);
+        }
         actf[i] = bf16_round(xo_silu_gate(gu[i], gu[I + i], limit, alpha, beta));
-      xo_i8_gemm(actf, 1, w2 + (size_t)e * H * (I / 2), s2 + (size_t)e * H * (I / 32), H, I,
-                 1.0f, accb, y);
+      }
+      xo_i8_gemm(actf, 1, w2e, s2e, H, I, 1.0f, accb, y);
+      for (int h = 0; h < H; ++h)
+        if (xo_i8_row_spread(s2e + (size_t)h * (I / 32), I) > 3)
+          y[h] = i8_fallback_dot(actf, w2e, s2e, H, I, h, wrow);
       for (int h = 0; h < H; ++h) o[h] += w * y[h];
     }
   }
-  free(xf); free(gu); free(accb); free(actf); free(y);
+  free(xf); free(gu); free(accb); free(actf); free(y); free(wrow);
   return 0;
 }

@@ -286,3 +286,95 @@ def test_quantiser_error_bounds(fmt):
     back = F.dequantize(fmt, q, s, gs)
     rel = float((back - w).norm() / w.norm())
     assert rel < {F.FMT_FP8: 0.04, F.FMT_MXFP4: 0.2, F.FMT_NVFP4: 0.15}[fmt]
+
+
+def _i8_marked_layer(seed=70):
+    """MXFP4 layer with three weight rows spread beyond 3 e8m0 steps: gate row 5
+    of expert 1 (5 steps), up row 9 of expert 2 (4), down row 7 of expert 3 (6)."""
+    E, H, I = 4, 256, 256
+    d = dense_to_numpy(F.FMT_MXFP4, make_dense_layer(F.FMT_MXFP4, E, H, I, seed=seed))
+    s13, s2 = d["s13"].copy(), d["s2"].copy()
+    for plane, e, row, spread in ((s13, 1, 5, 5), (s13, 2, I + 9, 4), (s2, 3, 7, 6)):
+        m = int(plane[e, row].min())
+        plane[e, row, 0], plane[e, row, 1] = m + spread, m
+    d["s13"], d["s2"] = s13, s2
+    return d, E, H, I
+
+
+def _deq_row(w, s, n):
+    """float64 dequantised MXFP4 row n of one expert ([N][K/2] codes, [N][K/32] e8m0)."""
+    e2m1 = np.array(F.E2M1_VALUES, np.float64)
+    v = np.empty(w.shape[1] * 2)
+    v[0::2], v[1::2] = e2m1[w[n] & 15], e2m1[w[n] >> 4]
+    return v * np.repeat(2.0 ** (s[n].astype(np.float64) - 127), 32)
+
+
+def _silu_bf16(g, u):
+    act = np.array([oracle.lib().xo_silu_gate(float(a), float(b), 0.0, 1.0, 0.0)
+                    for a, b in zip(g, u)], np.float32)
+    return oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(act))
+
+
+def test_i8_marked_rows_take_the_fp32_path():
+    """A token routed to one expert with weight 1: the layer's columns equal
+    the integer path (oracle.i8_gemm, pinned by its closed form above) except
+    the marked rows' columns, which equal the fp32 dot of the bf16 operand with
+    the dequantised row (float64 here) -- gate/up (expert 1, gate row 5) and
+    down (expert 3, row 7).  Without the fallback the integer path would use
+    the wrapped int8 weights and miss."""
+    d, E, H, I = _i8_marked_layer()
+    rng = np.random.default_rng(71)
+    x = oracle.f32_to_bf16_bits(rng.standard_normal((2, H)).astype(np.float32))
+    ids = np.array([[1], [3]], np.int32)
+    wts = np.ones((2, 1), np.float32)
+    got = oracle.moe_layer_i8(x, ids, wts, E, 0, H, I, d["w13"], d["s13"], d["w2"], d["s2"])
+    for t, e in ((0, 1), (1, 3)):
+        xf = oracle.bf16_bits_to_f32(x[t])
+        _, gu, _ = oracle.i8_gemm(xf[None, :], d["w13"][e], d["s13"][e])
+        gu = gu[0].astype(np.float64)
+        marked13 = [i for i in range(I)
+                    if np.ptp(d["s13"][e][i]) > 3 or np.ptp(d["s13"][e][I + i]) > 3]
+        for i in marked13:
+            gu[i] = np.dot(xf.astype(np.float64), _deq_row(d["w13"][e], d["s13"][e], i))
+            gu[I + i] = np.dot(xf.astype(np.float64), _deq_row(d["w13"][e], d["s13"][e], I + i))
+        act = _silu_bf16(gu[:I].astype(np.float32), gu[I:].astype(np.float32))
+        _, y, _ = oracle.i8_gemm(act[None, :], d["w2"][e], d["s2"][e])
+        y = y[0].astype(np.float64)
+        marked2 = [h for h in range(H) if np.ptp(d["s2"][e][h]) > 3]
+        for h in marked2:
+            y[h] = np.dot(act.astype(np.float64), _deq_row(d["w2"][e], d["s2"][e], h))
+        assert marked13 or marked2
+        np.testing.assert_allclose(got[t], y, rtol=1e-5, atol=1e-7)
+        # the wrapped integer weights would miss the marked columns
+        _, ywrap, _ = oracle.i8_gemm(act[None, :], d["w2"][e], d["s2"][e])
+        for h in marked2:
+            assert abs(ywrap[0, h] - y[h]) > 0.1 * abs(y[h]) + 1e-3
+
+
+@pytest.mark.skipif(not oracle.ref_available("avx512_vnni"),
+                    reason="reference engine VNNI build not available")
+def test_i8_marked_rows_vs_reference_engine():
+    """The reference engine with the ALIGN gate on routes the tiles holding
+    the marked rows to its fp32 path (its tiles are per CPU thread slice, so
+    which unmarked columns share that path depends on the thread count).  The
+    oracle's per-column choice is no further from the engine than the integer
+    path itself is from the fp32 layer."""
+    d, E, H, I = _i8_marked_layer()
+    rng = np.random.default_rng(72)
+    T, K = 8, 2
+    x = oracle.f32_to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    ids, wts = random_routing(T, K, E, seed=73)
+    got = oracle.moe_layer_i8(x, ids, wts, E, 0, H, I, d["w13"], d["s13"], d["w2"], d["s2"])
+    f32 = oracle.moe_layer(F.FMT_MXFP4, x, ids, wts, E, 0, H, I, d["w13"], d["s13"], d["w2"],
+                           d["s2"])
+    L = oracle.ref_lib("avx512_vnni")
+    eng = oracle.RefEngine(F.FMT_MXFP4, E, K, H, I, d["w13"], d["s13"], d["w2"], d["s2"],
+                           isa="avx512_vnni")
+    L.xref_set_int8(1, 1 << 30)
+    try:
+        ref = eng.forward(x, ids.astype(np.uint32), wts)
+    finally:
+        L.xref_set_int8(0, 0)
+        eng.close()
+    assert rel_l2(got, ref) <= rel_l2(got, f32)
+    assert rel_l2(ref, f32) < 0.1   # the engine did not run wrapped weights either

@@ -8,6 +8,14 @@
 //   ACC = sum_k a8 * w8'  (int32, exact; |ACC| <= 127*96*K)
 //   C   = float(ACC) * 2^(emin_n - 128 + crow)
 //
+// A weight row whose e8m0 spread exceeds 3 cannot take the integer path (the
+// reference routes such tiles to its fp32 path, moe_v2_packed4_w4a8.inc:
+// 1344-1366).  xtu_i8_prepare marks it (emin byte 0xFF, int8 weights 0); the
+// integer GEMMs leave its output column unwritten -- for gate/up the column
+// pair n of act when gate row n or up row n is marked -- and the fallback
+// kernels compute exactly those columns in fp32 from the MXFP4 weights and
+// the bf16 activations (the fp32 path's operands).
+//
 // The shifted int8 weights are expanded once per layer (xtu_i8_prepare) into
 // the P16 panel layout with 16 int8 per chunk, next to a per-row emin; the
 // GEMM then runs v_mfma_i32_32x32x32_i8 on LDS tiles with the same tile list
@@ -20,6 +28,7 @@ namespace xtu {
 namespace {
 
 constexpr int kBK = 128;   // k per step (64 measured 6% slower: twice the barriers)
+constexpr int kI8Marked = 0xFF;   // emin of a row that takes the fp32 fallback
 constexpr int kBN = 256;
 constexpr int kLDB = kBK + 16;   // LDS pitch in bytes
 
@@ -46,7 +55,8 @@ __global__ __launch_bounds__(256) void i8_emin_kernel(const uint8_t* __restrict_
       mn = min(mn, b);
       mx = max(mx, b);
     }
-  emin[(long)e * N + n] = (uint8_t)mn;
+  // a row the integer path cannot hold (spread > 3) is marked with 0xFF
+  emin[(long)e * N + n] = (uint8_t)(mx - mn > 3 ? kI8Marked : mn);
   atomicMax(dmax, mx - mn);
 }
 
@@ -69,7 +79,9 @@ __global__ __launch_bounds__(256) void i8_expand_kernel(const uint8_t* __restric
   const int n = (int)(p * 16 + r);
   const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(w + (long)e * w_estride + c * 16);
   const int b = s[(long)e * s_estride + scale_offset<kMXFP4>(p, sb4, q4 * 16 + r, K)];
-  const int d = b - emin[(long)e * N + n];
+  const int em = emin[(long)e * N + n];
+  const int d = em == kI8Marked ? 0 : b - em;
+  const bool zero = em == kI8Marked;   // marked row: int8 weights 0
   const int k0 = (int)(sb4 * 128 + q4 * 32);
   uint32_t outw[8];
 #pragma unroll
@@ -78,8 +90,8 @@ __global__ __launch_bounds__(256) void i8_expand_kernel(const uint8_t* __restric
 #pragma unroll
     for (int bb = 0; bb < 4; ++bb) {
       const uint32_t byte = (raw[dw] >> (8 * bb)) & 0xffu;
-      const uint32_t v0 = (uint32_t)(w4_of(byte & 15u) * (1 << d)) & 0xffu;
-      const uint32_t v1 = (uint32_t)(w4_of(byte >> 4) * (1 << d)) & 0xffu;
+      const uint32_t v0 = zero ? 0u : (uint32_t)(w4_of(byte & 15u) * (1 << d)) & 0xffu;
+      const uint32_t v1 = zero ? 0u : (uint32_t)(w4_of(byte >> 4) * (1 << d)) & 0xffu;
       const int j = bb * 2;   // k offset inside this dword's 8 values
       if (j < 4) lo |= (v0 << (8 * j)) | (v1 << (8 * (j + 1)));
       else hi |= (v0 << (8 * (j - 4))) | (v1 << (8 * (j - 3)));
@@ -310,13 +322,15 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8GemmArgs a) {
             a.acc_out[prow * N + gcol0] = acc[m][0][i];
             a.acc_out[prow * N + gcol1] = acc[m][1][i];
           }
+          // marked rows' columns are the fallback kernels' to write
           if (GU) {
             uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
-            act[prow * a.I + gcol0] = f32_to_bf16(silu_gate(c0, c1, a.limit, a.alpha, a.beta));
+            if (em0 != kI8Marked && em1 != kI8Marked)
+              act[prow * a.I + gcol0] = f32_to_bf16(silu_gate(c0, c1, a.limit, a.alpha, a.beta));
           } else {
             float* y = reinterpret_cast<float*>(a.out);
-            y[prow * a.H + gcol0] = c0;
-            y[prow * a.H + gcol1] = c1;
+            if (em0 != kI8Marked) y[prow * a.H + gcol0] = c0;
+            if (em1 != kI8Marked) y[prow * a.H + gcol1] = c1;
           }
         }
       }
@@ -325,6 +339,110 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8GemmArgs a) {
   else if (rows > 64) run(std::integral_constant<int, 3>{});
   else if (rows > 32) run(std::integral_constant<int, 2>{});
   else run(std::integral_constant<int, 1>{});
+}
+
+// fp32 value of MXFP4 weight (row n, k) of one expert matrix [N][K] (P16)
+__device__ __forceinline__ float mxfp4_at(const uint8_t* w, const uint8_t* s, int n, int k,
+                                          int K) {
+  const long p = n / 16, r = n % 16, sb = k / 128, q = (k % 128) / 32, j = k % 32;
+  const long nsb = K / 128;
+  const uint8_t byte = w[(((p * nsb + sb) * 4 + q) * 16 + r) * 16 + j / 2];
+  const int nib = (j & 1) ? (byte >> 4) : (byte & 15);
+  const int b = s[scale_offset<kMXFP4>(p, sb, (int)(q * 16 + r), K)];
+  return ldexpf(0.5f * (float)w4_of((uint32_t)nib), b - 127);   // e2m1 = w4 / 2, exact
+}
+
+struct I8FallbackArgs {
+  const uint16_t* x;          // gate/up: hidden rows [T][H]; down: act rows [A][I] (bf16)
+  const int32_t* sorted_tok;  // gate/up only
+  const uint8_t* w;           // MXFP4 P16 codes (expert-major)
+  const uint8_t* s;           // packed e8m0 scale groups
+  const int32_t* seg_start;
+  const int32_t* tile_expert;
+  const int32_t* tile_row0;
+  const int32_t* tile_lo;
+  const int32_t* tile_hi;
+  const int32_t* slot_map;
+  const int32_t* col_start;   // [n_slots + 1] CSR of marked columns per weight slot
+  const int32_t* cols;        // gate/up: column pair n in [0, I); down: column h
+  void* out;                  // act bf16 [A][I] / y fp32 [A][H]
+  int H, I, bm;
+  float limit, alpha, beta;
+};
+
+// One workgroup per m tile of the tile list; for each marked column of the
+// tile's weight slot, the marked weight row(s) are dequantised to fp32 in LDS
+// and every row of the tile takes its dot product with them: one wave per
+// row, lanes over k, reduced across the wave in a fixed order.
+template <bool GU>
+__global__ __launch_bounds__(256) void i8_fallback_kernel(I8FallbackArgs a) {
+  constexpr int kChunk = 2048;   // k per LDS fill
+  __shared__ float wl[2][kChunk];
+  const int tile = a.tile_lo[0] + blockIdx.x;
+  if (tile >= a.tile_hi[0]) return;
+  const int e = a.tile_expert[tile];
+  const int ws = a.slot_map ? a.slot_map[e] : e;
+  const int c0 = a.col_start[ws], c1 = a.col_start[ws + 1];
+  if (c0 == c1) return;
+  const int row0 = a.tile_row0[tile];
+  const int rows = min(a.bm, a.seg_start[e + 1] - row0);
+  const int K = GU ? a.H : a.I;
+  const int N = GU ? 2 * a.I : a.H;
+  const long w_es = WFmt<kMXFP4>::w_bytes(N, K), s_es = WFmt<kMXFP4>::s_bytes(N, K);
+  const uint8_t* we = a.w + (long)ws * w_es;
+  const uint8_t* se = a.s + (long)ws * s_es;
+  const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
+  for (int ci = c0; ci < c1; ++ci) {
+    const int col = a.cols[ci];
+    const int nr0 = col, nr1 = GU ? a.I + col : col;   // weight rows (gate, up) or (h)
+    // each wave owns rows w, w+4, ...: at most bm/4 partial sums per lane pair
+    float accg[32], accu[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) accg[i] = accu[i] = 0.f;
+    for (int k0 = 0; k0 < K; k0 += kChunk) {
+      const int kn = min(kChunk, K - k0);
+      __syncthreads();
+      for (int k = threadIdx.x; k < kn; k += 256) {
+        wl[0][k] = mxfp4_at(we, se, nr0, k0 + k, K);
+        if (GU) wl[1][k] = mxfp4_at(we, se, nr1, k0 + k, K);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int r = w + 4 * i;
+        if (r < rows) {
+          const long src = GU ? (long)a.sorted_tok[row0 + r] : (long)(row0 + r);
+          const uint16_t* xr = a.x + src * K + k0;
+          float g = 0.f, u = 0.f;
+          for (int k = lane; k < kn; k += 64) {
+            const float xv = __uint_as_float((uint32_t)xr[k] << 16);
+            g = __builtin_fmaf(xv, wl[0][k], g);
+            if (GU) u = __builtin_fmaf(xv, wl[1][k], u);
+          }
+          accg[i] += g;
+          accu[i] += u;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int r = w + 4 * i;
+      float g = accg[i], u = accu[i];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        g += __shfl_xor(g, off, 64);
+        if (GU) u += __shfl_xor(u, off, 64);
+      }
+      if (lane == 0 && r < rows) {
+        const long prow = row0 + r;
+        if (GU)
+          reinterpret_cast<uint16_t*>(a.out)[prow * a.I + col] =
+              f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
+        else
+          reinterpret_cast<float*>(a.out)[prow * a.H + col] = g;
+      }
+    }
+  }
 }
 
 }  // namespace
@@ -410,6 +528,27 @@ hipError_t xtu_i8_gemm_down(const int8_t* a8, const int32_t* crow, int H, int I,
                tile_expert, tile_row0, tile_lo, tile_hi, slot_map, y, acc_out, H, I, 0, 0.f,
                1.f, 0.f};
   return i8_gemm(false, a, max_tiles, stream);
+}
+
+hipError_t xtu_i8_fallback(int gate_up, const void* x, const int32_t* sorted_tok, int H, int I,
+                           const void* w, const void* s, const int32_t* slot_map,
+                           const int32_t* seg_start, const int32_t* tile_expert,
+                           const int32_t* tile_row0, const int32_t* tile_lo,
+                           const int32_t* tile_hi, int max_tiles, int bm,
+                           const int32_t* col_start, const int32_t* cols, void* out, float limit,
+                           float alpha, float beta, hipStream_t stream) {
+  XTU_CHECK_ARG(H > 0 && I > 0 && H % 256 == 0 && I % 128 == 0 && max_tiles >= 0);
+  XTU_CHECK_ARG(bm > 0 && bm <= 128);
+  XTU_CHECK_ARG(x && w && s && seg_start && tile_expert && tile_row0 && tile_lo && tile_hi &&
+                col_start && cols && out && (!gate_up || sorted_tok));
+  if (max_tiles == 0) return hipSuccess;
+  (void)hipGetLastError();
+  I8FallbackArgs a{(const uint16_t*)x, sorted_tok, (const uint8_t*)w, (const uint8_t*)s,
+                   seg_start, tile_expert, tile_row0, tile_lo, tile_hi, slot_map, col_start,
+                   cols, out, H, I, bm, limit, alpha, beta};
+  if (gate_up) i8_fallback_kernel<true><<<max_tiles, 256, 0, stream>>>(a);
+  else i8_fallback_kernel<false><<<max_tiles, 256, 0, stream>>>(a);
+  return hipPeekAtLastError();
 }
 
 }  // extern "C"

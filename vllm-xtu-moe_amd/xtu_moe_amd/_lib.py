@@ -66,6 +66,8 @@ SIGNATURES = {
                                  _i, _vp, _vp, _f, _f, _f, _vp]),
     "xtu_i8_gemm_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                               _vp, _vp]),
+    "xtu_i8_fallback": (_i, [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i,
+                             _vp, _vp, _vp, _f, _f, _f, _vp]),
 }
 
 # entry points whose int return value is a size/count, not a status

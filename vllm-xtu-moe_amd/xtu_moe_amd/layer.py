@@ -64,6 +64,7 @@ class ExpertWeights:
         self.fmt, self.H, self.I, self.E, self.n_shared = int(fmt), int(H), int(I), int(E), int(n_shared)
         self.w13, self.s13, self.w2, self.s2, self.gs13, self.gs2 = w13, s13, w2, s2, gs13, gs2
         self._i8 = None
+        self._i8_fb = None
         if self.H % 256 or self.I % 128:
             raise ValueError(f"unsupported shape H={H} I={I} (need H % 256 == 0, I % 128 == 0)")
 
@@ -106,7 +107,9 @@ class ExpertWeights:
 
     # ---------------------------------------------------------------- INT8
     def int8_planes(self):
-        """Shifted int8 weights + per-row emin for the INT8 ALIGN path (MXFP4 only)."""
+        """Shifted int8 weights + per-row emin for the INT8 ALIGN path (MXFP4
+        only).  Rows whose e8m0 spread exceeds 3 are marked (emin 0xFF); their
+        output columns take the fp32 fallback (int8_fallback_cols)."""
         if self._i8 is not None:
             return self._i8
         if self.fmt != FMT_MXFP4:
@@ -121,11 +124,35 @@ class ExpertWeights:
             emin = torch.empty((n, N), dtype=torch.uint8, device=dev)
             _lib.call("xtu_i8_prepare", _p(w), _p(s), n, N, K, _p(w8), _p(emin), _p(dmax), st)
             out += [w8, emin]
-        d = int(dmax.item())
-        if d > 3:
-            raise ValueError(f"INT8 ALIGN path needs per-row e8m0 spread <= 3, got {d}")
+        self._i8_fb = None
+        if int(dmax.item()) > 3:   # marked rows: CSR lists of their output columns per slot
+            I = self.I
+            m13 = (out[1] == I8_MARKED).cpu()
+            m13 = (m13[:, :I] | m13[:, I:])            # column pair n: gate row n or up row n
+            m2 = (out[3] == I8_MARKED).cpu()
+            self._i8_fb = _csr_cols(m13, dev) + _csr_cols(m2, dev)
         self._i8 = tuple(out)
         return self._i8
+
+    def int8_fallback_cols(self):
+        """None, or (start13, cols13, start2, cols2): per weight slot, the
+        gate/up column pairs and down columns the fp32 fallback computes."""
+        self.int8_planes()
+        return self._i8_fb
+
+
+I8_MARKED = 0xFF   # emin byte of a weight row that takes the fp32 fallback
+
+
+def _csr_cols(mask, device):
+    """Per-row boolean mask [slots][N] -> device (start [slots + 1], cols) int32."""
+    counts = mask.sum(1).to(torch.int32)
+    start = torch.zeros(mask.shape[0] + 1, dtype=torch.int32)
+    start[1:] = torch.cumsum(counts, 0)
+    cols = mask.nonzero()[:, 1].to(torch.int32)   # row-major: slot order, then column order
+    if cols.numel() == 0:
+        cols = torch.zeros(1, dtype=torch.int32)
+    return start.to(device), cols.to(device)
 
 
 def _cap_rows(n: int) -> int:
@@ -575,13 +602,23 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
         a8a = _buf("a8a", (max(A, 1), I), torch.int8, dev, st)
         cra = _buf("cra", (max(A, 1),), torch.int32, dev, st)
         _lib.call("xtu_i8_quant_rows", _p(x), T, H, _p(a8x), _p(crx), st)
+        fb = W.int8_fallback_cols()
         _lib.call("xtu_i8_gemm_gate_up", _p(a8x), _p(crx), _p(seg.sorted_tok), H, I, _p(w13_8),
                   _p(emin13), _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
                   _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), 0, lim, al, be, st)
+        if fb is not None:   # marked weight rows: their columns in fp32
+            _lib.call("xtu_i8_fallback", 1, _p(x), _p(seg.sorted_tok), H, I, _p(W.w13),
+                      _p(W.s13), _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
+                      _p(seg.tile_row0), lo, hi, seg.max_tiles, seg.bm, _p(fb[0]), _p(fb[1]),
+                      _p(act), lim, al, be, st)
         _lib.call("xtu_i8_quant_rows", _p(act), A, I, _p(a8a), _p(cra), st)
         _lib.call("xtu_i8_gemm_down", _p(a8a), _p(cra), H, I, _p(w2_8), _p(emin2), _p(slot_map),
                   _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo, hi,
                   seg.max_tiles, _p(y), 0, st)
+        if fb is not None:
+            _lib.call("xtu_i8_fallback", 0, _p(act), 0, H, I, _p(W.w2), _p(W.s2), _p(slot_map),
+                      _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo, hi,
+                      seg.max_tiles, seg.bm, _p(fb[2]), _p(fb[3]), _p(y), 0.0, 1.0, 0.0, st)
         return
     fmt = W.fmt
     if fmt == FMT_FP8:
