@@ -50,6 +50,9 @@ WORKLOADS = {
                                Ts=[1, 2, 4], limit=0.0, int8=False, graph=True),
     "ds-v3-fp8-prefill": dict(fmt="fp8", E=256, NS=1, H=7168, I=2048, K=8, router="grouped",
                               Ts=[8192], limit=0.0, int8=False, graph=False),
+    "ds-v3-mxfp4-prefill": dict(fmt="mxfp4", E=256, NS=1, H=7168, I=2048, K=8,
+                                router="grouped", Ts=[8192], limit=0.0, int8=False,
+                                graph=False),
     "qwen3-next-int8": dict(fmt="mxfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
                             Ts=[1, 4, 8192], limit=7.0, int8=True, graph=True),
     "qwen3-next-nvfp4": dict(fmt="nvfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
@@ -93,7 +96,7 @@ def main():
     from xtu_moe_amd import _lib
     from xtu_moe_amd import formats as F
     from xtu_moe_amd.layer import (_fp8pair_bufs, _p, _stream, gemm_tile_m, int8_align_on,
-                                   moe_forward, route, segmentation)
+                                   moe_forward, pair_gemm, route, segmentation)
     from xtu_moe_amd.synthetic import synth_layer
 
     cfg = WORKLOADS[args.workload]
@@ -278,7 +281,7 @@ def main():
             seg = segmentation(T, K, E, NS, bm, dev).run(i_, w_)
             st = _stream()
             fp8x = None
-            if not decode and not i8 and fmt == F.FMT_FP8:
+            if not decode and not i8 and pair_gemm(fmt):
                 fp8x = _fp8pair_bufs("x8", T, H, dev)
                 _lib.call("xtu_fp8pair_quant", _p(x_st), T, H, *[_p(t) for t in fp8x], st)
             if i8:
@@ -303,10 +306,11 @@ def main():
                           1.0, 0.0, st)
             elif fp8x is not None:
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
-                _lib.call("xtu_gemm8_gate_up", *[_p(t) for t in fp8x], _p(seg.sorted_tok), H, I,
-                          _p(W.w13), _p(W.s13), 0, 0, 0, _p(seg.seg_start), _p(seg.tile_expert),
-                          _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi, seg.max_tiles,
-                          _p(act), cfg["limit"], 1.0, 0.0, st)
+                _lib.call("xtu_gemm_pair_gate_up", fmt, *[_p(t) for t in fp8x],
+                          _p(seg.sorted_tok), H, I, _p(W.w13), _p(W.s13), 0, 0, 0,
+                          _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
+                          _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(act),
+                          cfg["limit"], 1.0, 0.0, st)
             else:
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
                 _lib.call("xtu_gemm_gate_up", fmt, _p(x_st), _p(seg.sorted_tok), H, I, _p(W.w13),
@@ -370,14 +374,17 @@ def main():
                 if tr.get("distinct_experts"):   # the counter run's own routing
                     tr["algorithmic_bytes"] = (tr["distinct_experts"] * e_bytes13 + Th * H * 2
                                                + (Th * K + Th * NS) * I * 2)
-    elif cfg["fmt"] == "fp8" and not cfg["int8"]:
-        # e4m3 x e4m3 MFMA; every algorithmic product is two MFMA products
+    elif pair_gemm(fmt) and not cfg["int8"]:
+        # scaled MFMA with an e4m3 A (FP8: e4m3 B; MXFP4: e2m1 B), which runs
+        # at the fp8 rate; every algorithmic product is two MFMA products
         # (the activation's hi and lo halves)
         ach = r["gate_up_TFLOPs"]
         roof = dict(bound="mfma", achieved=ach, peak=PEAK_TFLOPS["fp8"], unit="TFLOP/s",
                     frac=ach / PEAK_TFLOPS["fp8"], traffic=None, kernel="gemm8_kernel",
                     mfma_issue_frac=2.0 * ach / PEAK_TFLOPS["fp8"],
                     frac_of_bf16_peak=ach / PEAK_TFLOPS["bf16"])
+        if cfg["fmt"] == "mxfp4":
+            roof["frac_of_fp4_peak"] = ach / PEAK_TFLOPS["fp4"]
     else:
         dt = "int8" if cfg["int8"] else "bf16"
         roof = dict(bound="mfma", achieved=r["gate_up_TFLOPs"], peak=PEAK_TFLOPS[dt],
@@ -404,7 +411,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"mxfp4": "bf16-mfma/e2m1+e8m0",
+        "dtype": {"mxfp4": ("bf16-mfma/e2m1+e8m0" if decode_head or not pair_gemm(fmt)
+                            else "fp8xfp4-mfma/e4m3-pair x e2m1+e8m0"),
                   "fp8": ("bf16-mfma/e4m3+f32-block" if decode_head
                           else "fp8-mfma/e4m3-pair x e4m3+f32-block"),
                   "nvfp4": "bf16-mfma/e2m1+e4m3", "bf16": "bf16"}[cfg["fmt"]]

@@ -276,6 +276,30 @@ hipError_t xtu_gemm8_down(const uint8_t* hi, const uint8_t* lo, const uint8_t* s
                           float* y, hipStream_t stream);
 
 
+/* The same exact-pair GEMMs with the weight format as an argument: fmt 1
+ * (FP8, s = fp32 [N/128][K/128] block scales) or 2 (MXFP4, s = the packed
+ * e8m0 scale groups).  MXFP4 codes enter v_mfma_scale_f32_16x16x128_f8f6f4
+ * as fp4 B operands straight from P16 (lane 16q + r: k = 32q..32q+31 of row
+ * r) with their e8m0 byte as the B scale, so the product is exact with no
+ * dequantisation.  Replace _gate_up_kernel / _down_kernel
+ * (vllm_xiaotu_moe/gpu_prefill.py:232-390) for MXFP4 prefill. */
+hipError_t xtu_gemm_pair_gate_up(int fmt, const uint8_t* hi, const uint8_t* lo,
+                                 const uint8_t* shi, const uint8_t* slo,
+                                 const int32_t* sorted_tok, int H, int I, const void* w13,
+                                 const void* s13, long w_estride, long s_estride,
+                                 const int32_t* slot_map, const int32_t* seg_start,
+                                 const int32_t* tile_expert, const int32_t* tile_row0,
+                                 const int32_t* expert_tile_start, const int32_t* tile_lo,
+                                 const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                                 float alpha, float beta, hipStream_t stream);
+hipError_t xtu_gemm_pair_down(int fmt, const uint8_t* hi, const uint8_t* lo, const uint8_t* shi,
+                              const uint8_t* slo, int H, int I, const void* w2, const void* s2,
+                              long w_estride, long s_estride, const int32_t* slot_map,
+                              const int32_t* seg_start, const int32_t* tile_expert,
+                              const int32_t* tile_row0, const int32_t* expert_tile_start,
+                              const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                              float* y, hipStream_t stream);
+
 /* -------------------------------------- INT8-activation x FP4-code (ALIGN) path
  * Replaces the engine's ALIGN integer path (xiaotu_moe/csrc/moe/
  * moe_v2_packed4_w4a8.inc:478-586 xiaotu_predecode_block, :661-715

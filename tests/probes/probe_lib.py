@@ -15,6 +15,7 @@ SIGNATURES = {
     "xtu_probe_fp8": (_i, [_vp, _vp]),
     "xtu_probe_mfma": (_i, [_i, _vp, _vp, _vp, _vp]),
     "xtu_probe_exp": (_i, [_vp, _i, _vp, _vp, _vp]),
+    "xtu_probe_mfma_scaled_fp4b": (_i, [_vp, _vp, _vp, _vp, _vp, _vp]),
 }
 _LIB = None
 

@@ -103,6 +103,26 @@ __global__ void probe_exp_kernel(const float* __restrict__ x, int n, float* __re
   s[i] = xtu_sigmoid(x[i]);
 }
 
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+// one wave: raw per-lane operands and scale bytes of one
+// v_mfma_scale_f32_16x16x128_f8f6f4 with an fp8 (e4m3) A and an fp4 (e2m1)
+// B; C lane l holds rows 4*(l/16)+i of column l%16
+__global__ void probe_mfma_scaled_fp4b_kernel(const int* __restrict__ A, const int* __restrict__ B,
+                                              const uint8_t* __restrict__ sa,
+                                              const uint8_t* __restrict__ sb,
+                                              float* __restrict__ C) {
+  const int l = threadIdx.x;
+  i32x8_t a, b;
+  for (int i = 0; i < 8; ++i) {
+    a[i] = A[l * 8 + i];
+    b[i] = B[l * 8 + i];
+  }
+  f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+  c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, 0, sa[l], 0, sb[l]);
+  for (int i = 0; i < 4; ++i) C[l * 4 + i] = c[i];
+}
+
 }  // namespace
 }  // namespace xtu
 
@@ -140,6 +160,14 @@ hipError_t xtu_probe_mfma(int which, const void* A, const void* B, void* C, hipS
     probe_mfma32_kernel<<<1, 64, 0, stream>>>((const uint16_t*)A, (const uint16_t*)B, (float*)C);
   else
     probe_mfma_i8_kernel<<<1, 64, 0, stream>>>((const int8_t*)A, (const int8_t*)B, (int32_t*)C);
+  return hipPeekAtLastError();
+}
+
+hipError_t xtu_probe_mfma_scaled_fp4b(const int* A, const int* B, const uint8_t* sa,
+                                     const uint8_t* sb, float* C, hipStream_t stream) {
+  XTU_CHECK_ARG(A && B && sa && sb && C);
+  (void)hipGetLastError();
+  probe_mfma_scaled_fp4b_kernel<<<1, 64, 0, stream>>>(A, B, sa, sb, C);
   return hipPeekAtLastError();
 }
 

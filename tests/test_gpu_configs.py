@@ -212,3 +212,55 @@ def test_ds_v3_fp8_streamed_prefill():
     check_close(out[toks].cpu().numpy(), want, bf16_out=False, what="ds-v3 fp8 streamed")
     del W, store, pool
     torch.cuda.empty_cache()
+
+
+# ------------------------------------------------------ DeepSeek-V3 MXFP4 prefill
+@pytest.mark.parametrize("mode", ["pair", "bf16"])
+def test_ds_v3_mxfp4_prefill_t8192(mode, monkeypatch):
+    """DeepSeek-V3 shape with MXFP4 experts at T=8192, on the scaled fp8 x fp4
+    MFMA (exact activation pairs) and on the bf16-operand GEMM: sampled tokens
+    against the oracle, and the token-permutation bitwise property."""
+    monkeypatch.setenv(L.MXFP4_PREFILL_ENV, mode)
+    H, I, E, NS, K, T = 7168, 2048, 256, 1, 8, 8192
+    W = synth_layer(F.FMT_MXFP4, E, NS, H, I, seed=17, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(18)
+    x = torch.randn((T, H), generator=g, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((T, E), generator=g, device=DEV)
+    wts, ids = route(logits, top_k=K, scoring="sigmoid", n_group=8, topk_group=4,
+                     routed_scaling_factor=2.5)
+    out = moe_forward(x, ids, wts, W, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    toks = _toks(T, 6, seed=19)
+    ref = _sampled_oracle(F.FMT_MXFP4, W, x, ids, wts, toks)
+    check_close(out[toks].cpu().numpy(), ref, bf16_out=False, what="ds-v3 mxfp4 T=8192")
+    perm = torch.randperm(T, generator=torch.Generator().manual_seed(20)).to(DEV)
+    out_p = moe_forward(x[perm].contiguous(), ids[perm].contiguous(), wts[perm].contiguous(), W,
+                        out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(out_p, out[perm])
+    del W
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("T", [40, 700])
+def test_mxfp4_prefill_pair_and_bf16_paths(T, monkeypatch):
+    """MXFP4 prefill on the exact-pair fp4 MFMA and on the bf16-operand GEMM
+    (XTU_MXFP4_PREFILL=bf16): both against the oracle, with a SwiGLU clamp
+    and a shared expert."""
+    E, NS, H, I, K = 24, 1, 768, 384, 4
+    d = make_dense_layer(F.FMT_MXFP4, E + NS, H, I, seed=21)
+    W = ExpertWeights.from_dense(F.FMT_MXFP4, d["w13"], d["s13"], d["w2"], d["s2"], n_shared=NS,
+                                 device=DEV)
+    rng = np.random.default_rng(22)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    wts = (rng.random((T, K)) + 0.05).astype(np.float32)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
+    ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d), bf16_tensor_to_bits(x), ids,
+                       wts, E, NS, H, I, limit=4.0)
+    for mode in ("pair", "bf16"):
+        monkeypatch.setenv(L.MXFP4_PREFILL_ENV, mode)
+        assert L.pair_gemm(F.FMT_MXFP4) == (mode == "pair")
+        out = moe_forward(x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(wts).to(DEV),
+                          W, path="gemm", swiglu_limit=4.0, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"mxfp4 {mode} T={T}")

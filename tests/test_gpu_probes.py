@@ -107,3 +107,45 @@ def test_exp_sigmoid_bit_exact():
     ref_s = np.array([L.xo_sigmoid(float(v)) for v in x], np.float32)
     np.testing.assert_array_equal(e.cpu().numpy().view(np.uint32), ref_e.view(np.uint32))
     np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
+
+
+def test_scaled_mfma_fp8_a_fp4_b_layout():
+    """v_mfma_scale_f32_16x16x128_f8f6f4 with an e4m3 A and an e2m1 B, the
+    layout the MXFP4 prefill GEMM relies on: A lane 16q + r is row r with
+    bytes 0..15 = k 16q.. and bytes 16..31 = k 64 + 16q..; B lane 16g + c is
+    column c with nibble j (low nibble first) = k 32g + j -- one P16 MXFP4
+    chunk; the scale byte of row r (column c) for the 32-k block b comes from
+    lane 16b + r (16b + c).  Values are chosen so every sum is exact in fp32."""
+    rng = np.random.default_rng(11)
+    # e4m3 codes with exponent field 5..9 (|v| in [2^-2, 2^2 * 1.875]), random sign
+    a_codes = (rng.integers(5, 10, (16, 128)) << 3 | rng.integers(0, 8, (16, 128))
+               | (rng.integers(0, 2, (16, 128)) << 7)).astype(np.uint8)
+    b_codes = rng.integers(0, 16, (16, 128)).astype(np.uint8)    # [col][k] e2m1 nibbles
+    sa = rng.integers(126, 129, (16, 4)).astype(np.uint8)        # [row][block]
+    sb = rng.integers(126, 129, (16, 4)).astype(np.uint8)        # [col][block]
+    A = np.zeros((64, 32), np.uint8)
+    B = np.zeros((64, 32), np.uint8)
+    la, lb = np.zeros(64, np.uint8), np.zeros(64, np.uint8)
+    for q in range(4):
+        for r in range(16):
+            lane = 16 * q + r
+            A[lane, :16] = a_codes[r, 16 * q:16 * q + 16]
+            A[lane, 16:] = a_codes[r, 64 + 16 * q:64 + 16 * q + 16]
+            nib = b_codes[r, 32 * q:32 * q + 32]
+            B[lane, :16] = nib[0::2] | (nib[1::2] << 4)
+            la[lane], lb[lane] = sa[r, q], sb[r, q]
+    dev = "cuda"
+    tA = torch.from_numpy(A.view(np.int32).copy()).to(dev)
+    tB = torch.from_numpy(B.view(np.int32).copy()).to(dev)
+    tsa, tsb = torch.from_numpy(la).to(dev), torch.from_numpy(lb).to(dev)
+    C = torch.zeros(64 * 4, dtype=torch.float32, device=dev)
+    _lib.call("xtu_probe_mfma_scaled_fp4b", _p(tA), _p(tB), _p(tsa), _p(tsb), _p(C), _stream())
+    torch.cuda.synchronize()
+    c = C.cpu().numpy().reshape(64, 4)
+    got = np.zeros((16, 16))
+    for lane in range(64):
+        for i in range(4):
+            got[4 * (lane // 16) + i, lane % 16] = c[lane, i]
+    av = oracle.e4m3_table().astype(np.float64)[a_codes] * np.repeat(2.0 ** (sa - 127.0), 32, 1)
+    bv = E2M1.astype(np.float64)[b_codes] * np.repeat(2.0 ** (sb - 127.0), 32, 1)
+    np.testing.assert_array_equal(got, av @ bv.T)

@@ -12,7 +12,7 @@
 // (at least 2^-13.8 of its block's maximum); below that hi is subnormal and
 // the last bit may be rounded (an error under 2^-19 of the block maximum).
 //
-// Weights: the e4m3 codes go from the P16 layout straight into the MFMA B
+// Weights (FP8): the e4m3 codes go from the P16 layout straight into the MFMA B
 // operand.  The MFMA's 128-k reduction is exactly one 128 x 128 block of the
 // fp32 block scales, so each (16-row tile, panel) pair is
 //   part = mfma(hi, w, 0; scale sa) + mfma(lo, w, part; scale sa - 4)
@@ -20,6 +20,13 @@
 // which is the dequantised-fp32 product up to fp32 summation order -- no
 // operand is rounded.  Two fp8 MFMAs take the time of the four bf16 ones of
 // the same 128 k, and there is no weight dequantisation.
+//
+// Weights (MXFP4): the e2m1 codes go from the P16 layout straight into the
+// MFMA B operand as fp4 (an fp4 B lane 16q + r holds k = 32q..32q+31 of
+// column r, one P16 chunk, low nibble = even k; checked on the device) and
+// the chunk's e8m0 byte is the lane's B scale, so
+//   acc = mfma(hi, w, acc; sa, sw) ; acc = mfma(lo, w, acc; sa - 4, sw)
+// is the dequantised-fp32 product with no fold at all.
 //
 // MFMA operand layout (checked on the device): lane 16q + r holds row r;
 // operand bytes 0..15 are k = 16q..16q+15 and bytes 16..31 are
@@ -148,11 +155,14 @@ struct Gemm8Args {
 
 struct B8Step {
   i32x8_t w[kPW8];
-  float bs0, bs1;
+  float bs0, bs1;     // FP8: block scales of the two panel pairs
+  int sc[kPW8];       // MXFP4: the lane's e8m0 byte per panel
 };
 
-template <bool GU>
+template <bool GU, int WF>
 __global__ __launch_bounds__(kThreads8, 2) void gemm8_kernel(Gemm8Args a) {
+  static_assert(WF == kFP8 || WF == kMXFP4, "FP8 or MXFP4 weights");
+  constexpr bool MX = WF == kMXFP4;
   __shared__ __attribute__((aligned(16))) uint8_t As[2 * kBuf8];
 
   // ---- work item: (M tile, N block), XCD-contiguous, N block fastest
@@ -220,16 +230,20 @@ __global__ __launch_bounds__(kThreads8, 2) void gemm8_kernel(Gemm8Args a) {
     if (GU) pan[p] = (p < 2 ? 0 : a.I / 16) + (nb * 4 + w) * 2 + (p & 1);
     else pan[p] = (nb * 4 + w) * kPW8 + p;
   }
-  const long w_es = a.w_estride ? a.w_estride : (GU ? 2L * a.I * a.H : (long)a.H * a.I);
-  const long s_es = a.s_estride ? a.s_estride : (GU ? (2L * a.I / 128) * (a.H / 128) * 4
-                                                    : ((long)a.H / 128) * (a.I / 128) * 4);
+  const long nw = GU ? 2L * a.I : (long)a.H;   // weight rows
+  const long w_es = a.w_estride ? a.w_estride : WFmt<WF>::w_bytes(nw, K);
+  const long s_es = a.s_estride ? a.s_estride : WFmt<WF>::s_bytes(nw, K);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.w + (long)ws * w_es), 0, (int)w_es, kFlags8);
   const float* bsc = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(a.s) +
                                                     (long)ws * s_es);
   const int kb128 = K / 128;
   const int rb0 = pan[0] / 8, rb1 = pan[kPW8 / 2] / 8;
-  const int nsb = K / 64;
+  const int nsb = K / WFmt<WF>::kSB;
+  // MXFP4 scale groups of a panel: [groups][64 lanes][16 B], 16 super-blocks each
+  const int sgb = scale_groups(K, WFmt<kMXFP4>::kUG) * 1024;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(reinterpret_cast<const uint8_t*>(a.s) + (long)ws * s_es), 0, (int)s_es, kFlags8);
 
   auto load_a = [&](int s, u32x4_t (&ar)[kAP8], uint32_t& sw) {
 #pragma unroll
@@ -244,19 +258,34 @@ __global__ __launch_bounds__(kThreads8, 2) void gemm8_kernel(Gemm8Args a) {
     *reinterpret_cast<uint32_t*>(buf + slds) = sw;
   };
   auto load_b = [&](int s, B8Step& b) {
+    if constexpr (MX) {   // one fp4 chunk and its e8m0 byte per panel
 #pragma unroll
-    for (int p = 0; p < kPW8; ++p) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int p = 0; p < kPW8; ++p) {
         const u32x4_t v = __builtin_bit_cast(
             u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, lane * 16,
-                                                           (pan[p] * nsb + 2 * s + h) * 1024, 0));
+                                                           (pan[p] * nsb + s) * 1024, 0));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) b.w[p][4 * h + q] = (int)v[q];
+        for (int q = 0; q < 4; ++q) b.w[p][q] = (int)v[q];
+#pragma unroll
+        for (int q = 4; q < 8; ++q) b.w[p][q] = 0;
+        b.sc[p] = (int)__builtin_amdgcn_raw_buffer_load_b8(
+            rs, lane * 16 + (s % 16), pan[p] * sgb + (s / 16) * 1024, 0);
       }
+    } else {
+#pragma unroll
+      for (int p = 0; p < kPW8; ++p) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const u32x4_t v = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                           rw, lane * 16, (pan[p] * nsb + 2 * s + h) * 1024, 0));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) b.w[p][4 * h + q] = (int)v[q];
+        }
+      }
+      b.bs0 = bsc[rb0 * kb128 + s];
+      b.bs1 = bsc[rb1 * kb128 + s];
     }
-    b.bs0 = bsc[rb0 * kb128 + s];
-    b.bs1 = bsc[rb1 * kb128 + s];
   };
 
   // LDS byte offset of this lane's operand (row lane%16, k = 16q) and scale byte
@@ -286,6 +315,20 @@ __global__ __launch_bounds__(kThreads8, 2) void gemm8_kernel(Gemm8Args a) {
                             (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
         const i32x8_t al = {(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3],
                             (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
+        if constexpr (MX) {   // the weight scale is the MFMA's B scale: no fold
+#pragma unroll
+          for (int p0 = 0; p0 < kPW8; p0 += 2) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+              acc[m][p0 + j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                  ah, b.w[p0 + j], acc[m][p0 + j], 0, 4, 0, sh, 0, b.sc[p0 + j]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+              acc[m][p0 + j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                  al, b.w[p0 + j], acc[m][p0 + j], 0, 4, 0, sl, 0, b.sc[p0 + j]);
+          }
+          continue;
+        }
         // two panels at a time: the hi products of both, then the lo ones
         // (independent MFMA chains back to back), then the scaled fold
 #pragma unroll
@@ -375,13 +418,20 @@ __global__ __launch_bounds__(kThreads8, 2) void gemm8_kernel(Gemm8Args a) {
   else run(std::integral_constant<int, 1>{});
 }
 
-hipError_t launch_gemm8(bool gu, const Gemm8Args& a, int max_tiles, hipStream_t stream) {
+hipError_t launch_gemm8(int wf, bool gu, const Gemm8Args& a, int max_tiles,
+                        hipStream_t stream) {
   const long items = (long)max_tiles * (gu ? a.I / 128 : a.H / 256);
   const long grid = (items + 7) / 8 * 8;
   if (grid >= (1L << 31)) return hipErrorInvalidValue;
   if (grid == 0) return hipSuccess;
-  if (gu) gemm8_kernel<true><<<dim3((unsigned)grid), kThreads8, 0, stream>>>(a);
-  else gemm8_kernel<false><<<dim3((unsigned)grid), kThreads8, 0, stream>>>(a);
+  const dim3 g((unsigned)grid);
+  if (wf == kMXFP4) {
+    if (gu) gemm8_kernel<true, kMXFP4><<<g, kThreads8, 0, stream>>>(a);
+    else gemm8_kernel<false, kMXFP4><<<g, kThreads8, 0, stream>>>(a);
+  } else {
+    if (gu) gemm8_kernel<true, kFP8><<<g, kThreads8, 0, stream>>>(a);
+    else gemm8_kernel<false, kFP8><<<g, kThreads8, 0, stream>>>(a);
+  }
   return hipPeekAtLastError();
 }
 
@@ -424,7 +474,7 @@ hipError_t xtu_gemm8_gate_up(const uint8_t* hi, const uint8_t* lo, const uint8_t
   Gemm8Args a{hi, lo, shi, slo, sorted_tok, (const uint8_t*)w13, s13, seg_start, tile_expert,
               tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, act, H, I, w_estride,
               s_estride, limit, alpha, beta};
-  return launch_gemm8(true, a, max_tiles, stream);
+  return launch_gemm8(kFP8, true, a, max_tiles, stream);
 }
 
 hipError_t xtu_gemm8_down(const uint8_t* hi, const uint8_t* lo, const uint8_t* shi,
@@ -444,7 +494,53 @@ hipError_t xtu_gemm8_down(const uint8_t* hi, const uint8_t* lo, const uint8_t* s
   Gemm8Args a{hi, lo, shi, slo, nullptr, (const uint8_t*)w2, s2, seg_start, tile_expert,
               tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, y, H, I, w_estride,
               s_estride, 0.f, 1.f, 0.f};
-  return launch_gemm8(false, a, max_tiles, stream);
+  return launch_gemm8(kFP8, false, a, max_tiles, stream);
+}
+
+// Exact-pair grouped GEMMs for FP8 (fp32 block scales) or MXFP4 (packed e8m0
+// scale groups) weights: xtu_gemm8_* with the weight format as an argument.
+hipError_t xtu_gemm_pair_gate_up(int fmt, const uint8_t* hi, const uint8_t* lo,
+                                 const uint8_t* shi, const uint8_t* slo,
+                                 const int32_t* sorted_tok, int H, int I, const void* w13,
+                                 const void* s13, long w_estride, long s_estride,
+                                 const int32_t* slot_map, const int32_t* seg_start,
+                                 const int32_t* tile_expert, const int32_t* tile_row0,
+                                 const int32_t* expert_tile_start, const int32_t* tile_lo,
+                                 const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                                 float alpha, float beta, hipStream_t stream) {
+  XTU_CHECK_ARG(fmt == kFP8 || fmt == kMXFP4);
+  XTU_CHECK_ARG(H > 0 && I > 0 && H % 256 == 0 && I % 128 == 0 && H <= 65536);
+  XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
+  XTU_CHECK_ARG(w_estride < (1L << 31) && 2L * I * H < (1L << 31));
+  XTU_CHECK_ARG(hi && lo && shi && slo && sorted_tok && w13 && s13 && seg_start && tile_expert &&
+                tile_row0 && expert_tile_start && tile_lo && tile_hi && act);
+  if (max_tiles == 0) return hipSuccess;
+  (void)hipGetLastError();
+  Gemm8Args a{hi, lo, shi, slo, sorted_tok, (const uint8_t*)w13, (const float*)s13, seg_start,
+              tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, act, H, I,
+              w_estride, s_estride, limit, alpha, beta};
+  return launch_gemm8(fmt, true, a, max_tiles, stream);
+}
+
+hipError_t xtu_gemm_pair_down(int fmt, const uint8_t* hi, const uint8_t* lo, const uint8_t* shi,
+                              const uint8_t* slo, int H, int I, const void* w2, const void* s2,
+                              long w_estride, long s_estride, const int32_t* slot_map,
+                              const int32_t* seg_start, const int32_t* tile_expert,
+                              const int32_t* tile_row0, const int32_t* expert_tile_start,
+                              const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                              float* y, hipStream_t stream) {
+  XTU_CHECK_ARG(fmt == kFP8 || fmt == kMXFP4);
+  XTU_CHECK_ARG(H > 0 && I > 0 && H % 256 == 0 && I % 128 == 0 && I <= 65536);
+  XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
+  XTU_CHECK_ARG(w_estride < (1L << 31) && (long)H * I < (1L << 31));
+  XTU_CHECK_ARG(hi && lo && shi && slo && w2 && s2 && seg_start && tile_expert && tile_row0 &&
+                expert_tile_start && tile_lo && tile_hi && y);
+  if (max_tiles == 0) return hipSuccess;
+  (void)hipGetLastError();
+  Gemm8Args a{hi, lo, shi, slo, nullptr, (const uint8_t*)w2, (const float*)s2, seg_start,
+              tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, y, H, I,
+              w_estride, s_estride, 0.f, 1.f, 0.f};
+  return launch_gemm8(fmt, false, a, max_tiles, stream);
 }
 
 }  // extern "C"

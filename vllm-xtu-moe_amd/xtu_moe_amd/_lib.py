@@ -57,6 +57,10 @@ SIGNATURES = {
                                _vp, _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
     "xtu_gemm8_down": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp,
                             _vp, _vp, _i, _vp, _vp]),
+    "xtu_gemm_pair_gate_up": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp,
+                                   _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
+    "xtu_gemm_pair_down": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp,
+                                _vp, _vp, _vp, _vp, _i, _vp, _vp]),
     "xtu_copy_experts": (_i, [_i, _vp, _vp, _l, _vp, _l, _l, _vp]),
     "xtu_copy_2d": (_i, [_vp, _sz, _vp, _sz, _sz, _sz, _vp]),
     "xtu_i8_weight_bytes": (_sz, [_i, _i]),

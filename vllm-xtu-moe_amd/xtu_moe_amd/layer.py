@@ -370,13 +370,30 @@ def decode_max_tiles(A: int, max_active: int) -> int:
     return int(max_active) + max(int(A) - int(max_active), 0) // DECODE_TILE
 
 
+MXFP4_PREFILL_ENV = "XTU_MXFP4_PREFILL"
+
+
+MXFP4_PREFILL_DEFAULT = "bf16"
+
+
+def pair_gemm(fmt: int) -> bool:
+    """Whether the grouped GEMMs of this format run on the scaled fp8/fp4
+    MFMA with exact activation pairs: FP8 always; MXFP4 when
+    XTU_MXFP4_PREFILL=pair (default: the faster of the two as measured on
+    DeepSeek-V3 at T=8192, MXFP4_PREFILL_DEFAULT), else the bf16-operand
+    kernels (the e2m1 x e8m0 products are exact in bf16 either way)."""
+    fmt = int(fmt)
+    return fmt == FMT_FP8 or (fmt == FMT_MXFP4 and
+                              os.environ.get(MXFP4_PREFILL_ENV, MXFP4_PREFILL_DEFAULT) == "pair")
+
+
 def gemm_tile_m(fmt: int, int8: bool = False) -> int:
     """Rows per M tile of the grouped GEMM that runs for this format: INT8
-    ALIGN 128, FP8 weights the exact fp8-MFMA kernels, else the bf16-operand
-    kernels (the segmentation's tiles must match)."""
+    ALIGN 128, the exact-pair kernels (FP8, MXFP4) theirs, else the
+    bf16-operand kernels' (the segmentation's tiles must match)."""
     if int8:
         return 128
-    if int(fmt) == FMT_FP8:
+    if pair_gemm(fmt):
         return int(_lib.call("xtu_gemm8_tile_m"))
     return int(_lib.call("xtu_gemm_tile_m", int(fmt)))
 
@@ -621,19 +638,20 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
                       seg.max_tiles, seg.bm, _p(fb[2]), _p(fb[3]), _p(y), 0.0, 1.0, 0.0, st)
         return
     fmt = W.fmt
-    if fmt == FMT_FP8:
-        # exact FP8: activations split into e4m3 pairs, fp8 MFMA with the fp32
-        # block scale folded per 128-k block
+    if pair_gemm(fmt):
+        # exact pairs: activations split into e4m3 (hi, lo) with e8m0 scales;
+        # FP8 weights on the fp8 MFMA with the fp32 block scale folded per
+        # 128 k, MXFP4 weights as fp4 B operands with their e8m0 B scale
         xq = _fp8pair_bufs("x8", T, H, dev, st)
         aq = _fp8pair_bufs("a8", A, I, dev, st)
         _lib.call("xtu_fp8pair_quant", _p(x), T, H, *[_p(t) for t in xq], st)
-        _lib.call("xtu_gemm8_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
+        _lib.call("xtu_gemm_pair_gate_up", fmt, *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
                   _p(W.w13), _p(W.s13), 0, 0, _p(slot_map), _p(seg.seg_start),
                   _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi,
                   seg.max_tiles, _p(act), lim, al, be, st)
         _lib.call("xtu_fp8pair_quant", _p(act), A, I, *[_p(t) for t in aq], st)
-        _lib.call("xtu_gemm8_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(W.s2), 0, 0,
-                  _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
+        _lib.call("xtu_gemm_pair_down", fmt, *[_p(t) for t in aq], H, I, _p(W.w2), _p(W.s2), 0,
+                  0, _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
                   _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
         return
     _lib.call("xtu_gemm_gate_up", fmt, _p(x), _p(seg.sorted_tok), H, I, _p(W.w13), _p(W.s13),
