@@ -95,8 +95,9 @@ def main():
 
     from xtu_moe_amd import _lib
     from xtu_moe_amd import formats as F
-    from xtu_moe_amd.layer import (_fp8pair_bufs, _p, _stream, gemm_tile_m, int8_align_on,
-                                   moe_forward, pair_gemm, route, segmentation)
+    from xtu_moe_amd.layer import (_fp8pair_bufs, _mxpair_bufs, _p, _stream, gemm_tile_m,
+                                   int8_align_on, moe_forward, mx_pair_kernel, pair_gemm, route,
+                                   segmentation)
     from xtu_moe_amd.synthetic import synth_layer
 
     cfg = WORKLOADS[args.workload]
@@ -272,7 +273,7 @@ def main():
         # ---- dominant kernel alone (gate/up), cold cache, same stream
         seg = None
         gu_ms = []
-        bm = gemm_tile_m(fmt, i8)
+        bm = gemm_tile_m(fmt, i8, H, I)
         decode = T <= 16 and not i8
         act = torch.empty((T * K + T * NS, I), dtype=torch.bfloat16, device=dev)
         for s in range(args.steps):
@@ -280,8 +281,12 @@ def main():
             w_, i_ = route(lg_st, **rkw)
             seg = segmentation(T, K, E, NS, bm, dev).run(i_, w_)
             st = _stream()
-            fp8x = None
-            if not decode and not i8 and pair_gemm(fmt):
+            fp8x = mxx = None
+            if not decode and not i8 and mx_pair_kernel(fmt, H, I):
+                mxx = _mxpair_bufs("xm", T, H, dev)
+                s13p, _ = W.mx_pair_scales()
+                _lib.call("xtu_mx_pair_quant", _p(x_st), T, H, *[_p(t) for t in mxx], st)
+            elif not decode and not i8 and pair_gemm(fmt, H, I):
                 fp8x = _fp8pair_bufs("x8", T, H, dev)
                 _lib.call("xtu_fp8pair_quant", _p(x_st), T, H, *[_p(t) for t in fp8x], st)
             if i8:
@@ -304,6 +309,12 @@ def main():
                           _p(w13_8), _p(emin13), 0, _p(seg.seg_start), _p(seg.tile_expert),
                           _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), 0, cfg["limit"],
                           1.0, 0.0, st)
+            elif mxx is not None:
+                lo, hi = seg.tile_range_ptrs(0, E + NS)
+                _lib.call("xtu_mx_pair_gate_up", *[_p(t) for t in mxx], _p(seg.sorted_tok), H, I,
+                          _p(W.w13), _p(s13p), 0, 0, 0, _p(seg.seg_start), _p(seg.tile_expert),
+                          _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi, seg.max_tiles,
+                          _p(act), cfg["limit"], 1.0, 0.0, st)
             elif fp8x is not None:
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
                 _lib.call("xtu_gemm_pair_gate_up", fmt, *[_p(t) for t in fp8x],
@@ -374,13 +385,15 @@ def main():
                 if tr.get("distinct_experts"):   # the counter run's own routing
                     tr["algorithmic_bytes"] = (tr["distinct_experts"] * e_bytes13 + Th * H * 2
                                                + (Th * K + Th * NS) * I * 2)
-    elif pair_gemm(fmt) and not cfg["int8"]:
+    elif pair_gemm(fmt, H, I) and not cfg["int8"]:
         # scaled MFMA with an e4m3 A (FP8: e4m3 B; MXFP4: e2m1 B), which runs
         # at the fp8 rate; every algorithmic product is two MFMA products
         # (the activation's hi and lo halves)
         ach = r["gate_up_TFLOPs"]
         roof = dict(bound="mfma", achieved=ach, peak=PEAK_TFLOPS["fp8"], unit="TFLOP/s",
-                    frac=ach / PEAK_TFLOPS["fp8"], traffic=None, kernel="gemm8_kernel",
+                    frac=ach / PEAK_TFLOPS["fp8"], traffic=None,
+                    kernel=("mx_pair_gemm_kernel" if mx_pair_kernel(fmt, H, I)
+                            else "gemm8_kernel"),
                     mfma_issue_frac=2.0 * ach / PEAK_TFLOPS["fp8"],
                     frac_of_bf16_peak=ach / PEAK_TFLOPS["bf16"])
         if cfg["fmt"] == "mxfp4":
@@ -411,7 +424,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"mxfp4": ("bf16-mfma/e2m1+e8m0" if decode_head or not pair_gemm(fmt)
+        "dtype": {"mxfp4": ("bf16-mfma/e2m1+e8m0"
+                            if decode_head or not pair_gemm(fmt, H, I)
                             else "fp8xfp4-mfma/e4m3-pair x e2m1+e8m0"),
                   "fp8": ("bf16-mfma/e4m3+f32-block" if decode_head
                           else "fp8-mfma/e4m3-pair x e4m3+f32-block"),

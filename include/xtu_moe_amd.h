@@ -281,8 +281,9 @@ hipError_t xtu_gemm8_down(const uint8_t* hi, const uint8_t* lo, const uint8_t* s
  * e8m0 scale groups).  MXFP4 codes enter v_mfma_scale_f32_16x16x128_f8f6f4
  * as fp4 B operands straight from P16 (lane 16q + r: k = 32q..32q+31 of row
  * r) with their e8m0 byte as the B scale, so the product is exact with no
- * dequantisation.  Replace _gate_up_kernel / _down_kernel
- * (vllm_xiaotu_moe/gpu_prefill.py:232-390) for MXFP4 prefill. */
+ * dequantisation.  M tiles of xtu_gemm8_tile_m() rows.  Replace
+ * _gate_up_kernel / _down_kernel (vllm_xiaotu_moe/gpu_prefill.py:232-390)
+ * for MXFP4 prefill; xtu_mx_pair_* below is the faster form where it fits. */
 hipError_t xtu_gemm_pair_gate_up(int fmt, const uint8_t* hi, const uint8_t* lo,
                                  const uint8_t* shi, const uint8_t* slo,
                                  const int32_t* sorted_tok, int H, int I, const void* w13,
@@ -299,6 +300,39 @@ hipError_t xtu_gemm_pair_down(int fmt, const uint8_t* hi, const uint8_t* lo, con
                               const int32_t* tile_row0, const int32_t* expert_tile_start,
                               const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
                               float* y, hipStream_t stream);
+
+/* --------------------------------------- MXFP4 exact-pair GEMMs (32x32x64)
+ * The MXFP4 prefill GEMMs of the reference (vllm_xiaotu_moe/gpu_prefill.py:
+ * 232-390, _gate_up_kernel / _down_kernel) on v_mfma_scale_f32_32x32x64_
+ * f8f6f4 with operand layouts made for it:
+ *   xtu_mx_pair_quant: bf16 rows [M][K] -> interleaved e4m3 pairs hilo
+ *     [M][2K] (per 64 k: 64 bytes hi, 64 bytes lo) and e8m0 shi [M][K/32];
+ *     x = hi * 2^(shi-127) + lo * 2^(max(shi-4,0)-127) exactly (bf16 x).
+ *   xtu_mx_pair_scales: packed MXFP4 scale groups (E slots of s_estride
+ *     bytes, N rows, K) -> step-major [E][K/64][N/16][16][2] bytes.
+ *   xtu_mx_pair_gate_up / _down: as xtu_gemm_pair_* for fmt 2, with hilo,
+ *     shi and the step-major scales (s_estride 0: N * K / 32), M tiles of
+ *     xtu_mx_pair_tile_m() rows; shapes where xtu_mx_pair_fits(H, I). */
+int xtu_mx_pair_fits(int H, int I);
+int xtu_mx_pair_tile_m(void);
+hipError_t xtu_mx_pair_quant(const void* x, int M, int K, uint8_t* hilo, uint8_t* shi,
+                             hipStream_t stream);
+hipError_t xtu_mx_pair_scales(const uint8_t* s, int E, int N, int K, long s_estride, uint8_t* out,
+                              hipStream_t stream);
+hipError_t xtu_mx_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const int32_t* sorted_tok,
+                               int H, int I, const void* w13, const uint8_t* s13p,
+                               long w_estride, long s_estride, const int32_t* slot_map,
+                               const int32_t* seg_start, const int32_t* tile_expert,
+                               const int32_t* tile_row0, const int32_t* expert_tile_start,
+                               const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                               void* act, float limit, float alpha, float beta,
+                               hipStream_t stream);
+hipError_t xtu_mx_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int I, const void* w2,
+                            const uint8_t* s2p, long w_estride, long s_estride,
+                            const int32_t* slot_map, const int32_t* seg_start,
+                            const int32_t* tile_expert, const int32_t* tile_row0,
+                            const int32_t* expert_tile_start, const int32_t* tile_lo,
+                            const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream);
 
 /* -------------------------------------- INT8-activation x FP4-code (ALIGN) path
  * Replaces the engine's ALIGN integer path (xiaotu_moe/csrc/moe/

@@ -75,6 +75,12 @@ def test_library_loads_and_reports_version():
     assert rc == 1   # hipErrorInvalidValue
     assert all(_lib.load().xtu_gemm_tile_m(f) == 128 for f in range(4))
     assert _lib.load().xtu_gemm_tile_m(4) == 0
+    # exact-pair tiles: 64 rows (16x16x128 kernel), 128 on the MXFP4
+    # 32x32x64 kernel where the shape fits it
+    assert lib.xtu_gemm8_tile_m() == 64 and lib.xtu_mx_pair_tile_m() == 128
+    assert lib.xtu_mx_pair_fits(7168, 2048) == 1 and lib.xtu_mx_pair_fits(2048, 768) == 1
+    assert lib.xtu_mx_pair_fits(2880, 2880) == 0 and lib.xtu_mx_pair_fits(7168, 2176) == 0
+    assert lib.xtu_mx_pair_fits(32768, 2048) == 0   # activation scales of 128 rows exceed LDS
 
 
 PROBE_HEADER = os.path.join(os.path.dirname(os.path.abspath(__file__)), "probes", "xtu_probes.h")

@@ -259,7 +259,7 @@ def test_mxfp4_prefill_pair_and_bf16_paths(T, monkeypatch):
                        wts, E, NS, H, I, limit=4.0)
     for mode in ("pair", "bf16"):
         monkeypatch.setenv(L.MXFP4_PREFILL_ENV, mode)
-        assert L.pair_gemm(F.FMT_MXFP4) == (mode == "pair")
+        assert L.pair_gemm(F.FMT_MXFP4, H, I) == (mode == "pair")
         out = moe_forward(x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(wts).to(DEV),
                           W, path="gemm", swiglu_limit=4.0, out_dtype=torch.float32)
         torch.cuda.synchronize()

@@ -1,0 +1,117 @@
+"""MXFP4 exact-pair GEMMs on the 32x32x64 kernel (xtu_mx_pair_*): the
+interleaved activation pairs bit-exact against the planar quantiser's, the
+step-major scale re-layout bit-exact against the dense scales, and the layer
+against the oracle over tile shapes (single rows, partial and multi-tile
+experts, a shared expert, a SwiGLU clamp) and through a slot map on mutable
+planes (the ring / pool layout)."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_tensor_to_bits, check_close, dense_to_numpy, make_dense_layer, oracle_layer
+from xtu_moe_amd import _lib
+from xtu_moe_amd import formats as F
+from xtu_moe_amd import layer as L
+from xtu_moe_amd.layer import ExpertWeights, _p, _stream, moe_forward
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+@pytest.fixture(autouse=True)
+def _pair_mode(monkeypatch):
+    monkeypatch.setenv(L.MXFP4_PREFILL_ENV, "pair")
+
+
+@pytest.mark.parametrize("M,K", [(1, 256), (300, 1024), (37, 7168)])
+def test_interleaved_pairs_match_planar(M, K):
+    g = torch.Generator(device=DEV).manual_seed(M + K)
+    x = (torch.randn((M, K), generator=g, device=DEV) *
+         torch.exp2(torch.randint(-20, 12, (M, 1), generator=g, device=DEV).float())).to(torch.bfloat16)
+    x[0, :32] = 0        # an all-zero block
+    hi = torch.empty((M, K), dtype=torch.uint8, device=DEV)
+    lo, shi, slo = torch.empty_like(hi), torch.empty((M, K // 32), dtype=torch.uint8, device=DEV), \
+        torch.empty((M, K // 32), dtype=torch.uint8, device=DEV)
+    hilo = torch.empty((M, 2 * K), dtype=torch.uint8, device=DEV)
+    shi2 = torch.empty_like(shi)
+    st = _stream()
+    _lib.call("xtu_fp8pair_quant", _p(x), M, K, _p(hi), _p(lo), _p(shi), _p(slo), st)
+    _lib.call("xtu_mx_pair_quant", _p(x), M, K, _p(hilo), _p(shi2), st)
+    torch.cuda.synchronize()
+    il = hilo.view(M, K // 64, 2, 64)
+    assert torch.equal(il[:, :, 0].reshape(M, K), hi)
+    assert torch.equal(il[:, :, 1].reshape(M, K), lo)
+    assert torch.equal(shi2, shi)
+    # the lo scale the kernel derives is the one the planar quantiser writes
+    assert torch.equal(torch.clamp(shi.int() - 4, min=0).to(torch.uint8), slo)
+
+
+@pytest.mark.parametrize("N,K,pad", [(512, 256, 0), (4096, 7168, 0), (768, 1024, 4096)])
+def test_step_major_scales(N, K, pad):
+    E = 3
+    g = torch.Generator().manual_seed(N + K)
+    s = torch.randint(100, 140, (E, N, K // 32), generator=g, dtype=torch.uint8)
+    packed = F.pack_scales(F.FMT_MXFP4, s, N, K)
+    if pad:   # slots wider than the scale groups (a staging plane's row)
+        packed = torch.cat([packed, torch.zeros((E, pad), dtype=torch.uint8)], 1)
+    packed = packed.to(DEV)
+    out = torch.empty((E, N * K // 32), dtype=torch.uint8, device=DEV)
+    _lib.call("xtu_mx_pair_scales", _p(packed), E, N, K, packed.stride(0), _p(out), _stream())
+    torch.cuda.synchronize()
+    # [e][step][p][r][c] = s[e][16 p + r][2 step + c]
+    want = s.view(E, N // 16, 16, K // 64, 2).permute(0, 3, 1, 2, 4).reshape(E, -1)
+    assert torch.equal(out.cpu(), want)
+
+
+def _layer(E, NS, H, I, seed):
+    d = make_dense_layer(F.FMT_MXFP4, E + NS, H, I, seed=seed)
+    return d, ExpertWeights.from_dense(F.FMT_MXFP4, d["w13"], d["s13"], d["w2"], d["s2"],
+                                       n_shared=NS, device=DEV)
+
+
+@pytest.mark.parametrize("T,K,skew", [(1, 2, False), (40, 4, False), (700, 4, False), (900, 2, True)])
+def test_layer_against_oracle(T, K, skew):
+    E, NS, H, I = 16, 1, 1024, 512
+    d, W = _layer(E, NS, H, I, seed=30 + T)
+    assert L.mx_pair_kernel(F.FMT_MXFP4, H, I) and L.gemm_tile_m(F.FMT_MXFP4, False, H, I) == 128
+    rng = np.random.default_rng(31 + T)
+    if skew:   # experts 0 and 1 take most pairs: several full tiles and a partial one
+        ids = np.stack([np.array([rng.integers(0, 2), rng.integers(2, E)]) for _ in range(T)])
+    else:
+        ids = np.stack([rng.permutation(E)[:K] for _ in range(T)])
+    ids = ids.astype(np.int32)
+    wts = (rng.random((T, K)) + 0.05).astype(np.float32)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(32 + T)).to(torch.bfloat16)
+    out = moe_forward(x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(wts).to(DEV), W,
+                      path="gemm", swiglu_limit=5.0, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d), bf16_tensor_to_bits(x), ids,
+                       wts, E, NS, H, I, limit=5.0)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"mx pair T={T}")
+
+
+def test_slot_map_on_mutable_planes():
+    """Experts at permuted slots of planes flagged mutable (restaged in
+    place): the step-major scales are rebuilt per call, so restaging the
+    slots between two calls gives the new experts' results."""
+    E, NS, H, I, K, T = 8, 0, 1024, 256, 2, 300
+    d, W = _layer(E, NS, H, I, seed=40)
+    perm = torch.tensor([5, 2, 7, 0, 3, 6, 1, 4], dtype=torch.int64)
+    slots = ExpertWeights(F.FMT_MXFP4, H, I, E, 0, torch.empty_like(W.w13), torch.empty_like(W.s13),
+                          torch.empty_like(W.w2), torch.empty_like(W.s2), mutable=True)
+    rng = np.random.default_rng(41)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    wts = (rng.random((T, K)) + 0.05).astype(np.float32)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(42)).to(torch.bfloat16)
+    ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d), bf16_tensor_to_bits(x), ids,
+                       wts, E, NS, H, I)
+    xd, idd, wd = x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(wts).to(DEV)
+    for round_ in range(2):
+        p = perm if round_ == 0 else torch.roll(perm, 3)
+        for e in range(E):   # expert e at slot p[e]
+            for name in ("w13", "s13", "w2", "s2"):
+                getattr(slots, name)[p[e]].copy_(getattr(W, name)[e])
+        smap = p.to(torch.int32).to(DEV)
+        out = moe_forward(xd, idd, wd, slots, path="gemm", slot_map=smap, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"slot map round {round_}")

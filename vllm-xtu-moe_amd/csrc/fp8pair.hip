@@ -42,7 +42,7 @@
 // weights fit beside the accumulators at two waves per SIMD (96 rows spill).
 #include <type_traits>
 
-#include "weight_format.hpp"
+#include "pairgemm.hpp"
 
 namespace xtu {
 namespace {
@@ -62,19 +62,6 @@ constexpr int kFlags8 = 0x00020000;   // raw buffer resource, dword 3
 // bf16 rows -> (hi, lo, scale) pairs
 // ---------------------------------------------------------------------------
 
-// Exponent e of the block scale 2^e: the smallest e with amax / 2^e <= 448.
-__device__ __forceinline__ int pair_exponent(float amax) {
-  const uint32_t u = __float_as_uint(amax);
-  const int ex = (int)((u >> 23) & 0xff);
-  if (ex == 0) return -127;                 // zero or subnormal block
-  int e = ex - 127 - 8 + ((u & 0x7fffffu) > 0x600000u ? 1 : 0);   // 448 = 1.75 * 2^8
-  return e < -127 ? -127 : (e > 127 ? 127 : e);
-}
-
-__device__ __forceinline__ float pow2f(int e) {   // 2^e for e in [-126, 127]
-  return __uint_as_float((uint32_t)(e + 127) << 23);
-}
-
 // One thread per (row, 32-k block).
 __global__ __launch_bounds__(256) void fp8pair_quant_kernel(const uint16_t* __restrict__ x, int M,
                                                             int K, uint8_t* __restrict__ hi,
@@ -85,46 +72,15 @@ __global__ __launch_bounds__(256) void fp8pair_quant_kernel(const uint16_t* __re
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nb) return;
   const long row = i / (K / 32), blk = i % (K / 32);
-  const uint16_t* src = x + row * K + blk * 32;
-  float v[32];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const u32x4_t p = *reinterpret_cast<const u32x4_t*>(src + 8 * j);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      v[8 * j + 2 * w] = __uint_as_float(p[w] << 16);
-      v[8 * j + 2 * w + 1] = __uint_as_float(p[w] & 0xffff0000u);
-    }
-  }
-  float amax = 0.f;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-  const int e = pair_exponent(amax);
-  // x / 2^e in two exact power-of-two steps (e may be -127)
-  const float inv1 = pow2f(-(e / 2)), inv2 = pow2f(-(e - e / 2));
   uint32_t hw[8], lw[8];
-#pragma unroll
-  for (int j = 0; j < 32; j += 2) {
-    const float a = (v[j] * inv1) * inv2, b = (v[j + 1] * inv1) * inv2;
-    const int h = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
-    const float ra = (a - __builtin_amdgcn_cvt_f32_fp8(h, 0)) * 16.0f;
-    const float rb = (b - __builtin_amdgcn_cvt_f32_fp8(h, 1)) * 16.0f;
-    const int lv = __builtin_amdgcn_cvt_pk_fp8_f32(ra, rb, 0, false);
-    const int wi = j / 4, sh = (j % 4) * 8;
-    if ((j % 4) == 0) {
-      hw[wi] = 0u;
-      lw[wi] = 0u;
-    }
-    hw[wi] |= ((uint32_t)h & 0xffffu) << sh;
-    lw[wi] |= ((uint32_t)lv & 0xffffu) << sh;
-  }
+  const int sa = pair_split32(x + row * K + blk * 32, hw, lw);
   uint8_t* dh = hi + row * K + blk * 32;
   uint8_t* dl = lo + row * K + blk * 32;
   *reinterpret_cast<u32x4_t*>(dh) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
   *reinterpret_cast<u32x4_t*>(dh + 16) = u32x4_t{hw[4], hw[5], hw[6], hw[7]};
   *reinterpret_cast<u32x4_t*>(dl) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
   *reinterpret_cast<u32x4_t*>(dl + 16) = u32x4_t{lw[4], lw[5], lw[6], lw[7]};
-  const int sa = e + 127, sl = sa >= 4 ? sa - 4 : 0;
+  const int sl = sa >= 4 ? sa - 4 : 0;
   shi[i] = (uint8_t)sa;
   slo[i] = (uint8_t)sl;
 }

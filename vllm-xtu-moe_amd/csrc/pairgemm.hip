@@ -1,0 +1,478 @@
+// Exact-pair grouped GEMMs for MXFP4 weights on
+// v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 activations x e2m1 weights), with
+// the two operand layouts this kernel reads made for it:
+//
+// * activation pairs interleaved (xtu_mx_pair_quant): row r of the plane is
+//   [K/64 chunks][hi 64 B | lo 64 B], so the codes one 64-k step needs of a
+//   row are one 128-byte line; the e8m0 bytes stay [rows][K/32].
+// * weight scales step-major (xtu_mx_pair_scales, a re-layout of the packed
+//   MXFP4 scale groups): [expert][K/64][N/16 panels][16 rows][2] bytes (the
+//   two 32-k blocks of the step), so the scales of the work item's 512
+//   weight rows for one step are one or two contiguous runs.
+//
+// Per 64-k step and 32 x 32 block:
+//   acc = mfma(hi, w, acc; sa, sw) ; acc = mfma(lo, w, acc; sl, sw)
+// with sl = max(sa - 4, 0) -- the weight's e8m0 byte is the MFMA's B scale,
+// so every product is the dequantised-fp32 one and only the fp32 summation
+// order differs.
+//
+// Work item: 128 rows of one expert's sorted pairs (an m tile of the
+// segmentation, bm = 128) x 512 weight rows (gate/up: 256 gate rows and the
+// matching 256 up rows; down: 512 output columns), K in steps of 64.  Items
+// are expert-major, then N block, then m tile, dealt to the eight XCDs in
+// contiguous ranges.  Four waves, each 64 rows x 256 weight rows (2 x 8
+// blocks of 32 x 32, 256 accumulator registers).
+//
+// Operand layout of the 32x32x64 MFMA (checked on the device): lane l is row
+// (column) l % 32, h = l / 32; an e4m3 operand lane holds k = 16h..16h+15
+// (bytes 0-15) and 32+16h..32+16h+15 (bytes 16-31) of the 64-k block; an
+// e2m1 operand lane holds k = 32h..32h+31 (16 bytes, low nibble first) --
+// one P16 fp4 chunk; the e8m0 scale byte of a lane applies to its row
+// (column) and the 32-k block h.
+//
+// LDS: the activation scales of the item's 128 rows for all of K, loaded
+// once (with the rows' source indices); three stages of [A 128 rows x 128 B
+// | B 512 x 32 B | B scales 1 KB]
+// filled straight from memory by global_load_lds_dwordx4 / _dword (lane l's
+// bytes land at the instruction's LDS base + 16 l / 4 l, so each lane loads
+// the piece that belongs at its slot).  A row's eight 16-byte pieces (hi
+// 0-3, lo 4-7) sit at slot piece ^ (row & 7), B's two at slot
+// piece ^ ((col >> 3) & 1): the b128 fragment reads of consecutive rows hit
+// distinct banks.
+//
+// Step s (one barrier): issue the loads of step s + 2 into the stage last
+// read for step s - 1 (before the barrier of step s - 1); the MFMAs of row
+// block 0 on the fragments of step s (read during step s - 1); wait until
+// this wave's loads of step s + 1 have landed (the loads of step s + 2 may
+// still be in flight) and its LDS reads are done; barrier; read the
+// fragments of step s + 1; the MFMAs of row block 1.
+#include "pairgemm.hpp"
+
+namespace xtu {
+namespace {
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kPM = 128;            // rows per m tile
+constexpr int kPN = 512;            // weight rows per work item
+constexpr int kPThreads = 256;
+constexpr int kStages = 3;
+
+constexpr int kLA = kPM * 128;      // A codes [row][8 pieces of 16 B]
+constexpr int kLB = kPN * 32;       // B codes [col][2 pieces of 16 B]
+constexpr int kLBS = kPN * 2;       // B scales [col][2]
+constexpr int kStage = kLA + kLB + kLBS;
+constexpr int kStagesBytes = kStages * kStage;
+constexpr int kLdsMax = 160 * 1024;
+
+// LDS row stride of the activation scales: K/32 bytes padded to an odd
+// number of dwords (conflict-free byte reads of 32 consecutive rows)
+__host__ __device__ constexpr int asc_stride(int K) { return ((K / 32 + 4) / 8) * 8 + 4; }
+// the scale area rounded up to whole 256-byte load chunks, then the tile's
+// 128 source rows (int32)
+__host__ __device__ constexpr int asc_bytes(int K) { return (kPM * asc_stride(K) + 255) / 256 * 256; }
+__host__ __device__ constexpr int lds_bytes(int K) { return kStagesBytes + asc_bytes(K) + 4 * kPM; }
+
+// Memory-to-LDS loads (saddr form: a wave-uniform 64-bit base plus a 32-bit
+// lane offset; M0 holds the LDS address that lane 0's bytes go to).  Written
+// as asm so that the compiler does not make every later LDS read wait for
+// all of them; the pipeline waits with explicit vmcnt counts and barriers.
+__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, const uint8_t* dst) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "{m0}"((uint32_t)(uintptr_t)dst) : "memory");
+}
+__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, const uint8_t* dst) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(off), "s"(base), "{m0}"((uint32_t)(uintptr_t)dst) : "memory");
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8)
+constexpr int kLoadsPerStep = 9;    // loads per lane and step (A 4, B 4, B scales 1)
+constexpr int wait_vm_lgkm0(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
+
+struct MxPairArgs {
+  const uint8_t* hilo;        // gate/up: x pairs [T][2K]; down: act pairs [A][2K]
+  const uint8_t* shi;         // [rows][K/32] e8m0 of hi
+  const int32_t* sorted_tok;  // gate/up row gather
+  const uint8_t* w;           // P16 e2m1 codes, expert-major
+  const uint8_t* s;           // step-major e8m0 [K/64][N/16][16][2] per expert
+  const int32_t* seg_start;
+  const int32_t* tile_expert;
+  const int32_t* tile_row0;
+  const int32_t* expert_tile_start;
+  const int32_t* tile_lo;
+  const int32_t* tile_hi;
+  const int32_t* slot_map;
+  void* out;                  // gate/up: act bf16 [A][I]; down: y fp32 [A][H]
+  int H, I;
+  long w_estride, s_estride;
+  float limit, alpha, beta;
+};
+
+// ---------------------------------------------------------------------------
+// bf16 rows -> interleaved pairs; one thread per (row, 32-k block)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mx_pair_quant_kernel(const uint16_t* __restrict__ x, int M,
+                                                            int K, uint8_t* __restrict__ hilo,
+                                                            uint8_t* __restrict__ shi) {
+  const long nb = (long)M * (K / 32);
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nb) return;
+  const long row = i / (K / 32), blk = i % (K / 32);
+  uint32_t hw[8], lw[8];
+  const int sa = pair_split32(x + row * K + blk * 32, hw, lw);
+  uint8_t* d = hilo + row * 2L * K + (blk / 2) * 128 + (blk % 2) * 32;
+  *reinterpret_cast<u32x4_t*>(d) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+  *reinterpret_cast<u32x4_t*>(d + 16) = u32x4_t{hw[4], hw[5], hw[6], hw[7]};
+  *reinterpret_cast<u32x4_t*>(d + 64) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
+  *reinterpret_cast<u32x4_t*>(d + 80) = u32x4_t{lw[4], lw[5], lw[6], lw[7]};
+  shi[i] = (uint8_t)sa;
+}
+
+// ---------------------------------------------------------------------------
+// packed MXFP4 scale groups -> step-major; one thread per output byte
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mx_pair_scales_kernel(const uint8_t* __restrict__ s, int E,
+                                                             int N, int K, long s_estride,
+                                                             uint8_t* __restrict__ out) {
+  const long per = (long)N * (K / 32);
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)E * per) return;
+  const long e = i / per, o = i % per;
+  // o = ((step * N/16 + p) * 16 + r) * 2 + c: row 16 p + r, 32-k block 2 step + c
+  const int c = (int)(o % 2), r = (int)((o / 2) % 16);
+  const long p = (o / 32) % (N / 16), step = o / 32 / (N / 16);
+  const long j = 2 * step + c, sb = j / 4, q = j % 4;
+  const long sgb = scale_groups(K, WFmt<kMXFP4>::kUG) * 1024;
+  out[i] = s[e * s_estride + p * sgb + (sb / 16) * 1024 + (16 * q + r) * 16 + sb % 16];
+}
+
+// ---------------------------------------------------------------------------
+// grouped GEMM
+// ---------------------------------------------------------------------------
+template <bool GU>
+__global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+  // ---- work item
+  const int nbn = GU ? a.I / 256 : a.H / 512;
+  const int tlo = a.tile_lo[0];
+  const int total = (a.tile_hi[0] - tlo) * nbn;
+  const int per = (total + 7) / 8;
+  const int idx = blockIdx.x / 8;
+  if (idx >= per) return;
+  const int item = (blockIdx.x % 8) * per + idx;
+  if (item >= total) return;
+  const int j0 = tlo + item / nbn;
+  const int e = a.tile_expert[j0];
+  const int t0 = a.expert_tile_start[e];
+  const int ntl = a.expert_tile_start[e + 1] - t0;
+  const int local = tlo * nbn + item - t0 * nbn;
+  const int nb = local / ntl, tile = t0 + local % ntl;
+  const int ws = a.slot_map ? a.slot_map[e] : e;
+  const int row0 = a.tile_row0[tile];
+  const int rows = min(kPM, a.seg_start[e + 1] - row0);
+  const int K = GU ? a.H : a.I;
+  const int nsteps = K / 64;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int lane = tid % 64;
+  const int wm = w & 1, wn = w >> 1;
+  const int ascs = asc_stride(K);
+  uint8_t* asc = lds + kStagesBytes;
+  int32_t* srow = reinterpret_cast<int32_t*>(asc + asc_bytes(K));
+
+  // source row of every tile row (rows past the tile repeat its last row)
+  if (tid < kPM) {
+    const int rr = min(tid, rows - 1);
+    srow[tid] = GU ? a.sorted_tok[row0 + rr] : row0 + rr;
+  }
+  __syncthreads();
+
+  // Every load address is a wave-uniform base (scalar registers) plus a
+  // 32-bit per-lane offset: activation offsets are below rows * 2K < 2^32
+  // (the quantiser's bound), weight offsets below two panels.
+  //
+  // ---- A codes: instruction i of wave w covers tile rows 8 (4 w + i) ..
+  // + 8: lane l holds row 8 (4 w + i) + l / 8, slot l % 8, i.e. piece
+  // (l % 8) ^ (row & 7) = (l % 8) ^ (l / 8) of the row's 128-byte line
+  uint32_t aoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    aoff[i] = (uint32_t)srow[8 * (4 * w + i) + lane / 8] * (uint32_t)(2 * K) +
+              (uint32_t)(((lane % 8) ^ (lane / 8)) * 16);
+
+  // ---- weights.  Local weight row c in [0, 512): gate/up rows 0..255 are
+  // gate rows nb * 256 + c, rows 256..511 the up rows I + nb * 256 + c - 256;
+  // down rows nb * 512 + c.  Global P16 panel of local panel p (16 rows):
+  auto gpanel = [&](int p) -> long {
+    if (GU) return p < 16 ? nb * 16 + p : a.I / 16 + nb * 16 + (p - 16);
+    return nb * 32 + p;
+  };
+  const long nw = GU ? 2L * a.I : (long)a.H;
+  const long w_es = a.w_estride ? a.w_estride : WFmt<kMXFP4>::w_bytes(nw, K);
+  const long s_es = a.s_estride ? a.s_estride : nw * (K / 32);
+  const uint8_t* wexp = a.w + (long)ws * w_es;
+  const uint8_t* sexp = a.s + (long)ws * s_es;
+  // chunk c = 4 w + i (i < 4) holds panels 2c, 2c + 1 (adjacent in memory
+  // too): lane l -> column 32 c + l / 2 (panel 2c + l / 32, row (l / 2) % 16),
+  // slot l % 2 = piece (l % 2) ^ ((col >> 3) & 1) = (l % 2) ^ ((l / 16) & 1)
+  // of the step's two P16 chunks 2 (s % 2) + piece of super-block s / 2
+  const long wpanel = (long)(K / 128) * 1024;
+  const uint32_t boff = (uint32_t)((lane / 32) * wpanel +
+                                   ((((lane % 2) ^ ((lane / 16) & 1)) * 16 + (lane / 2) % 16) * 16));
+  // weight scales of step s: 32 bytes per panel, nw / 16 panels per step;
+  // wave w loads local bytes 256 w .. + 256 (gate/up: waves 0, 1 the gate
+  // run, 2, 3 the up run; down: one run of 1 KB)
+  const long srun = GU ? (w < 2 ? (long)nb * 512 + 256 * w : (long)(a.I / 16 + nb * 16) * 32 + 256 * (w - 2))
+                       : (long)nb * 1024 + 256 * w;
+  const long sstep = (nw / 16) * 32;
+
+  // one batch of loads (kLoadsPerStep per lane): step s into stage st
+  auto issue = [&](int s, int st) {
+    const uint8_t* sb = lds + st * kStage;
+    const uint8_t* ab = a.hilo + s * 128;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(ab, aoff[i], sb + (4 * w + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint8_t* wb = wexp + gpanel(2 * (4 * w + i)) * wpanel + (s / 2) * 1024 + (s % 2) * 512;
+      dma16(wb, boff, sb + kLA + (4 * w + i) * 1024);
+    }
+    dma4(sexp + s * sstep + srun, 4 * lane, sb + kLA + kLB + 256 * w);
+  };
+
+  // ---- activation scales of the tile's rows, all of K (row r at r * ascs):
+  // 256-byte chunks c = w, w + 4, ..., lane l -> dword 64 c + l of the area
+  // (pad dwords load the row's first dword).  Issued before the first batch
+  // of codes, so the wait for that batch covers them.
+  {
+    const int ascw = ascs / 4, nch = asc_bytes(K) / 256;
+    for (int c = w; c < nch; c += 4) {
+      const int d = 64 * c + lane;
+      const int r = min(d / ascw, kPM - 1), q = d % ascw;
+      dma4(a.shi, (uint32_t)srow[r] * (uint32_t)(K / 32) + 4 * (q < K / 128 ? q : 0), asc + 256 * c);
+    }
+  }
+
+  // ---- fragments of this lane
+  const int r32 = lane % 32, h = lane / 32;
+  int arow[2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) arow[mb] = 64 * wm + 32 * mb + r32;
+  int bcol[8];
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb)
+    bcol[cb] = GU ? (cb < 4 ? 0 : 256) + 128 * wn + 32 * (cb % 4) + r32 : 256 * wn + 32 * cb + r32;
+
+  f32x16_t acc[2][8];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mb][cb][i] = 0.f;
+
+  struct Frags {
+    i32x8_t a[2][2];   // [mb][plane]
+    int sa[2];         // e8m0 of hi; lo's is max(sa - 4, 0)
+    u32x4_t b[8];
+    int sb[8];
+  };
+  auto read_frags = [&](const uint8_t* buf, int s, Frags& f) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const int R = arow[mb];
+      f.sa[mb] = asc[R * ascs + 2 * s + h];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const uint8_t* base = buf + R * 128;
+        const u32x4_t x0 = *reinterpret_cast<const u32x4_t*>(base + 16 * ((4 * p + h) ^ (R & 7)));
+        const u32x4_t x1 = *reinterpret_cast<const u32x4_t*>(base + 16 * ((4 * p + 2 + h) ^ (R & 7)));
+        f.a[mb][p] = i32x8_t{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
+                             (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+      }
+    }
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) {
+      const int C = bcol[cb];
+      f.b[cb] = *reinterpret_cast<const u32x4_t*>(buf + kLA + C * 32 + 16 * (h ^ ((C >> 3) & 1)));
+      f.sb[cb] = buf[kLA + kLB + C * 2 + h];
+    }
+  };
+  auto mfma_rows = [&](const Frags& f, int mb) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int sa = p == 0 ? f.sa[mb] : (f.sa[mb] >= 4 ? f.sa[mb] - 4 : 0);
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) {
+        const u32x4_t x = f.b[cb];
+        const i32x8_t b = i32x8_t{(int)x[0], (int)x[1], (int)x[2], (int)x[3], 0, 0, 0, 0};
+        acc[mb][cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            f.a[mb][p], b, acc[mb][cb], 0, 4, 0, sa, 0, f.sb[cb]);
+      }
+    }
+  };
+
+  // ---- pipeline (nsteps = K / 64 is even and >= 8)
+  issue(0, 0);
+  issue(1, 1);
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoadsPerStep));   // scales, step 0 landed
+  __syncthreads();
+  Frags f0, f1;
+  read_frags(lds, 0, f0);
+  // steps s < nsteps - 2 issue the loads of step s + 2
+  auto step = [&](int s, Frags& cur, Frags& nxt) {
+    issue(s + 2, (s + 2) % kStages);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_rows(cur, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoadsPerStep));   // step s + 1 landed
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(lds + ((s + 1) % kStages) * kStage, s + 1, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_rows(cur, 1);
+  };
+  for (int s = 0; s < nsteps - 2; s += 2) {
+    step(s, f0, f1);
+    step(s + 1, f1, f0);
+  }
+  // step nsteps - 2: no more loads to issue
+  __builtin_amdgcn_sched_barrier(0);
+  mfma_rows(f0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+  read_frags(lds + ((nsteps - 1) % kStages) * kStage, nsteps - 1, f1);
+  __builtin_amdgcn_sched_barrier(0);
+  mfma_rows(f0, 1);
+  mfma_rows(f1, 0);
+  mfma_rows(f1, 1);
+
+  // ---- epilogue.  32x32 result lane layout: column l % 32, rows
+  // 8 (i / 4) + 4 (l / 32) + i % 4
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 64 * wm + 32 * mb + 8 * (i / 4) + 4 * h + (i % 4);
+      if (r >= rows) continue;
+      const long prow = row0 + r;
+      if constexpr (GU) {
+        uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+          const long col = (long)nb * 256 + 128 * wn + 32 * cb + r32;
+          act[prow * a.I + col] = f32_to_bf16(
+              silu_gate(acc[mb][cb][i], acc[mb][cb + 4][i], a.limit, a.alpha, a.beta));
+        }
+      } else {
+        float* y = reinterpret_cast<float*>(a.out);
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb)
+          y[prow * a.H + (long)nb * 512 + 256 * wn + 32 * cb + r32] = acc[mb][cb][i];
+      }
+    }
+  }
+}
+
+// Shapes the kernel takes: gate/up N blocks of 256, down of 512 (so K = H
+// and K = I are multiples of 256: an even number of 64-k steps, at least 4),
+// LDS for the activation scales of 128 rows.
+bool mx_fits(int H, int I) {
+  return H > 0 && I > 0 && I % 256 == 0 && H % 512 == 0 && lds_bytes(H) <= kLdsMax &&
+         lds_bytes(I) <= kLdsMax;
+}
+
+hipError_t launch(bool gu, const MxPairArgs& a, int max_tiles, hipStream_t stream) {
+  const long items = (long)max_tiles * (gu ? a.I / 256 : a.H / 512);
+  const long grid = (items + 7) / 8 * 8;
+  if (grid >= (1L << 31)) return hipErrorInvalidValue;
+  if (grid == 0) return hipSuccess;
+  const dim3 g((unsigned)grid);
+  const size_t lds = lds_bytes(gu ? a.H : a.I);
+  if (gu) mx_pair_gemm_kernel<true><<<g, kPThreads, lds, stream>>>(a);
+  else mx_pair_gemm_kernel<false><<<g, kPThreads, lds, stream>>>(a);
+  return hipPeekAtLastError();
+}
+
+}  // namespace
+}  // namespace xtu
+
+using namespace xtu;
+
+extern "C" {
+
+int xtu_mx_pair_fits(int H, int I) { return mx_fits(H, I) ? 1 : 0; }
+
+int xtu_mx_pair_tile_m(void) { return kPM; }
+
+hipError_t xtu_mx_pair_quant(const void* x, int M, int K, uint8_t* hilo, uint8_t* shi,
+                             hipStream_t stream) {
+  XTU_CHECK_ARG(M >= 0 && K > 0 && K % 128 == 0 && 2L * M * K < (1L << 32));
+  XTU_CHECK_ARG(M == 0 || (x && hilo && shi));
+  if (M == 0) return hipSuccess;
+  (void)hipGetLastError();
+  const long n = (long)M * (K / 32);
+  mx_pair_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
+      (const uint16_t*)x, M, K, hilo, shi);
+  return hipPeekAtLastError();
+}
+
+hipError_t xtu_mx_pair_scales(const uint8_t* s, int E, int N, int K, long s_estride, uint8_t* out,
+                              hipStream_t stream) {
+  XTU_CHECK_ARG(E >= 0 && N > 0 && N % 16 == 0 && K > 0 && K % 128 == 0);
+  XTU_CHECK_ARG(s_estride >= WFmt<kMXFP4>::s_bytes(N, K) && (long)E * N * (K / 32) < (1L << 40));
+  XTU_CHECK_ARG(E == 0 || (s && out));
+  if (E == 0) return hipSuccess;
+  (void)hipGetLastError();
+  const long n = (long)E * N * (K / 32);
+  mx_pair_scales_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(s, E, N, K, s_estride,
+                                                                          out);
+  return hipPeekAtLastError();
+}
+
+hipError_t xtu_mx_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const int32_t* sorted_tok,
+                               int H, int I, const void* w13, const uint8_t* s13p,
+                               long w_estride, long s_estride, const int32_t* slot_map,
+                               const int32_t* seg_start, const int32_t* tile_expert,
+                               const int32_t* tile_row0, const int32_t* expert_tile_start,
+                               const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                               void* act, float limit, float alpha, float beta,
+                               hipStream_t stream) {
+  XTU_CHECK_ARG(mx_fits(H, I));
+  XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
+  XTU_CHECK_ARG(w_estride < (1L << 31) && 2L * I * H < (1L << 32));
+  XTU_CHECK_ARG(hilo && shi && sorted_tok && w13 && s13p && seg_start && tile_expert &&
+                tile_row0 && expert_tile_start && tile_lo && tile_hi && act);
+  if (max_tiles == 0) return hipSuccess;
+  (void)hipGetLastError();
+  const MxPairArgs a{hilo, shi, sorted_tok, (const uint8_t*)w13, s13p, seg_start, tile_expert,
+                     tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, act, H, I,
+                     w_estride, s_estride, limit, alpha, beta};
+  return launch(true, a, max_tiles, stream);
+}
+
+hipError_t xtu_mx_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int I, const void* w2,
+                            const uint8_t* s2p, long w_estride, long s_estride,
+                            const int32_t* slot_map, const int32_t* seg_start,
+                            const int32_t* tile_expert, const int32_t* tile_row0,
+                            const int32_t* expert_tile_start, const int32_t* tile_lo,
+                            const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream) {
+  XTU_CHECK_ARG(mx_fits(H, I));
+  XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
+  XTU_CHECK_ARG(w_estride < (1L << 31) && (long)H * I < (1L << 31));
+  XTU_CHECK_ARG(hilo && shi && w2 && s2p && seg_start && tile_expert && tile_row0 &&
+                expert_tile_start && tile_lo && tile_hi && y);
+  if (max_tiles == 0) return hipSuccess;
+  (void)hipGetLastError();
+  const MxPairArgs a{hilo, shi, nullptr, (const uint8_t*)w2, s2p, seg_start, tile_expert,
+                     tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, y, H, I,
+                     w_estride, s_estride, 0.f, 1.f, 0.f};
+  return launch(false, a, max_tiles, stream);
+}
+
+}  // extern "C"

@@ -52,6 +52,14 @@ SIGNATURES = {
                            _i, _vp, _vp]),
     "xtu_combine": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
     "xtu_gemm8_tile_m": (_i, []),
+    "xtu_mx_pair_fits": (_i, [_i, _i]),
+    "xtu_mx_pair_tile_m": (_i, []),
+    "xtu_mx_pair_quant": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
+    "xtu_mx_pair_scales": (_i, [_vp, _i, _i, _i, _l, _vp, _vp]),
+    "xtu_mx_pair_gate_up": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
+                                 _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
+    "xtu_mx_pair_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _vp, _i, _vp, _vp]),
     "xtu_fp8pair_quant": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "xtu_gemm8_gate_up": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp,
                                _vp, _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
@@ -78,6 +86,7 @@ SIGNATURES = {
 _NOT_STATUS = {"xtu_version", "xtu_error_string", "xtu_segment_workspace_bytes",
                "xtu_route_segment_small_max_pairs",
                "xtu_segment_max_tiles", "xtu_gemm_tile_m", "xtu_gemm8_tile_m",
+               "xtu_mx_pair_fits", "xtu_mx_pair_tile_m",
                "xtu_decode_down_combine_ok", "xtu_decode_route_shared_ok",
                "xtu_i8_weight_bytes"}
 

@@ -211,4 +211,4 @@ def empty_slots(fmt, H, I, n_slots, like: HostExpertStore, device) -> ExpertWeig
         planes[name] = None if src is None else torch.empty((n_slots,) + tuple(src.shape[1:]),
                                                             dtype=src.dtype, device=device)
     return ExpertWeights(fmt, H, I, n_slots, 0, planes["w13"], planes["s13"], planes["w2"],
-                         planes["s2"], planes["gs13"], planes["gs2"])
+                         planes["s2"], planes["gs13"], planes["gs2"], mutable=True)

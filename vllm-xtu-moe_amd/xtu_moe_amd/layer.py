@@ -60,11 +60,16 @@ class ExpertWeights:
     fp32 [E+NS] (NVFP4 global scales) or None.
     """
 
-    def __init__(self, fmt, H, I, E, n_shared, w13, s13, w2, s2, gs13=None, gs2=None):
+    def __init__(self, fmt, H, I, E, n_shared, w13, s13, w2, s2, gs13=None, gs2=None, *,
+                 mutable=False):
         self.fmt, self.H, self.I, self.E, self.n_shared = int(fmt), int(H), int(I), int(E), int(n_shared)
         self.w13, self.s13, self.w2, self.s2, self.gs13, self.gs2 = w13, s13, w2, s2, gs13, gs2
+        # mutable: the planes are restaged in place (ring / pool slots), so
+        # nothing derived from them is cached
+        self.mutable = bool(mutable)
         self._i8 = None
         self._i8_fb = None
+        self._mxs = None
         if self.H % 256 or self.I % 128:
             raise ValueError(f"unsupported shape H={H} I={I} (need H % 256 == 0, I % 128 == 0)")
 
@@ -104,6 +109,30 @@ class ExpertWeights:
         s2p = pack_scales(fmt, mv(s2), H, I)
         E = Et - n_shared if E is None else E
         return cls(fmt, H, I, E, n_shared, w13p, s13p, w2p, s2p, mv(gs13), mv(gs2))
+
+    # ------------------------------------------------------ MXFP4 pair GEMM
+    def mx_pair_scales(self, stream=None):
+        """(s13, s2) re-laid step-major for the MXFP4 exact-pair GEMM:
+        [slot][K/64][N/16][16][2] e8m0 bytes.  Built once (a device kernel over
+        the packed scale groups) unless the planes are mutable, then per call
+        into a scratch buffer."""
+        if self._mxs is not None and not self.mutable:
+            return self._mxs
+        if self.fmt != FMT_MXFP4:
+            raise ValueError("step-major pair scales are for MXFP4 weights")
+        n, dev, st = self.n_experts, self.device, _stream(stream)
+        out = []
+        for (sc, N, K, tag) in ((self.s13, 2 * self.I, self.H, "mxs13"), (self.s2, self.H, self.I, "mxs2")):
+            shape = (n, N * (K // 32))
+            t = (_buf(tag, shape, torch.uint8, dev, st) if self.mutable else
+                 torch.empty(shape, dtype=torch.uint8, device=dev))
+            _lib.call("xtu_mx_pair_scales", _p(sc), n, N, K, sc.stride(0) * sc.element_size(),
+                      _p(t), st)
+            out.append(t)
+        if self.mutable:
+            return tuple(out)
+        self._mxs = tuple(out)
+        return self._mxs
 
     # ---------------------------------------------------------------- INT8
     def int8_planes(self):
@@ -373,27 +402,48 @@ def decode_max_tiles(A: int, max_active: int) -> int:
 MXFP4_PREFILL_ENV = "XTU_MXFP4_PREFILL"
 
 
-MXFP4_PREFILL_DEFAULT = "bf16"
+# "auto": the exact-pair GEMMs where the 32x32x64 MXFP4 kernel takes the shape
+# (faster than the bf16-operand kernels on DeepSeek-V3 at T=8192), else the
+# bf16-operand kernels; "pair" / "bf16" force one of the two
+MXFP4_PREFILL_DEFAULT = "auto"
 
 
-def pair_gemm(fmt: int) -> bool:
-    """Whether the grouped GEMMs of this format run on the scaled fp8/fp4
-    MFMA with exact activation pairs: FP8 always; MXFP4 when
-    XTU_MXFP4_PREFILL=pair (default: the faster of the two as measured on
-    DeepSeek-V3 at T=8192, MXFP4_PREFILL_DEFAULT), else the bf16-operand
-    kernels (the e2m1 x e8m0 products are exact in bf16 either way)."""
+def _mx_fits(H: int, I: int) -> bool:
+    return bool(_lib.call("xtu_mx_pair_fits", int(H), int(I)))
+
+
+def pair_gemm(fmt: int, H: int = 0, I: int = 0) -> bool:
+    """Whether the grouped GEMMs of this format (layer shape H, I) run on
+    the scaled fp8/fp4 MFMA with exact activation pairs: FP8 always; MXFP4
+    per XTU_MXFP4_PREFILL (default MXFP4_PREFILL_DEFAULT), else the
+    bf16-operand kernels (the e2m1 x e8m0 products are exact in bf16 either
+    way)."""
     fmt = int(fmt)
-    return fmt == FMT_FP8 or (fmt == FMT_MXFP4 and
-                              os.environ.get(MXFP4_PREFILL_ENV, MXFP4_PREFILL_DEFAULT) == "pair")
+    if fmt == FMT_FP8:
+        return True
+    if fmt != FMT_MXFP4:
+        return False
+    mode = os.environ.get(MXFP4_PREFILL_ENV, MXFP4_PREFILL_DEFAULT)
+    return mode == "pair" or (mode == "auto" and _mx_fits(H, I))
 
 
-def gemm_tile_m(fmt: int, int8: bool = False) -> int:
-    """Rows per M tile of the grouped GEMM that runs for this format: INT8
-    ALIGN 128, the exact-pair kernels (FP8, MXFP4) theirs, else the
-    bf16-operand kernels' (the segmentation's tiles must match)."""
+def mx_pair_kernel(fmt: int, H: int, I: int) -> bool:
+    """Whether the exact-pair GEMMs of this layer run on the MXFP4 32x32x64
+    kernel (interleaved activation pairs, step-major scales): MXFP4 on the
+    pair path where the shape fits it (I % 256, H % 512); otherwise the
+    16x16x128 exact-pair kernel."""
+    return int(fmt) == FMT_MXFP4 and pair_gemm(fmt, H, I) and _mx_fits(H, I)
+
+
+def gemm_tile_m(fmt: int, int8: bool = False, H: int = 0, I: int = 0) -> int:
+    """Rows per M tile of the grouped GEMM that runs for this format and
+    layer shape: INT8 ALIGN 128, the exact-pair kernels (FP8, MXFP4) theirs,
+    else the bf16-operand kernels' (the segmentation's tiles must match)."""
     if int8:
         return 128
-    if pair_gemm(fmt):
+    if pair_gemm(fmt, H, I):
+        if mx_pair_kernel(fmt, H, I):
+            return int(_lib.call("xtu_mx_pair_tile_m"))
         return int(_lib.call("xtu_gemm8_tile_m"))
     return int(_lib.call("xtu_gemm_tile_m", int(fmt)))
 
@@ -457,6 +507,12 @@ def _route_shared_ok(fmt, mode, T, E, K, router, H, I, NS) -> bool:
                           int(K), n_group, int(NS), int(H), int(I)))
 
 
+def _mxpair_bufs(tag, M, K, dev, stream=None):
+    """Interleaved activation pairs [M][2K] and their e8m0 bytes [M][K/32]."""
+    return (_buf(tag + "_hilo", (max(M, 1), 2 * K), torch.uint8, dev, stream),
+            _buf(tag + "_shi", (max(M, 1), K // 32), torch.uint8, dev, stream))
+
+
 def _fp8pair_bufs(tag, M, K, dev, stream=None):
     return (_buf(tag + "_hi", (max(M, 1), K), torch.uint8, dev, stream),
             _buf(tag + "_lo", (max(M, 1), K), torch.uint8, dev, stream),
@@ -510,7 +566,7 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         raise ValueError(f"decode path handles at most {DECODE_MAX_TOKENS} tokens")
     # decode: the gate/up and down kernels take the segmentation's 16-row
     # tiles as work slots (every row of a bucket, however many)
-    bm = DECODE_TILE if path == "decode" else gemm_tile_m(fmt, int8)
+    bm = DECODE_TILE if path == "decode" else gemm_tile_m(fmt, int8, W.H, W.I)
     seg = segmentation(T, K, E, NS, bm, dev, st)
     odt = out_dtype if out is None else out.dtype
     max_active = min(E, T * K) + NS
@@ -638,7 +694,22 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
                       seg.max_tiles, seg.bm, _p(fb[2]), _p(fb[3]), _p(y), 0.0, 1.0, 0.0, st)
         return
     fmt = W.fmt
-    if pair_gemm(fmt):
+    if mx_pair_kernel(fmt, H, I):
+        # exact pairs, interleaved, on the MXFP4 32x32x64 kernel
+        s13p, s2p = W.mx_pair_scales(st)
+        xq = _mxpair_bufs("xm", T, H, dev, st)
+        aq = _mxpair_bufs("am", A, I, dev, st)
+        _lib.call("xtu_mx_pair_quant", _p(x), T, H, *[_p(t) for t in xq], st)
+        _lib.call("xtu_mx_pair_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
+                  _p(W.w13), _p(s13p), 0, 0, _p(slot_map), _p(seg.seg_start),
+                  _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi,
+                  seg.max_tiles, _p(act), lim, al, be, st)
+        _lib.call("xtu_mx_pair_quant", _p(act), A, I, *[_p(t) for t in aq], st)
+        _lib.call("xtu_mx_pair_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(s2p), 0, 0,
+                  _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
+                  _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
+        return
+    if pair_gemm(fmt, H, I):
         # exact pairs: activations split into e4m3 (hi, lo) with e8m0 scales;
         # FP8 weights on the fp8 MFMA with the fp32 block scale folded per
         # 128 k, MXFP4 weights as fp4 B operands with their e8m0 B scale

@@ -177,7 +177,7 @@ def gpu_moe_layer_from_engine_tiled(engine, x, topk_ids, topk_weights, H: int, I
     for b, e in enumerate(streamed + res_list):
         id_map_h[e] = b
     id_map = id_map_h.to(device, non_blocking=True)
-    bm = gemm_tile_m(fmt)
+    bm = gemm_tile_m(fmt, False, H, I)
     seg = segmentation(T, K, E, NS, bm, device, st)
     seg.run(ids, wts, id_map, True, st)
     y = _buf("ring_y", (max(seg.A, 1), H), torch.float32, device, st)
