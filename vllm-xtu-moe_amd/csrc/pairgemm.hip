@@ -46,6 +46,8 @@
 // this wave's loads of step s + 1 have landed (the loads of step s + 2 may
 // still be in flight) and its LDS reads are done; barrier; read the
 // fragments of step s + 1; the MFMAs of row block 1.
+#include <type_traits>
+
 #include "pairgemm.hpp"
 
 namespace xtu {
@@ -229,18 +231,23 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
                        : (long)nb * 1024 + 256 * w;
   const long sstep = (nw / 16) * 32;
 
-  // one batch of loads (kLoadsPerStep per lane): step s into stage st
-  auto issue = [&](int s, int st) {
+  // load d (0..kLoadsPerStep-1) of the batch of step s into stage st:
+  // 0-3 A codes, 4-7 B codes, 8 B scales
+  auto issue_one = [&](int s, int st, int d) {
     const uint8_t* sb = lds + st * kStage;
-    const uint8_t* ab = a.hilo + s * 128;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(ab, aoff[i], sb + (4 * w + i) * 1024);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    if (d < 4) {
+      dma16(a.hilo + s * 128, aoff[d], sb + (4 * w + d) * 1024);
+    } else if (d < 8) {
+      const int i = d - 4;
       const uint8_t* wb = wexp + gpanel(2 * (4 * w + i)) * wpanel + (s / 2) * 1024 + (s % 2) * 512;
       dma16(wb, boff, sb + kLA + (4 * w + i) * 1024);
+    } else {
+      dma4(sexp + s * sstep + srun, 4 * lane, sb + kLA + kLB + 256 * w);
     }
-    dma4(sexp + s * sstep + srun, 4 * lane, sb + kLA + kLB + 256 * w);
+  };
+  auto issue = [&](int s, int st) {
+#pragma unroll
+    for (int d = 0; d < kLoadsPerStep; ++d) issue_one(s, st, d);
   };
 
   // ---- activation scales of the tile's rows, all of K (row r at r * ascs):
@@ -256,11 +263,14 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
     }
   }
 
-  // ---- fragments of this lane
+  // ---- fragments of this lane.  Wave w takes the 32-row blocks wm and
+  // wm + 2 of the tile, so a tile of at most 64 rows leaves every wave one
+  // live block (the waves then run the one-block loop below)
   const int r32 = lane % 32, h = lane / 32;
   int arow[2];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) arow[mb] = 64 * wm + 32 * mb + r32;
+  for (int mb = 0; mb < 2; ++mb) arow[mb] = 32 * (2 * mb + wm) + r32;
+  const bool two_blocks = 32 * (2 + wm) < rows;
   int bcol[8];
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb)
@@ -280,77 +290,106 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
     u32x4_t b[8];
     int sb[8];
   };
-  auto read_frags = [&](const uint8_t* buf, int s, Frags& f) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const int R = arow[mb];
-      f.sa[mb] = asc[R * ascs + 2 * s + h];
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const uint8_t* base = buf + R * 128;
-        const u32x4_t x0 = *reinterpret_cast<const u32x4_t*>(base + 16 * ((4 * p + h) ^ (R & 7)));
-        const u32x4_t x1 = *reinterpret_cast<const u32x4_t*>(base + 16 * ((4 * p + 2 + h) ^ (R & 7)));
-        f.a[mb][p] = i32x8_t{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
-                             (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
-      }
-    }
-#pragma unroll
-    for (int cb = 0; cb < 8; ++cb) {
-      const int C = bcol[cb];
-      f.b[cb] = *reinterpret_cast<const u32x4_t*>(buf + kLA + C * 32 + 16 * (h ^ ((C >> 3) & 1)));
-      f.sb[cb] = buf[kLA + kLB + C * 2 + h];
-    }
-  };
-  auto mfma_rows = [&](const Frags& f, int mb) {
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int sa = p == 0 ? f.sa[mb] : (f.sa[mb] >= 4 ? f.sa[mb] - 4 : 0);
-#pragma unroll
-      for (int cb = 0; cb < 8; ++cb) {
-        const u32x4_t x = f.b[cb];
-        const i32x8_t b = i32x8_t{(int)x[0], (int)x[1], (int)x[2], (int)x[3], 0, 0, 0, 0};
-        acc[mb][cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-            f.a[mb][p], b, acc[mb][cb], 0, 4, 0, sa, 0, f.sb[cb]);
-      }
+  // fragment read k of step s from the stage at buf: 0-7 B block k (codes
+  // and scale), 8-11 A row block (k - 8) / 2 plane (k - 8) % 2, 12-13 the A
+  // scale of row block k - 12
+  constexpr int kReads = 14;
+  auto read_one = [&](const uint8_t* buf, int s, Frags& f, int k) {
+    if (k < 8) {
+      const int C = bcol[k];
+      f.b[k] = *reinterpret_cast<const u32x4_t*>(buf + kLA + C * 32 + 16 * (h ^ ((C >> 3) & 1)));
+      f.sb[k] = buf[kLA + kLB + C * 2 + h];
+    } else if (k < 12) {
+      const int mb = (k - 8) / 2, p = (k - 8) % 2, R = arow[mb];
+      const uint8_t* base = buf + R * 128;
+      const u32x4_t x0 = *reinterpret_cast<const u32x4_t*>(base + 16 * ((4 * p + h) ^ (R & 7)));
+      const u32x4_t x1 = *reinterpret_cast<const u32x4_t*>(base + 16 * ((4 * p + 2 + h) ^ (R & 7)));
+      f.a[mb][p] = i32x8_t{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
+                           (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+    } else {
+      f.sa[k - 12] = asc[arow[k - 12] * ascs + 2 * s + h];
     }
   };
-
-  // ---- pipeline (nsteps = K / 64 is even and >= 8)
+  // MFMA j (0..15) of row block mb: plane j / 8, B block j % 8
+  auto mfma_one = [&](const Frags& f, int mb, int j) {
+    const int p = j / 8, cb = j % 8;
+    const int sa = p == 0 ? f.sa[mb] : (f.sa[mb] >= 4 ? f.sa[mb] - 4 : 0);
+    const u32x4_t x = f.b[cb];
+    const i32x8_t b = i32x8_t{(int)x[0], (int)x[1], (int)x[2], (int)x[3], 0, 0, 0, 0};
+    acc[mb][cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[mb][p], b, acc[mb][cb], 0, 4,
+                                                                  0, sa, 0, f.sb[cb]);
+  };
+  // ---- pipeline (nsteps = K / 64 is even and >= 4)
   issue(0, 0);
   issue(1, 1);
   __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoadsPerStep));   // scales, step 0 landed
   __syncthreads();
-  Frags f0, f1;
-  read_frags(lds, 0, f0);
-  // steps s < nsteps - 2 issue the loads of step s + 2
-  auto step = [&](int s, Frags& cur, Frags& nxt) {
-    issue(s + 2, (s + 2) % kStages);
+  // Step s < nsteps - 2 (LIVE row blocks, 16 LIVE MFMAs): the first half of
+  // the MFMAs of step s with the loads of step s + 2 issued between them,
+  // the wait and barrier, then the second half with the fragment reads of
+  // step s + 1 between them (the order is pinned: no instruction moves
+  // across a sched_barrier).  MFMA j: row block j / 16, plane (j / 8) % 2,
+  // B block j % 8.
+  auto run = [&](auto live_c) {
+    constexpr int LIVE = decltype(live_c)::value;
+    constexpr int M = 16 * LIVE, H2 = M / 2;
+    auto mfma_j = [&](const Frags& f, int j) { mfma_one(f, j / 16, j % 16); };
+    // reads this variant needs: B 0-7, A row block 0 (8, 9), its scale (12),
+    // and with two blocks A row block 1 (10, 11) and its scale (13)
+    auto read_k = [&](int n) { return LIVE == 2 ? n : (n < 10 ? n : 12); };
+    constexpr int kR = LIVE == 2 ? kReads : 11;
+    auto step = [&](int s, Frags& cur, Frags& nxt) {
+      __builtin_amdgcn_sched_barrier(0);
+      int d = 0;
+#pragma unroll
+      for (int j = 0; j < H2; ++j) {
+        mfma_j(cur, j);
+        if ((LIVE == 1 || j % 2 == 1) && d < kLoadsPerStep) issue_one(s + 2, (s + 2) % kStages, d++);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (; d < kLoadsPerStep; ++d) issue_one(s + 2, (s + 2) % kStages, d);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoadsPerStep));   // step s + 1 landed
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      const uint8_t* buf = lds + ((s + 1) % kStages) * kStage;
+      int n = 0;
+#pragma unroll
+      for (int j = H2; j < M; ++j) {
+        if (n < kR) read_one(buf, s + 1, nxt, read_k(n++));
+        if (LIVE == 1 && n < kR) read_one(buf, s + 1, nxt, read_k(n++));
+        mfma_j(cur, j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (; n < kR; ++n) read_one(buf, s + 1, nxt, read_k(n));
+    };
+    Frags f0, f1;
+#pragma unroll
+    for (int n = 0; n < kR; ++n) read_one(lds, 0, f0, read_k(n));
+    for (int s = 0; s < nsteps - 2; s += 2) {
+      step(s, f0, f1);
+      step(s + 1, f1, f0);
+    }
+    // step nsteps - 2: no more loads to issue
     __builtin_amdgcn_sched_barrier(0);
-    mfma_rows(cur, 0);
+#pragma unroll
+    for (int j = 0; j < H2; ++j) mfma_j(f0, j);
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoadsPerStep));   // step s + 1 landed
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    read_frags(lds + ((s + 1) % kStages) * kStage, s + 1, nxt);
+#pragma unroll
+    for (int n = 0; n < kR; ++n) read_one(lds + ((nsteps - 1) % kStages) * kStage, nsteps - 1, f1, read_k(n));
     __builtin_amdgcn_sched_barrier(0);
-    mfma_rows(cur, 1);
+#pragma unroll
+    for (int j = H2; j < M; ++j) mfma_j(f0, j);
+#pragma unroll
+    for (int j = 0; j < M; ++j) mfma_j(f1, j);
   };
-  for (int s = 0; s < nsteps - 2; s += 2) {
-    step(s, f0, f1);
-    step(s + 1, f1, f0);
-  }
-  // step nsteps - 2: no more loads to issue
-  __builtin_amdgcn_sched_barrier(0);
-  mfma_rows(f0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
-  __syncthreads();
-  __builtin_amdgcn_sched_barrier(0);
-  read_frags(lds + ((nsteps - 1) % kStages) * kStage, nsteps - 1, f1);
-  __builtin_amdgcn_sched_barrier(0);
-  mfma_rows(f0, 1);
-  mfma_rows(f1, 0);
-  mfma_rows(f1, 1);
+  if (two_blocks) run(std::integral_constant<int, 2>{});
+  else run(std::integral_constant<int, 1>{});
 
   // ---- epilogue.  32x32 result lane layout: column l % 32, rows
   // 8 (i / 4) + 4 (l / 32) + i % 4
@@ -358,7 +397,7 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
   for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int r = 64 * wm + 32 * mb + 8 * (i / 4) + 4 * h + (i % 4);
+      const int r = 32 * (2 * mb + wm) + 8 * (i / 4) + 4 * h + (i % 4);
       if (r >= rows) continue;
       const long prow = row0 + r;
       if constexpr (GU) {
