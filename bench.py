@@ -1,8 +1,11 @@
 """Benchmark of the quantized MoE expert layer on one MI355X.
 
-Default workload: DeepSeek-V3-shaped MoE layer at decode with MXFP4 experts
-(H=7168, 256 routed experts + 1 shared, I=2048, grouped-sigmoid routing with
-8 groups / top-4 groups / top-8 and routed scaling 2.5), T = 1, 2, 4 tokens.
+Default run (ds-v3-mxfp4): DeepSeek-V3-shaped MoE layer at decode with MXFP4
+experts (H=7168, 256 routed experts + 1 shared, I=2048, grouped-sigmoid
+routing with 8 groups / top-4 groups / top-8 and routed scaling 2.5), T = 1,
+2, 4 tokens, then the same layer at prefill T = 8192 with MXFP4 and with FP8
+(128x128 block-scaled) experts, PREFILL_STEPS timed steps each, reported
+under config.prefill with their own MFMA roofline.
 A step is one pass of the layer (routing from logits -> segmentation ->
 gate/up+SwiGLU -> down -> combine) over a fresh batch of synthetic tokens
 (x ~ N(0,1) bf16, logits ~ N(0,1)), weights N(0,0.02) quantised and resident in
@@ -21,7 +24,8 @@ The JSON line reports tokens/s at the largest T (value), the layer time, and:
   cpu_baseline  the reference xiaotu-moe AVX-512 engine (oracle/_ref, built
                 from the reference sources) on the host cores, on a bounded
                 sample of the same workload.
-Other workloads (--workload): ds-v3-fp8-prefill, qwen3-next-int8,
+Single workloads (--workload): ds-v3-mxfp4-decode, ds-v3-mxfp4-prefill,
+ds-v3-fp8-prefill, qwen3-next-int8,
 qwen3-next-nvfp4, mixtral-tiny-bf16, and ds-v3-fp8-streamed: the FP8 layer at
 T = 8192 with Zipf(1.1)-skewed router logits, the 64 most-routed experts (and
 the shared one) resident in a pool, every other routed expert streamed from
@@ -34,6 +38,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -64,6 +69,9 @@ WORKLOADS = {
                                tile_e=16, nslots=4, zipf=1.1),
 }
 PCIE_GEN5_X16_GBS = 64.0   # per direction, before protocol overhead
+DEFAULT_SET = "ds-v3-mxfp4"   # decode T=1,2,4 plus the two prefill layers below
+PREFILL_SET = ("ds-v3-mxfp4-prefill", "ds-v3-fp8-prefill")
+PREFILL_STEPS = 5
 CHAIN = 8                  # layers per decode graph
 
 
@@ -76,7 +84,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="ds-v3-mxfp4-decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default=DEFAULT_SET, choices=sorted(WORKLOADS) + [DEFAULT_SET])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-flush", action="store_true", help="keep caches warm between steps")
@@ -90,6 +98,44 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == DEFAULT_SET:
+        return bench_default(args)
+    line = bench_one(args)
+    if line is not None:
+        print(json.dumps(line), flush=True)
+
+
+def bench_default(args):
+    """The headline set: the decode workload's line (value = tok/s at T=4)
+    with the two DeepSeek-V3 prefill layers at T = 8192 (MXFP4 and FP8,
+    PREFILL_STEPS timed steps each) under config.prefill."""
+    import gc
+
+    import torch
+
+    a = argparse.Namespace(**vars(args))
+    a.workload = "ds-v3-mxfp4-decode"
+    line = bench_one(a)
+    pre = {}
+    for wl in PREFILL_SET:
+        gc.collect()
+        torch.cuda.empty_cache()
+        b = argparse.Namespace(**vars(args))
+        b.workload, b.no_cpu_baseline, b.no_traffic = wl, True, True
+        b.steps, b.warmup = min(args.steps, PREFILL_STEPS), min(args.warmup, 2)
+        pl = bench_one(b)
+        r = pl["config"]["per_T"]["8192"]
+        pre[wl] = dict(T=8192, steps=b.steps, warmup=b.warmup, layer_ms=r["layer_ms"],
+                       tok_s=r["tok_s"], gate_up_ms=r["gate_up_ms"],
+                       gate_up_TFLOPs=r["gate_up_TFLOPs"], dtype=pl["dtype"],
+                       distinct_experts=r["distinct_experts"], roofline=pl["roofline"])
+    line["config"]["workload"] = DEFAULT_SET
+    line["config"]["prefill"] = pre
+    print(json.dumps(line), flush=True)
+
+
+def bench_one(args):
+    """One workload; returns its JSON line (the streamed workload prints its own)."""
     import numpy as np
     import torch
 
@@ -102,7 +148,8 @@ def main():
 
     cfg = WORKLOADS[args.workload]
     if "resident" in cfg:
-        return streamed(args, cfg)
+        streamed(args, cfg)
+        return None
     if args.pmc_child:
         return pmc_child(args, cfg, args.pmc_child)
     fmt = F.fmt_of(cfg["fmt"])
@@ -440,7 +487,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 COPY_BYTES = 256 << 20   # calibration copy for the memory counters
@@ -729,9 +776,32 @@ def cpu_baseline(cfg, W, T, rkw, seconds, dev):
     med = float(np.median(times))
     isa = {2: "avx512_vnni", 1: "avx512", 0: "scalar"}[int(L.xref_isa())]
     return dict(value=Ts / med, unit="tok/s", cores=threads, kind="reference",
-                ms_per_layer=med * 1e3,
+                ms_per_layer=med * 1e3, host=host_cpu(), engine_isa=isa,
                 sample=(f"reference MOE_V2::forward_many ({isa}), {Ts} tokens x {K}+{NS} experts "
                         f"({U + NS} distinct), median of {len(times)} calls after 2 warm-ups"))
+
+
+def host_cpu():
+    """lscpu's model, sockets, NUMA nodes, logical CPUs and AVX-512 / AMX
+    flags, plus the CPUs this process may run on."""
+    info = {"cpus_allowed": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return info
+    kv = {}
+    for ln in out.splitlines():
+        if ":" in ln:
+            k, v = ln.split(":", 1)
+            kv[k.strip()] = v.strip()
+    for key, name in (("Model name", "model"), ("Socket(s)", "sockets"),
+                      ("NUMA node(s)", "numa_nodes"), ("CPU(s)", "logical_cpus"),
+                      ("Thread(s) per core", "threads_per_core")):
+        if key in kv:
+            info[name] = kv[key]
+    flags = kv.get("Flags", "").split()
+    info["isa"] = sorted(f for f in flags if f.startswith(("avx512", "amx")) or f == "avx2")
+    return info
 
 
 if __name__ == "__main__":
