@@ -332,7 +332,7 @@ def bench_one(args):
             if not decode and not i8 and mx_pair_kernel(fmt, H, I):
                 mxx = _mxpair_bufs("xm", T, H, dev)
                 s13p, _ = W.mx_pair_scales()
-                _lib.call("xtu_mx_pair_quant", _p(x_st), T, H, *[_p(t) for t in mxx], st)
+                _lib.call("xtu_pair_quant_il", _p(x_st), T, H, *[_p(t) for t in mxx], st)
             elif not decode and not i8 and pair_gemm(fmt, H, I):
                 fp8x = _fp8pair_bufs("x8", T, H, dev)
                 _lib.call("xtu_fp8pair_quant", _p(x_st), T, H, *[_p(t) for t in fp8x], st)

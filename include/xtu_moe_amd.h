@@ -305,7 +305,7 @@ hipError_t xtu_gemm_pair_down(int fmt, const uint8_t* hi, const uint8_t* lo, con
  * The MXFP4 prefill GEMMs of the reference (vllm_xiaotu_moe/gpu_prefill.py:
  * 232-390, _gate_up_kernel / _down_kernel) on v_mfma_scale_f32_32x32x64_
  * f8f6f4 with operand layouts made for it:
- *   xtu_mx_pair_quant: bf16 rows [M][K] -> interleaved e4m3 pairs hilo
+ *   xtu_pair_quant_il: bf16 rows [M][K] -> interleaved e4m3 pairs hilo
  *     [M][2K] (per 64 k: 64 bytes hi, 64 bytes lo) and e8m0 shi [M][K/32];
  *     x = hi * 2^(shi-127) + lo * 2^(max(shi-4,0)-127) exactly (bf16 x).
  *   xtu_mx_pair_scales: packed MXFP4 scale groups (E slots of s_estride
@@ -315,7 +315,7 @@ hipError_t xtu_gemm_pair_down(int fmt, const uint8_t* hi, const uint8_t* lo, con
  *     xtu_mx_pair_tile_m() rows; shapes where xtu_mx_pair_fits(H, I). */
 int xtu_mx_pair_fits(int H, int I);
 int xtu_mx_pair_tile_m(void);
-hipError_t xtu_mx_pair_quant(const void* x, int M, int K, uint8_t* hilo, uint8_t* shi,
+hipError_t xtu_pair_quant_il(const void* x, int M, int K, uint8_t* hilo, uint8_t* shi,
                              hipStream_t stream);
 hipError_t xtu_mx_pair_scales(const uint8_t* s, int E, int N, int K, long s_estride, uint8_t* out,
                               hipStream_t stream);

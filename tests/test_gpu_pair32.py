@@ -1,4 +1,4 @@
-"""MXFP4 exact-pair GEMMs on the 32x32x64 kernel (xtu_mx_pair_*): the
+"""MXFP4 exact-pair GEMMs on the 32x32x64 scaled MFMA (xtu_mx_pair_*): the
 interleaved activation pairs bit-exact against the planar quantiser's, the
 step-major scale re-layout bit-exact against the dense scales, and the layer
 against the oracle over tile shapes (single rows, partial and multi-tile
@@ -36,7 +36,7 @@ def test_interleaved_pairs_match_planar(M, K):
     shi2 = torch.empty_like(shi)
     st = _stream()
     _lib.call("xtu_fp8pair_quant", _p(x), M, K, _p(hi), _p(lo), _p(shi), _p(slo), st)
-    _lib.call("xtu_mx_pair_quant", _p(x), M, K, _p(hilo), _p(shi2), st)
+    _lib.call("xtu_pair_quant_il", _p(x), M, K, _p(hilo), _p(shi2), st)
     torch.cuda.synchronize()
     il = hilo.view(M, K // 64, 2, 64)
     assert torch.equal(il[:, :, 0].reshape(M, K), hi)
@@ -63,17 +63,25 @@ def test_step_major_scales(N, K, pad):
     assert torch.equal(out.cpu(), want)
 
 
-def _layer(E, NS, H, I, seed):
-    d = make_dense_layer(F.FMT_MXFP4, E + NS, H, I, seed=seed)
-    return d, ExpertWeights.from_dense(F.FMT_MXFP4, d["w13"], d["s13"], d["w2"], d["s2"],
-                                       n_shared=NS, device=DEV)
+FMTS = [F.FMT_MXFP4]
 
 
+def _layer(fmt, E, NS, H, I, seed):
+    d = make_dense_layer(fmt, E + NS, H, I, seed=seed)
+    return d, ExpertWeights.from_dense(fmt, d["w13"], d["s13"], d["w2"], d["s2"], n_shared=NS,
+                                       device=DEV)
+
+
+def _on_kernel(fmt, H, I):
+    return L.mx_pair_kernel(fmt, H, I) and L.gemm_tile_m(fmt, False, H, I) == 128
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,K,skew", [(1, 2, False), (40, 4, False), (700, 4, False), (900, 2, True)])
-def test_layer_against_oracle(T, K, skew):
+def test_layer_against_oracle(fmt, T, K, skew):
     E, NS, H, I = 16, 1, 1024, 512
-    d, W = _layer(E, NS, H, I, seed=30 + T)
-    assert L.mx_pair_kernel(F.FMT_MXFP4, H, I) and L.gemm_tile_m(F.FMT_MXFP4, False, H, I) == 128
+    d, W = _layer(fmt, E, NS, H, I, seed=30 + T)
+    assert _on_kernel(fmt, H, I)
     rng = np.random.default_rng(31 + T)
     if skew:   # experts 0 and 1 take most pairs: several full tiles and a partial one
         ids = np.stack([np.array([rng.integers(0, 2), rng.integers(2, E)]) for _ in range(T)])
@@ -85,26 +93,27 @@ def test_layer_against_oracle(T, K, skew):
     out = moe_forward(x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(wts).to(DEV), W,
                       path="gemm", swiglu_limit=5.0, out_dtype=torch.float32)
     torch.cuda.synchronize()
-    ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d), bf16_tensor_to_bits(x), ids,
-                       wts, E, NS, H, I, limit=5.0)
-    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"mx pair T={T}")
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I,
+                       limit=5.0)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"pair32 fmt={fmt} T={T}")
 
 
-def test_slot_map_on_mutable_planes():
+@pytest.mark.parametrize("fmt", FMTS)
+def test_slot_map_on_mutable_planes(fmt):
     """Experts at permuted slots of planes flagged mutable (restaged in
     place): the step-major scales are rebuilt per call, so restaging the
     slots between two calls gives the new experts' results."""
     E, NS, H, I, K, T = 8, 0, 1024, 256, 2, 300
-    d, W = _layer(E, NS, H, I, seed=40)
+    d, W = _layer(fmt, E, NS, H, I, seed=40)
+    assert _on_kernel(fmt, H, I)
     perm = torch.tensor([5, 2, 7, 0, 3, 6, 1, 4], dtype=torch.int64)
-    slots = ExpertWeights(F.FMT_MXFP4, H, I, E, 0, torch.empty_like(W.w13), torch.empty_like(W.s13),
+    slots = ExpertWeights(fmt, H, I, E, 0, torch.empty_like(W.w13), torch.empty_like(W.s13),
                           torch.empty_like(W.w2), torch.empty_like(W.s2), mutable=True)
     rng = np.random.default_rng(41)
     ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
     wts = (rng.random((T, K)) + 0.05).astype(np.float32)
     x = torch.randn((T, H), generator=torch.Generator().manual_seed(42)).to(torch.bfloat16)
-    ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d), bf16_tensor_to_bits(x), ids,
-                       wts, E, NS, H, I)
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I)
     xd, idd, wd = x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(wts).to(DEV)
     for round_ in range(2):
         p = perm if round_ == 0 else torch.roll(perm, 3)

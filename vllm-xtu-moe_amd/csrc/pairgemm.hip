@@ -2,7 +2,7 @@
 // v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 activations x e2m1 weights), with
 // the two operand layouts this kernel reads made for it:
 //
-// * activation pairs interleaved (xtu_mx_pair_quant): row r of the plane is
+// * activation pairs interleaved (xtu_pair_quant_il): row r of the plane is
 //   [K/64 chunks][hi 64 B | lo 64 B], so the codes one 64-k step needs of a
 //   row are one 128-byte line; the e8m0 bytes stay [rows][K/32].
 // * weight scales step-major (xtu_mx_pair_scales, a re-layout of the packed
@@ -67,31 +67,10 @@ constexpr int kStage = kLA + kLB + kLBS;
 constexpr int kStagesBytes = kStages * kStage;
 constexpr int kLdsMax = 160 * 1024;
 
-// LDS row stride of the activation scales: K/32 bytes padded to an odd
-// number of dwords (conflict-free byte reads of 32 consecutive rows)
-__host__ __device__ constexpr int asc_stride(int K) { return ((K / 32 + 4) / 8) * 8 + 4; }
-// the scale area rounded up to whole 256-byte load chunks, then the tile's
-// 128 source rows (int32)
-__host__ __device__ constexpr int asc_bytes(int K) { return (kPM * asc_stride(K) + 255) / 256 * 256; }
-__host__ __device__ constexpr int lds_bytes(int K) { return kStagesBytes + asc_bytes(K) + 4 * kPM; }
+// the activation-scale area of 128 rows, then the tile's 128 source rows
+__host__ __device__ constexpr int lds_bytes(int K) { return kStagesBytes + asc_bytes(K, kPM) + 4 * kPM; }
 
-// Memory-to-LDS loads (saddr form: a wave-uniform 64-bit base plus a 32-bit
-// lane offset; M0 holds the LDS address that lane 0's bytes go to).  Written
-// as asm so that the compiler does not make every later LDS read wait for
-// all of them; the pipeline waits with explicit vmcnt counts and barriers.
-__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, const uint8_t* dst) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(off), "s"(base), "{m0}"((uint32_t)(uintptr_t)dst) : "memory");
-}
-__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, const uint8_t* dst) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
-               :: "v"(off), "s"(base), "{m0}"((uint32_t)(uintptr_t)dst) : "memory");
-}
-
-// s_waitcnt immediates (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
-// 6:4, lgkmcnt 11:8)
 constexpr int kLoadsPerStep = 9;    // loads per lane and step (A 4, B 4, B scales 1)
-constexpr int wait_vm_lgkm0(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
 
 struct MxPairArgs {
   const uint8_t* hilo;        // gate/up: x pairs [T][2K]; down: act pairs [A][2K]
@@ -183,7 +162,7 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
   const int wm = w & 1, wn = w >> 1;
   const int ascs = asc_stride(K);
   uint8_t* asc = lds + kStagesBytes;
-  int32_t* srow = reinterpret_cast<int32_t*>(asc + asc_bytes(K));
+  int32_t* srow = reinterpret_cast<int32_t*>(asc + asc_bytes(K, kPM));
 
   // source row of every tile row (rows past the tile repeat its last row)
   if (tid < kPM) {
@@ -255,7 +234,7 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
   // (pad dwords load the row's first dword).  Issued before the first batch
   // of codes, so the wait for that batch covers them.
   {
-    const int ascw = ascs / 4, nch = asc_bytes(K) / 256;
+    const int ascw = ascs / 4, nch = asc_bytes(K, kPM) / 256;
     for (int c = w; c < nch; c += 4) {
       const int d = 64 * c + lane;
       const int r = min(d / ascw, kPM - 1), q = d % ascw;
@@ -449,7 +428,7 @@ int xtu_mx_pair_fits(int H, int I) { return mx_fits(H, I) ? 1 : 0; }
 
 int xtu_mx_pair_tile_m(void) { return kPM; }
 
-hipError_t xtu_mx_pair_quant(const void* x, int M, int K, uint8_t* hilo, uint8_t* shi,
+hipError_t xtu_pair_quant_il(const void* x, int M, int K, uint8_t* hilo, uint8_t* shi,
                              hipStream_t stream) {
   XTU_CHECK_ARG(M >= 0 && K > 0 && K % 128 == 0 && 2L * M * K < (1L << 32));
   XTU_CHECK_ARG(M == 0 || (x && hilo && shi));

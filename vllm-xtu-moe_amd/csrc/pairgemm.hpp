@@ -61,4 +61,35 @@ __device__ __forceinline__ int pair_split32(const uint16_t* src, uint32_t hw[8],
   return e + 127;
 }
 
+// ---------------------------------------------------------------------------
+// pieces of the LDS-staged pair GEMM (pairgemm.hip)
+// ---------------------------------------------------------------------------
+
+// Memory-to-LDS loads (saddr form: a wave-uniform 64-bit base plus a 32-bit
+// lane offset; M0 holds the LDS address that lane 0's bytes go to).  Written
+// as asm so that the compiler does not make every later LDS read wait for
+// all of them; the pipelines wait with explicit vmcnt counts and barriers.
+__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, const uint8_t* dst) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "{m0}"((uint32_t)(uintptr_t)dst) : "memory");
+}
+__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, const uint8_t* dst) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(off), "s"(base), "{m0}"((uint32_t)(uintptr_t)dst) : "memory");
+}
+
+// s_waitcnt immediate for vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+__host__ __device__ constexpr int wait_vm_lgkm0(int n) {
+  return 0x0070 | (n & 15) | ((n >> 4) << 14);
+}
+
+// LDS row stride of a tile's activation scales: K/32 bytes padded to an odd
+// number of dwords (conflict-free byte reads of 32 consecutive rows), and the
+// area of `rows` rows rounded up to whole 256-byte load chunks
+__host__ __device__ constexpr int asc_stride(int K) { return ((K / 32 + 4) / 8) * 8 + 4; }
+__host__ __device__ constexpr int asc_bytes(int K, int rows) {
+  return (rows * asc_stride(K) + 255) / 256 * 256;
+}
+
 }  // namespace xtu

@@ -54,7 +54,7 @@ SIGNATURES = {
     "xtu_gemm8_tile_m": (_i, []),
     "xtu_mx_pair_fits": (_i, [_i, _i]),
     "xtu_mx_pair_tile_m": (_i, []),
-    "xtu_mx_pair_quant": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
+    "xtu_pair_quant_il": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "xtu_mx_pair_scales": (_i, [_vp, _i, _i, _i, _l, _vp, _vp]),
     "xtu_mx_pair_gate_up": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
                                  _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),

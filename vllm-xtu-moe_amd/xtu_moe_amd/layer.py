@@ -699,12 +699,12 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
         s13p, s2p = W.mx_pair_scales(st)
         xq = _mxpair_bufs("xm", T, H, dev, st)
         aq = _mxpair_bufs("am", A, I, dev, st)
-        _lib.call("xtu_mx_pair_quant", _p(x), T, H, *[_p(t) for t in xq], st)
+        _lib.call("xtu_pair_quant_il", _p(x), T, H, *[_p(t) for t in xq], st)
         _lib.call("xtu_mx_pair_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
                   _p(W.w13), _p(s13p), 0, 0, _p(slot_map), _p(seg.seg_start),
                   _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi,
                   seg.max_tiles, _p(act), lim, al, be, st)
-        _lib.call("xtu_mx_pair_quant", _p(act), A, I, *[_p(t) for t in aq], st)
+        _lib.call("xtu_pair_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
         _lib.call("xtu_mx_pair_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(s2p), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
                   _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
