@@ -22,9 +22,12 @@
 //
 // Dequantisation: MXFP4 (e2m1 x e8m0) and NVFP4 (e2m1 x e4m3) products are
 // exact in bf16; NVFP4's per-expert global scale multiplies the fp32 result.
-// FP8 operands are bf16(e4m3 * block scale), rounded to nearest even -- the
-// reference's GPU FP8 kernels form the same operand (gpu_prefill_fp8.py:
-// 148-149, 195-196).
+// FP8 weights taken by this kernel become bf16(e4m3 * block scale), rounded
+// to nearest even -- the operand the reference's GPU FP8 kernels form
+// (gpu_prefill_fp8.py:148-149, 195-196).  That rounding misses the layer
+// tolerance at DeepSeek-V3 size, so the layer's FP8 prefill runs the exact
+// activation-pair GEMM of fp8pair.hip instead; this branch stays reachable
+// only through xtu_gemm_gate_up / xtu_gemm_down with the FP8 format code.
 //
 // gate/up: panels 0,1 of a wave are gate rows and panels 2,3 the up rows of
 // the same output columns, so each lane holds (g, u) of the same element and
