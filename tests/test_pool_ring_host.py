@@ -147,3 +147,24 @@ def test_staging_bytes_counts_the_ring():
     per = F.algorithmic_bytes(F.FMT_FP8, 2 * I, H) + F.algorithmic_bytes(F.FMT_FP8, H, I)
     b = R.staging_bytes(256, H, I, ns=4, fmt=F.FMT_FP8, tile_e=16)
     assert b == 4 * 16 * per
+
+
+# ------------------------------------------------------- slot-plane weights
+def test_slot_planes_size_what_is_derived_from_them():
+    """A pool's layer view claims E routed + NS shared experts but its planes
+    hold only the pool's slots: per-expert work derived from the planes (the
+    step-major MXFP4 scales, the INT8 weights) must cover the slots only."""
+    from xtu_moe_amd import formats as F
+    from xtu_moe_amd.layer import ExpertWeights
+    H, I, S = 512, 256, 6
+    mk = lambda N, K: torch.zeros((S, N * F.row_bytes(F.FMT_MXFP4, K)), dtype=torch.uint8)
+    sc = lambda N, K: torch.zeros((S, F.scale_bytes(F.FMT_MXFP4, N, K)), dtype=torch.uint8)
+    W = ExpertWeights(F.FMT_MXFP4, H, I, 16, 1, mk(2 * I, H), sc(2 * I, H), mk(H, I), sc(H, I),
+                      mutable=True)
+    assert W.n_experts == 17 and W.n_slots == S
+    with pytest.raises(ValueError):     # planes of different expert counts
+        ExpertWeights(F.FMT_MXFP4, H, I, 16, 1, mk(2 * I, H), sc(2 * I, H)[:4], mk(H, I),
+                      sc(H, I))
+    src = inspect.getsource(ExpertWeights.mx_pair_scales) + inspect.getsource(
+        ExpertWeights.int8_planes)
+    assert "self.n_experts" not in src

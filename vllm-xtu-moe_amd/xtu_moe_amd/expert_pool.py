@@ -215,9 +215,11 @@ class LayerPool:
                               torch.arange(self.nslots, self.nslots + self.n_shared,
                                            dtype=torch.int32, device=self.dev)])
         from .layer import ExpertWeights
+        # bucket b's weights are slot slot_map[b] of the pool planes, which
+        # hold nslots + n_shared experts, not E + n_shared
         W = ExpertWeights(self.engine.fmt, self.H, self.I, E, self.n_shared, self.planes.w13,
                           self.planes.s13, self.planes.w2, self.planes.s2, self.planes.gs13,
-                          self.planes.gs2)
+                          self.planes.gs2, mutable=True)
         return moe_forward(x, topk_ids, topk_weights, W, id_map=id_map, slot_map=slot_map, **kw)
 
     # ------------------------------------------------------------- swaps

@@ -72,10 +72,20 @@ class ExpertWeights:
         self._mxs = None
         if self.H % 256 or self.I % 128:
             raise ValueError(f"unsupported shape H={H} I={I} (need H % 256 == 0, I % 128 == 0)")
+        rows = {t.shape[0] for t in (w13, s13, w2, s2, gs13, gs2) if t is not None}
+        if len(rows) != 1:
+            raise ValueError(f"weight planes hold different expert counts: {sorted(rows)}")
 
     @property
     def n_experts(self) -> int:
         return self.E + self.n_shared
+
+    @property
+    def n_slots(self) -> int:
+        """Experts the planes hold.  Equal to n_experts, except for slot
+        planes (a pool's, a ring's) read through a slot_map, which may hold
+        fewer: whatever is derived from the planes covers these rows only."""
+        return int(self.w13.shape[0])
 
     @property
     def device(self):
@@ -120,7 +130,7 @@ class ExpertWeights:
             return self._mxs
         if self.fmt != FMT_MXFP4:
             raise ValueError("step-major pair scales are for MXFP4 weights")
-        n, dev, st = self.n_experts, self.device, _stream(stream)
+        n, dev, st = self.n_slots, self.device, _stream(stream)
         out = []
         for (sc, N, K, tag) in ((self.s13, 2 * self.I, self.H, "mxs13"), (self.s2, self.H, self.I, "mxs2")):
             shape = (n, N * (K // 32))
@@ -138,12 +148,15 @@ class ExpertWeights:
     def int8_planes(self):
         """Shifted int8 weights + per-row emin for the INT8 ALIGN path (MXFP4
         only).  Rows whose e8m0 spread exceeds 3 are marked (emin 0xFF); their
-        output columns take the fp32 fallback (int8_fallback_cols)."""
-        if self._i8 is not None:
+        output columns take the fp32 fallback (int8_fallback_cols).  Cached,
+        except for mutable planes, whose contents change between calls: for
+        those each call prepares them again (and int8_fallback_cols then
+        returns that call's fallback columns)."""
+        if self._i8 is not None and not self.mutable:
             return self._i8
         if self.fmt != FMT_MXFP4:
             raise ValueError("the INT8-activation path needs MXFP4 (e8m0) weights")
-        n = self.n_experts
+        n = self.n_slots
         dev = self.device
         out = []
         st = _stream()
@@ -166,7 +179,8 @@ class ExpertWeights:
     def int8_fallback_cols(self):
         """None, or (start13, cols13, start2, cols2): per weight slot, the
         gate/up column pairs and down columns the fp32 fallback computes."""
-        self.int8_planes()
+        if self._i8 is None:
+            self.int8_planes()
         return self._i8_fb
 
 
