@@ -397,6 +397,52 @@ hipError_t xtu_copy_experts(int n, const int32_t* experts, const void* src, long
 hipError_t xtu_copy_2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width,
                        size_t height, hipStream_t stream);
 
+/* ------------------------------------------------ pool-miss split
+ * Pairs whose expert is resident in the GPU pool run on the device, the
+ * others on a host engine; the results are added
+ * (vllm_xiaotu_moe/mixed_experts.py:2956-3186).
+ *
+ * xtu_pin_split: the pool path's pin mask (vllm_xiaotu_moe/pin_mask_triton.py:
+ * 53-85).  For each of n pairs, bad = id < 0 || id >= n_local, sl =
+ * slotmap[id], res = !bad && sl >= n_local:
+ *   cpu_ids = res||bad ? 0 : id,  cpu_w = res||bad ? 0 : w,
+ *   part_ids = res ? sl - n_local : -1,  part_w = res ? w : 0,
+ * *hits += resident pairs (hits may be NULL). */
+hipError_t xtu_pin_split(const int32_t* ids, const float* wts, int n, const int32_t* slotmap,
+                         int n_local, int32_t* cpu_ids, float* cpu_w, int32_t* part_ids,
+                         float* part_w, unsigned long long* hits, hipStream_t stream);
+/* Host engine over the pinned host copy of a layer (the reference engine's
+ * CPU MoE behind cpu_decode, xiaotu_moe/csrc/python_binding/binding.cpp:
+ * 859-1296).  w13_nodes / w2_nodes: ns NUMA-node buffers of P16 rows
+ * ([expert][gate rows | up rows] and [expert][rows] of the node; strides in
+ * bytes per expert); s13 / s2: packed scale groups (fp4) or fp32 block
+ * scales (fp8); gs13 / gs2: NVFP4 global scales.  isa: -1 best available, 0
+ * portable, 2 AVX-512.  max_tokens > 0 allocates the pinned staging of
+ * xtu_cpu_decode (max_tokens rows of max_topk pairs); 0 = host-only engine.
+ * The weights are read in place and must outlive the engine. */
+hipError_t xtu_cpu_engine_create(int fmt, int H, int I, int n_experts, int ns,
+                                 const void* const* w13_nodes, long w13_estride,
+                                 const void* const* w2_nodes, long w2_estride, const void* s13,
+                                 long s13_estride, const void* s2, long s2_estride,
+                                 const float* gs13, const float* gs2, float limit, float alpha,
+                                 float beta, int n_threads, int isa, int max_tokens, int max_topk,
+                                 void** engine);
+hipError_t xtu_cpu_engine_info(const void* engine, int* isa, int* threads);
+/* Synchronous, host memory: out [T][H] fp32 = sum over pairs with
+ * 0 <= id < n_experts and w != 0 of w * expert(x); x bf16 [T][H]. */
+hipError_t xtu_cpu_forward(void* engine, int T, int K, const void* x, const int32_t* ids,
+                           const float* wts, float* out);
+/* cpu_decode (binding.cpp:859): on `stream`, device x/ids/wts -> pinned
+ * staging, a host-function node runs the engine, pinned fp32 result -> out
+ * [T][H] on the device.  Allocates nothing: may be captured into a HIP graph
+ * (the captured call lives until the engine is destroyed).  T <= max_tokens,
+ * K <= max_topk; calls on one engine share its staging (one stream). */
+hipError_t xtu_cpu_decode(void* engine, int T, int K, const void* x, const int32_t* ids,
+                          const float* wts, float* out, hipStream_t stream);
+/* After every stream that ran its calls is synchronised and the graphs that
+ * captured them are destroyed. */
+hipError_t xtu_cpu_engine_destroy(void* engine);
+
 #ifdef __cplusplus
 }
 #endif

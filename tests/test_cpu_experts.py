@@ -1,0 +1,112 @@
+"""Host expert engine (the CPU half of the pool-miss split) against the
+oracle, on the CPU: every format, one and two NUMA-node shards, the AVX-512
+and the portable kernels, invalid ids / zero weights / an expert listed
+twice by one token, and bit-identical results for any thread count (each
+output element is summed in a fixed order)."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_tensor_to_bits, check_close, dense_to_numpy, make_dense_layer
+import oracle
+from xtu_moe_amd import formats as F
+from xtu_moe_amd.cpu_experts import ISA_AVX512, ISA_PORTABLE, CpuExperts
+from xtu_moe_amd.host_store import HostExpertStore
+from xtu_moe_amd.layer import ExpertWeights
+
+FMTS = [F.FMT_BF16, F.FMT_FP8, F.FMT_MXFP4, F.FMT_NVFP4]
+E, H, I = 6, 256, 256
+
+
+def _avx512_ok():
+    try:
+        flags = open("/proc/cpuinfo").read()
+        return all(f in flags for f in ("avx512f", "avx512bw", "avx512dq", "avx512vl"))
+    except OSError:
+        return False
+
+
+ISAS = [ISA_PORTABLE] + ([ISA_AVX512] if _avx512_ok() else [])
+
+
+def _layer(fmt, seed=0, std=0.05):
+    d = make_dense_layer(fmt, E, H, I, seed=seed, std=std)
+    W = ExpertWeights.from_dense(fmt, d["w13"], d["s13"], d["w2"], d["s2"], d["gs13"], d["gs2"],
+                                 E=E, device="cpu")
+    return W, dense_to_numpy(fmt, d)
+
+
+def _batch(T, K, seed):
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    wts = (rng.random((T, K)) + 0.05).astype(np.float32)
+    ids[0, -1] = ids[0, 0]                       # one token lists an expert twice
+    if T > 2:
+        ids[1, 0], ids[2, 1] = -1, E + 2          # invalid ids add nothing
+        wts[2, 0] = 0.0                           # nor do zero weights
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn((T, H), generator=g)).to(torch.bfloat16)
+    return x, ids, wts
+
+
+def _oracle(fmt, dn, x, ids, wts, limit=0.0):
+    ok = (ids >= 0) & (ids < E)
+    return oracle.moe_layer(fmt, bf16_tensor_to_bits(x), np.where(ok, ids, -1).astype(np.int32),
+                            np.where(ok, wts, 0).astype(np.float32), E, 0, H, I, dn["w13"],
+                            dn["s13"], dn["w2"], dn["s2"], dn["gs13"], dn["gs2"], limit=limit)
+
+
+@pytest.mark.parametrize("isa", ISAS)
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("ns", [1, 2])
+def test_host_engine_matches_oracle(fmt, ns, isa):
+    W, dn = _layer(fmt, seed=fmt)
+    store = HostExpertStore.from_weights(W, ns=ns, pin=False)
+    limit = 7.0 if fmt == F.FMT_MXFP4 else 0.0
+    eng = CpuExperts.from_store(store, isa=isa, n_threads=4, swiglu_limit=limit)
+    try:
+        assert eng.isa == isa
+        for T, K in ((1, 2), (5, 4), (9, 3)):
+            x, ids, wts = _batch(T, K, seed=T)
+            out = eng.forward(x, torch.from_numpy(ids), torch.from_numpy(wts))
+            ref = _oracle(fmt, dn, x, ids, wts, limit=limit)
+            check_close(out.numpy(), ref, bf16_out=False,
+                        what=f"{F.FMT_NAMES[fmt]} ns={ns} isa={isa} T={T}")
+    finally:
+        eng.close()
+
+
+@pytest.mark.parametrize("fmt", [F.FMT_MXFP4, F.FMT_FP8])
+def test_thread_count_does_not_change_bits(fmt):
+    W, _ = _layer(fmt, seed=3)
+    x, ids, wts = _batch(7, 4, seed=11)
+    outs = []
+    for thr in (1, 3, 8):
+        eng = CpuExperts.from_weights(W, n_threads=thr)
+        try:
+            outs.append(eng.forward(x, torch.from_numpy(ids), torch.from_numpy(wts)))
+        finally:
+            eng.close()
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+
+
+def test_no_valid_pairs_gives_zeros_and_bad_layouts_are_refused():
+    W, _ = _layer(F.FMT_MXFP4)
+    eng = CpuExperts.from_weights(W, n_threads=2)
+    try:
+        x = torch.ones((3, H), dtype=torch.bfloat16)
+        out = torch.full((3, H), 5.0)
+        eng.forward(x, torch.full((3, 2), -1, dtype=torch.int32), torch.ones((3, 2)), out=out)
+        assert torch.count_nonzero(out) == 0
+        with pytest.raises(ValueError):   # out must be fp32 [T, H]
+            eng.forward(x, torch.zeros((3, 2), dtype=torch.int32), torch.ones((3, 2)),
+                        out=torch.empty((3, H + 16)))
+        # a host-only engine has no staging for the stream bridge
+        assert eng.cpu_decode(None, 3, 2, 0, 0, 0, 0) == -2
+    finally:
+        eng.close()
+    with pytest.raises(ValueError):       # shards must hold whole 16-row panels
+        HostExpertStore.from_weights(W, ns=3, pin=False)
+    w13 = W.w13.contiguous()
+    with pytest.raises(RuntimeError):     # NVFP4 needs its global scales
+        CpuExperts(F.FMT_NVFP4, H, I, E, [w13], [W.w2.contiguous()], W.s13, W.s2, None, None)

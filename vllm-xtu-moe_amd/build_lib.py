@@ -1,7 +1,8 @@
 """Build the gfx950 HIP library libxtu_moe_amd.so in-tree.
 
-Each csrc/*.hip is compiled for gfx950 with hipcc (in parallel), then linked
-into xtu_moe_amd/lib/libxtu_moe_amd.so, which the Python package loads with
+Each csrc/*.hip is compiled for gfx950 with hipcc and each csrc/*.cpp (host
+code only: the host expert engine) with g++, in parallel, then linked into
+xtu_moe_amd/lib/libxtu_moe_amd.so, which the Python package loads with
 ctypes.  Packed-fp32 VALU instructions are disabled for all device code.
 The test-only probe library (tests/probes/probes.hip ->
 tests/probes/libxtu_probes.so) is built beside it, separately.
@@ -31,21 +32,30 @@ CFLAGS = [
 ]
 
 
+CXX = os.environ.get("CXX", "g++")
+# host code: no -march (the library runs on other hosts); AVX-512 paths are
+# compiled per function and chosen at run time
+CXXFLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-pthread", "-fvisibility=hidden"]
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CFLAGS, "-I", CSRC, "-c", src, "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [CXX, *CXXFLAGS, "-I", CSRC, "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *CFLAGS, "-I", CSRC, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # the host pass does not know the device-only target feature; that note is harmless
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src}:\n{err}")
+        raise RuntimeError(f"{cmd[0]} failed for {src}:\n{err}")
     return obj
 
 
 def build(verbose: bool = True) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
     os.makedirs(OBJ_DIR, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     with_probes = os.path.exists(PROBE_SRC)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs) + 1)) as ex:
         objs = list(ex.map(_compile, srcs + ([PROBE_SRC] if with_probes else [])))
@@ -60,7 +70,7 @@ def build(verbose: bool = True) -> str:
 
 def _link(objs, out):
     tmp = out + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link of {out} failed:\n{r.stderr}")

@@ -78,6 +78,13 @@ SIGNATURES = {
                                  _i, _vp, _vp, _f, _f, _f, _vp]),
     "xtu_i8_gemm_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                               _vp, _vp]),
+    "xtu_pin_split": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "xtu_cpu_engine_create": (_i, [_i, _i, _i, _i, _i, _vp, _l, _vp, _l, _vp, _l, _vp, _l, _vp,
+                                   _vp, _f, _f, _f, _i, _i, _i, _i, _vp]),
+    "xtu_cpu_engine_info": (_i, [_vp, _vp, _vp]),
+    "xtu_cpu_forward": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
+    "xtu_cpu_decode": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "xtu_cpu_engine_destroy": (_i, [_vp]),
     "xtu_i8_fallback": (_i, [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i,
                              _vp, _vp, _vp, _f, _f, _f, _vp]),
 }

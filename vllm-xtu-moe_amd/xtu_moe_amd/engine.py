@@ -69,6 +69,7 @@ class _Engine:
                                                 opt(w2_scale), opt(w13_global_scale),
                                                 opt(w2_global_scale), device=dev)
         self._store = None
+        self._cpu = []          # host engines; the last one is current (see _host_engine)
 
     # ------------------------------------------------------------ forward
     def forward_many(self, qlen: int, top_k: int, expert_ids, weights, x, out):
@@ -113,6 +114,53 @@ class _Engine:
         if ns < 2 or W.I % (16 * ns) or W.H % (16 * ns):
             return 1
         return ns
+
+    # ------------------------------------------------ host decode bridge
+    def _host_engine(self, max_qlen: int = 0, top_k: int = 0):
+        """The host engine with staging for at least max_qlen tokens of
+        top_k pairs (at least 64 tokens, as the reference pre-sizes), or None
+        when it would have to grow inside a graph capture.  A grown engine
+        replaces the current one; the old one stays alive, since captured
+        graphs may still replay into its staging."""
+        from .cpu_experts import CpuExperts
+        c = self.cfg
+        need_t = max(64, int(max_qlen))
+        need_k = max(int(c.top_k or 0), int(top_k), 1)
+        cur = self._cpu[-1] if self._cpu else None
+        if cur is not None and cur.max_tokens >= need_t and cur.max_topk >= need_k:
+            return cur
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            return None
+        lim = c.swiglu_limit if c.activation_type == 1 else 0.0
+        if cur is not None:
+            need_t, need_k = max(need_t, cur.max_tokens), max(need_k, cur.max_topk)
+        eng = CpuExperts.from_store(self.host_store(), swiglu_limit=lim,
+                                    swiglu_alpha=c.swiglu_alpha, swiglu_beta=c.swiglu_beta,
+                                    max_tokens=need_t, max_topk=need_k)
+        self._cpu.append(eng)
+        return eng
+
+    def prepare_decode_buffers(self, max_qlen: int, top_k: int) -> None:
+        """Size the pinned decode staging before any graph capture
+        (binding.cpp:848-858)."""
+        if int(max_qlen) > 0 and int(top_k) > 0:
+            self._host_engine(max_qlen, top_k)
+
+    def cpu_decode(self, stream, qlen, top_k, hidden, expert_ids, weights, out_gpu,
+                   layer: int = -1, defer: int = 0) -> int:
+        """binding.cpp:859-1296: on `stream`, out_gpu[:qlen] (fp32 [qlen, H],
+        device) = this layer's experts computed on the host for hidden (bf16
+        [qlen, H]), expert_ids (int32) and weights (fp32) [qlen, top_k] (device
+        tensors or pointers), through pinned staging and a host-function node
+        (graph-capturable).  0 = queued; -1 = out_gpu too small; -2 = the
+        staging would have to grow during a capture (call
+        prepare_decode_buffers first).  Ids outside [0, expert_num + shared)
+        and zero weights add nothing."""
+        eng = self._host_engine(qlen, top_k)
+        if eng is None:
+            return -2
+        return eng.cpu_decode(stream, qlen, top_k, hidden, expert_ids, weights, out_gpu, layer,
+                              defer)
 
     def shard_geometry(self) -> dict:
         return self.host_store().shard_geometry()

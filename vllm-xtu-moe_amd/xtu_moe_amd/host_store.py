@@ -31,15 +31,12 @@ PLANES = ("w13", "s13", "w2", "s2", "gs13", "gs2")
 WHICH = {0: "w13", 1: "w2", 2: "s13", 3: "s2", 4: "gs13", 5: "gs2"}
 
 
-def _pinned_like(t, rows=None, cols=None):
-    shape = (t.shape[0] if rows is None else rows,) + ((t.shape[1],) if cols is None else (cols,))
-    return torch.empty(shape, dtype=t.dtype, pin_memory=True)
-
-
 class HostExpertStore:
     """Pinned host copy of a layer's experts (routed [0, E), shared after)."""
 
-    def __init__(self, fmt, H, I, E, n_shared, planes: dict, ns: int = 1):
+    def __init__(self, fmt, H, I, E, n_shared, planes: dict, ns: int = 1, pin: bool = True):
+        """pin=False keeps the shards in pageable memory (a host-only store
+        for the host engine; the DMA paths want pinned memory)."""
         self.fmt, self.H, self.I, self.E, self.n_shared = int(fmt), int(H), int(I), int(E), int(n_shared)
         ns = int(ns)
         if ns < 1 or self.I % (16 * ns) or self.H % (16 * ns):
@@ -55,20 +52,20 @@ class HostExpertStore:
         self.w13_shard, self.w2_shard = [], []
         w13, w2 = planes["w13"], planes["w2"]
         for node in range(ns):
-            a = torch.empty((n, 2 * self.w13_cbytes), dtype=torch.uint8, pin_memory=True)
+            a = torch.empty((n, 2 * self.w13_cbytes), dtype=torch.uint8, pin_memory=pin)
             g0 = node * self.w13_cbytes
             u0 = self.I * self.rb13 + g0
             a[:, :self.w13_cbytes].copy_(w13[:, g0:g0 + self.w13_cbytes])
             a[:, self.w13_cbytes:].copy_(w13[:, u0:u0 + self.w13_cbytes])
             self.w13_shard.append(a)
-            b = torch.empty((n, self.w2_cbytes), dtype=torch.uint8, pin_memory=True)
+            b = torch.empty((n, self.w2_cbytes), dtype=torch.uint8, pin_memory=pin)
             d0 = node * self.w2_cbytes
             b.copy_(w2[:, d0:d0 + self.w2_cbytes])
             self.w2_shard.append(b)
         self.planes = {name: planes[name] for name in ("s13", "s2", "gs13", "gs2")}
 
     @classmethod
-    def from_weights(cls, W: ExpertWeights, ns: int = 1) -> "HostExpertStore":
+    def from_weights(cls, W: ExpertWeights, ns: int = 1, pin: bool = True) -> "HostExpertStore":
         planes = {}
         for name in PLANES:
             t = getattr(W, name)
@@ -78,10 +75,10 @@ class HostExpertStore:
             if name in ("w13", "w2"):   # copied into the pinned node shards
                 planes[name] = t.cpu()
                 continue
-            h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+            h = torch.empty(t.shape, dtype=t.dtype, pin_memory=pin)
             h.copy_(t, non_blocking=False)
             planes[name] = h
-        return cls(W.fmt, W.H, W.I, W.E, W.n_shared, planes, ns=ns)
+        return cls(W.fmt, W.H, W.I, W.E, W.n_shared, planes, ns=ns, pin=pin)
 
     @property
     def n_experts(self) -> int:
