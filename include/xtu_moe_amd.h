@@ -397,6 +397,34 @@ hipError_t xtu_copy_experts(int n, const int32_t* experts, const void* src, long
 hipError_t xtu_copy_2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width,
                        size_t height, hipStream_t stream);
 
+/* ------------------------------------------------ reference-signature small-M ABI
+ * The reference's native moe4_smallm_* entry points (xiaotu_moe/csrc/
+ * moe4_smallm.cu:346-430), same names, arguments and meaning, over the
+ * pool's K-major MXFP4 planes: W [S][K/2][N] (byte (j, n) = codes of k = 2j,
+ * 2j+1, low nibble first), SC [S][K/32][N] e8m0.  Up to 8 rows per expert.
+ * They ADD into Y (fp32; the caller zeroes it), with float atomics as the
+ * reference kernels.  K % 32 == 0, N % 4 == 0.
+ *   gu:  Y[r][n] += sum_k W[row(e)][k][n] X[tok[r]][k], rows r of segment
+ *        seg2exp[z] (row(e) = slot_map ? slot_map[e] - slot_base : e); X bf16
+ *   dn:  Y[tok[r]][n] += wts[r] sum_k W[row(e)][k][n] X[r][k]; X fp32 act rows
+ *   gu2: Y[e*8+c][n] += ..., rows c = the first 8 pairs (t, j) with
+ *        ids[t][j] == e, e < nexp; X bf16 [T][K]
+ *   dn2: Y[t_c][n] += wts[t_c][j_c] sum_k W[e][k][n] X[e*8+c][k]; X fp32 */
+hipError_t moe4_smallm_init(void);
+hipError_t moe4_smallm_gu(const void* W, const void* SC, const void* X, void* Y,
+                          const int* seg2exp, const int* seg_start, const int* tok,
+                          const int* slot_map, int slot_base, int nseg, int K, int N,
+                          hipStream_t stream);
+hipError_t moe4_smallm_dn(const void* W, const void* SC, const void* X, void* Y,
+                          const int* seg2exp, const int* seg_start, const int* tok,
+                          const float* wts, const int* slot_map, int slot_base, int nseg, int K,
+                          int N, hipStream_t stream);
+hipError_t moe4_smallm_gu2(const void* W, const void* SC, const void* X, void* Y, const int* ids,
+                           int T, int TOPSEL, int nexp, int K, int N, hipStream_t stream);
+hipError_t moe4_smallm_dn2(const void* W, const void* SC, const void* X, void* Y, const int* ids,
+                           const float* wts, int T, int TOPSEL, int nexp, int K, int N,
+                           hipStream_t stream);
+
 /* ------------------------------------------------ pool-miss split
  * Pairs whose expert is resident in the GPU pool run on the device, the
  * others on a host engine; the results are added

@@ -17,7 +17,7 @@ def _prototypes():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     out = {}
-    for m in re.finditer(r"([A-Za-z_][\w\s\*]*?)\b(xtu_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.S):
+    for m in re.finditer(r"([A-Za-z_][\w\s\*]*?)\b((?:xtu|moe4_smallm)_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.S):
         ret, name, args = m.group(1).strip(), m.group(2), m.group(3).strip()
         params = [] if args in ("", "void") else [a.strip() for a in args.split(",")]
         out[name] = (ret, params)

@@ -78,6 +78,11 @@ SIGNATURES = {
                                  _i, _vp, _vp, _f, _f, _f, _vp]),
     "xtu_i8_gemm_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                               _vp, _vp]),
+    "moe4_smallm_init": (_i, []),
+    "moe4_smallm_gu": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "moe4_smallm_dn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "moe4_smallm_gu2": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "moe4_smallm_dn2": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "xtu_pin_split": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "xtu_cpu_engine_create": (_i, [_i, _i, _i, _i, _i, _vp, _l, _vp, _l, _vp, _l, _vp, _l, _vp,
                                    _vp, _f, _f, _f, _i, _i, _i, _i, _vp]),
