@@ -443,8 +443,10 @@ hipError_t xtu_pin_split(const int32_t* ids, const float* wts, int n, const int3
  * CPU MoE behind cpu_decode, xiaotu_moe/csrc/python_binding/binding.cpp:
  * 859-1296).  w13_nodes / w2_nodes: ns NUMA-node buffers of P16 rows
  * ([expert][gate rows | up rows] and [expert][rows] of the node; strides in
- * bytes per expert); s13 / s2: packed scale groups (fp4) or fp32 block
- * scales (fp8); gs13 / gs2: NVFP4 global scales.  isa: -1 best available, 0
+ * bytes per expert); s13 / s2: packed scale groups (fp4), fp32 block
+ * scales (fp8), or fp32 [N][K/group_k] row scales (fmt 4, INT4/WNA16:
+ * value = code - 8, the engine's MOE_WNA16, moe_v2_packed4_base.inc:1-20,
+ * :1594); gs13 / gs2: NVFP4 global scales.  isa: -1 best available, 0
  * portable, 2 AVX-512.  max_tokens > 0 allocates the pinned staging of
  * xtu_cpu_decode (max_tokens rows of max_topk pairs); 0 = host-only engine.
  * The weights are read in place and must outlive the engine. */
@@ -452,9 +454,9 @@ hipError_t xtu_cpu_engine_create(int fmt, int H, int I, int n_experts, int ns,
                                  const void* const* w13_nodes, long w13_estride,
                                  const void* const* w2_nodes, long w2_estride, const void* s13,
                                  long s13_estride, const void* s2, long s2_estride,
-                                 const float* gs13, const float* gs2, float limit, float alpha,
-                                 float beta, int n_threads, int isa, int max_tokens, int max_topk,
-                                 void** engine);
+                                 const float* gs13, const float* gs2, int group_k, float limit,
+                                 float alpha, float beta, int n_threads, int isa, int max_tokens,
+                                 int max_topk, void** engine);
 hipError_t xtu_cpu_engine_info(const void* engine, int* isa, int* threads);
 /* Synchronous, host memory: out [T][H] fp32 = sum over pairs with
  * 0 <= id < n_experts and w != 0 of w * expert(x); x bf16 [T][H]. */

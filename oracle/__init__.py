@@ -25,7 +25,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB = None
 _REF = {}
 
-FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4 = 0, 1, 2, 3
+FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4, FMT_INT4 = 0, 1, 2, 3, 4
 
 
 def build(force: bool = False) -> None:
@@ -62,6 +62,7 @@ def lib():
         L.xo_route_grouped_sigmoid.argtypes = [vp, vp, i, i, i, i, i, f, i, vp, vp]
         L.xo_segment.argtypes = [vp, vp, i, i, i, i, i, vp, vp, vp, vp, vp]
         L.xo_moe_layer.argtypes = [i] * 7 + [vp] * 9 + [f] * 3 + [vp]
+        L.xo_moe_layer_g.argtypes = [i] * 8 + [vp] * 9 + [f] * 3 + [vp]
         L.xo_moe_layer_i8.argtypes = [i] * 6 + [vp] * 7 + [f] * 3 + [vp]
         L.xo_i8_gemm.argtypes = [vp, i, vp, vp, i, i, f, vp, vp]
         L.xo_i8_quant_row.argtypes = [vp, i, vp]
@@ -152,16 +153,19 @@ def segment(ids: np.ndarray, wts: np.ndarray, E: int, n_shared: int = 0,
 # ---------------------------------------------------------------- expert math
 def moe_layer(fmt: int, x_bf16: np.ndarray, ids, wts, E: int, n_shared: int, H: int, I: int,
               w13, s13, w2, s2, gs13=None, gs2=None, limit=0.0, alpha=1.0, beta=0.0):
-    """out[T][H] fp32 of the dequantized-fp32 layer (CPU-engine semantics)."""
+    """out[T][H] fp32 of the dequantized-fp32 layer (CPU-engine semantics).
+    INT4 (fmt 4): s13 / s2 fp32 [E, N, K/group], the group read off their
+    shape."""
     x = np.ascontiguousarray(x_bf16, np.uint16)
     ids = np.ascontiguousarray(ids, np.int32)
     wts = np.ascontiguousarray(wts, np.float32)
     T, K = ids.shape
     out = np.zeros((T, H), np.float32)
     arrs = [np.ascontiguousarray(a) if a is not None else None for a in (w13, s13, gs13, w2, s2, gs2)]
-    rc = lib().xo_moe_layer(fmt, T, K, E, n_shared, H, I, _p(x), _p(ids), _p(wts),
-                            *[_p(a) for a in arrs], float(limit), float(alpha), float(beta),
-                            _p(out))
+    gk = H // s13.shape[-1] if fmt == 4 else 0
+    rc = lib().xo_moe_layer_g(fmt, gk, T, K, E, n_shared, H, I, _p(x), _p(ids), _p(wts),
+                              *[_p(a) for a in arrs], float(limit), float(alpha), float(beta),
+                              _p(out))
     assert rc == 0
     return out
 
@@ -256,7 +260,8 @@ def ref_lib(isa: str | None = None):
 class RefEngine:
     """The reference ``MOE_V2`` CPU engine over dense checkpoint-layout weights.
 
-    fmt: FMT_BF16 / FMT_FP8 / FMT_MXFP4 / FMT_NVFP4.  For NVFP4 the e4m3 scale
+    fmt: FMT_BF16 / FMT_FP8 / FMT_MXFP4 / FMT_NVFP4 / FMT_INT4 (the engine's
+    WNA16 traits; fp32 scales [E, N, K/group]).  For NVFP4 the e4m3 scale
     bytes are handed to the engine as fp32 (exact) with the per-expert global
     scale passed separately, as the engine's NVFP4 traits expect.
     """
@@ -265,7 +270,9 @@ class RefEngine:
                  limit=0.0, alpha=1.0, beta=0.0, isa=None):
         self.L = ref_lib(isa)
         gn, gk = {FMT_BF16: (1, 1), FMT_FP8: (128, 128), FMT_MXFP4: (1, 32),
-                  FMT_NVFP4: (1, 16)}[fmt]
+                  FMT_NVFP4: (1, 16), FMT_INT4: (1, 0)}[fmt]
+        if fmt == FMT_INT4:
+            gk = H // s13.shape[-1]
         if fmt == FMT_NVFP4:
             t = e4m3_table()
             s13 = t[np.asarray(s13)]

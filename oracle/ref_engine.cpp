@@ -10,7 +10,7 @@
 //   * Traits::gate_up_slice_batched                   (xiaotu_moe/csrc/moe/moe_v2.hpp:300)
 //   * xiaotu_int8::set_activation / set_cur_tokens    (xiaotu_moe/csrc/moe/xiaotu_int8_mode.h)
 // Traits: BF16WeightTraits (moe_v2.hpp:343), FP8WeightTraits (moe_v2_fp8.hpp:549),
-// MXFP4WeightTraits / NVFP4WeightTraits (moe_v2_packed4_*.inc).
+// MXFP4WeightTraits / NVFP4WeightTraits / WNA16WeightTraits (moe_v2_packed4_*.inc).
 #include <cstdint>
 #include <cstdio>
 #include <exception>
@@ -24,7 +24,7 @@ using namespace xiaotu_moe;
 
 namespace {
 
-enum Kind { kBF16 = 0, kFP8 = 1, kMXFP4 = 2, kNVFP4 = 3 };
+enum Kind { kBF16 = 0, kFP8 = 1, kMXFP4 = 2, kNVFP4 = 3, kWNA16 = 4 };
 
 struct Handle {
   int kind;
@@ -88,6 +88,7 @@ void* xref_create(int kind, int E, int topk, int H, int I, int group_n, int grou
       case kFP8: h->eng = make<FP8WeightTraits>(c, w13, w2, s13, s2, nullptr, nullptr); break;
       case kMXFP4: h->eng = make<MXFP4WeightTraits>(c, w13, w2, s13, s2, nullptr, nullptr); break;
       case kNVFP4: h->eng = make<NVFP4WeightTraits>(c, w13, w2, s13, s2, gs13, gs2); break;
+      case kWNA16: h->eng = make<WNA16WeightTraits>(c, w13, w2, s13, s2, nullptr, nullptr); break;
       default: delete h; return nullptr;
     }
     return h;
@@ -106,6 +107,7 @@ int xref_forward(void* hv, int M, int K, const uint32_t* ids, const float* wts,
     case kFP8: fwd<FP8WeightTraits>(h->eng, M, K, ids, wts, x, out); break;
     case kMXFP4: fwd<MXFP4WeightTraits>(h->eng, M, K, ids, wts, x, out); break;
     case kNVFP4: fwd<NVFP4WeightTraits>(h->eng, M, K, ids, wts, x, out); break;
+    case kWNA16: fwd<WNA16WeightTraits>(h->eng, M, K, ids, wts, x, out); break;
     default: return -1;
   }
   return 0;
@@ -119,6 +121,7 @@ void xref_destroy(void* hv) {
     case kFP8: del<FP8WeightTraits>(h->eng); break;
     case kMXFP4: del<MXFP4WeightTraits>(h->eng); break;
     case kNVFP4: del<NVFP4WeightTraits>(h->eng); break;
+    case kWNA16: del<WNA16WeightTraits>(h->eng); break;
   }
   delete h;
 }

@@ -14,8 +14,9 @@
  *   xo_expf / xo_sigmoid             within 2 ulp of libm expf over a dense sweep
  *   routers                          brute force (sort-based) on tiny E; textbook
  *   xo_segment                       numpy stable argsort restatement + brute force
- *   xo_moe_layer (bf16/fp8/mxfp4/nvfp4) vs the compiled reference engine
- *                                    (oracle/_ref) forward_many, rel err ~1e-6
+ *   xo_moe_layer (bf16/fp8/mxfp4/nvfp4/int4) vs the compiled reference
+ *                                    engine (oracle/_ref) forward_many, rel
+ *                                    err ~1e-6 (int4: MOE_WNA16 traits)
  *   xo_i8_* (INT8 ALIGN)             int32 accumulators bit-exact against an
  *                                    int64 closed form built from the codec
  *                                    tables (brute force); the layer (marked
@@ -308,12 +309,24 @@ int xo_segment(const int32_t* ids, const float* wts, int T, int K, int E, int n_
 /*            e8m0 (moe_v2_packed4_w4a8.inc:1966-2003)                        */
 /*   3 NVFP4: as MXFP4 with s13 [E][2I][H/16] e4m3 bytes and a per-expert    */
 /*            fp32 global scale gs13[E] (gpu_prefill.py:111-127, 290-297)    */
+/*   4 INT4 (WNA16): nibbles as MXFP4, value = nibble - 8, times an fp32     */
+/*            scale s13 [E][2I][H/gk] (moe_v2_packed4_base.inc:4-16, :1594)  */
 /* ------------------------------------------------------------------------ */
-enum { XO_BF16 = 0, XO_FP8 = 1, XO_MXFP4 = 2, XO_NVFP4 = 3 };
+enum { XO_BF16 = 0, XO_FP8 = 1, XO_MXFP4 = 2, XO_NVFP4 = 3, XO_INT4 = 4 };
 
-/* dequantize row n (of N) of one expert's [N][K] weight into out[K] */
-static void deq_row(int fmt, const void* w, const void* s, const float* gs, int e, int N, int K,
-                    int n, float* out) {
+/* dequantize row n (of N) of one expert's [N][K] weight into out[K]; gk is
+ * INT4's k per scale */
+static void deq_row(int fmt, int gk, const void* w, const void* s, const float* gs, int e, int N,
+                    int K, int n, float* out) {
+  if (fmt == XO_INT4) {
+    const uint8_t* r = (const uint8_t*)w + ((size_t)e * N + n) * (K / 2);
+    const float* sc = (const float*)s + ((size_t)e * N + n) * (K / gk);
+    for (int k = 0; k < K; ++k) {
+      const int nib = (k & 1) ? (r[k / 2] >> 4) : (r[k / 2] & 15);
+      out[k] = (float)(nib - 8) * sc[k / gk];
+    }
+    return;
+  }
   if (fmt == XO_BF16) {
     const uint16_t* r = (const uint16_t*)w + ((size_t)e * N + n) * K;
     for (int k = 0; k < K; ++k) out[k] = xo_bf16_to_f32(r[k]);
@@ -346,32 +359,34 @@ float xo_silu_gate(float g, float u, float limit, float alpha, float beta) {
 
 /* One expert applied to one bf16 row x[H]: y[H] (fp32). Also returns the bf16
  * activation row (act_out[I], may be NULL). */
-static void expert_row(int fmt, const void* w13, const void* s13, const float* gs13,
+static void expert_row(int fmt, int gk, const void* w13, const void* s13, const float* gs13,
                        const void* w2, const void* s2, const float* gs2, int e, int H, int I,
                        const float* xf, float limit, float alpha, float beta, float* wrow,
                        float* actf, float* y) {
   for (int i = 0; i < I; ++i) {
     double g = 0.0, u = 0.0;
-    deq_row(fmt, w13, s13, gs13, e, 2 * I, H, i, wrow);
+    deq_row(fmt, gk, w13, s13, gs13, e, 2 * I, H, i, wrow);
     for (int k = 0; k < H; ++k) g += (double)xf[k] * wrow[k];
-    deq_row(fmt, w13, s13, gs13, e, 2 * I, H, I + i, wrow);
+    deq_row(fmt, gk, w13, s13, gs13, e, 2 * I, H, I + i, wrow);
     for (int k = 0; k < H; ++k) u += (double)xf[k] * wrow[k];
     actf[i] = bf16_round(xo_silu_gate((float)g, (float)u, limit, alpha, beta));
   }
   for (int h = 0; h < H; ++h) {
     double d = 0.0;
-    deq_row(fmt, w2, s2, gs2, e, H, I, h, wrow);
+    deq_row(fmt, gk, w2, s2, gs2, e, H, I, h, wrow);
     for (int i = 0; i < I; ++i) d += (double)actf[i] * wrow[i];
     y[h] = (float)d;
   }
 }
 
 /* Full layer: out[T][H] fp32.  Experts [0,E) routed, [E, E+n_shared) shared
- * (weight 1, after the routed pairs).  Returns 0 on success. */
-int xo_moe_layer(int fmt, int T, int K, int E, int n_shared, int H, int I,
-                 const uint16_t* x, const int32_t* ids, const float* wts, const void* w13,
-                 const void* s13, const float* gs13, const void* w2, const void* s2,
-                 const float* gs2, float limit, float alpha, float beta, float* out) {
+ * (weight 1, after the routed pairs).  gk: INT4's k per scale (ignored for
+ * the other formats).  Returns 0 on success. */
+int xo_moe_layer_g(int fmt, int gk, int T, int K, int E, int n_shared, int H, int I,
+                   const uint16_t* x, const int32_t* ids, const float* wts, const void* w13,
+                   const void* s13, const float* gs13, const void* w2, const void* s2,
+                   const float* gs2, float limit, float alpha, float beta, float* out) {
+  if (fmt == XO_INT4 && (gk <= 0 || H % gk || I % gk)) return -1;
   const int mx = H > I ? H : I;
   float* xf = (float*)malloc(sizeof(float) * (size_t)H);
   float* wrow = (float*)malloc(sizeof(float) * (size_t)mx);
@@ -396,12 +411,21 @@ int xo_moe_layer(int fmt, int T, int K, int E, int n_shared, int H, int I,
         e = E + (r - K);
         w = 1.0f;
       }
-      expert_row(fmt, w13, s13, gs13, w2, s2, gs2, e, H, I, xf, limit, alpha, beta, wrow, actf, y);
+      expert_row(fmt, gk, w13, s13, gs13, w2, s2, gs2, e, H, I, xf, limit, alpha, beta, wrow,
+                 actf, y);
       for (int h = 0; h < H; ++h) o[h] += w * y[h];
     }
   }
   free(xf); free(wrow); free(actf); free(y);
   return 0;
+}
+
+int xo_moe_layer(int fmt, int T, int K, int E, int n_shared, int H, int I,
+                 const uint16_t* x, const int32_t* ids, const float* wts, const void* w13,
+                 const void* s13, const float* gs13, const void* w2, const void* s2,
+                 const float* gs2, float limit, float alpha, float beta, float* out) {
+  return xo_moe_layer_g(fmt, 0, T, K, E, n_shared, H, I, x, ids, wts, w13, s13, gs13, w2, s2,
+                        gs2, limit, alpha, beta, out);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -510,7 +534,7 @@ int xo_i8_row_spread(const uint8_t* srow, int K) {
 static float i8_fallback_dot(const float* a, const uint8_t* w, const uint8_t* s, int N, int K,
                              int n, float* wrow) {
   double d = 0.0;
-  deq_row(XO_MXFP4, w, s, NULL, 0, N, K, n, wrow);
+  deq_row(XO_MXFP4, 0, w, s, NULL, 0, N, K, n, wrow);
   for (int k = 0; k < K; ++k) d += (double)a[k] * wrow[k];
   return (float)d;
 }

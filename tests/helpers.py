@@ -1,6 +1,8 @@
 """Shared test helpers: seeded synthetic layers and the parity tolerance."""
 from __future__ import annotations
 
+import types
+
 import numpy as np
 import torch
 
@@ -75,3 +77,43 @@ def random_routing(T, K, E, seed=0, invalid_frac=0.0, zero_frac=0.0):
         m = rng.random((T, K)) < zero_frac
         wts[m] = 0.0
     return ids, wts
+
+
+# ------------------------------------------------------------- INT4 (WNA16)
+def int4_dense(E_, H_, I_, group, seed):
+    """Dense INT4 checkpoint tensors (engine layout) of E_ experts."""
+    g = torch.Generator().manual_seed(seed)
+    w13 = torch.randn((E_, 2 * I_, H_), generator=g) * 0.05
+    w2 = torch.randn((E_, H_, I_), generator=g) * 0.05
+    a, b = F.quantize_int4(w13, group)
+    c, e = F.quantize_int4(w2, group)
+    return dict(w13=a, s13=b, w2=c, s2=e, gs13=None, gs2=None)
+
+
+def gptq_pack(codes):
+    """codes [E, N, K] (0..15) -> GPTQ int32 [E, K/8, N], nibble i of a word = k 8j+i."""
+    c = codes.to(torch.int64).reshape(codes.shape[0], codes.shape[1], -1, 8)
+    word = sum(c[..., i] << (4 * i) for i in range(8))
+    word = torch.where(word >= 2 ** 31, word - 2 ** 32, word)
+    return word.to(torch.int32).transpose(1, 2).contiguous()
+
+
+def unpack_nibbles(b):
+    """[..., K/2] bytes -> [..., K] codes, low nibble first."""
+    return torch.stack([b & 15, b >> 4], -1).reshape(*b.shape[:-1], b.shape[-1] * 2)
+
+
+def int4_layer(E_, H_, I_, seed):
+    """A GPTQ-style INT4 layer object (int32 qweight / transposed scales /
+    symmetric qzeros) and its dense tensors."""
+    d = int4_dense(E_, H_, I_, 128, seed)
+    d["s13"], d["s2"] = d["s13"].half().float(), d["s2"].half().float()   # GPTQ keeps fp16
+    P = torch.nn.Parameter
+    layer = types.SimpleNamespace(
+        w13_qweight=P(gptq_pack(unpack_nibbles(d["w13"])), requires_grad=False),
+        w2_qweight=P(gptq_pack(unpack_nibbles(d["w2"])), requires_grad=False),
+        w13_scales=P(d["s13"].transpose(1, 2).half(), requires_grad=False),
+        w2_scales=P(d["s2"].transpose(1, 2).half(), requires_grad=False),
+        w13_qzeros=torch.full((E_, H_ // 128, 2 * I_ // 8), 0x77777777, dtype=torch.int32),
+        top_k=3, renormalize=True, swiglu_limit=7.0)
+    return d, layer

@@ -3,18 +3,21 @@ oracle, on the CPU: every format, one and two NUMA-node shards, the AVX-512
 and the portable kernels, invalid ids / zero weights / an expert listed
 twice by one token, and bit-identical results for any thread count (each
 output element is summed in a fixed order)."""
+import types
+
 import numpy as np
 import pytest
 import torch
 
-from helpers import bf16_tensor_to_bits, check_close, dense_to_numpy, make_dense_layer
+from helpers import (bf16_tensor_to_bits, check_close, dense_to_numpy, gptq_pack, int4_dense,
+                     int4_layer, make_dense_layer, unpack_nibbles)
 import oracle
 from xtu_moe_amd import formats as F
 from xtu_moe_amd.cpu_experts import ISA_AVX512, ISA_PORTABLE, CpuExperts
 from xtu_moe_amd.host_store import HostExpertStore
 from xtu_moe_amd.layer import ExpertWeights
 
-FMTS = [F.FMT_BF16, F.FMT_FP8, F.FMT_MXFP4, F.FMT_NVFP4]
+FMTS = [F.FMT_BF16, F.FMT_FP8, F.FMT_MXFP4, F.FMT_NVFP4, F.FMT_INT4]
 E, H, I = 6, 256, 256
 
 
@@ -110,3 +113,78 @@ def test_no_valid_pairs_gives_zeros_and_bad_layouts_are_refused():
     w13 = W.w13.contiguous()
     with pytest.raises(RuntimeError):     # NVFP4 needs its global scales
         CpuExperts(F.FMT_NVFP4, H, I, E, [w13], [W.w2.contiguous()], W.s13, W.s2, None, None)
+
+
+# --------------------------------------------------------------- INT4 / WNA16
+@pytest.mark.parametrize("group", [32, 64])
+def test_int4_groups_host_engine(group):
+    d = int4_dense(E, H, I, group, seed=group)
+    W = ExpertWeights.from_dense(F.FMT_INT4, d["w13"], d["s13"], d["w2"], d["s2"], E=E,
+                                 device="cpu")
+    assert W.group_k == group
+    dn = dense_to_numpy(F.FMT_INT4, d)
+    for isa in ISAS:
+        eng = CpuExperts.from_weights(W, isa=isa, n_threads=3)
+        try:
+            x, ids, wts = _batch(6, 3, seed=group)
+            out = eng.forward(x, torch.from_numpy(ids), torch.from_numpy(wts))
+            check_close(out.numpy(), _oracle(F.FMT_INT4, dn, x, ids, wts), bf16_out=False,
+                        what=f"int4 group {group} isa {isa}")
+        finally:
+            eng.close()
+
+
+def test_gptq_repack_and_zero_points():
+    from xtu_moe_amd.mixed_experts import repack_gptq_int4, require_symmetric_zero_points
+    d = int4_dense(3, 256, 128, 128, seed=2)
+    codes = unpack_nibbles(d["w13"])                     # [E, 2I, H]
+    qw = gptq_pack(codes)                        # [E, H/8, 2I]
+    w, s = repack_gptq_int4(qw, d["s13"].transpose(1, 2).contiguous())
+    assert torch.equal(w, d["w13"]) and torch.equal(s, d["s13"])
+    ok = types.SimpleNamespace(w13_qzeros=torch.full((3, 2, 32), 0x77777777, dtype=torch.int32))
+    require_symmetric_zero_points(ok, ("w13_qzeros",))
+    bad = types.SimpleNamespace(w13_qzeros=torch.full((3, 2, 32), 0x77777775, dtype=torch.int32))
+    with pytest.raises(NotImplementedError):
+        require_symmetric_zero_points(bad, ("w13_qzeros",))
+
+
+def test_int4_hook_on_host_tensors_matches_oracle():
+    from xtu_moe_amd.mixed_experts import XiaotuExpertsInt4
+    d, layer = int4_layer(E, H, I, seed=5)
+    hook = XiaotuExpertsInt4(quant_config=types.SimpleNamespace(group_size=128, desc_act=False))
+    hook.process_weights_after_loading(layer)
+    x, ids, wts = _batch(5, 3, seed=8)
+    out = hook.apply(x, None, None, topk_ids=torch.from_numpy(ids),
+                     topk_weights=torch.from_numpy(wts))
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (5, H)
+    ref = _oracle(F.FMT_INT4, dense_to_numpy(F.FMT_INT4, d), x, ids, wts, limit=7.0)
+    check_close(out.float().numpy(), ref, bf16_out=True, what="int4 hook")
+    with pytest.raises(NotImplementedError):
+        XiaotuExpertsInt4(quant_config=types.SimpleNamespace(group_size=128, desc_act=True)
+                          ).process_weights_after_loading(layer)
+
+
+def test_wna16_engine_forward_many():
+    from xtu_moe_amd.engine import MOE_WNA16, MOEConfigV2
+    d = int4_dense(E, H, I, 128, seed=9)
+    cfg = MOEConfigV2(expert_num=E, top_k=3, hidden_size=H, intermediate_size=I, groupN=1,
+                      groupK=128)
+    eng = MOE_WNA16(cfg, d["w13"], d["w2"], d["s13"], d["s2"])
+    x, ids, wts = _batch(4, 3, seed=10)
+    out = torch.empty((4, H))
+    eng.forward_many(4, 3, torch.from_numpy(ids), torch.from_numpy(wts), x, out)
+    check_close(out.numpy(), _oracle(F.FMT_INT4, dense_to_numpy(F.FMT_INT4, d), x, ids, wts),
+                bf16_out=False, what="MOE_WNA16.forward_many")
+
+
+def test_nvfp4_second_level_scales():
+    from xtu_moe_amd.mixed_experts import nvfp4_global_scales
+    g2 = torch.tensor([0.5, 2.0])
+    a, b = nvfp4_global_scales(torch.tensor([[0.5, 0.5], [1.5, 1.5]]), g2)
+    assert torch.equal(a, torch.tensor([0.5, 1.5])) and torch.equal(b, g2)
+    a, _ = nvfp4_global_scales(torch.tensor([0.25, 4.0]), g2)
+    assert torch.equal(a, torch.tensor([0.25, 4.0]))
+    with pytest.raises(RuntimeError):          # gate and up differ
+        nvfp4_global_scales(torch.tensor([[0.5, 0.5], [1.5, 1.0]]), g2)
+    with pytest.raises(RuntimeError):          # not loaded
+        nvfp4_global_scales(torch.zeros(2, 2), g2)

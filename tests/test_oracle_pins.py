@@ -186,7 +186,7 @@ def _dense_f64_layer(fmt, d, x_bits, ids, wts, E, NS, H, I, limit=0.0):
     return out
 
 
-FMTS = [F.FMT_BF16, F.FMT_FP8, F.FMT_MXFP4, F.FMT_NVFP4]
+FMTS = [F.FMT_BF16, F.FMT_FP8, F.FMT_MXFP4, F.FMT_NVFP4, F.FMT_INT4]
 
 
 @pytest.mark.parametrize("fmt", FMTS)

@@ -36,6 +36,10 @@ namespace {
 // ---------------------------------------------------------------------------
 alignas(64) const float kE2M1[16] = {0.f,  0.5f,  1.f,  1.5f,  2.f,  3.f,  4.f,  6.f,
                                      -0.f, -0.5f, -1.f, -1.5f, -2.f, -3.f, -4.f, -6.f};
+// int4 centred at 8 (WNA16): code c is worth c - 8
+alignas(64) const float kI4[16] = {-8.f, -7.f, -6.f, -5.f, -4.f, -3.f, -2.f, -1.f,
+                                   0.f,  1.f,  2.f,  3.f,  4.f,  5.f,  6.f,  7.f};
+constexpr bool is_nib(int fmt) { return fmt == kMXFP4 || fmt == kNVFP4 || fmt == kINT4; }
 
 struct Tables {
   float e4m3[256];   // OCP e4m3fn
@@ -103,17 +107,24 @@ inline int scale_groups(int fmt, int K) {
 // position of k in the decoder's order (fp4: a 32-k chunk is its 16 even k,
 // then its 16 odd k; other formats: k order)
 inline int kpos(int fmt, int k) {
-  if (fmt == kMXFP4 || fmt == kNVFP4) return (k & ~31) | ((k & 1) << 4) | ((k & 31) >> 1);
+  if (is_nib(fmt)) return (k & ~31) | ((k & 1) << 4) | ((k & 31) >> 1);
   return k;
 }
 
 // one 16-row panel of a [N][K] matrix of one expert
 struct PanelRef {
   const uint8_t* w;   // 16 rows, K/sb_k super-blocks of 1 KiB
-  const uint8_t* s;   // fp4: the panel's scale groups; fp8: fp32 scales of its 128-row block
+  const uint8_t* s;   // fp4: the panel's scale groups; fp8: fp32 scales of its 128-row block;
+                      // int4: fp32 scales of its first row ([16][K/gk])
   float gs;           // NVFP4 global scale
   int K;
+  int gk;             // int4: k per scale
 };
+
+// int4: the fp32 scale of row r for the 32-k chunk starting at k0
+inline float i4_scale(const PanelRef& P, int r, int k0) {
+  return reinterpret_cast<const float*>(P.s)[(size_t)r * (P.K / P.gk) + k0 / P.gk];
+}
 
 // ---------------------------------------------------------------------------
 // portable panel kernel: a row at a time
@@ -123,7 +134,17 @@ void decode_row(const PanelRef& P, int r, float* w) {
   const int nsb = P.K / sb_k(FMT);
   for (int sb = 0; sb < nsb; ++sb) {
     const uint8_t* blk = P.w + (size_t)sb * 1024;
-    if constexpr (FMT == kMXFP4 || FMT == kNVFP4) {
+    if constexpr (FMT == kINT4) {
+      for (int q = 0; q < 4; ++q) {
+        const uint8_t* c = blk + q * 256 + r * 16;
+        const float sc = i4_scale(P, r, sb * 128 + q * 32);
+        float* o = w + sb * 128 + q * 32;
+        for (int j = 0; j < 16; ++j) {
+          o[j] = kI4[c[j] & 15] * sc;
+          o[16 + j] = kI4[c[j] >> 4] * sc;
+        }
+      }
+    } else if constexpr (FMT == kMXFP4 || FMT == kNVFP4) {
       const uint8_t* sg = P.s + (size_t)(sb / scale_ug(FMT)) * 1024;
       for (int q = 0; q < 4; ++q) {
         const uint8_t* c = blk + q * 256 + r * 16;
@@ -188,12 +209,12 @@ void tile512(const PanelRef& P, const float* const* xt, int r0, float* out) {
   for (int a = 0; a < RR; ++a)
     for (int t = 0; t < TT; ++t) acc[a][t] = _mm512_setzero_ps();
   const int nsb = P.K / sb_k(FMT);
-  if constexpr (FMT == kMXFP4 || FMT == kNVFP4) {
-    const __m512 lut = _mm512_load_ps(kE2M1);
+  if constexpr (is_nib(FMT)) {
+    const __m512 lut = _mm512_load_ps(FMT == kINT4 ? kI4 : kE2M1);
     const __m512i m15 = _mm512_set1_epi32(15);
     for (int sb = 0; sb < nsb; ++sb) {
       const uint8_t* blk = P.w + (size_t)sb * 1024;
-      const uint8_t* sg = P.s + (size_t)(sb / scale_ug(FMT)) * 1024;
+      const uint8_t* sg = FMT == kINT4 ? nullptr : P.s + (size_t)(sb / scale_ug(FMT)) * 1024;
       for (int q = 0; q < 4; ++q) {
         const int k0 = sb * 128 + q * 32;
         __m512 xa[TT], xb[TT];
@@ -208,7 +229,9 @@ void tile512(const PanelRef& P, const float* const* xt, int r0, float* out) {
           __m512 wl = _mm512_permutexvar_ps(_mm512_and_si512(v, m15), lut);
           __m512 wh = _mm512_permutexvar_ps(_mm512_srli_epi32(v, 4), lut);
           __m512 sc;
-          if constexpr (FMT == kMXFP4) {
+          if constexpr (FMT == kINT4) {
+            sc = _mm512_set1_ps(i4_scale(P, r, k0));
+          } else if constexpr (FMT == kMXFP4) {
             sc = _mm512_set1_ps(kTab.e8m0[sg[(q * 16 + r) * 16 + sb % 16]]);
           } else {
             const uint8_t* sp = sg + (q * 16 + r) * 16 + (sb % 8) * 2;
@@ -292,6 +315,7 @@ PanelFn pick_panel(int fmt, int isa) {
       case kBF16: return panel512<kBF16>;
       case kFP8: return panel512<kFP8>;
       case kMXFP4: return panel512<kMXFP4>;
+      case kINT4: return panel512<kINT4>;
       default: return panel512<kNVFP4>;
     }
   }
@@ -299,6 +323,7 @@ PanelFn pick_panel(int fmt, int isa) {
     case kBF16: return panel_scalar<kBF16>;
     case kFP8: return panel_scalar<kFP8>;
     case kMXFP4: return panel_scalar<kMXFP4>;
+    case kINT4: return panel_scalar<kINT4>;
     default: return panel_scalar<kNVFP4>;
   }
 }
@@ -450,6 +475,7 @@ struct Engine {
     P.s = scale_of(d.s13, d.s13_estride, sg13, e, p, d.H);
     P.gs = d.gs13 ? d.gs13[e] : 1.f;
     P.K = d.H;
+    P.gk = d.group_k;
     return P;
   }
   // panel p of expert e's w2 ([H][I])
@@ -460,18 +486,20 @@ struct Engine {
     P.s = scale_of(d.s2, d.s2_estride, sg2, e, p, d.I);
     P.gs = d.gs2 ? d.gs2[e] : 1.f;
     P.K = d.I;
+    P.gk = d.group_k;
     return P;
   }
   const uint8_t* scale_of(const uint8_t* s, size_t estride, size_t sg, int e, int p, int K) const {
     if (!s) return nullptr;
     const uint8_t* base = s + (size_t)e * estride;
     if (d.fmt == kFP8) return base + (size_t)((16 * p) / 128) * (K / 128) * sizeof(float);
+    if (d.fmt == kINT4) return base + (size_t)16 * p * (K / d.group_k) * sizeof(float);
     return base + (size_t)p * sg;
   }
 };
 
 std::string check_layer(const LayerDesc& d) {
-  if (d.fmt < kBF16 || d.fmt > kNVFP4) return "unknown weight format";
+  if (d.fmt < kBF16 || d.fmt > kINT4) return "unknown weight format";
   if (d.H <= 0 || d.I <= 0 || d.n_experts <= 0) return "H, I and the expert count must be positive";
   if (d.ns < 1 || d.ns > kMaxShards) return "shard count must be in [1, 8]";
   if (d.H % (16 * d.ns) || d.I % (16 * d.ns)) return "H and I must split into 16-row panels per shard";
@@ -482,6 +510,10 @@ std::string check_layer(const LayerDesc& d) {
     if (!d.w13[n] || !d.w2[n]) return "missing weight shard";
   if (d.fmt != kBF16 && (!d.s13 || !d.s2)) return "missing scales";
   if (d.fmt == kNVFP4 && (!d.gs13 || !d.gs2)) return "missing NVFP4 global scales";
+  if (d.fmt == kINT4 && !(d.group_k == 32 || d.group_k == 64 || d.group_k == 128))
+    return "INT4 scale groups must be 32, 64 or 128 k";
+  if (d.fmt == kINT4 && (d.H % d.group_k || d.I % d.group_k))
+    return "H and I must be whole INT4 scale groups";
   return "";
 }
 

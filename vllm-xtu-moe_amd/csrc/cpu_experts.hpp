@@ -9,7 +9,8 @@
 // scales.  No second host copy is made.
 //
 // Arithmetic: dequantised weights (exactly: e2m1 x e8m0, e2m1 x fp32(e4m3 x
-// global), e4m3 x fp32 block scale, bf16) times fp32(x) summed in fp32; the
+// global), e4m3 x fp32 block scale, bf16, (int4 code - 8) x fp32 group scale)
+// times fp32(x) summed in fp32; the
 // clamped SwiGLU activation rounded to bf16 (as the reference engine stores
 // it); down in fp32; out[t] = sum over the token's pairs of w * y, the pairs
 // taken in ascending expert order (a fixed order: results do not depend on
@@ -21,7 +22,7 @@
 
 namespace xtu_cpu {
 
-enum { kBF16 = 0, kFP8 = 1, kMXFP4 = 2, kNVFP4 = 3 };
+enum { kBF16 = 0, kFP8 = 1, kMXFP4 = 2, kNVFP4 = 3, kINT4 = 4 };
 constexpr int kMaxShards = 8;
 
 struct LayerDesc {
@@ -31,8 +32,10 @@ struct LayerDesc {
   const uint8_t* w13[kMaxShards] = {};     // node n: [expert][gate rows | up rows], P16
   const uint8_t* w2[kMaxShards] = {};      // node n: [expert][rows], P16
   size_t w13_estride = 0, w2_estride = 0;  // bytes per expert inside a node buffer
-  const uint8_t* s13 = nullptr;            // fp4: packed scale groups; fp8: fp32 [2I/128][H/128]
-  const uint8_t* s2 = nullptr;             // fp4: packed scale groups; fp8: fp32 [H/128][I/128]
+  const uint8_t* s13 = nullptr;            // fp4: packed scale groups; fp8: fp32 [2I/128][H/128];
+                                           // int4: fp32 [2I][H/group_k]
+  const uint8_t* s2 = nullptr;             // likewise for [H][I]
+  int group_k = 0;                         // int4: k per scale (32, 64 or 128)
   size_t s13_estride = 0, s2_estride = 0;  // bytes per expert
   const float* gs13 = nullptr;             // NVFP4 per-expert global scales
   const float* gs2 = nullptr;

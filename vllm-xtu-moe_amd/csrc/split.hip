@@ -112,18 +112,20 @@ hipError_t xtu_pin_split(const int32_t* ids, const float* wts, int n, const int3
 // xiaotu_moe/csrc/python_binding/binding.cpp:859-1296, run_moe_and_ep).
 // w13_nodes / w2_nodes: ns node buffers ([expert][gate rows | up rows] and
 // [expert][rows] of the node, P16; strides in bytes per expert); s13 / s2:
-// packed scale groups (fp4) or fp32 block scales (fp8), per expert stride;
-// gs13 / gs2: NVFP4 global scales.  isa: -1 best available, 0 portable, 2
-// AVX-512.  max_tokens > 0 allocates the pinned staging that xtu_cpu_decode
+// packed scale groups (fp4), fp32 block scales (fp8) or fp32 [N][K/group_k]
+// row scales (int4, format 4), per expert stride; gs13 / gs2: NVFP4 global
+// scales; group_k: int4's k per scale (32, 64, 128; else ignored).  isa: -1
+// best available, 0 portable, 2 AVX-512.  max_tokens > 0 allocates the
+// pinned staging that xtu_cpu_decode
 // uses (max_tokens rows, max_topk pairs per row); 0 makes a host-only engine.
 // The weights are read in place: they must outlive the engine.
 hipError_t xtu_cpu_engine_create(int fmt, int H, int I, int n_experts, int ns,
                                  const void* const* w13_nodes, long w13_estride,
                                  const void* const* w2_nodes, long w2_estride, const void* s13,
                                  long s13_estride, const void* s2, long s2_estride,
-                                 const float* gs13, const float* gs2, float limit, float alpha,
-                                 float beta, int n_threads, int isa, int max_tokens, int max_topk,
-                                 void** engine) {
+                                 const float* gs13, const float* gs2, int group_k, float limit,
+                                 float alpha, float beta, int n_threads, int isa, int max_tokens,
+                                 int max_topk, void** engine) {
   XTU_CHECK_ARG(engine && w13_nodes && w2_nodes && ns >= 1 && ns <= xtu_cpu::kMaxShards);
   XTU_CHECK_ARG(w13_estride > 0 && w2_estride > 0 && s13_estride >= 0 && s2_estride >= 0);
   XTU_CHECK_ARG(max_tokens >= 0 && max_topk >= 0 && (max_tokens == 0 || max_topk > 0));
@@ -149,6 +151,7 @@ hipError_t xtu_cpu_engine_create(int fmt, int H, int I, int n_experts, int ns,
   d.s2_estride = (size_t)s2_estride;
   d.gs13 = gs13;
   d.gs2 = gs2;
+  d.group_k = group_k;
   XTU_CHECK_ARG(xtu_cpu::check_layer(d).empty());
   xtu_cpu::Engine* eng = xtu_cpu::engine_new(d, n_threads, isa);
   XTU_CHECK_ARG(eng != nullptr);

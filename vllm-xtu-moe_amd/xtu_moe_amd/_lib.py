@@ -85,7 +85,7 @@ SIGNATURES = {
     "moe4_smallm_dn2": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "xtu_pin_split": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "xtu_cpu_engine_create": (_i, [_i, _i, _i, _i, _i, _vp, _l, _vp, _l, _vp, _l, _vp, _l, _vp,
-                                   _vp, _f, _f, _f, _i, _i, _i, _i, _vp]),
+                                   _vp, _i, _f, _f, _f, _i, _i, _i, _i, _vp]),
     "xtu_cpu_engine_info": (_i, [_vp, _vp, _vp]),
     "xtu_cpu_forward": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
     "xtu_cpu_decode": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),

@@ -51,7 +51,7 @@ class CpuExperts:
     (needs a GPU runtime); 0 makes a host-only engine (``forward``)."""
 
     def __init__(self, fmt, H, I, n_experts, w13_nodes, w2_nodes, s13=None, s2=None, gs13=None,
-                 gs2=None, *, swiglu_limit=0.0, swiglu_alpha=1.0, swiglu_beta=0.0,
+                 gs2=None, *, group_k=0, swiglu_limit=0.0, swiglu_alpha=1.0, swiglu_beta=0.0,
                  n_threads=None, isa=ISA_AUTO, max_tokens=0, max_topk=16):
         self.fmt, self.H, self.I, self.n_experts = int(fmt), int(H), int(I), int(n_experts)
         ns = len(w13_nodes)
@@ -71,7 +71,7 @@ class CpuExperts:
         eng = ctypes.c_void_p()
         _lib.call("xtu_cpu_engine_create", self.fmt, self.H, self.I, self.n_experts, ns,
                   ctypes.addressof(n13), es(w13_nodes[0]), ctypes.addressof(n2), es(w2_nodes[0]),
-                  _ptr(s13), es(s13), _ptr(s2), es(s2), _ptr(gs13), _ptr(gs2),
+                  _ptr(s13), es(s13), _ptr(s2), es(s2), _ptr(gs13), _ptr(gs2), int(group_k),
                   float(swiglu_limit), float(swiglu_alpha), float(swiglu_beta),
                   int(n_threads or host_threads()), int(isa), self.max_tokens, self.max_topk,
                   ctypes.addressof(eng))
@@ -84,6 +84,7 @@ class CpuExperts:
     def from_store(cls, store, **kw) -> "CpuExperts":
         """Over a ``HostExpertStore`` (its node shards and scale planes)."""
         p = store.planes
+        kw.setdefault("group_k", getattr(store, "group_k", 0))
         return cls(store.fmt, store.H, store.I, store.n_experts, store.w13_shard, store.w2_shard,
                    p.get("s13"), p.get("s2"), p.get("gs13"), p.get("gs2"), **kw)
 
@@ -91,6 +92,7 @@ class CpuExperts:
     def from_weights(cls, W, **kw) -> "CpuExperts":
         """Over host copies of an ``ExpertWeights`` (one node shard)."""
         h = lambda t: None if t is None else t.detach().to("cpu").contiguous()
+        kw.setdefault("group_k", getattr(W, "group_k", 0))
         return cls(W.fmt, W.H, W.I, W.E + W.n_shared, [h(W.w13)], [h(W.w2)], h(W.s13), h(W.s2),
                    h(W.gs13), h(W.gs2), **kw)
 

@@ -52,24 +52,30 @@ class MOEConfigV2:
 class _Engine:
     FMT = None
     GROUP = (1, 1)   # (groupN, groupK) the checkpoint scales use
+    HOST = False     # weights kept in host memory, computed by the host engine
 
     def __init__(self, cfg: MOEConfigV2, w13_weight, w2_weight, w13_scale=0, w2_scale=0,
                  w13_global_scale=0, w2_global_scale=0, device=None):
         if cfg.expert_num <= 0 or cfg.hidden_size <= 0 or cfg.intermediate_size <= 0:
             raise ValueError("MOEConfigV2: expert_num, hidden_size, intermediate_size must be set")
         gn, gk = self.GROUP
-        if cfg.groupN and (cfg.groupN, cfg.groupK) != (gn, gk):
+        if self.FMT == F.FMT_INT4:
+            if cfg.groupN not in (0, 1) or (cfg.groupK and cfg.groupK not in F.INT4_GROUPS):
+                raise ValueError(f"MOE_WNA16: groupN must be 1 and groupK one of {F.INT4_GROUPS}")
+        elif cfg.groupN and (cfg.groupN, cfg.groupK) != (gn, gk):
             raise ValueError(f"{type(self).__name__}: groupN/groupK must be {gn}/{gk}")
         if cfg.int8_activation and self.FMT != F.FMT_MXFP4:
             raise ValueError("int8_activation needs MXFP4 (e8m0) weights")
         self.cfg = cfg
         opt = lambda v: None if (v is None or isinstance(v, int)) else v
-        dev = torch.device(device) if device is not None else torch.device("cuda")
+        dev = (torch.device("cpu") if self.HOST else
+               torch.device(device) if device is not None else torch.device("cuda"))
         self.weights = ExpertWeights.from_dense(self.FMT, w13_weight, opt(w13_scale), w2_weight,
                                                 opt(w2_scale), opt(w13_global_scale),
                                                 opt(w2_global_scale), device=dev)
         self._store = None
         self._cpu = []          # host engines; the last one is current (see _host_engine)
+        self._fwd = None        # host-only engine of forward_many (host-format engines)
 
     # ------------------------------------------------------------ forward
     def forward_many(self, qlen: int, top_k: int, expert_ids, weights, x, out):
@@ -181,6 +187,31 @@ class _Engine:
                                                            spitch, width, height, stream)
 
 
+class MOE_WNA16(_Engine):
+    """INT4 W4A16 (WNA16) experts: code - 8 times an fp32 scale per (row,
+    group_k k).  The reference's MOE_WNA16 is a CPU engine
+    (binding.cpp:1514; moe_v2_packed4_base.inc:1594), and so is this one: the
+    weights stay in host memory and forward_many / cpu_prefill / cpu_decode
+    run the host engine (cpu_experts.CpuExperts)."""
+    FMT = F.FMT_INT4
+    GROUP = (1, 128)
+    HOST = True
+
+    def forward_many(self, qlen: int, top_k: int, expert_ids, weights, x, out):
+        c = self.cfg
+        if self._fwd is None:
+            from .cpu_experts import CpuExperts
+            lim = c.swiglu_limit if c.activation_type == 1 else 0.0
+            self._fwd = CpuExperts.from_weights(self.weights, swiglu_limit=lim,
+                                                swiglu_alpha=c.swiglu_alpha,
+                                                swiglu_beta=c.swiglu_beta)
+        ids = expert_ids.reshape(qlen, top_k).to(torch.int32).cpu()
+        res = self._fwd.forward(x.reshape(qlen, c.hidden_size).to(torch.bfloat16).cpu(), ids,
+                                weights.reshape(qlen, top_k).float().cpu())
+        out.view(qlen, c.hidden_size).copy_(res)
+        return out
+
+
 class MOE_BF16(_Engine):
     FMT = F.FMT_BF16
     GROUP = (1, 1)
@@ -202,4 +233,4 @@ class MOE_NVFP4(_Engine):
 
 
 ENGINES = {"MOE_BF16": MOE_BF16, "MOE_FP8": MOE_FP8, "MOE_MXFP4": MOE_MXFP4,
-           "MOE_NVFP4": MOE_NVFP4}
+           "MOE_NVFP4": MOE_NVFP4, "MOE_WNA16": MOE_WNA16}

@@ -23,8 +23,14 @@ from __future__ import annotations
 
 import torch
 
-FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4 = 0, 1, 2, 3
-FMT_NAMES = {FMT_BF16: "bf16", FMT_FP8: "fp8", FMT_MXFP4: "mxfp4", FMT_NVFP4: "nvfp4"}
+FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4, FMT_INT4 = 0, 1, 2, 3, 4
+FMT_NAMES = {FMT_BF16: "bf16", FMT_FP8: "fp8", FMT_MXFP4: "mxfp4", FMT_NVFP4: "nvfp4",
+             FMT_INT4: "int4"}
+# INT4 / WNA16 (the engine's MOE_WNA16): nibble codes (low nibble = even k),
+# value = code - 8, times an fp32 scale per (row, group of INT4_GROUP k);
+# computed by the host engine
+INT4_GROUPS = (32, 64, 128)
+INT4_GROUP = 128
 
 E2M1_VALUES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
                -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0)
@@ -89,8 +95,23 @@ def quantize_fp8_block(w: torch.Tensor):
     return q.view(torch.uint8).reshape(*lead, N, K).contiguous(), s.float().contiguous()
 
 
+def quantize_int4(w: torch.Tensor, group: int = INT4_GROUP):
+    """w [..., N, K] -> (codes [..., N, K/2] u8 (value = code - 8), fp32 scales
+    [..., N, K/group]): symmetric, the group maximum at +-7 steps."""
+    *lead, N, K = w.shape
+    wb = w.float().reshape(*lead, N, K // group, group)
+    amax = wb.abs().amax(-1)
+    s = torch.where(amax > 0, amax / 7.0, torch.ones_like(amax))
+    q = torch.round(wb / s[..., None]).clamp(-8, 7).to(torch.int16) + 8
+    codes = q.to(torch.uint8).reshape(*lead, N, K)
+    return _pack_nibbles(codes).contiguous(), s.float().contiguous()
+
+
 def quantize(fmt: int, w: torch.Tensor):
     """Dense checkpoint tensors (w, s, gs) of `w` [E, N, K] in format `fmt`."""
+    if fmt == FMT_INT4:
+        c, s = quantize_int4(w)
+        return c, s, None
     if fmt == FMT_MXFP4:
         c, s = quantize_mxfp4(w)
         return c, s, None
@@ -115,9 +136,12 @@ def dequantize(fmt: int, w: torch.Tensor, s=None, gs=None) -> torch.Tensor:
         v = w.view(torch.float8_e4m3fn).float()
         E, N, K = v.shape
         return (v.reshape(E, N // 128, 128, K // 128, 128) * s[:, :, None, :, None]).reshape(E, N, K)
-    lut = torch.tensor(E2M1_VALUES, dtype=torch.float32, device=w.device)
+    vals = (tuple(float(c - 8) for c in range(16)) if fmt == FMT_INT4 else E2M1_VALUES)
+    lut = torch.tensor(vals, dtype=torch.float32, device=w.device)
     lo, hi = lut[(w & 15).long()], lut[(w >> 4).long()]
     v = torch.stack([lo, hi], -1).reshape(*w.shape[:-1], w.shape[-1] * 2)
+    if fmt == FMT_INT4:
+        return v * s.float().repeat_interleave(v.shape[-1] // s.shape[-1], -1)
     if fmt == FMT_MXFP4:
         return v * torch.exp2(s.float() - 127.0).repeat_interleave(32, -1)
     sc = e4m3_table(w.device)[s.long()] * gs[:, None, None]
@@ -126,7 +150,8 @@ def dequantize(fmt: int, w: torch.Tensor, s=None, gs=None) -> torch.Tensor:
 
 # ---------------------------------------------------------------------- packing
 def row_bytes(fmt: int, K: int) -> int:
-    return {FMT_BF16: 2 * K, FMT_FP8: K, FMT_MXFP4: K // 2, FMT_NVFP4: K // 2}[fmt]
+    return {FMT_BF16: 2 * K, FMT_FP8: K, FMT_MXFP4: K // 2, FMT_NVFP4: K // 2,
+            FMT_INT4: K // 2}[fmt]
 
 
 def pack_weight(fmt: int, w: torch.Tensor) -> torch.Tensor:
@@ -161,8 +186,10 @@ def scale_groups(fmt: int, K: int) -> int:
     return (K // 128 + ug - 1) // ug
 
 
-def scale_bytes(fmt: int, N: int, K: int) -> int:
+def scale_bytes(fmt: int, N: int, K: int, group: int = INT4_GROUP) -> int:
     """Packed scale bytes of one [N, K] matrix (per expert)."""
+    if fmt == FMT_INT4:
+        return N * (K // group) * 4
     if fmt in SCALE_GROUP:
         return N // 16 * scale_groups(fmt, K) * 1024
     if fmt == FMT_FP8:
@@ -175,6 +202,12 @@ def pack_scales(fmt: int, s, N: int, K: int):
     if s is None or fmt == FMT_BF16:
         return None
     E = s.shape[0]
+    if fmt == FMT_INT4:   # fp32 [E, N, K/group], kept in row order for the host engine
+        g = int4_group_of(s, K)
+        if s.dtype != torch.float32 or s.dim() != 3 or s.shape[1] != N:
+            raise ValueError(f"INT4 scales must be fp32 [E, {N}, {K}/group], got {s.dtype} "
+                             f"{tuple(s.shape)}")
+        return s.contiguous().reshape(E, N * (K // g))
     if fmt == FMT_FP8:
         if s.dtype != torch.float32 or tuple(s.shape[1:]) != (N // 128, K // 128):
             raise ValueError(f"FP8 block scales must be fp32 [E, {N // 128}, {K // 128}], "
@@ -197,10 +230,22 @@ def pack_scales(fmt: int, s, N: int, K: int):
     return d.contiguous().reshape(E, -1)
 
 
+def int4_group_of(s, K: int) -> int:
+    """The k per scale of INT4 scales [E, N, K/group] (32, 64 or 128)."""
+    if s.dim() != 3 or s.shape[-1] == 0 or K % s.shape[-1]:
+        raise ValueError(f"INT4 scales {tuple(s.shape)} do not split K={K} into groups")
+    g = K // s.shape[-1]
+    if g not in INT4_GROUPS:
+        raise ValueError(f"INT4 group of {g} k is not supported (groups: {INT4_GROUPS})")
+    return g
+
+
 def unpack_scales(fmt: int, p, N: int, K: int):
     if p is None or fmt == FMT_BF16:
         return None
     E = p.shape[0]
+    if fmt == FMT_INT4:
+        return p.reshape(E, N, -1)
     if fmt == FMT_FP8:
         return p.reshape(E, N // 128, K // 128)
     ug, nsb = SCALE_GROUP[fmt], K // 128
@@ -217,9 +262,9 @@ def unpack_scales(fmt: int, p, N: int, K: int):
 def algorithmic_bytes(fmt: int, N: int, K: int) -> int:
     """Bytes a weight stream of one [N, K] matrix must read: codes plus one
     scale per scaling block (no layout padding)."""
-    w = N * K * {FMT_BF16: 2.0, FMT_FP8: 1.0, FMT_MXFP4: 0.5, FMT_NVFP4: 0.5}[fmt]
+    w = N * K * {FMT_BF16: 2.0, FMT_FP8: 1.0, FMT_MXFP4: 0.5, FMT_NVFP4: 0.5, FMT_INT4: 0.5}[fmt]
     s = {FMT_BF16: 0, FMT_FP8: (N // 128) * (K // 128) * 4, FMT_MXFP4: N * K // 32,
-         FMT_NVFP4: N * K // 16 + 4}[fmt]
+         FMT_NVFP4: N * K // 16 + 4, FMT_INT4: N * (K // INT4_GROUP) * 4}[fmt]
     return int(w + s)
 
 

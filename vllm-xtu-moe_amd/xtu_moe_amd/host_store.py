@@ -34,10 +34,13 @@ WHICH = {0: "w13", 1: "w2", 2: "s13", 3: "s2", 4: "gs13", 5: "gs2"}
 class HostExpertStore:
     """Pinned host copy of a layer's experts (routed [0, E), shared after)."""
 
-    def __init__(self, fmt, H, I, E, n_shared, planes: dict, ns: int = 1, pin: bool = True):
+    def __init__(self, fmt, H, I, E, n_shared, planes: dict, ns: int = 1, pin: bool = True,
+                 group_k: int = 0):
         """pin=False keeps the shards in pageable memory (a host-only store
-        for the host engine; the DMA paths want pinned memory)."""
+        for the host engine; the DMA paths want pinned memory).  group_k:
+        INT4's k per scale."""
         self.fmt, self.H, self.I, self.E, self.n_shared = int(fmt), int(H), int(I), int(E), int(n_shared)
+        self.group_k = int(group_k)
         ns = int(ns)
         if ns < 1 or self.I % (16 * ns) or self.H % (16 * ns):
             raise ValueError(f"{ns} shards need I={I} and H={H} divisible by 16*{ns}")
@@ -78,7 +81,8 @@ class HostExpertStore:
             h = torch.empty(t.shape, dtype=t.dtype, pin_memory=pin)
             h.copy_(t, non_blocking=False)
             planes[name] = h
-        return cls(W.fmt, W.H, W.I, W.E, W.n_shared, planes, ns=ns, pin=pin)
+        return cls(W.fmt, W.H, W.I, W.E, W.n_shared, planes, ns=ns, pin=pin,
+                   group_k=getattr(W, "group_k", 0))
 
     @property
     def n_experts(self) -> int:

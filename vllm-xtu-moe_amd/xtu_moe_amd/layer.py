@@ -16,7 +16,8 @@ import os
 import torch
 
 from . import _lib
-from .formats import (FMT_BF16, FMT_FP8, FMT_MXFP4, FMT_NVFP4, pack_scales, pack_weight)
+from .formats import (FMT_BF16, FMT_FP8, FMT_INT4, FMT_MXFP4, FMT_NVFP4, INT4_GROUPS,
+                      int4_group_of, pack_scales, pack_weight)
 
 DECODE_MAX_TOKENS = 16
 DECODE_TILE = 16     # rows per work slot of the decode kernels (one MFMA M tile)
@@ -61,8 +62,12 @@ class ExpertWeights:
     """
 
     def __init__(self, fmt, H, I, E, n_shared, w13, s13, w2, s2, gs13=None, gs2=None, *,
-                 mutable=False):
+                 mutable=False, group_k=0):
         self.fmt, self.H, self.I, self.E, self.n_shared = int(fmt), int(H), int(I), int(E), int(n_shared)
+        # INT4 (WNA16): k per fp32 scale (the planes keep [N][K/group_k] per expert)
+        self.group_k = int(group_k) if self.fmt == FMT_INT4 else 0
+        if self.fmt == FMT_INT4 and self.group_k not in INT4_GROUPS:
+            raise ValueError(f"INT4 weights need group_k in {INT4_GROUPS}, got {group_k}")
         self.w13, self.s13, self.w2, self.s2, self.gs13, self.gs2 = w13, s13, w2, s2, gs13, gs2
         # mutable: the planes are restaged in place (ring / pool slots), so
         # nothing derived from them is cached
@@ -113,12 +118,17 @@ class ExpertWeights:
 
         if fmt == FMT_FP8:
             s13, s2 = _fp8_block_scales(s13), _fp8_block_scales(s2)
+        gk = 0
+        if fmt == FMT_INT4:
+            gk = int4_group_of(s13, H)
+            if int4_group_of(s2, I) != gk:
+                raise ValueError("INT4 gate/up and down scales use different groups")
         w13p = pack_weight(fmt, mv(w13))
         w2p = pack_weight(fmt, mv(w2))
         s13p = pack_scales(fmt, mv(s13), 2 * I, H)
         s2p = pack_scales(fmt, mv(s2), H, I)
         E = Et - n_shared if E is None else E
-        return cls(fmt, H, I, E, n_shared, w13p, s13p, w2p, s2p, mv(gs13), mv(gs2))
+        return cls(fmt, H, I, E, n_shared, w13p, s13p, w2p, s2p, mv(gs13), mv(gs2), group_k=gk)
 
     # ------------------------------------------------------ MXFP4 pair GEMM
     def mx_pair_scales(self, stream=None):
@@ -551,6 +561,9 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     """
     if x.dtype != torch.bfloat16 or not x.is_contiguous():
         raise ValueError("x must be contiguous bf16 [T, H]")
+    if W.fmt == FMT_INT4:
+        raise ValueError("INT4 (WNA16) experts run on the host engine (cpu_experts.CpuExperts, "
+                         "engine.MOE_WNA16), as the reference's MOE_WNA16 does")
     T, K = topk_ids.shape
     H, I, E, NS = W.H, W.I, W.E, W.n_shared
     if x.shape != (T, H):

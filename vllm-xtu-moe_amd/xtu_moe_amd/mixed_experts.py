@@ -9,11 +9,13 @@ given (topk_weights, topk_ids) (modular path) or routes from router_logits
 0), and returns [T, H] in hidden_states.dtype, written into `output` when
 given; ``apply_router_weight_on_input`` raises.  Format subclasses fix the
 scale attribute names and the scale groups (:3308-3476): BF16 1x1, MXFP4
-1x32, FP8 128x128 (and NVFP4 1x16 with per-expert global scales).
+1x32, FP8 128x128, NVFP4 1x16 with per-expert second-level scales, and INT4
+(WNA16) 1xgroup with the GPTQ / compressed-tensors repack.
 
 Here the experts run on the HIP library with the layer's weights packed once
-into the device layout; vLLM itself is not needed (an ``activation`` of
-None or a string name is accepted when vLLM's enum is absent).
+into the device layout (INT4 on the host engine, as the reference's
+MOE_WNA16); vLLM itself is not needed (an ``activation`` of None or a string
+name is accepted when vLLM's enum is absent).
 """
 from __future__ import annotations
 
@@ -73,6 +75,19 @@ class XiaotuExperts:
 
     # ---------------------------------------------------------- loading
     def process_weights_after_loading(self, layer) -> None:
+        self._read_layer_attrs(layer)
+        w13, w2 = layer.w13_weight, layer.w2_weight
+        s13 = self._find(layer, self._scale_attrs[0])
+        s2 = self._find(layer, self._scale_attrs[1])
+        g13, g2 = self._global_scales(layer)
+        dev = torch.device("cuda") if not w13.is_cuda else w13.device
+        self._weights = ExpertWeights.from_dense(self._fmt, self._weight_view(w13), s13,
+                                                 self._weight_view(w2), s2, g13, g2, device=dev)
+
+    def _global_scales(self, layer):
+        return None, None
+
+    def _read_layer_attrs(self, layer) -> None:
         self._layer_ref = layer
         for name in _ROUTING_ATTRS + _SWIGLU_ATTRS + ("top_k",):
             if hasattr(layer, name):
@@ -85,14 +100,6 @@ class XiaotuExperts:
                 if isinstance(b, torch.Tensor):
                     self.e_score_correction_bias = b
                     break
-        w13, w2 = layer.w13_weight, layer.w2_weight
-        s13 = self._find(layer, self._scale_attrs[0])
-        s2 = self._find(layer, self._scale_attrs[1])
-        g13 = self._find(layer, self._global_scale_attrs[0])
-        g2 = self._find(layer, self._global_scale_attrs[1])
-        dev = torch.device("cuda") if not w13.is_cuda else w13.device
-        self._weights = ExpertWeights.from_dense(self._fmt, self._weight_view(w13), s13,
-                                                 self._weight_view(w2), s2, g13, g2, device=dev)
 
     @staticmethod
     def _find(layer, name):
@@ -171,9 +178,9 @@ class XiaotuExperts:
                   swiglu_beta=float(self.swiglu_beta or 0.0),
                   out=output if direct else None, out_dtype=odt)
         if topk_weights is not None and topk_ids is not None:
-            res = moe_forward(x, topk_ids.to(torch.int32).contiguous(),
-                              topk_weights.to(torch.float32).contiguous(), self._weights, **kw)
-        elif (expert_map is None and self.custom_routing_function is None
+            res = self._experts(x, topk_ids.to(torch.int32).contiguous(),
+                                topk_weights.to(torch.float32).contiguous(), kw)
+        elif (self._monolithic and expert_map is None and self.custom_routing_function is None
               and router_logits is not None):
             # monolithic path: routing (+ segmentation, + the shared experts'
             # gate/up at decode sizes) inside the layer's own launches
@@ -185,8 +192,7 @@ class XiaotuExperts:
             topk_weights, topk_ids = self._select_topk(hidden_states, router_logits)
             if expert_map is not None:
                 topk_ids, topk_weights = self._local_ids(expert_map, topk_ids, topk_weights)
-            res = moe_forward(x, topk_ids.contiguous(), topk_weights.contiguous(), self._weights,
-                              **kw)
+            res = self._experts(x, topk_ids.contiguous(), topk_weights.contiguous(), kw)
         if direct:
             return output
         res = res.to(hidden_states.dtype)
@@ -194,6 +200,15 @@ class XiaotuExperts:
             output.copy_(res)
             return output
         return res
+
+    # routing, segmentation and the experts in the layer's own launches when
+    # the router logits are given (GPU formats)
+    _monolithic = True
+
+    def _experts(self, x, ids, wts, kw):
+        """The experts over routed pairs: out [T, H] (kw: swiglu_*, out,
+        out_dtype)."""
+        return moe_forward(x, ids, wts, self._weights, **kw)
 
     def _router_args(self, router_logits) -> dict:
         lg = router_logits
@@ -236,3 +251,179 @@ class XiaotuExpertsNvfp4(XiaotuExperts):
 
     def _weight_view(self, w):
         return w.data if isinstance(w, torch.nn.Parameter) else w
+
+    def _global_scales(self, layer):
+        return nvfp4_global_scales(self._find(layer, self._global_scale_attrs[0]),
+                                   self._find(layer, self._global_scale_attrs[1]),
+                                   getattr(layer, "prefix", "?"))
+
+
+def nvfp4_global_scales(g13, g2, where: str = "?"):
+    """The per-expert fp32 second-level scales (weight_scale_2) as the
+    kernels take them: one scalar per expert for gate/up and one for down.
+
+    Checkpoints give w13's as [E] or [E, 2] (gate, up); the kernels multiply
+    the gate and up results by the same scalar, so [E, 2] is taken only when
+    the two columns are equal, and refused otherwise (taking either would be a
+    silent wrong answer), as the reference's GPU path does
+    (vllm_xiaotu_moe/hybrid_model.py:1490-1520).  All-zero scales mean the
+    loader did not fill them and are refused as well (hybrid_model.py:
+    1545-1554).  The e4m3 group scale times this scalar is the reference's
+    fold (hybrid_model.py:1522-1570: fp32 e4m3(s) * scale_2, applied to the
+    e2m1 value); the kernels form the same product."""
+    if g13 is None or g2 is None:
+        raise ValueError(f"[xtu-nvfp4] {where}: weight_scale_2 planes missing")
+    g13 = g13.detach().to(torch.float32)
+    g2 = g2.detach().to(torch.float32).reshape(-1)
+    if g13.dim() == 2 and g13.shape[1] > 1:
+        ne = int((g13[:, 0] != g13[:, 1:].amax(1)).sum() + (g13[:, 0] != g13[:, 1:].amin(1)).sum())
+        if ne:
+            raise RuntimeError(
+                f"[xtu-nvfp4] {where}: gate/up weight_scale_2 differ for some experts; the "
+                "kernels take one second-level scale per expert for gate and up")
+    g13 = g13[:, 0] if g13.dim() == 2 else g13.reshape(-1)
+    if float(g13.abs().max()) == 0.0 or float(g2.abs().max()) == 0.0:
+        raise RuntimeError(f"[xtu-nvfp4] {where}: weight_scale_2 is all zero (not loaded)")
+    if g13.shape[0] != g2.shape[0]:
+        raise ValueError(f"[xtu-nvfp4] {where}: {g13.shape[0]} gate/up vs {g2.shape[0]} down "
+                         "second-level scales")
+    return g13.contiguous(), g2.contiguous()
+
+
+# ----------------------------------------------------------------- INT4 / WNA16
+def repack_gptq_int4(w, s):
+    """GPTQ / compressed-tensors INT4 to the engine layout
+    (vllm_xiaotu_moe/mixed_experts.py:3394-3418): weights int32 [E, K/8, N]
+    (eight nibbles per int32 along K, the lowest nibble the first k) become
+    uint8 [E, N, K/2] (low nibble = even k), scales [E, K/group, N] become
+    fp32 [E, N, K/group].  Weights already uint8 [E, N, K/2] pass through with
+    their scales [E, N, K/group]."""
+    w = w.data if isinstance(w, torch.nn.Parameter) else w
+    s = s.data if isinstance(s, torch.nn.Parameter) else s
+    if w.dtype == torch.int32:
+        w = w.detach().to("cpu").transpose(1, 2).contiguous().view(torch.uint8)
+        s = s.detach().to("cpu").transpose(1, 2)
+    elif w.dtype != torch.uint8:
+        raise NotImplementedError(f"INT4 experts take int32 (GPTQ / compressed-tensors) or uint8 "
+                                  f"(engine layout) weights, got {w.dtype}")
+    return w.detach().to("cpu").contiguous(), s.detach().to("cpu").to(torch.float32).contiguous()
+
+
+def require_symmetric_zero_points(layer, names) -> None:
+    """Refuse asymmetric int4: the engine's value is code - 8, which is
+    symmetric quantisation (effective zero point 8).  GPTQ packs zero points
+    minus one in int32 (so a symmetric checkpoint holds 7s); compressed-tensors
+    may hold 8 directly; either is accepted (mixed_experts.py:3420-3452)."""
+    for name in names:
+        qz = getattr(layer, name, None)
+        if qz is None:
+            continue
+        b = (qz.data if isinstance(qz, torch.nn.Parameter) else qz).detach().to("cpu").contiguous()
+        packed = b.dtype in (torch.int32, torch.int16)
+        u8 = b.view(torch.uint8) if b.dtype != torch.uint8 else b
+        nib = torch.cat(((u8 & 15).reshape(-1), (u8 >> 4).reshape(-1))).to(torch.int16)
+        if packed:
+            nib = nib + 1
+        vals = torch.unique(nib)
+        if not bool(torch.all((vals == 7) | (vals == 8))):
+            raise NotImplementedError(
+                f"INT4 experts implement symmetric quantisation only (zero point 8); {name} "
+                f"holds zero points {sorted(int(v) for v in vals.tolist())[:8]}")
+
+
+class XiaotuExpertsInt4(XiaotuExperts):
+    """INT4 W4A16 group-quantised experts (WNA16): the reference's
+    XiaotuCPUExpertsInt4 / MOE_WNA16 (vllm_xiaotu_moe/mixed_experts.py:
+    3363-3476).  The checkpoint is repacked once at load (GPTQ /
+    compressed-tensors int32 -> engine bytes, scales transposed), symmetric
+    zero points and sequential K order (no desc_act) are required, and the
+    experts run where the reference runs them, on the host engine: through
+    the graph-capturable cpu_decode bridge for device tensors (batches up to
+    the pre-sized staging, XTU_CD_PREALLOC_TOKENS, default 512), synchronously
+    beyond it, directly for host tensors."""
+
+    _fmt = F.FMT_INT4
+    _scale_attrs = (("w13_scales", "w13_weight_scale"), ("w2_scales", "w2_weight_scale"))
+    _w_names = (("w13_qweight", "w13_weight_packed", "w13_weight"),
+                ("w2_qweight", "w2_weight_packed", "w2_weight"))
+    _z_names = ("w13_qzeros", "w13_weight_zero_point", "w2_qzeros", "w2_weight_zero_point")
+    _group_n, _group_k = 1, 128
+    _monolithic = False
+
+    def __init__(self, moe_config=None, quant_config=None):
+        super().__init__(moe_config, quant_config)
+        self._host = None
+
+    @classmethod
+    def _find_any(cls, layer, names):
+        for n in names:
+            t = cls._find(layer, n)
+            if t is not None:
+                return t
+        return None
+
+    def process_weights_after_loading(self, layer) -> None:
+        from .cpu_experts import CpuExperts
+        from .host_store import HostExpertStore
+        import os
+        self._read_layer_attrs(layer)
+        w13 = self._find_any(layer, self._w_names[0])
+        w2 = self._find_any(layer, self._w_names[1])
+        if w13 is None or w2 is None:
+            raise NotImplementedError("INT4 experts found no int4 weight tensors on the layer "
+                                      f"(looked for {self._w_names[0]} / {self._w_names[1]})")
+        if bool(getattr(self.quant_config, "desc_act", False)):
+            raise NotImplementedError("INT4 experts assume sequential K order (GPTQ desc_act / "
+                                      "g_idx reordering is not supported)")
+        group = int(getattr(self.quant_config, "group_size", 0) or 0) or 128
+        if w13.dtype == torch.int32:
+            require_symmetric_zero_points(layer, self._z_names)
+        s13 = self._find_any(layer, self._scale_attrs[0])
+        s2 = self._find_any(layer, self._scale_attrs[1])
+        if s13 is None or s2 is None:
+            raise NotImplementedError("INT4 experts found no group scales on the layer")
+        w13, s13 = repack_gptq_int4(w13, s13)
+        w2, s2 = repack_gptq_int4(w2, s2)
+        ok = (w13.dim() == 3 and w2.dim() == 3 and w13.shape[2] * 2 == w2.shape[1]
+              and w2.shape[2] * 2 == w13.shape[1] // 2)
+        if not ok:
+            raise NotImplementedError(
+                f"INT4 experts cannot take w13 {tuple(w13.shape)} / w2 {tuple(w2.shape)}: "
+                "expected the byte-packed [E, 2I, H/2] / [E, H, I/2] layout (AWQ's N-packed "
+                "layout is not supported)")
+        H, I = int(w2.shape[1]), int(w13.shape[1]) // 2
+        if s13.shape[-1] * group != H or s2.shape[-1] * group != I:
+            raise ValueError(f"INT4 scales {tuple(s13.shape)} / {tuple(s2.shape)} do not match "
+                             f"group_size {group} for H={H}, I={I}")
+        self._weights = ExpertWeights.from_dense(F.FMT_INT4, w13, s13, w2, s2, device="cpu")
+        gpu = torch.cuda.is_available()
+        store = HostExpertStore.from_weights(self._weights, pin=gpu)
+        pre = int(os.environ.get("XTU_CD_PREALLOC_TOKENS", "512") or 512) if gpu else 0
+        self._host = CpuExperts.from_store(
+            store, swiglu_limit=float(self.swiglu_limit or 0.0),
+            swiglu_alpha=float(self.swiglu_alpha if self.swiglu_alpha is not None else 1.0),
+            swiglu_beta=float(self.swiglu_beta or 0.0), max_tokens=pre,
+            max_topk=max(int(self.top_k or 1), 1))
+        self._store = store
+
+    def _experts(self, x, ids, wts, kw):
+        eng = self._host
+        T, K = ids.shape
+        odt, out = kw.get("out_dtype", torch.float32), kw.get("out")
+        if not x.is_cuda:
+            res = eng.forward(x, ids.cpu(), wts.cpu())
+        elif T <= eng.max_tokens and K <= eng.max_topk:
+            res = _scratch("int4_out", (T, eng.H), torch.float32, x.device)
+            rc = eng.cpu_decode(torch.cuda.current_stream(x.device).cuda_stream, T, K, x,
+                                ids.to(torch.int32).contiguous(),
+                                wts.to(torch.float32).contiguous(), res)
+            if rc:
+                raise RuntimeError(f"INT4 host engine refused the batch (cpu_decode {rc})")
+        else:   # beyond the staging: a synchronous host forward (not capturable)
+            torch.cuda.current_stream(x.device).synchronize()
+            res = eng.forward(x.cpu(), ids.cpu(), wts.cpu()).to(x.device)
+        if out is not None:
+            out.copy_(res)
+            return out
+        # the device result sits in a reused buffer: hand out a copy
+        return res.to(odt, copy=True) if x.is_cuda else res.to(odt)
