@@ -143,6 +143,7 @@ def bench_one(args):
     from xtu_moe_amd import formats as F
     from xtu_moe_amd.layer import (_fp8pair_bufs, _mxpair_bufs, _p, _stream, gemm_tile_m,
                                    int8_align_on, moe_forward, mx_pair_kernel, pair_gemm, route,
+                                   fp8_pair32_use,
                                    segmentation)
     from xtu_moe_amd.synthetic import synth_layer
 
@@ -320,7 +321,8 @@ def bench_one(args):
         # ---- dominant kernel alone (gate/up), cold cache, same stream
         seg = None
         gu_ms = []
-        bm = gemm_tile_m(fmt, i8, H, I)
+        bm = gemm_tile_m(fmt, i8, H, I, W)
+        f8q = not (T <= 16 and not i8) and not i8 and fp8_pair32_use(W)
         decode = T <= 16 and not i8
         act = torch.empty((T * K + T * NS, I), dtype=torch.bfloat16, device=dev)
         for s in range(args.steps):
@@ -328,8 +330,11 @@ def bench_one(args):
             w_, i_ = route(lg_st, **rkw)
             seg = segmentation(T, K, E, NS, bm, dev).run(i_, w_)
             st = _stream()
-            fp8x = mxx = None
-            if not decode and not i8 and mx_pair_kernel(fmt, H, I):
+            fp8x = mxx = f8x = None
+            if f8q:
+                f8x = _mxpair_bufs("xm", T, H, dev)
+                _lib.call("xtu_pair_quant_il", _p(x_st), T, H, *[_p(t) for t in f8x], st)
+            elif not decode and not i8 and mx_pair_kernel(fmt, H, I):
                 mxx = _mxpair_bufs("xm", T, H, dev)
                 s13p, _ = W.mx_pair_scales()
                 _lib.call("xtu_pair_quant_il", _p(x_st), T, H, *[_p(t) for t in mxx], st)
@@ -356,6 +361,12 @@ def bench_one(args):
                           _p(w13_8), _p(emin13), 0, _p(seg.seg_start), _p(seg.tile_expert),
                           _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), 0, cfg["limit"],
                           1.0, 0.0, st)
+            elif f8x is not None:
+                lo, hi = seg.tile_range_ptrs(0, E + NS)
+                _lib.call("xtu_f8_pair_gate_up", *[_p(t) for t in f8x], _p(seg.sorted_tok), H, I,
+                          _p(W.w13), _p(W.s13), 0, 0, 0, _p(seg.seg_start), _p(seg.tile_expert),
+                          _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi, seg.max_tiles,
+                          _p(act), cfg["limit"], 1.0, 0.0, st)
             elif mxx is not None:
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
                 _lib.call("xtu_mx_pair_gate_up", *[_p(t) for t in mxx], _p(seg.sorted_tok), H, I,
@@ -440,6 +451,7 @@ def bench_one(args):
         roof = dict(bound="mfma", achieved=ach, peak=PEAK_TFLOPS["fp8"], unit="TFLOP/s",
                     frac=ach / PEAK_TFLOPS["fp8"], traffic=None,
                     kernel=("mx_pair_gemm_kernel" if mx_pair_kernel(fmt, H, I)
+                            else "f8_pair_gemm_kernel" if fp8_pair32_use(W)
                             else "gemm8_kernel"),
                     mfma_issue_frac=2.0 * ach / PEAK_TFLOPS["fp8"],
                     frac_of_bf16_peak=ach / PEAK_TFLOPS["bf16"])

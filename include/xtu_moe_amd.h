@@ -397,6 +397,31 @@ hipError_t xtu_copy_experts(int n, const int32_t* experts, const void* src, long
 hipError_t xtu_copy_2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width,
                        size_t height, hipStream_t stream);
 
+/* FP8 prefill on v_mfma_scale_f32_32x32x64_f8f6f4, both operands staged in
+ * LDS by direct loads (replaces gate_up_kernel_fp8 / down_kernel_fp8,
+ * vllm_xiaotu_moe/gpu_prefill_fp8.py:101-205).  Activation pairs
+ * interleaved (xtu_pair_quant_il); weights FP8 P16 with fp32 block scales
+ * [N/128][K/128] per expert, every one finite and positive with max/min at
+ * most 2^32 (the caller checks; the block scale is applied by rescaling the
+ * accumulators by s(kb-1)/s(kb) at each 128-k block and by the last scale
+ * at the end).  M tiles of xtu_f8_pair_tile_m()
+ * rows; shapes where xtu_f8_pair_fits(H, I). */
+int xtu_f8_pair_fits(int H, int I);
+int xtu_f8_pair_tile_m(void);
+hipError_t xtu_f8_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const int32_t* sorted_tok,
+                               int H, int I, const void* w13, const float* s13, long w_estride,
+                               long s_estride, const int32_t* slot_map, const int32_t* seg_start,
+                               const int32_t* tile_expert, const int32_t* tile_row0,
+                               const int32_t* expert_tile_start, const int32_t* tile_lo,
+                               const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                               float alpha, float beta, hipStream_t stream);
+hipError_t xtu_f8_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int I, const void* w2,
+                            const float* s2, long w_estride, long s_estride,
+                            const int32_t* slot_map, const int32_t* seg_start,
+                            const int32_t* tile_expert, const int32_t* tile_row0,
+                            const int32_t* expert_tile_start, const int32_t* tile_lo,
+                            const int32_t* tile_hi, int max_tiles, void* y, hipStream_t stream);
+
 /* ------------------------------------------------ reference-signature small-M ABI
  * The reference's native moe4_smallm_* entry points (xiaotu_moe/csrc/
  * moe4_smallm.cu:346-430), same names, arguments and meaning, over the

@@ -81,6 +81,12 @@ def test_library_loads_and_reports_version():
     assert lib.xtu_mx_pair_fits(7168, 2048) == 1 and lib.xtu_mx_pair_fits(2048, 768) == 1
     assert lib.xtu_mx_pair_fits(2880, 2880) == 0 and lib.xtu_mx_pair_fits(7168, 2176) == 0
     assert lib.xtu_mx_pair_fits(32768, 2048) == 0   # activation scales of 128 rows exceed LDS
+    # FP8 32x32x64 kernel: 128 rows; H in 256-column down blocks, I in 128-row
+    # scale blocks, activation scales of 128 rows in LDS
+    assert lib.xtu_f8_pair_tile_m() == 128
+    assert lib.xtu_f8_pair_fits(7168, 2048) == 1 and lib.xtu_f8_pair_fits(2048, 768) == 1
+    assert lib.xtu_f8_pair_fits(2880, 2880) == 0 and lib.xtu_f8_pair_fits(7168, 2112) == 0
+    assert lib.xtu_f8_pair_fits(32768, 2048) == 0
 
 
 PROBE_HEADER = os.path.join(os.path.dirname(os.path.abspath(__file__)), "probes", "xtu_probes.h")

@@ -38,12 +38,18 @@ CXX = os.environ.get("CXX", "g++")
 CXXFLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-pthread", "-fvisibility=hidden"]
 
 
+# per-file device flags: the FP8 pair kernel rescales its accumulators with
+# VALU multiplies, so its MFMA results live in VGPRs (no AGPR round trips)
+EXTRA = {"f8pair32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
     if src.endswith(".cpp"):
         cmd = [CXX, *CXXFLAGS, "-I", CSRC, "-c", src, "-o", obj]
     else:
-        cmd = [HIPCC, *CFLAGS, "-I", CSRC, "-c", src, "-o", obj]
+        cmd = [HIPCC, *CFLAGS, *EXTRA.get(os.path.basename(src), []), "-I", CSRC, "-c", src,
+               "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # the host pass does not know the device-only target feature; that note is harmless
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)

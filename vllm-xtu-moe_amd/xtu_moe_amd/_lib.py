@@ -78,6 +78,12 @@ SIGNATURES = {
                                  _i, _vp, _vp, _f, _f, _f, _vp]),
     "xtu_i8_gemm_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                               _vp, _vp]),
+    "xtu_f8_pair_fits": (_i, [_i, _i]),
+    "xtu_f8_pair_tile_m": (_i, []),
+    "xtu_f8_pair_gate_up": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
+                                 _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
+    "xtu_f8_pair_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _vp, _i, _vp, _vp]),
     "moe4_smallm_init": (_i, []),
     "moe4_smallm_gu": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "moe4_smallm_dn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
@@ -98,7 +104,8 @@ SIGNATURES = {
 _NOT_STATUS = {"xtu_version", "xtu_error_string", "xtu_segment_workspace_bytes",
                "xtu_route_segment_small_max_pairs",
                "xtu_segment_max_tiles", "xtu_gemm_tile_m", "xtu_gemm8_tile_m",
-               "xtu_mx_pair_fits", "xtu_mx_pair_tile_m",
+               "xtu_mx_pair_fits", "xtu_mx_pair_tile_m", "xtu_f8_pair_fits",
+               "xtu_f8_pair_tile_m",
                "xtu_decode_down_combine_ok", "xtu_decode_route_shared_ok",
                "xtu_i8_weight_bytes"}
 

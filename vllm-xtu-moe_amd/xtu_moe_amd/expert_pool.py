@@ -220,6 +220,7 @@ class LayerPool:
         W = ExpertWeights(self.engine.fmt, self.H, self.I, E, self.n_shared, self.planes.w13,
                           self.planes.s13, self.planes.w2, self.planes.s2, self.planes.gs13,
                           self.planes.gs2, mutable=True)
+        kw.setdefault("fp8_scales_ok", self.engine.fp8_scales_bounded())
         return moe_forward(x, topk_ids, topk_weights, W, id_map=id_map, slot_map=slot_map, **kw)
 
     # ------------------------------------------------------------- swaps

@@ -22,7 +22,7 @@ import torch
 
 from . import _lib
 from . import formats as F
-from .layer import ExpertWeights, _p, _stream
+from .layer import ExpertWeights, _p, _stream, fp8_block_scales_bounded
 
 PLANES = ("w13", "s13", "w2", "s2", "gs13", "gs2")
 # the reference's plane numbering for copy_hostbuf_to_device(which, ...);
@@ -87,6 +87,16 @@ class HostExpertStore:
     @property
     def n_experts(self) -> int:
         return self.E + self.n_shared
+
+    def fp8_scales_bounded(self) -> bool:
+        """FP8: fp8_block_scales_bounded over every expert's scales, read from
+        the host copy once (device slot planes filled from this store hold
+        these scales, so their kernel choice follows this answer)."""
+        if self.fmt != F.FMT_FP8:
+            return False
+        if getattr(self, "_fp8_pos", None) is None:
+            self._fp8_pos = fp8_block_scales_bounded(self.planes["s13"], self.planes["s2"])
+        return self._fp8_pos
 
     def row_bytes(self, name) -> int:
         """Bytes of one expert in plane `name`."""

@@ -11,6 +11,7 @@ shape for the life of the process (as the reference does with its
 """
 from __future__ import annotations
 
+import math
 import os
 
 import torch
@@ -75,6 +76,7 @@ class ExpertWeights:
         self._i8 = None
         self._i8_fb = None
         self._mxs = None
+        self._fp8_pos = None
         if self.H % 256 or self.I % 128:
             raise ValueError(f"unsupported shape H={H} I={I} (need H % 256 == 0, I % 128 == 0)")
         rows = {t.shape[0] for t in (w13, s13, w2, s2, gs13, gs2) if t is not None}
@@ -153,6 +155,18 @@ class ExpertWeights:
             return tuple(out)
         self._mxs = tuple(out)
         return self._mxs
+
+    # ---------------------------------------------------------------- FP8
+    def fp8_scales_bounded(self) -> bool:
+        """fp8_block_scales_bounded over this layer's scales (checked once;
+        inside a graph capture an unchecked set counts as unbounded, so the
+        capture takes the kernel without ratios)."""
+        if self._fp8_pos is not None:
+            return self._fp8_pos
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            return False
+        self._fp8_pos = fp8_block_scales_bounded(self.s13, self.s2)
+        return self._fp8_pos
 
     # ---------------------------------------------------------------- INT8
     def int8_planes(self):
@@ -424,6 +438,43 @@ def decode_max_tiles(A: int, max_active: int) -> int:
 
 
 MXFP4_PREFILL_ENV = "XTU_MXFP4_PREFILL"
+FP8_PREFILL_ENV = "XTU_FP8_PREFILL"
+
+
+FP8_RATIO_MAX = 2.0 ** 32
+
+
+def fp8_block_scales_bounded(*scales) -> bool:
+    """Every FP8 block scale finite and positive, and the largest at most
+    2^32 times the smallest: the 32x32x64 kernel carries its accumulators in
+    units of the current block's scale and rescales them by s(kb-1)/s(kb) at
+    each block boundary, which this bound keeps far from fp32 overflow."""
+    lo, hi = math.inf, 0.0
+    for s in scales:
+        s = s.float()
+        if not bool(torch.isfinite(s).all()):
+            return False
+        lo, hi = min(lo, float(s.min())), max(hi, float(s.max()))
+    return lo > 0 and hi <= lo * FP8_RATIO_MAX
+
+
+def fp8_pair32_use(W, scales_ok=None) -> bool:
+    """Whether an FP8 layer's prefill GEMMs run on the 32x32x64 kernel with
+    LDS-staged operands (xtu_f8_pair_*): XTU_FP8_PREFILL "auto" (default) or
+    "pair32", the shape fits and the block scales are bounded
+    (fp8_block_scales_bounded; the kernel rescales by their ratios), checked
+    once on immutable weights and stated by the caller for slot planes (pool,
+    ring: `scales_ok`, from the host store's copy); else the 16x16x128 kernel
+    (xtu_gemm8_*, "v1")."""
+    if W is None or W.fmt != FMT_FP8:
+        return False
+    if os.environ.get(FP8_PREFILL_ENV, "auto") == "v1":
+        return False
+    if not bool(_lib.call("xtu_f8_pair_fits", int(W.H), int(W.I))):
+        return False
+    if W.mutable:
+        return bool(scales_ok)
+    return W.fp8_scales_bounded()
 
 
 # "auto": the exact-pair GEMMs where the 32x32x64 MXFP4 kernel takes the shape
@@ -459,12 +510,16 @@ def mx_pair_kernel(fmt: int, H: int, I: int) -> bool:
     return int(fmt) == FMT_MXFP4 and pair_gemm(fmt, H, I) and _mx_fits(H, I)
 
 
-def gemm_tile_m(fmt: int, int8: bool = False, H: int = 0, I: int = 0) -> int:
+def gemm_tile_m(fmt: int, int8: bool = False, H: int = 0, I: int = 0, W=None,
+                fp8_scales_ok=None) -> int:
     """Rows per M tile of the grouped GEMM that runs for this format and
-    layer shape: INT8 ALIGN 128, the exact-pair kernels (FP8, MXFP4) theirs,
-    else the bf16-operand kernels' (the segmentation's tiles must match)."""
+    layer shape (and weights W, when given): INT8 ALIGN 128, the exact-pair
+    kernels (FP8, MXFP4) theirs, else the bf16-operand kernels' (the
+    segmentation's tiles must match)."""
     if int8:
         return 128
+    if fp8_pair32_use(W, fp8_scales_ok):
+        return int(_lib.call("xtu_f8_pair_tile_m"))
     if pair_gemm(fmt, H, I):
         if mx_pair_kernel(fmt, H, I):
             return int(_lib.call("xtu_mx_pair_tile_m"))
@@ -547,7 +602,7 @@ def _fp8pair_bufs(tag, M, K, dev, stream=None):
 def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0, swiglu_alpha=1.0,
                 swiglu_beta=0.0, out=None, out_dtype=torch.bfloat16, path="auto", int8=False,
                 drop_zero=True, id_map=None, slot_map=None, stream=None, return_seg=False,
-                router=None):
+                router=None, fp8_scales_ok=None):
     """Routed (+shared) experts of one layer; returns out [T, H].
 
     path: "auto" (decode kernels for T <= 16, grouped GEMMs otherwise),
@@ -558,6 +613,8 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     [E+NS] bucket -> weight slot.  router: dict(logits=, scoring=, bias=,
     n_group=, topk_group=, routed_scaling_factor=, renormalize=) routes from
     logits first, writing topk_ids / topk_weights (int32 / fp32 buffers).
+    fp8_scales_ok: for FP8 slot planes, whether their block scales are
+    bounded (fp8_block_scales_bounded).
     """
     if x.dtype != torch.bfloat16 or not x.is_contiguous():
         raise ValueError("x must be contiguous bf16 [T, H]")
@@ -593,7 +650,7 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         raise ValueError(f"decode path handles at most {DECODE_MAX_TOKENS} tokens")
     # decode: the gate/up and down kernels take the segmentation's 16-row
     # tiles as work slots (every row of a bucket, however many)
-    bm = DECODE_TILE if path == "decode" else gemm_tile_m(fmt, int8, W.H, W.I)
+    bm = DECODE_TILE if path == "decode" else gemm_tile_m(fmt, int8, W.H, W.I, W, fp8_scales_ok)
     seg = segmentation(T, K, E, NS, bm, dev, st)
     odt = out_dtype if out is None else out.dtype
     max_active = min(E, T * K) + NS
@@ -675,16 +732,18 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
         y = _buf("y", (max(A, 1), H), torch.float32, dev, st)
         expert_pass(x, seg, W, 0, E + NS, y, slot_map=slot_map, int8=int8,
                     swiglu_limit=swiglu_limit, swiglu_alpha=swiglu_alpha,
-                    swiglu_beta=swiglu_beta, stream=st)
+                    swiglu_beta=swiglu_beta, stream=st, fp8_scales_ok=fp8_scales_ok)
     combine(seg, y, wts, out, stream=st)
     return (out, seg) if return_seg else out
 
 
 def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None, int8=False,
-                swiglu_limit=0.0, swiglu_alpha=1.0, swiglu_beta=0.0, stream=None):
+                swiglu_limit=0.0, swiglu_alpha=1.0, swiglu_beta=0.0, stream=None,
+                fp8_scales_ok=None):
     """Grouped gate/up (+ SwiGLU-clamp) and down GEMMs for the sorted pairs of
     buckets [b0, b1), weights of bucket b at slot slot_map[b] of W (identity
-    without a map); writes their fp32 rows of y [A, H]."""
+    without a map); writes their fp32 rows of y [A, H].  The segmentation's
+    tile height must be gemm_tile_m(..., W, fp8_scales_ok)'s."""
     T, H = x.shape
     I = W.I
     A = seg.A
@@ -721,6 +780,21 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
                       seg.max_tiles, seg.bm, _p(fb[2]), _p(fb[3]), _p(y), 0.0, 1.0, 0.0, st)
         return
     fmt = W.fmt
+    if fp8_pair32_use(W, fp8_scales_ok):
+        # exact pairs, interleaved, on the FP8 32x32x64 kernel (block scales
+        # applied by accumulator rescaling)
+        xq = _mxpair_bufs("xm", T, H, dev, st)
+        aq = _mxpair_bufs("am", A, I, dev, st)
+        _lib.call("xtu_pair_quant_il", _p(x), T, H, *[_p(t) for t in xq], st)
+        _lib.call("xtu_f8_pair_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
+                  _p(W.w13), _p(W.s13), 0, 0, _p(slot_map), _p(seg.seg_start),
+                  _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi,
+                  seg.max_tiles, _p(act), lim, al, be, st)
+        _lib.call("xtu_pair_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
+        _lib.call("xtu_f8_pair_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(W.s2), 0, 0,
+                  _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
+                  _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
+        return
     if mx_pair_kernel(fmt, H, I):
         # exact pairs, interleaved, on the MXFP4 32x32x64 kernel
         s13p, s2p = W.mx_pair_scales(st)

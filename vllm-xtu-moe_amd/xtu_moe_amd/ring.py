@@ -177,12 +177,13 @@ def gpu_moe_layer_from_engine_tiled(engine, x, topk_ids, topk_weights, H: int, I
     for b, e in enumerate(streamed + res_list):
         id_map_h[e] = b
     id_map = id_map_h.to(device, non_blocking=True)
-    bm = gemm_tile_m(fmt, False, H, I)
+    te = int(tile_e) if tile_e else staging_tile_experts(E)
+    ring = _ring_for(engine, te, nslots, device)
+    f8ok = engine.fp8_scales_bounded()   # slot planes hold the store's scales
+    bm = gemm_tile_m(fmt, False, H, I, ring.slots[0], f8ok)
     seg = segmentation(T, K, E, NS, bm, device, st)
     seg.run(ids, wts, id_map, True, st)
     y = _buf("ring_y", (max(seg.A, 1), H), torch.float32, device, st)
-    te = int(tile_e) if tile_e else staging_tile_experts(E)
-    ring = _ring_for(engine, te, nslots, device)
     ntile = (len(streamed) + te - 1) // te
     ring_map = ring.slot_map(E + NS)
     moved = 0
@@ -206,7 +207,7 @@ def gpu_moe_layer_from_engine_tiled(engine, x, topk_ids, topk_weights, H: int, I
     ring.side.wait_stream(st)   # ids / routing are ready before the first copy
     for t in range(min(ntile, ring.nslots)):
         issue(t)
-    kw = dict(swiglu_limit=swiglu_limit, stream=st)
+    kw = dict(swiglu_limit=swiglu_limit, stream=st, fp8_scales_ok=f8ok)
     # resident and shared experts first, from the pool's planes: they need no
     # copy, so their GEMMs run while the first tiles are in flight
     if res_list or NS:
