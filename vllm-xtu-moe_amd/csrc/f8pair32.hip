@@ -1,6 +1,7 @@
 // Exact-pair grouped GEMMs for FP8 weights (e4m3 codes, fp32 128 x 128 block
 // scales) on v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 x e4m3), both operands
-// staged through LDS by direct-to-LDS loads, three stages deep.
+// staged through LDS by direct-to-LDS loads, four stages deep (three where
+// LDS does not hold four).
 //
 // Activations: the interleaved e4m3 pairs of xtu_pair_quant_il (row r is
 // [K/64][hi 64 B | lo 64 B], e8m0 bytes [rows][K/32]), as for MXFP4.
@@ -32,9 +33,10 @@
 // 2 + h of its P16 super-block; the e8m0 scale of an A lane applies to its
 // row and the 32-k block h.
 //
-// Pipeline (as the MXFP4 kernel): step s issues the loads of step s + 2
-// between the first half of its MFMAs, waits for step s + 1 and meets the
-// barrier, then reads the fragments of step s + 1 between the second half.
+// Pipeline: step s issues the loads of step s + STAGES - 1 between the first
+// half of its MFMAs, waits for step s + 1 and meets the barrier, then reads
+// the fragments of step s + 1 between the second half.  A step is 16 MFMAs
+// per wave (half the MXFP4 kernel's), so the loads need the deeper lead.
 #include <type_traits>
 
 #include "pairgemm.hpp"
@@ -47,17 +49,15 @@ typedef int i32x8_t __attribute__((ext_vector_type(8)));
 constexpr int kQM = 128;            // rows per m tile
 constexpr int kQN = 256;            // weight rows per work item
 constexpr int kQThreads = 256;
-constexpr int kQStages = 3;
 constexpr int kQLA = kQM * 128;     // A codes [row][8 pieces of 16 B]
 constexpr int kQLB = kQN * 64;      // B codes: 16 panels x 1 KiB
 constexpr int kQStage = kQLA + kQLB;
-constexpr int kQStagesBytes = kQStages * kQStage;
 constexpr int kQLdsMax = 160 * 1024;
 constexpr int kQLoads = 8;          // loads per lane and step (A 4, B 4)
 
 // stages | activation scales | source rows | ratios [2][K/128] + finals [2]
-__host__ __device__ constexpr int q_lds_bytes(int K) {
-  return kQStagesBytes + asc_bytes(K, kQM) + 4 * kQM + 4 * (2 * (K / 128) + 2);
+__host__ __device__ constexpr int q_lds_bytes(int stages, int K) {
+  return stages * kQStage + asc_bytes(K, kQM) + 4 * kQM + 4 * (2 * (K / 128) + 2);
 }
 
 struct F8PairArgs {
@@ -79,8 +79,9 @@ struct F8PairArgs {
   float limit, alpha, beta;
 };
 
-template <bool GU>
+template <bool GU, int STAGES>
 __global__ __launch_bounds__(kQThreads, 1) void f8_pair_gemm_kernel(F8PairArgs a) {
+  constexpr int LEAD = STAGES - 1;   // steps of loads in flight ahead of the MFMAs
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
   // ---- work item
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(kQThreads, 1) void f8_pair_gemm_kernel(F8PairArgs a
   const int lane = tid % 64;
   const int wm = w & 1, wn = w >> 1;
   const int ascs = asc_stride(K);
-  uint8_t* asc = lds + kQStagesBytes;
+  uint8_t* asc = lds + STAGES * kQStage;
   int32_t* srow = reinterpret_cast<int32_t*>(asc + asc_bytes(K, kQM));
   float* ratio = reinterpret_cast<float*>(srow + kQM);   // [2][nkb], then finals [2]
 
@@ -245,13 +246,17 @@ __global__ __launch_bounds__(kQThreads, 1) void f8_pair_gemm_kernel(F8PairArgs a
     }
   };
 
-  // ---- pipeline (nsteps = K / 64 is even and >= 4)
-  issue_one(0, 0, 0);
+  // ---- pipeline: the loads of step s + LEAD are issued during step s
+  // (nsteps = K / 64 is even and >= 2)
 #pragma unroll
-  for (int d = 1; d < kQLoads; ++d) issue_one(0, 0, d);
+  for (int p = 0; p < LEAD; ++p) {
+    if (p < nsteps) {
 #pragma unroll
-  for (int d = 0; d < kQLoads; ++d) issue_one(1, 1, d);
-  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kQLoads));   // scales, step 0 landed
+      for (int d = 0; d < kQLoads; ++d) issue_one(p, p, d);
+    }
+  }
+  if (nsteps >= LEAD) __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0((LEAD - 1) * kQLoads));
+  else __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));   // scales, step 0 landed
   __syncthreads();
   auto run = [&](auto live_c) {
     constexpr int LIVE = decltype(live_c)::value;
@@ -261,91 +266,95 @@ __global__ __launch_bounds__(kQThreads, 1) void f8_pair_gemm_kernel(F8PairArgs a
     // and with two blocks A row block 1 (6, 7) and its scale (9)
     auto read_k = [&](int n) { return LIVE == 2 ? n : (n < 6 ? n : 8); };
     constexpr int kR = LIVE == 2 ? kReads : 7;
-    // Two row blocks: the rescale of a 32 x 32 block is spread over the MFMAs
-    // of the other row block (the multiplies issue while they run): row
-    // block 0's at the second half of the odd step before a block start
-    // (after its last MFMA of the step), row block 1's at the first half of
-    // the even step (before its first).  Step 0 multiplies by ratio 1.  One
+    // Step s: the MFMAs of step s (fragments in cur); ISSUE: the loads of
+    // step s + LEAD between the first half; NEXT: wait for step s + 1, the
+    // barrier, and its fragments (into nxt) between the second half.
+    // Rescaling with two row blocks: a 32 x 32 block's multiplies follow an
+    // MFMA of the other row block (they issue while it runs): row block 0's
+    // at the second half of an odd step before a block start (after its last
+    // MFMA of block kb - 1), row block 1's at the first half of the even step
+    // (before its first MFMA of block kb; step 0 multiplies by ratio 1).  One
     // row block: all of it at the even step's start.
-    auto step = [&](auto odd_c, int s, Frags& cur, Frags& nxt) {
+    auto step = [&](auto odd_c, auto issue_c, auto next_c, int s, Frags& cur, Frags& nxt) {
       constexpr bool ODD = decltype(odd_c)::value;
+      constexpr bool ISSUE = decltype(issue_c)::value;
+      constexpr bool NEXT = decltype(next_c)::value;
+      constexpr bool RS0 = LIVE == 2 && ODD && NEXT;   // row block 0, ratio (s + 1) / 2
+      constexpr bool RS1 = LIVE == 2 && !ODD;          // row block 1, ratio s / 2
       float rr[4];
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (LIVE == 1 && !ODD) {
         if (s > 0) rescale_all(1, s / 2);
       }
-      if constexpr (LIVE == 2) {
+      if constexpr (RS0 || RS1) {
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) rr[cb] = ratio_of(cb, ODD ? (s + 1) / 2 : s / 2);
       }
       __builtin_amdgcn_sched_barrier(0);
+      const int sn = s + LEAD, stn = sn % STAGES;
       int d = 0;
 #pragma unroll
       for (int j = 0; j < H2; ++j) {
         mfma_j(cur, j);
-        if constexpr (LIVE == 2 && !ODD) {
+        if constexpr (RS1) {
           if (j < 4) rescale_one(1, j, rr[j]);
         }
-        if (d < kQLoads) issue_one(s + 2, (s + 2) % kQStages, d++);
-        if (LIVE == 1 && d < kQLoads) issue_one(s + 2, (s + 2) % kQStages, d++);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (; d < kQLoads; ++d) issue_one(s + 2, (s + 2) % kQStages, d);
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kQLoads));   // step s + 1 landed
-      __syncthreads();
-      __builtin_amdgcn_sched_barrier(0);
-      const uint8_t* buf = lds + ((s + 1) % kQStages) * kQStage;
-      int n = 0;
-#pragma unroll
-      for (int j = H2; j < M; ++j) {
-        if (n < kR) read_one(buf, s + 1, nxt, read_k(n++));
-        if (n < kR) read_one(buf, s + 1, nxt, read_k(n++));
-        mfma_j(cur, j);
-        if constexpr (LIVE == 2 && ODD) {
-          if (j - H2 < 4) rescale_one(0, j - H2, rr[j - H2]);
+        if constexpr (ISSUE) {
+          if (d < kQLoads) issue_one(sn, stn, d++);
+          if (LIVE == 1 && d < kQLoads) issue_one(sn, stn, d++);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      if constexpr (ISSUE) {
 #pragma unroll
-      for (; n < kR; ++n) read_one(buf, s + 1, nxt, read_k(n));
+        for (; d < kQLoads; ++d) issue_one(sn, stn, d);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NEXT) {
+        // step s + 1 landed: with ISSUE the later LEAD - 1 steps may still
+        // be in flight; in the last steps wait for everything
+        if constexpr (ISSUE) __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0((LEAD - 1) * kQLoads));
+        else __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* buf = lds + ((s + 1) % STAGES) * kQStage;
+        int n = 0;
+#pragma unroll
+        for (int j = H2; j < M; ++j) {
+          if (n < kR) read_one(buf, s + 1, nxt, read_k(n++));
+          if (n < kR) read_one(buf, s + 1, nxt, read_k(n++));
+          mfma_j(cur, j);
+          if constexpr (RS0) {
+            if (j - H2 < 4) rescale_one(0, j - H2, rr[j - H2]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (; n < kR; ++n) read_one(buf, s + 1, nxt, read_k(n));
+      } else {
+#pragma unroll
+        for (int j = H2; j < M; ++j) mfma_j(cur, j);
+      }
     };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
     Frags f0, f1;
 #pragma unroll
     for (int n = 0; n < kR; ++n) read_one(lds, 0, f0, read_k(n));
-    for (int s = 0; s < nsteps - 2; s += 2) {
-      step(std::false_type{}, s, f0, f1);
-      step(std::true_type{}, s + 1, f1, f0);
+    int s = 0;
+    for (; s + 1 + LEAD < nsteps; s += 2) {   // both steps issue
+      step(F_{}, T_{}, T_{}, s, f0, f1);
+      step(T_{}, T_{}, T_{}, s + 1, f1, f0);
     }
-    // steps nsteps - 2 (a block start) and nsteps - 1: no more loads
-    // (with two row blocks, row block 0 was rescaled in step nsteps - 3)
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (LIVE == 1) rescale_all(1, nkb - 1);
-    float rl[4];
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) rl[cb] = ratio_of(cb, nkb - 1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < H2; ++j) {
-      mfma_j(f0, j);
-      if constexpr (LIVE == 2) {
-        if (j < 4) rescale_one(1, j, rl[j]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    // the rest: four steps (LEAD 3, nsteps >= 4), the first of them issuing
+    // the last loads, or two
+    if (LEAD == 3 && nsteps - s == 4) {
+      step(F_{}, T_{}, T_{}, s, f0, f1);
+      step(T_{}, F_{}, T_{}, s + 1, f1, f0);
+      s += 2;
     }
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int n = 0; n < kR; ++n)
-      read_one(lds + ((nsteps - 1) % kQStages) * kQStage, nsteps - 1, f1, read_k(n));
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = H2; j < M; ++j) mfma_j(f0, j);
-#pragma unroll
-    for (int j = 0; j < M; ++j) mfma_j(f1, j);
+    step(F_{}, F_{}, T_{}, s, f0, f1);
+    step(T_{}, F_{}, F_{}, s + 1, f1, f0);
   };
   if (two_blocks) run(std::integral_constant<int, 2>{});
   else run(std::integral_constant<int, 1>{});
@@ -385,8 +394,8 @@ __global__ __launch_bounds__(kQThreads, 1) void f8_pair_gemm_kernel(F8PairArgs a
 // number of 64-k steps, at least 4), LDS for the activation scales of 128
 // rows.
 bool f8_fits(int H, int I) {
-  return H > 0 && I > 0 && I % 128 == 0 && H % 256 == 0 && q_lds_bytes(H) <= kQLdsMax &&
-         q_lds_bytes(I) <= kQLdsMax;
+  return H > 0 && I > 0 && I % 128 == 0 && H % 256 == 0 && q_lds_bytes(3, H) <= kQLdsMax &&
+         q_lds_bytes(3, I) <= kQLdsMax;
 }
 
 hipError_t f8_launch(bool gu, const F8PairArgs& a, int max_tiles, hipStream_t stream) {
@@ -395,9 +404,14 @@ hipError_t f8_launch(bool gu, const F8PairArgs& a, int max_tiles, hipStream_t st
   if (grid >= (1L << 31)) return hipErrorInvalidValue;
   if (grid == 0) return hipSuccess;
   const dim3 g((unsigned)grid);
-  const size_t lds = q_lds_bytes(gu ? a.H : a.I);
-  if (gu) f8_pair_gemm_kernel<true><<<g, kQThreads, lds, stream>>>(a);
-  else f8_pair_gemm_kernel<false><<<g, kQThreads, lds, stream>>>(a);
+  // four stages (three steps of loads ahead) where LDS holds them
+  const int K = gu ? a.H : a.I;
+  const bool deep = q_lds_bytes(4, K) <= kQLdsMax;
+  const size_t lds = q_lds_bytes(deep ? 4 : 3, K);
+  if (gu && deep) f8_pair_gemm_kernel<true, 4><<<g, kQThreads, lds, stream>>>(a);
+  else if (gu) f8_pair_gemm_kernel<true, 3><<<g, kQThreads, lds, stream>>>(a);
+  else if (deep) f8_pair_gemm_kernel<false, 4><<<g, kQThreads, lds, stream>>>(a);
+  else f8_pair_gemm_kernel<false, 3><<<g, kQThreads, lds, stream>>>(a);
   return hipPeekAtLastError();
 }
 
