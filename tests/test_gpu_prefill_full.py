@@ -5,11 +5,13 @@ hold at any size, and sampled tokens against the oracle.
 * Token permutation: each output row is reduced in a fixed order that does
   not depend on the row's position in its M tile or on the other tokens, so
   permuting the batch permutes the output bit for bit.
-* Sampled tokens: the oracle's dequantised-fp32 layer for three tokens of
-  the batch (only their experts, at full H and I); the layer's bf16 output
+* Sampled tokens: the oracle's dequantised-fp32 layer for sixteen tokens of
+  the batch (the first, the last, one in the middle and 13 drawn at random;
+  only their experts, at full H and I); the layer's bf16 output
   within max-abs 2e-2 (plus half a bf16 ulp of the value) and rel-L2 5e-3.
-  The FP8 prefill GEMM is exact (e4m3 weights against exact e4m3 activation
-  pairs on the scaled fp8 MFMA, fp32 accumulation); what remains is the bf16
+  The FP8 prefill GEMM is exact up to fp32 rounding (e4m3 weights against
+  exact e4m3 activation pairs on the scaled fp8 MFMA, fp32 accumulation, the
+  block scales applied by accumulator rescaling); what remains is the bf16
   rounding of act before down and of the output, so the comparison is made
   on the bf16 outputs the layer returns and the fp32 rel-L2 is held to the
   same 5e-3.
@@ -55,7 +57,8 @@ def test_token_permutation_is_bitwise_equivariant(layer):
 
 def test_sampled_tokens_match_oracle(layer):
     W, x, ids, wts, out = layer
-    toks = [0, T // 2 + 17, T - 1]
+    rng = np.random.default_rng(7)
+    toks = sorted({0, T // 2 + 17, T - 1, *rng.choice(T, 13, replace=False).tolist()})
     ids_s = ids[toks].cpu().numpy()
     used = np.unique(ids_s)
     remap = {int(e): i for i, e in enumerate(used)}
