@@ -153,6 +153,34 @@ def test_fused_small_route_segment_bit_exact(T, E, K, NS, mode):
     assert int(seg.n_tiles.item()) == ets[-1]
 
 
+@pytest.mark.parametrize("T,E,K,renorm", [(128, 8, 2, True), (500, 8, 2, True),
+                                           (40, 32, 8, True), (300, 16, 3, False),
+                                           (7, 8, 2, False)])
+def test_lane_softmax_route_segment_bit_exact(T, E, K, renorm):
+    """Softmax over at most 32 experts, one thread per token, fused with the
+    segmentation (any batch of at most 1024 pairs): ids, weights and the
+    segmentation bit-exact, with exact ties and equal logits planted."""
+    rng = np.random.default_rng(T + 3 * E + K)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[::4, 1] = logits[::4, 0]
+    logits[2::7] = np.round(logits[2::7] * 2) / 2
+    logits[5::11, :] = 0.25                       # every expert tied
+    dev = torch.device("cuda")
+    seg = L.segmentation(T, K, E, 0, 128, dev)
+    assert seg.small
+    ids = torch.empty((T, K), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, K), dtype=torch.float32, device=dev)
+    seg.run_small(0, ids, wts, logits=torch.from_numpy(logits).to(dev), renormalize=renorm)
+    torch.cuda.synchronize()
+    rids, rwts = oracle.route_softmax_topk(logits, K, renormalize=renorm)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_array_equal(wts.cpu().numpy().view(np.uint32), rwts.view(np.uint32))
+    ref = oracle.segment(rids, rwts, E, 0, True)
+    np.testing.assert_array_equal(seg.seg_start.cpu().numpy(), ref["seg_start"])
+    for k in ("sorted_pair", "sorted_tok", "inv"):
+        np.testing.assert_array_equal(getattr(seg, k).cpu().numpy()[: seg.A], ref[k])
+
+
 @pytest.mark.parametrize("case", ["grouped_ties_bias", "softmax_ties", "given_ids_idmap",
                                   "grouped_bm4"])
 def test_tiny_route_segment_edge_cases(case):

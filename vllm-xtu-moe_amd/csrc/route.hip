@@ -538,18 +538,161 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
   return x;
 }
 
+constexpr int kFewNB = 64;   // bucket count of the ballot segmentation
+
 struct SegSmem {
   int ids[kSmallMaxA];
   float w[kSmallMaxA];
   int bk[kSmallMaxA];
   int cnt[kSmallMaxNB];
   int wsum[3][16];
+  int wc[kFewNB][16];          // ballot segmentation: pairs of bucket v in wave q
+  int bstart[kFewNB];
 };
 
+// Stable counting sort of the A <= NT pairs (pair p in thread p) over NB <=
+// kFewNB buckets: per wave, one ballot per bucket gives each pair its rank
+// among the wave's pairs of its bucket and the wave's count; one wave scans
+// the bucket totals.  Position = bucket start + the bucket's pairs in
+// earlier waves + rank: the same stable order as the counting sort.
+template <int NT>
+__device__ __forceinline__ void segment_few_buckets(const SmallArgs& a, SegSmem& g, int A, int TK,
+                                                    int NB) {
+  constexpr int NW = NT / kWave;
+  const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
+  const int K = a.K, E = a.E, NS = a.NS;
+  int b = -1;
+  float w = 1.0f;
+  if (tid < A) {
+    if (tid < TK) {
+      int e = g.ids[tid];
+      w = g.w[tid];
+      if (a.id_map && e >= 0 && e < E) e = a.id_map[e];
+      b = (e < 0 || e >= E) ? (E + NS) : e;
+      if (a.drop_zero && w == 0.0f) b = E + NS;
+    } else {
+      b = E + (tid - TK) % NS;
+    }
+  }
+  int rank = 0;
+  for (int v = 0; v < NB; ++v) {
+    const unsigned long long m = __ballot(b == v);
+    if (lane == 0) g.wc[v][wv] = __popcll(m);
+    if (b == v)
+      rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+  }
+  __syncthreads();
+  if (wv == 0) {
+    // lane v: bucket v's rows, its start; active entries and tile lists
+    int c = 0;
+    if (lane < NB)
+      for (int q = 0; q < NW; ++q) c += g.wc[lane][q];
+    const int start = wave_incl_scan(c) - c;
+    const bool live = lane < NB - 1 && c > 0;
+    const unsigned long long am = __ballot(live);
+    const int ai = __builtin_amdgcn_mbcnt_hi((uint32_t)(am >> 32),
+                                             __builtin_amdgcn_mbcnt_lo((uint32_t)am, 0u));
+    const int nt = (lane < NB - 1) ? (c + a.bm - 1) / a.bm : 0;
+    const int tinc = wave_incl_scan(nt);
+    const int t0 = tinc - nt;
+    if (lane < NB) {
+      g.bstart[lane] = start;
+      a.seg_start[lane] = start;
+      a.expert_tile_start[lane] = t0;
+    }
+    if (live) {
+      a.active[ai] = lane;
+      for (int j = 0; j < nt; ++j) {
+        a.tile_expert[t0 + j] = lane;
+        a.tile_row0[t0 + j] = start + j * a.bm;
+      }
+    }
+    if (lane == 0) {
+      const int n_til = __builtin_amdgcn_readlane(tinc, 63);
+      a.seg_start[NB] = A;
+      a.expert_tile_start[NB] = n_til;
+      a.n_active[0] = __popcll(am);
+      a.n_tiles[0] = n_til;
+    }
+  }
+  __syncthreads();
+  if (tid < A) {
+    int pos = g.bstart[b] + rank;
+    for (int q = 0; q < wv; ++q) pos += g.wc[b][q];
+    a.sorted_pair[pos] = tid;
+    a.inv[tid] = pos;
+    a.sorted_tok[pos] = tid < TK ? tid / K : (tid - TK) / NS;
+    a.sorted_wts[pos] = tid < TK ? w : 1.0f;
+  }
+}
+
+// Softmax top-K of one token by one thread, for at most kLaneE experts and
+// kLaneK choices: the selection scan in (score desc, index asc) order and
+// the weights in the same fp32 sequence as route_token (e^(l_k - lmax), the
+// sum over the K chosen in selection order, or over all E in index order
+// without renormalisation; one correctly rounded division each).
+constexpr int kLaneE = 32, kLaneK = 8;
+
+__device__ __forceinline__ void route_token_lane(const float* __restrict__ l, int E, int K,
+                                                 int renorm, int32_t* ids_out, float* wts_out,
+                                                 int32_t* ids_lds, float* wts_lds) {
+  float v[kLaneE];
+#pragma unroll
+  for (int e = 0; e < kLaneE; ++e) v[e] = e < E ? l[e] : 0.f;
+  int sel[kLaneK];
+  float sv[kLaneK];
+  uint32_t used = 0u;
+#pragma unroll
+  for (int k = 0; k < kLaneK; ++k) {
+    if (k < K) {
+      int best = -1;
+      float bv = 0.f;
+#pragma unroll
+      for (int e = 0; e < kLaneE; ++e) {
+        if (e < E && !((used >> e) & 1u) && (best < 0 || better(v[e], e, bv, best))) {
+          best = e;
+          bv = v[e];
+        }
+      }
+      sel[k] = best;
+      sv[k] = bv;
+      used |= 1u << best;
+    }
+  }
+  const float lmax = sv[0];
+  float ev[kLaneK];
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kLaneK; ++k) {
+    if (k < K) {
+      ev[k] = xtu_expf(sv[k] - lmax);
+      sum = sum + ev[k];
+    }
+  }
+  if (!renorm) {
+    sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kLaneE; ++e)
+      if (e < E) sum = sum + xtu_expf(v[e] - lmax);
+  }
+#pragma unroll
+  for (int k = 0; k < kLaneK; ++k) {
+    if (k < K) {
+      const float w = __fdiv_rn(ev[k], sum);
+      ids_out[k] = sel[k];
+      wts_out[k] = w;
+      ids_lds[k] = sel[k];
+      wts_lds[k] = w;
+    }
+  }
+}
+
 // One workgroup of NT threads.  MODE 0: softmax routing, 1: grouped sigmoid
-// routing (NT/256 teams route that many tokens at a time), 2: ids/wts given.
-// Then the whole segmentation.
-template <int MODE, int NT>
+// routing (NT/256 teams route that many tokens at a time; LANE: softmax over
+// at most kLaneE experts, one thread per token), 2: ids/wts given.  Then the
+// whole segmentation.
+template <int MODE, int NT, bool LANE = false, bool FEW = false>
 __global__ __launch_bounds__(NT) void route_seg_small_kernel(SmallArgs a) {
   __shared__ SegSmem g;
   extern __shared__ float route_lds[];
@@ -557,7 +700,11 @@ __global__ __launch_bounds__(NT) void route_seg_small_kernel(SmallArgs a) {
   const int tid = threadIdx.x;
   const int T = a.T, K = a.K, E = a.E, NS = a.NS;
   const int TK = T * K, A = TK + T * NS, NB = E + NS + 1;
-  if (MODE < 2) {
+  if (MODE == 0 && LANE) {
+    for (int t = tid; t < T; t += NT)
+      route_token_lane(a.logits + (long)t * E, E, K, a.renorm, a.ids + (long)t * K,
+                       a.wts + (long)t * K, g.ids + t * K, g.w + t * K);
+  } else if (MODE < 2) {
     // NT / 256 teams of 256 threads route that many tokens at a time
     constexpr int NTEAM = NT / 256;
     const int team = tid / 256, ttid = tid % 256;
@@ -576,6 +723,11 @@ __global__ __launch_bounds__(NT) void route_seg_small_kernel(SmallArgs a) {
       g.ids[p] = a.ids[p];
       g.w[p] = a.wts[p];
     }
+  }
+  if constexpr (FEW) {   // A <= NT pairs over NB <= kFewNB buckets
+    __syncthreads();
+    segment_few_buckets<NT>(a, g, A, TK, NB);
+    return;
   }
   for (int e = tid; e < NB; e += NT) g.cnt[e] = 0;
   __syncthreads();
@@ -706,8 +858,17 @@ hipError_t launch_small(const SmallArgs& a, hipStream_t stream) {
     }
     return hipSuccess;
   }
+  // few buckets: the ballot segmentation, one pair per thread
+  const long A = (long)a.T * a.K + (long)a.T * a.NS;
+  const bool few = a.E + a.NS + 1 <= kFewNB && A <= 1024;
   if constexpr (MODE == 2) {
-    route_seg_small_kernel<MODE, 256><<<1, 256, 0, stream>>>(a);
+    if (few && A <= 256) route_seg_small_kernel<2, 256, false, true><<<1, 256, 0, stream>>>(a);
+    else if (few) route_seg_small_kernel<2, 1024, false, true><<<1, 1024, 0, stream>>>(a);
+    else route_seg_small_kernel<MODE, 256><<<1, 256, 0, stream>>>(a);
+  } else if (MODE == 0 && a.E <= kLaneE && a.K <= kLaneK) {
+    // few experts: one thread per token, no routing barriers (few buckets)
+    if (A <= 256) route_seg_small_kernel<0, 256, true, true><<<1, 256, 0, stream>>>(a);
+    else route_seg_small_kernel<0, 1024, true, true><<<1, 1024, 0, stream>>>(a);
   } else {
     const int nc = (MODE == 1 ? a.n_group : (a.E + 31) / 32) * a.K;
     const size_t team_lds = route_team_words(a.E, nc) * sizeof(float);

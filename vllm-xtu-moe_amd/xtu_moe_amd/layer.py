@@ -28,6 +28,7 @@ SMALL_MAX_PAIRS = 1024
 # plus the three-launch segmentation is faster (measured: 95 us vs ~17 us for
 # 128 tokens over 8 experts).
 SMALL_ROUTE_MAX_TOKENS = 16
+LANE_ROUTE_MAX_E, LANE_ROUTE_MAX_K = 32, 8   # softmax routed by one thread per token
 
 
 def _p(t) -> int:
@@ -677,7 +678,11 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
                   be, st)
     elif router is not None:
         mode = rmode
-        if seg.small and 0 < T <= SMALL_ROUTE_MAX_TOKENS:
+        # the fused route + segmentation: tiny batches, or softmax over few
+        # experts (one thread per token) for any batch the small path holds
+        if seg.small and T > 0 and (T <= SMALL_ROUTE_MAX_TOKENS
+                                    or (mode == 0 and E <= LANE_ROUTE_MAX_E
+                                        and K <= LANE_ROUTE_MAX_K)):
             seg.run_small(mode, ids, wts, logits=router["logits"], bias=router.get("bias"),
                           n_group=router.get("n_group", 1), topk_group=router.get("topk_group", 1),
                           routed_scaling=router.get("routed_scaling_factor", 1.0),
