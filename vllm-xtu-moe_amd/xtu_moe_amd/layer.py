@@ -83,6 +83,10 @@ class ExpertWeights:
         rows = {t.shape[0] for t in (w13, s13, w2, s2, gs13, gs2) if t is not None}
         if len(rows) != 1:
             raise ValueError(f"weight planes hold different expert counts: {sorted(rows)}")
+        # FP8: the prefill kernel choice is fixed when the weights are built,
+        # so a graph captured later takes the same kernel as eager calls
+        if self.fmt == FMT_FP8 and not self.mutable:
+            self.fp8_scales_bounded()
 
     @property
     def n_experts(self) -> int:
