@@ -1,4 +1,5 @@
-"""The decode layer recorded into a HIP graph: every replay (with eager work and
+"""Layers recorded into a HIP graph (decode, and routed batches on the grouped
+GEMMs and the exact-pair kernels): every replay (with eager work and
 synchronisations between replays, and fresh inputs copied into the static
 buffers) must equal the eager result bit for bit."""
 import numpy as np
@@ -6,6 +7,7 @@ import pytest
 import torch
 
 from xtu_moe_amd import formats as F
+from xtu_moe_amd import layer as L
 from xtu_moe_amd.layer import moe_forward, route
 from xtu_moe_amd.synthetic import synth_layer
 
@@ -59,19 +61,29 @@ def test_decode_graph_replays_match_eager(fmt):
         del junk
 
 
-@pytest.mark.parametrize("case", ["decode-split", "gemm-128"])
+@pytest.mark.parametrize("case", ["decode-split", "gemm-128", "fp8-pair32", "mxfp4-pair32"])
 def test_routed_layer_graph_replays_match_eager(case):
     """moe_forward routing from logits inside the graph: the decode layer whose
-    routing launch also runs the shared expert (T = 1), and a 128-token batch
-    on the multi-workgroup router and the grouped GEMMs."""
+    routing launch also runs the shared expert (T = 1), a 128-token batch
+    routed one thread per token in the routing + segmentation launch on the
+    grouped GEMMs, and 300-token batches on the exact-pair 32x32x64 kernels
+    (FP8 with its block-scale rescaling, MXFP4)."""
     dev = torch.device("cuda")
     if case == "decode-split":
         fmt, H, I, E, NS, K, T = F.FMT_MXFP4, 1024, 256, 256, 1, 8, 1
+        rt = dict(scoring="sigmoid", n_group=8, topk_group=4, routed_scaling_factor=2.5)
+    elif case in ("fp8-pair32", "mxfp4-pair32"):
+        fmt = F.FMT_FP8 if case == "fp8-pair32" else F.FMT_MXFP4
+        H, I, E, NS, K, T = 1024, 512, 16, 1, 4, 300
         rt = dict(scoring="sigmoid", n_group=8, topk_group=4, routed_scaling_factor=2.5)
     else:
         fmt, H, I, E, NS, K, T = F.FMT_BF16, 1024, 512, 8, 0, 2, 128
         rt = dict(scoring="softmax", renormalize=True)
     W = synth_layer(fmt, E, NS, H, I, seed=5, device=dev)
+    if case == "fp8-pair32":
+        assert L.fp8_pair32_use(W) and L.gemm_tile_m(fmt, False, H, I, W) == 128
+    if case == "mxfp4-pair32":
+        assert L.mx_pair_kernel(fmt, H, I) and L.gemm_tile_m(fmt, False, H, I) == 128
     g = torch.Generator(device=dev).manual_seed(1)
     xs = [torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
     lgs = [torch.randn((T, E), generator=g, device=dev) for _ in range(4)]
