@@ -142,7 +142,7 @@ def bench_one(args):
     from xtu_moe_amd import _lib
     from xtu_moe_amd import formats as F
     from xtu_moe_amd.layer import (_fp8pair_bufs, _mxpair_bufs, _p, _stream, gemm_tile_m,
-                                   int8_align_on, moe_forward, mx_pair_kernel, pair_gemm, route,
+                                   int8_align_on, moe_forward, mx_pair_kernel, mx_tri, pair_gemm, route,
                                    fp8_pair32_use,
                                    segmentation)
     from xtu_moe_amd.synthetic import synth_layer
@@ -335,9 +335,10 @@ def bench_one(args):
                 f8x = _mxpair_bufs("xm", T, H, dev)
                 _lib.call("xtu_pair_quant_il", _p(x_st), T, H, *[_p(t) for t in f8x], st)
             elif not decode and not i8 and mx_pair_kernel(fmt, H, I):
+                mxk = "tri" if mx_tri(fmt, H, I) else "pair"
                 mxx = _mxpair_bufs("xm", T, H, dev)
                 s13p, _ = W.mx_pair_scales()
-                _lib.call("xtu_pair_quant_il", _p(x_st), T, H, *[_p(t) for t in mxx], st)
+                _lib.call(f"xtu_{mxk}_quant_il", _p(x_st), T, H, *[_p(t) for t in mxx], st)
             elif not decode and not i8 and pair_gemm(fmt, H, I):
                 fp8x = _fp8pair_bufs("x8", T, H, dev)
                 _lib.call("xtu_fp8pair_quant", _p(x_st), T, H, *[_p(t) for t in fp8x], st)
@@ -369,7 +370,7 @@ def bench_one(args):
                           _p(act), cfg["limit"], 1.0, 0.0, st)
             elif mxx is not None:
                 lo, hi = seg.tile_range_ptrs(0, E + NS)
-                _lib.call("xtu_mx_pair_gate_up", *[_p(t) for t in mxx], _p(seg.sorted_tok), H, I,
+                _lib.call(f"xtu_mx_{mxk}_gate_up", *[_p(t) for t in mxx], _p(seg.sorted_tok), H, I,
                           _p(W.w13), _p(s13p), 0, 0, 0, _p(seg.seg_start), _p(seg.tile_expert),
                           _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi, seg.max_tiles,
                           _p(act), cfg["limit"], 1.0, 0.0, st)
@@ -443,6 +444,16 @@ def bench_one(args):
                 if tr.get("distinct_experts"):   # the counter run's own routing
                     tr["algorithmic_bytes"] = (tr["distinct_experts"] * e_bytes13 + Th * H * 2
                                                + (Th * K + Th * NS) * I * 2)
+    elif mx_tri(fmt, H, I) and not cfg["int8"] and not decode_head:
+        # fp6 / fp4 A (activation triples) x e2m1 B on the double-rate
+        # 32x32x64 MFMA: the fp6/fp4 peak; every algorithmic product is three
+        # MFMA products (the activation's three pieces)
+        ach = r["gate_up_TFLOPs"]
+        roof = dict(bound="mfma", achieved=ach, peak=PEAK_TFLOPS["fp4"], unit="TFLOP/s",
+                    frac=ach / PEAK_TFLOPS["fp4"], traffic=None, kernel="mx_pair_gemm_kernel",
+                    mfma_issue_frac=3.0 * ach / PEAK_TFLOPS["fp4"],
+                    frac_of_fp8_peak=ach / PEAK_TFLOPS["fp8"],
+                    frac_of_bf16_peak=ach / PEAK_TFLOPS["bf16"])
     elif pair_gemm(fmt, H, I) and not cfg["int8"]:
         # scaled MFMA with an e4m3 A (FP8: e4m3 B; MXFP4: e2m1 B), which runs
         # at the fp8 rate; every algorithmic product is two MFMA products
@@ -485,6 +496,8 @@ def bench_one(args):
         "vs_baseline": None,
         "dtype": {"mxfp4": ("bf16-mfma/e2m1+e8m0"
                             if decode_head or not pair_gemm(fmt, H, I)
+                            else "fp6xfp4-mfma/e2m3,e2m3,e2m1-triple x e2m1+e8m0"
+                            if mx_tri(fmt, H, I)
                             else "fp8xfp4-mfma/e4m3-pair x e2m1+e8m0"),
                   "fp8": ("bf16-mfma/e4m3+f32-block" if decode_head
                           else "fp8-mfma/e4m3-pair x e4m3+f32-block"),

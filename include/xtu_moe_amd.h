@@ -334,6 +334,37 @@ hipError_t xtu_mx_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int 
                             const int32_t* expert_tile_start, const int32_t* tile_lo,
                             const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream);
 
+/* The same MXFP4 GEMMs on the double-rate fp6 / fp4 MFMA (fp6 or fp4 A
+ * operand against fp4 B runs at twice the fp8 x fp4 rate on 32x32x64):
+ *   xtu_tri_quant_il: bf16 rows [M][K] -> activation triples q [M][2K]
+ *     (per 64 k and 32-k half h: 64 bytes at 64h, [p1 24 B | p2 24 B |
+ *     p3 16 B], p1 p2 e2m3 codes packed 6 bits each, p3 e2m1 codes 4 bits
+ *     each, k order) and e8m0 sq [M][K/32] = e + 127;
+ *     x ~= 2^e (p1 + p2/16 + p3/256), each piece the round-to-nearest-even
+ *     of the remainder of the previous ones, e the smallest exponent with
+ *     max|x| <= 7.5 * 2^e; |error| <= 2^(e-9) < 2^-10.9 * max|x| of the
+ *     32-k block (pieces whose scale byte would be negative are zero).
+ *   xtu_mx_tri_gate_up / _down: as xtu_mx_pair_gate_up / _down (same
+ *     arguments, tiles, shapes), on q and sq: three MFMAs per block and
+ *     step (scales sq, sq-4, sq-8) instead of the pair's two.
+ * No counterpart in the reference: its Triton kernels run these GEMMs on
+ * bf16 operands; the triples are this library's operand format. */
+hipError_t xtu_tri_quant_il(const void* x, int M, int K, uint8_t* q, uint8_t* sq,
+                            hipStream_t stream);
+hipError_t xtu_mx_tri_gate_up(const uint8_t* q, const uint8_t* sq, const int32_t* sorted_tok,
+                              int H, int I, const void* w13, const uint8_t* s13p, long w_estride,
+                              long s_estride, const int32_t* slot_map, const int32_t* seg_start,
+                              const int32_t* tile_expert, const int32_t* tile_row0,
+                              const int32_t* expert_tile_start, const int32_t* tile_lo,
+                              const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                              float alpha, float beta, hipStream_t stream);
+hipError_t xtu_mx_tri_down(const uint8_t* q, const uint8_t* sq, int H, int I, const void* w2,
+                           const uint8_t* s2p, long w_estride, long s_estride,
+                           const int32_t* slot_map, const int32_t* seg_start,
+                           const int32_t* tile_expert, const int32_t* tile_row0,
+                           const int32_t* expert_tile_start, const int32_t* tile_lo,
+                           const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream);
+
 /* -------------------------------------- INT8-activation x FP4-code (ALIGN) path
  * Replaces the engine's ALIGN integer path (xiaotu_moe/csrc/moe/
  * moe_v2_packed4_w4a8.inc:478-586 xiaotu_predecode_block, :661-715

@@ -215,12 +215,14 @@ def test_ds_v3_fp8_streamed_prefill():
 
 
 # ------------------------------------------------------ DeepSeek-V3 MXFP4 prefill
-@pytest.mark.parametrize("mode", ["pair", "bf16"])
+@pytest.mark.parametrize("mode", ["tri", "pair", "bf16"])
 def test_ds_v3_mxfp4_prefill_t8192(mode, monkeypatch):
-    """DeepSeek-V3 shape with MXFP4 experts at T=8192, on the scaled fp8 x fp4
-    MFMA (exact activation pairs) and on the bf16-operand GEMM: sampled tokens
-    against the oracle, and the token-permutation bitwise property."""
+    """DeepSeek-V3 shape with MXFP4 experts at T=8192, on the double-rate fp6
+    / fp4 MFMA (activation triples), the scaled fp8 x fp4 MFMA (exact
+    activation pairs) and the bf16-operand GEMM: sampled tokens against the
+    oracle, and the token-permutation bitwise property."""
     monkeypatch.setenv(L.MXFP4_PREFILL_ENV, mode)
+    assert L.mx_tri(F.FMT_MXFP4, 7168, 2048) == (mode == "tri")
     H, I, E, NS, K, T = 7168, 2048, 256, 1, 8, 8192
     W = synth_layer(F.FMT_MXFP4, E, NS, H, I, seed=17, device=DEV)
     g = torch.Generator(device=DEV).manual_seed(18)

@@ -1,14 +1,20 @@
-"""MXFP4 exact-pair GEMMs on the 32x32x64 scaled MFMA (xtu_mx_pair_*): the
-interleaved activation pairs bit-exact against the planar quantiser's, the
-step-major scale re-layout bit-exact against the dense scales, and the layer
-against the oracle over tile shapes (single rows, partial and multi-tile
-experts, a shared expert, a SwiGLU clamp) and through a slot map on mutable
-planes (the ring / pool layout)."""
+"""MXFP4 GEMMs on the 32x32x64 scaled MFMA, with exact e4m3 activation pairs
+(xtu_mx_pair_*) and with activation triples on the double-rate fp6 / fp4
+MFMA (xtu_mx_tri_*): the interleaved activation pairs bit-exact against the
+planar quantiser's, the triples bit-exact against their CPU restatement
+(tests/tri_ref.py), the step-major scale re-layout bit-exact against the
+dense scales, and the layer against the oracle in both modes over tile
+shapes (single rows, partial and multi-tile experts, a shared expert, a
+SwiGLU clamp) and through a slot map on mutable planes (the ring / pool
+layout)."""
+import os
+
 import numpy as np
 import pytest
 import torch
 
 from helpers import bf16_tensor_to_bits, check_close, dense_to_numpy, make_dense_layer, oracle_layer
+from tri_ref import tri_split
 from xtu_moe_amd import _lib
 from xtu_moe_amd import formats as F
 from xtu_moe_amd import layer as L
@@ -18,9 +24,37 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
 
 
-@pytest.fixture(autouse=True)
-def _pair_mode(monkeypatch):
-    monkeypatch.setenv(L.MXFP4_PREFILL_ENV, "pair")
+@pytest.fixture(params=["pair", "tri"])
+def mode(request, monkeypatch):
+    monkeypatch.setenv(L.MXFP4_PREFILL_ENV, request.param)
+    return request.param
+
+
+def test_triples_match_restatement():
+    """xtu_tri_quant_il bytes and scale bytes equal tri_ref.tri_split's, on
+    N(0,1) rows, rows of widely scaled blocks, and blocks at the edges (near
+    the bf16 maximum, below the pieces' scale range, zeros, negative zeros,
+    values on the e2m3 grid)."""
+    x = torch.cat([_tri_rows(), torch.randn((37, 1024), generator=torch.Generator().manual_seed(5))
+                   .to(torch.bfloat16)])
+    for M, K, xx in ((x.shape[0], 1024, x), (1, 256, x[:1, :256]), (9, 7168, None)):
+        if xx is None:
+            xx = (torch.randn((M, K), generator=torch.Generator().manual_seed(6)) *
+                  torch.exp2(torch.randint(-30, 30, (M, 1), generator=torch.Generator()
+                                           .manual_seed(7)).float())).to(torch.bfloat16)
+        xx = xx.contiguous()
+        q = torch.empty((M, 2 * K), dtype=torch.uint8, device=DEV)
+        sq = torch.empty((M, K // 32), dtype=torch.uint8, device=DEV)
+        _lib.call("xtu_tri_quant_il", _p(xx.to(DEV)), M, K, _p(q), _p(sq), _stream())
+        torch.cuda.synchronize()
+        wq, wsq, _ = tri_split(xx)
+        assert np.array_equal(sq.cpu().numpy(), wsq), (M, K)
+        assert np.array_equal(q.cpu().numpy(), wq), (M, K)
+
+
+def _tri_rows():
+    from test_tri_ref import _rows
+    return _rows()
 
 
 @pytest.mark.parametrize("M,K", [(1, 256), (300, 1024), (37, 7168)])
@@ -73,12 +107,14 @@ def _layer(fmt, E, NS, H, I, seed):
 
 
 def _on_kernel(fmt, H, I):
-    return L.mx_pair_kernel(fmt, H, I) and L.gemm_tile_m(fmt, False, H, I) == 128
+    mode = "tri" if L.mx_tri(fmt, H, I) else "pair"
+    return (L.mx_pair_kernel(fmt, H, I) and L.gemm_tile_m(fmt, False, H, I) == 128
+            and os.environ.get(L.MXFP4_PREFILL_ENV) == mode)
 
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,K,skew", [(1, 2, False), (40, 4, False), (700, 4, False), (900, 2, True)])
-def test_layer_against_oracle(fmt, T, K, skew):
+def test_layer_against_oracle(fmt, T, K, skew, mode):
     E, NS, H, I = 16, 1, 1024, 512
     d, W = _layer(fmt, E, NS, H, I, seed=30 + T)
     assert _on_kernel(fmt, H, I)
@@ -95,11 +131,11 @@ def test_layer_against_oracle(fmt, T, K, skew):
     torch.cuda.synchronize()
     ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I,
                        limit=5.0)
-    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"pair32 fmt={fmt} T={T}")
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"{mode} fmt={fmt} T={T}")
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-def test_slot_map_on_mutable_planes(fmt):
+def test_slot_map_on_mutable_planes(fmt, mode):
     """Experts at permuted slots of planes flagged mutable (restaged in
     place): the step-major scales are rebuilt per call, so restaging the
     slots between two calls gives the new experts' results."""

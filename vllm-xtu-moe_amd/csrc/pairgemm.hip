@@ -111,6 +111,26 @@ __global__ __launch_bounds__(256) void mx_pair_quant_kernel(const uint16_t* __re
   shi[i] = (uint8_t)sa;
 }
 
+// bf16 rows -> interleaved triples; one thread per (row, 32-k block): the
+// block's 64 bytes [p1 24 B | p2 24 B | p3 16 B] at byte 64 (blk % 2) of
+// the row's 128-byte line of step blk / 2
+__global__ __launch_bounds__(256) void mx_tri_quant_kernel(const uint16_t* __restrict__ x, int M,
+                                                           int K, uint8_t* __restrict__ q,
+                                                           uint8_t* __restrict__ sq) {
+  const long nb = (long)M * (K / 32);
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nb) return;
+  const long row = i / (K / 32), blk = i % (K / 32);
+  uint32_t p1[6], p2[6], p3[4];
+  const int s = tri_split32(x + row * K + blk * 32, p1, p2, p3);
+  uint8_t* d = q + row * 2L * K + (blk / 2) * 128 + (blk % 2) * 64;
+  *reinterpret_cast<u32x4_t*>(d) = u32x4_t{p1[0], p1[1], p1[2], p1[3]};
+  *reinterpret_cast<u32x4_t*>(d + 16) = u32x4_t{p1[4], p1[5], p2[0], p2[1]};
+  *reinterpret_cast<u32x4_t*>(d + 32) = u32x4_t{p2[2], p2[3], p2[4], p2[5]};
+  *reinterpret_cast<u32x4_t*>(d + 48) = u32x4_t{p3[0], p3[1], p3[2], p3[3]};
+  sq[i] = (uint8_t)s;
+}
+
 // ---------------------------------------------------------------------------
 // packed MXFP4 scale groups -> step-major; one thread per output byte
 // ---------------------------------------------------------------------------
@@ -132,7 +152,10 @@ __global__ __launch_bounds__(256) void mx_pair_scales_kernel(const uint8_t* __re
 // ---------------------------------------------------------------------------
 // grouped GEMM
 // ---------------------------------------------------------------------------
-template <bool GU>
+// TRI: activation triples (fp6, fp6, fp4 pieces, mx_tri_quant_kernel) on
+// the double-rate fp6 / fp4 x fp4 MFMA, three MFMAs per 32 x 32 block and
+// step; else exact e4m3 pairs, two MFMAs at the fp8 rate.
+template <bool GU, bool TRI>
 __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -263,9 +286,15 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[mb][cb][i] = 0.f;
 
+  // A pieces per row block: the lane's four 16-byte LDS pieces.  Pairs:
+  // plane p = pieces 2p, 2p + 1 (k 16h.. and 32 + 16h.. of the row's hi or
+  // lo 64 bytes); triples: the lane's 64 bytes of its k-half h, p1 = dwords
+  // 0-5, p2 = 6-11, p3 = 12-15.
+  constexpr int kPieces = TRI ? 3 : 2;      // MFMAs per 32 x 32 block and step
+  constexpr int kBlockMfma = 8 * kPieces;   // per row block and step
   struct Frags {
-    i32x8_t a[2][2];   // [mb][plane]
-    int sa[2];         // e8m0 of hi; lo's is max(sa - 4, 0)
+    u32x4_t a[2][4];   // [mb][piece]
+    int sa[2];         // e8m0 byte of the row block's first piece
     u32x4_t b[8];
     int sb[8];
   };
@@ -279,24 +308,49 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
       f.b[k] = *reinterpret_cast<const u32x4_t*>(buf + kLA + C * 32 + 16 * (h ^ ((C >> 3) & 1)));
       f.sb[k] = buf[kLA + kLB + C * 2 + h];
     } else if (k < 12) {
+      // half p of row block mb: pairs plane p (pieces 4p + h, 4p + 2 + h);
+      // triples pieces 4h + 2p, 4h + 2p + 1
       const int mb = (k - 8) / 2, p = (k - 8) % 2, R = arow[mb];
       const uint8_t* base = buf + R * 128;
-      const u32x4_t x0 = *reinterpret_cast<const u32x4_t*>(base + 16 * ((4 * p + h) ^ (R & 7)));
-      const u32x4_t x1 = *reinterpret_cast<const u32x4_t*>(base + 16 * ((4 * p + 2 + h) ^ (R & 7)));
-      f.a[mb][p] = i32x8_t{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
-                           (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+      const int q0 = TRI ? 4 * h + 2 * p : 4 * p + h, q1 = TRI ? q0 + 1 : q0 + 2;
+      f.a[mb][2 * p] = *reinterpret_cast<const u32x4_t*>(base + 16 * (q0 ^ (R & 7)));
+      f.a[mb][2 * p + 1] = *reinterpret_cast<const u32x4_t*>(base + 16 * (q1 ^ (R & 7)));
     } else {
       f.sa[k - 12] = asc[arow[k - 12] * ascs + 2 * s + h];
     }
   };
-  // MFMA j (0..15) of row block mb: plane j / 8, B block j % 8
+  // MFMA j (0 .. kBlockMfma-1) of row block mb: piece j / 8, B block j % 8;
+  // piece p's scale byte is sa - 4p (clamped at 0, where the quantiser
+  // leaves the piece zero)
   auto mfma_one = [&](const Frags& f, int mb, int j) {
     const int p = j / 8, cb = j % 8;
-    const int sa = p == 0 ? f.sa[mb] : (f.sa[mb] >= 4 ? f.sa[mb] - 4 : 0);
+    const int sa = p == 0 ? f.sa[mb] : (f.sa[mb] >= 4 * p ? f.sa[mb] - 4 * p : 0);
     const u32x4_t x = f.b[cb];
     const i32x8_t b = i32x8_t{(int)x[0], (int)x[1], (int)x[2], (int)x[3], 0, 0, 0, 0};
-    acc[mb][cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[mb][p], b, acc[mb][cb], 0, 4,
-                                                                  0, sa, 0, f.sb[cb]);
+    const u32x4_t* A = f.a[mb];
+    if constexpr (TRI) {
+      if (p == 0) {
+        const i32x8_t av{(int)A[0][0], (int)A[0][1], (int)A[0][2], (int)A[0][3],
+                         (int)A[1][0], (int)A[1][1], 0, 0};
+        acc[mb][cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, b, acc[mb][cb], 2, 4,
+                                                                      0, sa, 0, f.sb[cb]);
+      } else if (p == 1) {
+        const i32x8_t av{(int)A[1][2], (int)A[1][3], (int)A[2][0], (int)A[2][1],
+                         (int)A[2][2], (int)A[2][3], 0, 0};
+        acc[mb][cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, b, acc[mb][cb], 2, 4,
+                                                                      0, sa, 0, f.sb[cb]);
+      } else {
+        const i32x8_t av{(int)A[3][0], (int)A[3][1], (int)A[3][2], (int)A[3][3], 0, 0, 0, 0};
+        acc[mb][cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, b, acc[mb][cb], 4, 4,
+                                                                      0, sa, 0, f.sb[cb]);
+      }
+    } else {
+      const u32x4_t x0 = A[2 * p], x1 = A[2 * p + 1];
+      const i32x8_t av{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
+                       (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+      acc[mb][cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, b, acc[mb][cb], 0, 4,
+                                                                    0, sa, 0, f.sb[cb]);
+    }
   };
   // ---- pipeline (nsteps = K / 64 is even and >= 4)
   issue(0, 0);
@@ -307,12 +361,12 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
   // the MFMAs of step s with the loads of step s + 2 issued between them,
   // the wait and barrier, then the second half with the fragment reads of
   // step s + 1 between them (the order is pinned: no instruction moves
-  // across a sched_barrier).  MFMA j: row block j / 16, plane (j / 8) % 2,
-  // B block j % 8.
+  // across a sched_barrier).  MFMA j: row block j / kBlockMfma, piece
+  // (j / 8) % kPieces, B block j % 8.
   auto run = [&](auto live_c) {
     constexpr int LIVE = decltype(live_c)::value;
-    constexpr int M = 16 * LIVE, H2 = M / 2;
-    auto mfma_j = [&](const Frags& f, int j) { mfma_one(f, j / 16, j % 16); };
+    constexpr int M = kBlockMfma * LIVE, H2 = M / 2;
+    auto mfma_j = [&](const Frags& f, int j) { mfma_one(f, j / kBlockMfma, j % kBlockMfma); };
     // reads this variant needs: B 0-7, A row block 0 (8, 9), its scale (12),
     // and with two blocks A row block 1 (10, 11) and its scale (13)
     auto read_k = [&](int n) { return LIVE == 2 ? n : (n < 10 ? n : 12); };
@@ -405,15 +459,17 @@ bool mx_fits(int H, int I) {
          lds_bytes(I) <= kLdsMax;
 }
 
-hipError_t launch(bool gu, const MxPairArgs& a, int max_tiles, hipStream_t stream) {
+hipError_t launch(bool gu, bool tri, const MxPairArgs& a, int max_tiles, hipStream_t stream) {
   const long items = (long)max_tiles * (gu ? a.I / 256 : a.H / 512);
   const long grid = (items + 7) / 8 * 8;
   if (grid >= (1L << 31)) return hipErrorInvalidValue;
   if (grid == 0) return hipSuccess;
   const dim3 g((unsigned)grid);
   const size_t lds = lds_bytes(gu ? a.H : a.I);
-  if (gu) mx_pair_gemm_kernel<true><<<g, kPThreads, lds, stream>>>(a);
-  else mx_pair_gemm_kernel<false><<<g, kPThreads, lds, stream>>>(a);
+  if (gu && tri) mx_pair_gemm_kernel<true, true><<<g, kPThreads, lds, stream>>>(a);
+  else if (gu) mx_pair_gemm_kernel<true, false><<<g, kPThreads, lds, stream>>>(a);
+  else if (tri) mx_pair_gemm_kernel<false, true><<<g, kPThreads, lds, stream>>>(a);
+  else mx_pair_gemm_kernel<false, false><<<g, kPThreads, lds, stream>>>(a);
   return hipPeekAtLastError();
 }
 
@@ -453,14 +509,14 @@ hipError_t xtu_mx_pair_scales(const uint8_t* s, int E, int N, int K, long s_estr
   return hipPeekAtLastError();
 }
 
-hipError_t xtu_mx_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const int32_t* sorted_tok,
-                               int H, int I, const void* w13, const uint8_t* s13p,
-                               long w_estride, long s_estride, const int32_t* slot_map,
-                               const int32_t* seg_start, const int32_t* tile_expert,
-                               const int32_t* tile_row0, const int32_t* expert_tile_start,
-                               const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
-                               void* act, float limit, float alpha, float beta,
-                               hipStream_t stream) {
+static hipError_t gate_up(bool tri, const uint8_t* hilo, const uint8_t* shi,
+                          const int32_t* sorted_tok, int H, int I, const void* w13,
+                          const uint8_t* s13p, long w_estride, long s_estride,
+                          const int32_t* slot_map, const int32_t* seg_start,
+                          const int32_t* tile_expert, const int32_t* tile_row0,
+                          const int32_t* expert_tile_start, const int32_t* tile_lo,
+                          const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                          float alpha, float beta, hipStream_t stream) {
   XTU_CHECK_ARG(mx_fits(H, I));
   XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(w_estride < (1L << 31) && 2L * I * H < (1L << 32));
@@ -471,15 +527,15 @@ hipError_t xtu_mx_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const in
   const MxPairArgs a{hilo, shi, sorted_tok, (const uint8_t*)w13, s13p, seg_start, tile_expert,
                      tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, act, H, I,
                      w_estride, s_estride, limit, alpha, beta};
-  return launch(true, a, max_tiles, stream);
+  return launch(true, tri, a, max_tiles, stream);
 }
 
-hipError_t xtu_mx_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int I, const void* w2,
-                            const uint8_t* s2p, long w_estride, long s_estride,
-                            const int32_t* slot_map, const int32_t* seg_start,
-                            const int32_t* tile_expert, const int32_t* tile_row0,
-                            const int32_t* expert_tile_start, const int32_t* tile_lo,
-                            const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream) {
+static hipError_t down(bool tri, const uint8_t* hilo, const uint8_t* shi, int H, int I,
+                       const void* w2, const uint8_t* s2p, long w_estride, long s_estride,
+                       const int32_t* slot_map, const int32_t* seg_start,
+                       const int32_t* tile_expert, const int32_t* tile_row0,
+                       const int32_t* expert_tile_start, const int32_t* tile_lo,
+                       const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream) {
   XTU_CHECK_ARG(mx_fits(H, I));
   XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(w_estride < (1L << 31) && (long)H * I < (1L << 31));
@@ -490,7 +546,64 @@ hipError_t xtu_mx_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int 
   const MxPairArgs a{hilo, shi, nullptr, (const uint8_t*)w2, s2p, seg_start, tile_expert,
                      tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, y, H, I,
                      w_estride, s_estride, 0.f, 1.f, 0.f};
-  return launch(false, a, max_tiles, stream);
+  return launch(false, tri, a, max_tiles, stream);
+}
+
+hipError_t xtu_mx_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const int32_t* sorted_tok,
+                               int H, int I, const void* w13, const uint8_t* s13p,
+                               long w_estride, long s_estride, const int32_t* slot_map,
+                               const int32_t* seg_start, const int32_t* tile_expert,
+                               const int32_t* tile_row0, const int32_t* expert_tile_start,
+                               const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
+                               void* act, float limit, float alpha, float beta,
+                               hipStream_t stream) {
+  return gate_up(false, hilo, shi, sorted_tok, H, I, w13, s13p, w_estride, s_estride, slot_map,
+                 seg_start, tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi,
+                 max_tiles, act, limit, alpha, beta, stream);
+}
+
+hipError_t xtu_mx_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int I, const void* w2,
+                            const uint8_t* s2p, long w_estride, long s_estride,
+                            const int32_t* slot_map, const int32_t* seg_start,
+                            const int32_t* tile_expert, const int32_t* tile_row0,
+                            const int32_t* expert_tile_start, const int32_t* tile_lo,
+                            const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream) {
+  return down(false, hilo, shi, H, I, w2, s2p, w_estride, s_estride, slot_map, seg_start,
+              tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi, max_tiles, y, stream);
+}
+
+hipError_t xtu_tri_quant_il(const void* x, int M, int K, uint8_t* q, uint8_t* sq,
+                            hipStream_t stream) {
+  XTU_CHECK_ARG(M >= 0 && K > 0 && K % 128 == 0 && 2L * M * K < (1L << 32));
+  XTU_CHECK_ARG(M == 0 || (x && q && sq));
+  if (M == 0) return hipSuccess;
+  (void)hipGetLastError();
+  const long n = (long)M * (K / 32);
+  mx_tri_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>((const uint16_t*)x, M, K,
+                                                                        q, sq);
+  return hipPeekAtLastError();
+}
+
+hipError_t xtu_mx_tri_gate_up(const uint8_t* q, const uint8_t* sq, const int32_t* sorted_tok,
+                              int H, int I, const void* w13, const uint8_t* s13p, long w_estride,
+                              long s_estride, const int32_t* slot_map, const int32_t* seg_start,
+                              const int32_t* tile_expert, const int32_t* tile_row0,
+                              const int32_t* expert_tile_start, const int32_t* tile_lo,
+                              const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                              float alpha, float beta, hipStream_t stream) {
+  return gate_up(true, q, sq, sorted_tok, H, I, w13, s13p, w_estride, s_estride, slot_map,
+                 seg_start, tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi,
+                 max_tiles, act, limit, alpha, beta, stream);
+}
+
+hipError_t xtu_mx_tri_down(const uint8_t* q, const uint8_t* sq, int H, int I, const void* w2,
+                           const uint8_t* s2p, long w_estride, long s_estride,
+                           const int32_t* slot_map, const int32_t* seg_start,
+                           const int32_t* tile_expert, const int32_t* tile_row0,
+                           const int32_t* expert_tile_start, const int32_t* tile_lo,
+                           const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream) {
+  return down(true, q, sq, H, I, w2, s2p, w_estride, s_estride, slot_map, seg_start, tile_expert,
+              tile_row0, expert_tile_start, tile_lo, tile_hi, max_tiles, y, stream);
 }
 
 }  // extern "C"

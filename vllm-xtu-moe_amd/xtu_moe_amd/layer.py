@@ -482,9 +482,10 @@ def fp8_pair32_use(W, scales_ok=None) -> bool:
     return W.fp8_scales_bounded()
 
 
-# "auto": the exact-pair GEMMs where the 32x32x64 MXFP4 kernel takes the shape
-# (faster than the bf16-operand kernels on DeepSeek-V3 at T=8192), else the
-# bf16-operand kernels; "pair" / "bf16" force one of the two
+# "auto": the 32x32x64 MXFP4 kernel on activation triples (fp6/fp6/fp4
+# pieces, double-rate MFMA) where it takes the shape, else the bf16-operand
+# kernels; "tri" the same; "pair" exact e4m3 pairs (the 32x32x64 kernel where
+# it fits, else the 16x16x128 one); "bf16" the bf16-operand kernels
 MXFP4_PREFILL_DEFAULT = "auto"
 
 
@@ -504,15 +505,23 @@ def pair_gemm(fmt: int, H: int = 0, I: int = 0) -> bool:
     if fmt != FMT_MXFP4:
         return False
     mode = os.environ.get(MXFP4_PREFILL_ENV, MXFP4_PREFILL_DEFAULT)
-    return mode == "pair" or (mode == "auto" and _mx_fits(H, I))
+    return mode == "pair" or (mode in ("auto", "tri") and _mx_fits(H, I))
 
 
 def mx_pair_kernel(fmt: int, H: int, I: int) -> bool:
-    """Whether the exact-pair GEMMs of this layer run on the MXFP4 32x32x64
-    kernel (interleaved activation pairs, step-major scales): MXFP4 on the
-    pair path where the shape fits it (I % 256, H % 512); otherwise the
+    """Whether the GEMMs of this layer run on the MXFP4 32x32x64 kernel
+    (interleaved activation pairs or triples, step-major scales): MXFP4 on
+    the pair path where the shape fits it (I % 256, H % 512); otherwise the
     16x16x128 exact-pair kernel."""
     return int(fmt) == FMT_MXFP4 and pair_gemm(fmt, H, I) and _mx_fits(H, I)
+
+
+def mx_tri(fmt: int, H: int, I: int) -> bool:
+    """Whether the MXFP4 32x32x64 kernel takes activation triples (fp6, fp6,
+    fp4 pieces on the double-rate MFMA; XTU_MXFP4_PREFILL "auto" or "tri")
+    rather than exact e4m3 pairs ("pair")."""
+    mode = os.environ.get(MXFP4_PREFILL_ENV, MXFP4_PREFILL_DEFAULT)
+    return mode in ("auto", "tri") and mx_pair_kernel(fmt, H, I)
 
 
 def gemm_tile_m(fmt: int, int8: bool = False, H: int = 0, I: int = 0, W=None,
@@ -805,17 +814,19 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
                   _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
         return
     if mx_pair_kernel(fmt, H, I):
-        # exact pairs, interleaved, on the MXFP4 32x32x64 kernel
+        # activation triples (double-rate fp6/fp4 MFMA) or exact pairs,
+        # interleaved, on the MXFP4 32x32x64 kernel
+        kind = "tri" if mx_tri(fmt, H, I) else "pair"
         s13p, s2p = W.mx_pair_scales(st)
         xq = _mxpair_bufs("xm", T, H, dev, st)
         aq = _mxpair_bufs("am", A, I, dev, st)
-        _lib.call("xtu_pair_quant_il", _p(x), T, H, *[_p(t) for t in xq], st)
-        _lib.call("xtu_mx_pair_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
+        _lib.call(f"xtu_{kind}_quant_il", _p(x), T, H, *[_p(t) for t in xq], st)
+        _lib.call(f"xtu_mx_{kind}_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
                   _p(W.w13), _p(s13p), 0, 0, _p(slot_map), _p(seg.seg_start),
                   _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi,
                   seg.max_tiles, _p(act), lim, al, be, st)
-        _lib.call("xtu_pair_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
-        _lib.call("xtu_mx_pair_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(s2p), 0, 0,
+        _lib.call(f"xtu_{kind}_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
+        _lib.call(f"xtu_mx_{kind}_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(s2p), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
                   _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
         return
