@@ -265,7 +265,7 @@ __global__ __launch_bounds__(kQThreads, 1) void f8_pair_gemm_kernel(F8PairArgs a
     // reads this variant needs: B 0-3, A row block 0 (4, 5), its scale (8),
     // and with two blocks A row block 1 (6, 7) and its scale (9)
     auto read_k = [&](int n) { return LIVE == 2 ? n : (n < 6 ? n : 8); };
-    constexpr int kR = LIVE == 2 ? kReads : 7;
+    constexpr int kR = LIVE == 2 ? kReads : (LIVE == 1 ? 7 : 0);
     // Step s: the MFMAs of step s (fragments in cur); ISSUE: the loads of
     // step s + LEAD between the first half; NEXT: wait for step s + 1, the
     // barrier, and its fragments (into nxt) between the second half.
@@ -356,8 +356,11 @@ __global__ __launch_bounds__(kQThreads, 1) void f8_pair_gemm_kernel(F8PairArgs a
     step(F_{}, F_{}, T_{}, s, f0, f1);
     step(T_{}, F_{}, F_{}, s + 1, f1, f0);
   };
+  // a wave whose blocks both lie past the tile (tiles of at most 32 rows,
+  // wm = 1) keeps its part of the loads and barriers and computes nothing
   if (two_blocks) run(std::integral_constant<int, 2>{});
-  else run(std::integral_constant<int, 1>{});
+  else if (32 * wm < rows) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, 0>{});
 
   // ---- epilogue: the last block's scale, then the 32x32 result layout
   // (column l % 32, rows 8 (i / 4) + 4 (l / 32) + i % 4)

@@ -266,8 +266,8 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
   }
 
   // ---- fragments of this lane.  Wave w takes the 32-row blocks wm and
-  // wm + 2 of the tile, so a tile of at most 64 rows leaves every wave one
-  // live block (the waves then run the one-block loop below)
+  // wm + 2 of the tile, so a tile of at most 64 rows leaves every wave at
+  // most one live block (the waves then run the one-block loop below)
   const int r32 = lane % 32, h = lane / 32;
   int arow[2];
 #pragma unroll
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
     // reads this variant needs: B 0-7, A row block 0 (8, 9), its scale (12),
     // and with two blocks A row block 1 (10, 11) and its scale (13)
     auto read_k = [&](int n) { return LIVE == 2 ? n : (n < 10 ? n : 12); };
-    constexpr int kR = LIVE == 2 ? kReads : 11;
+    constexpr int kR = LIVE == 2 ? kReads : (LIVE == 1 ? 11 : 0);
     auto step = [&](int s, Frags& cur, Frags& nxt) {
       __builtin_amdgcn_sched_barrier(0);
       int d = 0;
@@ -421,8 +421,11 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
 #pragma unroll
     for (int j = 0; j < M; ++j) mfma_j(f1, j);
   };
+  // a wave whose blocks both lie past the tile (tiles of at most 32 rows,
+  // wm = 1) keeps its part of the loads and barriers and computes nothing
   if (two_blocks) run(std::integral_constant<int, 2>{});
-  else run(std::integral_constant<int, 1>{});
+  else if (32 * wm < rows) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, 0>{});
 
   // ---- epilogue.  32x32 result lane layout: column l % 32, rows
   // 8 (i / 4) + 4 (l / 32) + i % 4
