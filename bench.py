@@ -134,6 +134,30 @@ def bench_default(args):
     print(json.dumps(line), flush=True)
 
 
+def hook_for(cfg, W):
+    """The quant-method hook of this workload's format (XiaotuExperts*) over
+    device weights W, with the routing and SwiGLU attributes the layer would
+    carry: the state process_weights_after_loading leaves (the checkpoint
+    repack is skipped; the weights are already in the kernels' layout)."""
+    import types
+
+    from xtu_moe_amd import mixed_experts as ME
+
+    cls = {"mxfp4": ME.XiaotuExpertsMxfp4, "fp8": ME.XiaotuExpertsFp8,
+           "nvfp4": ME.XiaotuExpertsNvfp4, "bf16": ME.XiaotuExpertsBF16}[cfg["fmt"]]
+    grouped = cfg["router"] == "grouped"
+    lay = types.SimpleNamespace(top_k=cfg["K"], renormalize=True, use_grouped_topk=grouped,
+                                scoring_func="sigmoid" if grouped else "softmax",
+                                num_expert_group=8 if grouped else None,
+                                topk_group=4 if grouped else None,
+                                routed_scaling_factor=2.5 if grouped else 1.0,
+                                swiglu_limit=cfg["limit"] or None)
+    hook = cls()
+    hook._read_layer_attrs(lay)
+    hook._weights = W
+    return hook
+
+
 def bench_one(args):
     """One workload; returns its JSON line (the streamed workload prints its own)."""
     import numpy as np
@@ -259,8 +283,10 @@ def bench_one(args):
         wall = time.time() - wall0
         layer_ms = [a.elapsed_time(b) for a, b in ev]
 
-        # ---- layer chain: CHAIN distinct layers in one graph, time / CHAIN
-        chain_ms = []
+        # ---- layer chain: CHAIN distinct layers in one graph, time / CHAIN;
+        # once through moe_forward, once through the quant-method hook's
+        # apply (the call vLLM makes), each layer's output the next one's input
+        chain_ms, hook_ms = [], []
         chain_active = []
         if graph is not None:
             c_lg = [torch.empty((T, E), dtype=torch.float32, device=dev) for _ in chain_Ws]
@@ -268,50 +294,62 @@ def bench_one(args):
             c_ids = [torch.empty((T, K), dtype=torch.int32, device=dev) for _ in chain_Ws]
             c_wts = [torch.empty((T, K), dtype=torch.float32, device=dev) for _ in chain_Ws]
 
-            def chain_step():
-                xin = x_st
-                for l, Wl in enumerate(chain_Ws):
-                    rt_l = dict(rt, logits=c_lg[l])
-                    moe_forward(xin, c_ids[l], c_wts[l], Wl, swiglu_limit=cfg["limit"],
-                                out=c_out[l], int8=i8, router=rt_l)
-                    xin = c_out[l]
+            def fwd_layer(l, xin):
+                moe_forward(xin, c_ids[l], c_wts[l], chain_Ws[l], swiglu_limit=cfg["limit"],
+                            out=c_out[l], int8=i8, router=dict(rt, logits=c_lg[l]))
+
+            hooks = [hook_for(cfg, Wl) for Wl in chain_Ws] if not i8 else None
+
+            def hook_layer(l, xin):
+                hooks[l].apply(xin, None, None, router_logits=c_lg[l], output=c_out[l])
 
             def chain_load(s):
                 x_st.copy_(xs[s % len(xs)])
                 for l in range(len(chain_Ws)):
                     c_lg[l].copy_(lgs[(s + l) % len(lgs)])
 
-            chain_load(0)
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                for _ in range(2):
+            def time_chain(layer):
+                def chain_step():
+                    xin = x_st
+                    for l in range(len(chain_Ws)):
+                        layer(l, xin)
+                        xin = c_out[l]
+
+                chain_load(0)
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    for _ in range(2):
+                        chain_step()
+                torch.cuda.current_stream().wait_stream(side)
+                cgraph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(cgraph):
                     chain_step()
-            torch.cuda.current_stream().wait_stream(side)
-            cgraph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(cgraph):
-                chain_step()
-            torch.cuda.synchronize()
-            for s in range(args.warmup):
-                chain_load(s)
-                cgraph.replay()
-            torch.cuda.synchronize()
-            cev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for _ in range(args.steps)]
-            for s in range(args.steps):
-                if not args.no_flush:
-                    flush.add_(1.0)
-                chain_load(args.warmup + s)
-                cev[s][0].record()
-                cgraph.replay()
-                cev[s][1].record()
-            torch.cuda.synchronize()
-            chain_ms = [a.elapsed_time(b) / len(chain_Ws) for a, b in cev]
+                torch.cuda.synchronize()
+                for s in range(args.warmup):
+                    chain_load(s)
+                    cgraph.replay()
+                torch.cuda.synchronize()
+                cev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                       for _ in range(args.steps)]
+                for s in range(args.steps):
+                    if not args.no_flush:
+                        flush.add_(1.0)
+                    chain_load(args.warmup + s)
+                    cev[s][0].record()
+                    cgraph.replay()
+                    cev[s][1].record()
+                torch.cuda.synchronize()
+                del cgraph
+                return [a.elapsed_time(b) / len(chain_Ws) for a, b in cev]
+
+            chain_ms = time_chain(fwd_layer)
+            if hooks is not None:
+                hook_ms = time_chain(hook_layer)
             for s in range(args.steps):
                 for l in range(len(chain_Ws)):
                     w_, i_ = route(lgs[(args.warmup + s + l) % len(lgs)], **rkw)
                     chain_active.append(len(torch.unique(i_)) + NS)
-            del cgraph
         # distinct experts per step (algorithmic bytes), re-derived outside timing
         for s in range(args.steps):
             load(args.warmup + s)
@@ -407,6 +445,7 @@ def bench_one(args):
 
         A = T * K + T * NS
         single_ms = float(np.mean(layer_ms))
+        hook_layer_ms = float(np.mean(hook_ms)) if hook_ms else None
         if chain_ms:   # per-layer time inside the layer-chain graph
             layer_ms, n_active = chain_ms, chain_active
         mean_layer = float(np.mean(layer_ms))
@@ -423,9 +462,12 @@ def bench_one(args):
                           graph=graph is not None, wall_s=wall,
                           event_overhead_us=ev_overhead * 1e3, gate_up_bytes=gu_bytes,
                           single_layer_graph_ms=single_ms, int8_activation=bool(i8),
-                          layer_chain=len(chain_Ws) if chain_ms else 1)
+                          layer_chain=len(chain_Ws) if chain_ms else 1,
+                          hook_layer_ms=hook_layer_ms)
         log(f"[bench] T={T}: layer {mean_layer * 1e3:.1f} us ({results[T]['layer_GBs']:.0f} GB/s; "
-            f"single-layer graph {single_ms * 1e3:.1f} us), "
+            f"single-layer graph {single_ms * 1e3:.1f} us"
+            + (f"; through the hook's apply {hook_layer_ms * 1e3:.1f} us" if hook_layer_ms else "")
+            + "), "
             f"gate_up {mean_gu * 1e3:.1f} us ({results[T]['gate_up_GBs']:.0f} GB/s, "
             f"{results[T]['gate_up_TFLOPs']:.0f} TFLOP/s), |D|={mean_active:.1f}")
 
