@@ -360,14 +360,17 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     // a skipped pair reads row 0 and is not added
     bool ok[KC];
     f32x4_t v[KC + NSC];
+    // y rows are read exactly once: streaming (nontemporal) loads
 #pragma unroll
     for (int j = 0; j < KC; ++j) {
       ok[j] = pos[j] < trash && w[j] != 0.f;
-      v[j] = *reinterpret_cast<const f32x4_t*>(y + (long)(ok[j] ? pos[j] : 0) * H + h);
+      v[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4_t*>(y + (long)(ok[j] ? pos[j] : 0) * H + h));
     }
 #pragma unroll
     for (int s = 0; s < NSC; ++s)
-      v[KC + s] = *reinterpret_cast<const f32x4_t*>(y + (long)pos[KC + s] * H + h);
+      v[KC + s] = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4_t*>(y + (long)pos[KC + s] * H + h));
 #pragma unroll
     for (int j = 0; j < KC; ++j) acc = ok[j] ? acc + w[j] * v[j] : acc;
 #pragma unroll
@@ -377,12 +380,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       const int pos = inv[t * K + k];
       const float w = wts[t * K + k];
       if (pos >= trash || w == 0.f) continue;
-      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(y + (long)pos * H + h);
+      const f32x4_t v =
+          __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(y + (long)pos * H + h));
       acc += w * v;
     }
     for (int s = 0; s < NS; ++s) {
-      const f32x4_t v =
-          *reinterpret_cast<const f32x4_t*>(y + (long)inv[T * K + t * NS + s] * H + h);
+      const f32x4_t v = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4_t*>(y + (long)inv[T * K + t * NS + s] * H + h));
       acc += v;
     }
   }
