@@ -58,17 +58,18 @@ typedef int i32x8_t __attribute__((ext_vector_type(8)));
 constexpr int kPM = 128;            // rows per m tile
 constexpr int kPN = 512;            // weight rows per work item
 constexpr int kPThreads = 256;
-constexpr int kStages = 3;
 
 constexpr int kLA = kPM * 128;      // A codes [row][8 pieces of 16 B]
 constexpr int kLB = kPN * 32;       // B codes [col][2 pieces of 16 B]
 constexpr int kLBS = kPN * 2;       // B scales [col][2]
 constexpr int kStage = kLA + kLB + kLBS;
-constexpr int kStagesBytes = kStages * kStage;
 constexpr int kLdsMax = 160 * 1024;
 
-// the activation-scale area of 128 rows, then the tile's 128 source rows
-__host__ __device__ constexpr int lds_bytes(int K) { return kStagesBytes + asc_bytes(K, kPM) + 4 * kPM; }
+// stages, the activation-scale area of 128 rows, then the tile's 128 source
+// rows
+__host__ __device__ constexpr int lds_bytes(int stages, int K) {
+  return stages * kStage + asc_bytes(K, kPM) + 4 * kPM;
+}
 
 constexpr int kLoadsPerStep = 9;    // loads per lane and step (A 4, B 4, B scales 1)
 
@@ -155,8 +156,9 @@ __global__ __launch_bounds__(256) void mx_pair_scales_kernel(const uint8_t* __re
 // TRI: activation triples (fp6, fp6, fp4 pieces, mx_tri_quant_kernel) on
 // the double-rate fp6 / fp4 x fp4 MFMA, three MFMAs per 32 x 32 block and
 // step; else exact e4m3 pairs, two MFMAs at the fp8 rate.
-template <bool GU, bool TRI>
+template <bool GU, bool TRI, int STAGES>
 __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a) {
+  constexpr int LEAD = STAGES - 1;   // steps of loads in flight ahead of the MFMAs
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
   // ---- work item
@@ -184,7 +186,7 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
   const int lane = tid % 64;
   const int wm = w & 1, wn = w >> 1;
   const int ascs = asc_stride(K);
-  uint8_t* asc = lds + kStagesBytes;
+  uint8_t* asc = lds + STAGES * kStage;
   int32_t* srow = reinterpret_cast<int32_t*>(asc + asc_bytes(K, kPM));
 
   // source row of every tile row (rows past the tile repeat its last row)
@@ -352,17 +354,19 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
                                                                     0, sa, 0, f.sb[cb]);
     }
   };
-  // ---- pipeline (nsteps = K / 64 is even and >= 4)
-  issue(0, 0);
-  issue(1, 1);
-  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoadsPerStep));   // scales, step 0 landed
+  // ---- pipeline (nsteps = K / 64 is even and >= 4): the loads of the
+  // first LEAD steps, then step 0's fragments
+#pragma unroll
+  for (int p = 0; p < LEAD; ++p) issue(p, p);
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0((LEAD - 1) * kLoadsPerStep));   // scales, step 0 landed
   __syncthreads();
-  // Step s < nsteps - 2 (LIVE row blocks, 16 LIVE MFMAs): the first half of
-  // the MFMAs of step s with the loads of step s + 2 issued between them,
-  // the wait and barrier, then the second half with the fragment reads of
-  // step s + 1 between them (the order is pinned: no instruction moves
-  // across a sched_barrier).  MFMA j: row block j / kBlockMfma, piece
-  // (j / 8) % kPieces, B block j % 8.
+  // Step s (LIVE row blocks, kBlockMfma LIVE MFMAs): the first half of its
+  // MFMAs with the loads of step s + LEAD issued between them (ISSUE), the
+  // wait and barrier, then the second half with the fragment reads of step
+  // s + 1 between them (NEXT; the order is pinned: no instruction moves
+  // across a sched_barrier).  The flags are compile-time, so the
+  // steady-state loop has no branch between its MFMAs.  MFMA j: row block
+  // j / kBlockMfma, piece (j / 8) % kPieces, B block j % 8.
   auto run = [&](auto live_c) {
     constexpr int LIVE = decltype(live_c)::value;
     constexpr int M = kBlockMfma * LIVE, H2 = M / 2;
@@ -371,55 +375,67 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
     // and with two blocks A row block 1 (10, 11) and its scale (13)
     auto read_k = [&](int n) { return LIVE == 2 ? n : (n < 10 ? n : 12); };
     constexpr int kR = LIVE == 2 ? kReads : (LIVE == 1 ? 11 : 0);
-    auto step = [&](int s, Frags& cur, Frags& nxt) {
+    auto step = [&](auto issue_c, auto next_c, int s, Frags& cur, Frags& nxt) {
+      constexpr bool ISSUE = decltype(issue_c)::value;
+      constexpr bool NEXT = decltype(next_c)::value;
+      const int sn = s + LEAD, stn = sn % STAGES;
       __builtin_amdgcn_sched_barrier(0);
       int d = 0;
 #pragma unroll
       for (int j = 0; j < H2; ++j) {
         mfma_j(cur, j);
-        if ((LIVE == 1 || j % 2 == 1) && d < kLoadsPerStep) issue_one(s + 2, (s + 2) % kStages, d++);
+        if constexpr (ISSUE) {
+          if ((LIVE == 1 || j % 2 == 1) && d < kLoadsPerStep) issue_one(sn, stn, d++);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
+      if constexpr (ISSUE) {
 #pragma unroll
-      for (; d < kLoadsPerStep; ++d) issue_one(s + 2, (s + 2) % kStages, d);
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoadsPerStep));   // step s + 1 landed
-      __syncthreads();
-      __builtin_amdgcn_sched_barrier(0);
-      const uint8_t* buf = lds + ((s + 1) % kStages) * kStage;
-      int n = 0;
-#pragma unroll
-      for (int j = H2; j < M; ++j) {
-        if (n < kR) read_one(buf, s + 1, nxt, read_k(n++));
-        if (LIVE == 1 && n < kR) read_one(buf, s + 1, nxt, read_k(n++));
-        mfma_j(cur, j);
-        __builtin_amdgcn_sched_barrier(0);
+        for (; d < kLoadsPerStep; ++d) issue_one(sn, stn, d);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NEXT) {
+        // step s + 1 landed: with ISSUE the later LEAD - 1 steps may still
+        // be in flight; in the last steps wait for everything
+        if constexpr (ISSUE) __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0((LEAD - 1) * kLoadsPerStep));
+        else __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* buf = lds + ((s + 1) % STAGES) * kStage;
+        int n = 0;
 #pragma unroll
-      for (; n < kR; ++n) read_one(buf, s + 1, nxt, read_k(n));
+        for (int j = H2; j < M; ++j) {
+          if (n < kR) read_one(buf, s + 1, nxt, read_k(n++));
+          if (LIVE == 1 && n < kR) read_one(buf, s + 1, nxt, read_k(n++));
+          mfma_j(cur, j);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (; n < kR; ++n) read_one(buf, s + 1, nxt, read_k(n));
+      } else {
+#pragma unroll
+        for (int j = H2; j < M; ++j) mfma_j(cur, j);
+      }
     };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
     Frags f0, f1;
 #pragma unroll
     for (int n = 0; n < kR; ++n) read_one(lds, 0, f0, read_k(n));
-    for (int s = 0; s < nsteps - 2; s += 2) {
-      step(s, f0, f1);
-      step(s + 1, f1, f0);
+    int s = 0;
+    for (; s + 1 + LEAD < nsteps; s += 2) {   // both steps issue
+      step(T_{}, T_{}, s, f0, f1);
+      step(T_{}, T_{}, s + 1, f1, f0);
     }
-    // step nsteps - 2: no more loads to issue
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < H2; ++j) mfma_j(f0, j);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int n = 0; n < kR; ++n) read_one(lds + ((nsteps - 1) % kStages) * kStage, nsteps - 1, f1, read_k(n));
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = H2; j < M; ++j) mfma_j(f0, j);
-#pragma unroll
-    for (int j = 0; j < M; ++j) mfma_j(f1, j);
+    // the rest (nsteps - s is even): with LEAD 3 and four steps left, the
+    // first of them issues the last loads
+    if (LEAD == 3 && nsteps - s == 4) {
+      step(T_{}, T_{}, s, f0, f1);
+      step(F_{}, T_{}, s + 1, f1, f0);
+      s += 2;
+    }
+    step(F_{}, T_{}, s, f0, f1);
+    step(F_{}, F_{}, s + 1, f1, f0);
   };
   // a wave whose blocks both lie past the tile (tiles of at most 32 rows,
   // wm = 1) keeps its part of the loads and barriers and computes nothing
@@ -456,10 +472,20 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
 
 // Shapes the kernel takes: gate/up N blocks of 256, down of 512 (so K = H
 // and K = I are multiples of 256: an even number of 64-k steps, at least 4),
-// LDS for the activation scales of 128 rows.
+// LDS for three stages and the activation scales of 128 rows.
 bool mx_fits(int H, int I) {
-  return H > 0 && I > 0 && I % 256 == 0 && H % 512 == 0 && lds_bytes(H) <= kLdsMax &&
-         lds_bytes(I) <= kLdsMax;
+  return H > 0 && I > 0 && I % 256 == 0 && H % 512 == 0 && lds_bytes(3, H) <= kLdsMax &&
+         lds_bytes(3, I) <= kLdsMax;
+}
+
+// three stages (loads two steps ahead); a fourth stage for the down pass
+// (K = 2048 leaves LDS for it) measured no faster at DeepSeek-V3 T = 8192
+constexpr int kStages = 3;
+
+template <bool GU, bool TRI>
+hipError_t launch_k(dim3 g, int K, const MxPairArgs& a, hipStream_t stream) {
+  mx_pair_gemm_kernel<GU, TRI, kStages><<<g, kPThreads, lds_bytes(kStages, K), stream>>>(a);
+  return hipPeekAtLastError();
 }
 
 hipError_t launch(bool gu, bool tri, const MxPairArgs& a, int max_tiles, hipStream_t stream) {
@@ -468,12 +494,11 @@ hipError_t launch(bool gu, bool tri, const MxPairArgs& a, int max_tiles, hipStre
   if (grid >= (1L << 31)) return hipErrorInvalidValue;
   if (grid == 0) return hipSuccess;
   const dim3 g((unsigned)grid);
-  const size_t lds = lds_bytes(gu ? a.H : a.I);
-  if (gu && tri) mx_pair_gemm_kernel<true, true><<<g, kPThreads, lds, stream>>>(a);
-  else if (gu) mx_pair_gemm_kernel<true, false><<<g, kPThreads, lds, stream>>>(a);
-  else if (tri) mx_pair_gemm_kernel<false, true><<<g, kPThreads, lds, stream>>>(a);
-  else mx_pair_gemm_kernel<false, false><<<g, kPThreads, lds, stream>>>(a);
-  return hipPeekAtLastError();
+  const int K = gu ? a.H : a.I;
+  if (gu && tri) return launch_k<true, true>(g, K, a, stream);
+  if (gu) return launch_k<true, false>(g, K, a, stream);
+  if (tri) return launch_k<false, true>(g, K, a, stream);
+  return launch_k<false, false>(g, K, a, stream);
 }
 
 }  // namespace
