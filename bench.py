@@ -121,7 +121,7 @@ def bench_default(args):
         gc.collect()
         torch.cuda.empty_cache()
         b = argparse.Namespace(**vars(args))
-        b.workload, b.no_cpu_baseline, b.no_traffic = wl, True, True
+        b.workload, b.no_cpu_baseline = wl, True
         b.steps, b.warmup = min(args.steps, PREFILL_STEPS), min(args.warmup, 2)
         pl = bench_one(b)
         r = pl["config"]["per_T"]["8192"]
@@ -474,6 +474,22 @@ def bench_one(args):
     Th = max(cfg["Ts"])
     r = results[Th]
     decode_head = Th <= 16
+
+    def prefill_traffic(roof, kernel):
+        """HBM bytes of one prefill gate/up launch from the counter runs, next
+        to its algorithmic bytes (weights of the distinct experts once, the
+        quantised activation rows with their scales, the act rows written)."""
+        if args.no_traffic:
+            return
+        tr = measure_traffic(args.workload, Th, timeout=300, kernel=kernel)
+        if tr is None:
+            return
+        roof["traffic"] = tr["bytes"]
+        roof["traffic_detail"] = tr
+        if tr.get("distinct_experts"):
+            tr["algorithmic_bytes"] = (tr["distinct_experts"] * e_bytes13 + Th * (2 * H + H // 32)
+                                       + (Th * K + Th * NS) * I * 2)
+
     if decode_head:
         roof = dict(bound="hbm", achieved=r["gate_up_GBs"], peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=r["gate_up_GBs"] / HBM_PEAK_GBS, traffic=None,
@@ -496,6 +512,7 @@ def bench_one(args):
                     mfma_issue_frac=3.0 * ach / PEAK_TFLOPS["fp4"],
                     frac_of_fp8_peak=ach / PEAK_TFLOPS["fp8"],
                     frac_of_bf16_peak=ach / PEAK_TFLOPS["bf16"])
+        prefill_traffic(roof, "mx_pair_gemm_kernel<true")
     elif pair_gemm(fmt, H, I) and not cfg["int8"]:
         # scaled MFMA with an e4m3 A (FP8: e4m3 B; MXFP4: e2m1 B), which runs
         # at the fp8 rate; every algorithmic product is two MFMA products
@@ -508,6 +525,8 @@ def bench_one(args):
                             else "gemm8_kernel"),
                     mfma_issue_frac=2.0 * ach / PEAK_TFLOPS["fp8"],
                     frac_of_bf16_peak=ach / PEAK_TFLOPS["bf16"])
+        if roof["kernel"] == "f8_pair_gemm_kernel":
+            prefill_traffic(roof, "f8_pair_gemm_kernel<true")
         if cfg["fmt"] == "mxfp4":
             roof["frac_of_fp4_peak"] = ach / PEAK_TFLOPS["fp4"]
     else:
@@ -562,13 +581,16 @@ COPY_BYTES = 256 << 20   # calibration copy for the memory counters
 
 def pmc_child(args, cfg, T):
     """Run under rocprofv3 --pmc by measure_traffic: three cold-cache launches
-    of the decode gate/up kernel at T tokens, then one device-to-device copy
-    of COPY_BYTES (the counter calibration)."""
+    of the dominant gate/up kernel at T tokens (the decode kernel for T <= 16;
+    the MXFP4 triple or FP8 pair prefill kernel otherwise, after its
+    quantiser), then one device-to-device copy of COPY_BYTES (the counter
+    calibration)."""
     import torch
 
     from xtu_moe_amd import _lib
     from xtu_moe_amd import formats as F
-    from xtu_moe_amd.layer import _p, _stream, route, segmentation
+    from xtu_moe_amd.layer import (_mxpair_bufs, _p, _stream, fp8_pair32_use, gemm_tile_m,
+                                   mx_tri, route, segmentation)
     from xtu_moe_amd.synthetic import synth_layer
 
     fmt = F.fmt_of(cfg["fmt"])
@@ -582,15 +604,35 @@ def pmc_child(args, cfg, T):
     lg = torch.randn((T, E), generator=gen, device=dev)
     rkw = dict(top_k=K, scoring="sigmoid", n_group=8, topk_group=4, routed_scaling_factor=2.5)
     w_, i_ = route(lg, **rkw)
-    seg = segmentation(T, K, E, NS, 128, dev).run(i_, w_)
+    prefill = T > 16
+    bm = gemm_tile_m(fmt, False, H, I, W) if prefill else 128
+    seg = segmentation(T, K, E, NS, bm, dev).run(i_, w_)
     act = torch.empty((T * K + T * NS, I), dtype=torch.bfloat16, device=dev)
     flush = torch.empty(256 << 20, dtype=torch.float32, device=dev)
     st = _stream()
+    if prefill:
+        if mx_tri(fmt, H, I):
+            kind, s13 = "mx_tri", W.mx_pair_scales(st)[0]
+            qname = "xtu_tri_quant_il"
+        elif fp8_pair32_use(W):
+            kind, s13, qname = "f8_pair", W.s13, "xtu_pair_quant_il"
+        else:
+            raise SystemExit("no counter child for this prefill kernel")
+        xq = _mxpair_bufs("xm", T, H, dev, st)
+        _lib.call(qname, _p(x), T, H, *[_p(t) for t in xq], st)
+        lo, hi = seg.tile_range_ptrs(0, E + NS)
     for _ in range(3):
         flush.add_(1.0)
-        _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13), _p(W.gs13),
-                  0, 0, 0, _p(seg.sorted_tok), _p(seg.seg_start), _p(seg.active), 0,
-                  _p(seg.n_active), min(E, T * K) + NS, _p(act), cfg["limit"], 1.0, 0.0, st)
+        if prefill:
+            _lib.call(f"xtu_{kind}_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
+                      _p(W.w13), _p(s13), 0, 0, 0, _p(seg.seg_start), _p(seg.tile_expert),
+                      _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi, seg.max_tiles,
+                      _p(act), cfg["limit"], 1.0, 0.0, st)
+        else:
+            _lib.call("xtu_decode_gate_up", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13),
+                      _p(W.gs13), 0, 0, 0, _p(seg.sorted_tok), _p(seg.seg_start),
+                      _p(seg.active), 0, _p(seg.n_active), min(E, T * K) + NS, _p(act),
+                      cfg["limit"], 1.0, 0.0, st)
     torch.cuda.synchronize()
     src = torch.ones(COPY_BYTES, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
@@ -600,11 +642,12 @@ def pmc_child(args, cfg, T):
     print(f"[pmc-child] distinct experts {len(torch.unique(i_)) + NS}", flush=True)
 
 
-def measure_traffic(workload, T, timeout=150):
-    """HBM bytes per launch of the decode gate/up kernel from two rocprofv3
-    counter runs of pmc_child (FETCH_SIZE, then WRITE_SIZE, in KiB per
-    dispatch), each scaled by the same counter's reading for a device copy of
-    known size.  None when rocprofv3 is unavailable or a run fails."""
+def measure_traffic(workload, T, timeout=150, kernel="decode_gate_up"):
+    """HBM bytes per launch of the gate/up kernel whose name contains `kernel`
+    from two rocprofv3 counter runs of pmc_child (FETCH_SIZE, then WRITE_SIZE,
+    in KiB per dispatch), each scaled by the same counter's reading for a
+    device copy of known size.  None when rocprofv3 is unavailable or a run
+    fails."""
     import csv
     import shutil
     import subprocess
@@ -636,16 +679,17 @@ def measure_traffic(workload, T, timeout=150):
                         path = os.path.join(root, f)
             if path is None:
                 return None
-            kern, copy = [], []
-            for row in csv.DictReader(open(path)):
-                name, v = row["Kernel_Name"], float(row["Counter_Value"]) * 1024.0
-                if "decode_gate_up" in name:
-                    kern.append(v)
-                elif "copyBuffer" in name or "copy" in name.lower():
-                    copy.append(v)
-            if not kern or not copy or max(copy) <= 0:
+            # the calibration copy is the first copy dispatched after the
+            # last launch of the kernel (the weight synthesis before them
+            # issues copies of its own)
+            rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"]))
+            kern = [float(r["Counter_Value"]) * 1024.0 for r in rows if kernel in r["Kernel_Name"]]
+            last = max((i for i, r in enumerate(rows) if kernel in r["Kernel_Name"]), default=-1)
+            copy = [float(r["Counter_Value"]) * 1024.0 for r in rows[last + 1:]
+                    if "copy" in r["Kernel_Name"].lower()][:1]
+            if not kern or not copy or copy[0] <= 0:
                 return None
-            factor = COPY_BYTES / max(copy)
+            factor = COPY_BYTES / copy[0]
             res[ctr] = dict(raw=sum(kern) / len(kern), factor=factor,
                             bytes=sum(kern) / len(kern) * factor)
     except (OSError, subprocess.SubprocessError, ValueError, KeyError) as exc:
