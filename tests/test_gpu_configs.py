@@ -246,9 +246,10 @@ def test_ds_v3_mxfp4_prefill_t8192(mode, monkeypatch):
 
 @pytest.mark.parametrize("T", [40, 700])
 def test_mxfp4_prefill_pair_and_bf16_paths(T, monkeypatch):
-    """MXFP4 prefill on the exact-pair fp4 MFMA and on the bf16-operand GEMM
-    (XTU_MXFP4_PREFILL=bf16): both against the oracle, with a SwiGLU clamp
-    and a shared expert."""
+    """MXFP4 prefill at a shape the 32x32x64 kernel does not take (I = 384):
+    "pair" runs the 16x16x128 exact-pair kernel, "bf16" the bf16-operand
+    GEMM, and "tri" (the default's mode) falls back to the bf16-operand GEMM;
+    each against the oracle, with a SwiGLU clamp and a shared expert."""
     E, NS, H, I, K = 24, 1, 768, 384, 4
     d = make_dense_layer(F.FMT_MXFP4, E + NS, H, I, seed=21)
     W = ExpertWeights.from_dense(F.FMT_MXFP4, d["w13"], d["s13"], d["w2"], d["s2"], n_shared=NS,
@@ -259,7 +260,7 @@ def test_mxfp4_prefill_pair_and_bf16_paths(T, monkeypatch):
     x = torch.randn((T, H), generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
     ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d), bf16_tensor_to_bits(x), ids,
                        wts, E, NS, H, I, limit=4.0)
-    for mode in ("pair", "bf16"):
+    for mode in ("pair", "bf16", "tri"):
         monkeypatch.setenv(L.MXFP4_PREFILL_ENV, mode)
         assert L.pair_gemm(F.FMT_MXFP4, H, I) == (mode == "pair")
         out = moe_forward(x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(wts).to(DEV),

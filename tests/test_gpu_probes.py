@@ -111,7 +111,8 @@ def test_exp_sigmoid_bit_exact():
 
 def test_scaled_mfma_fp8_a_fp4_b_layout():
     """v_mfma_scale_f32_16x16x128_f8f6f4 with an e4m3 A and an e2m1 B, the
-    layout the MXFP4 prefill GEMM relies on: A lane 16q + r is row r with
+    layout the 16x16x128 exact-pair kernel relies on (MXFP4 and FP8 prefill
+    at shapes the 32x32x64 kernels do not take): A lane 16q + r is row r with
     bytes 0..15 = k 16q.. and bytes 16..31 = k 64 + 16q..; B lane 16g + c is
     column c with nibble j (low nibble first) = k 32g + j -- one P16 MXFP4
     chunk; the scale byte of row r (column c) for the 32-k block b comes from

@@ -495,10 +495,11 @@ def _mx_fits(H: int, I: int) -> bool:
 
 def pair_gemm(fmt: int, H: int = 0, I: int = 0) -> bool:
     """Whether the grouped GEMMs of this format (layer shape H, I) run on
-    the scaled fp8/fp4 MFMA with exact activation pairs: FP8 always; MXFP4
-    per XTU_MXFP4_PREFILL (default MXFP4_PREFILL_DEFAULT), else the
-    bf16-operand kernels (the e2m1 x e8m0 products are exact in bf16 either
-    way)."""
+    the scaled f8f6f4 MFMA: FP8 always (exact e4m3 activation pairs); MXFP4
+    per XTU_MXFP4_PREFILL (default MXFP4_PREFILL_DEFAULT: activation triples
+    where the 32x32x64 kernel takes the shape, exact pairs with "pair"),
+    else the bf16-operand kernels (the e2m1 x e8m0 products are exact in
+    bf16 either way)."""
     fmt = int(fmt)
     if fmt == FMT_FP8:
         return True
