@@ -266,3 +266,8 @@ def test_engine_shard_abi_reassembles_device_layout(monkeypatch):
     # bad requests return 0, as the reference's do
     assert eng.copy_hostbuf_to_device(0, 5, w13.data_ptr(), st) == 0
     assert eng.copy_hostbuf_to_device_2d(0, 0, 0, w13.data_ptr(), e13, 2 * c13, c13, E + 1, st) == 0
+    # negative or zero sizes and pitches are refused before any copy is queued
+    for bad in ((-1, c13, e13, 2 * c13), (E, -c13, e13, 2 * c13), (E, c13, -e13, 2 * c13),
+                (E, c13, e13, -2 * c13), (0, c13, e13, 2 * c13)):
+        h, wdt, dp, sp = bad
+        assert eng.copy_hostbuf_to_device_2d(0, 0, 0, w13.data_ptr(), dp, sp, wdt, h, st) == 0

@@ -124,3 +124,68 @@ def test_routed_layer_graph_replays_match_eager(case):
         np.testing.assert_array_equal(out_st.view(torch.int16).cpu().numpy(),
                                       eager.view(torch.int16).cpu().numpy())
         del junk
+
+
+def test_graph_replay_after_eager_calls_on_many_streams():
+    """A layer captured into a graph, then eager calls of larger batches on
+    forty fresh streams (more than torch's stream pool, so one of them is
+    the capture stream again and its scratch grows), then replays: each
+    replay equals the eager result of the captured batch bit for bit, and
+    that result matches the oracle (scratch a graph holds is never handed
+    back to the allocator)."""
+    import oracle
+    from helpers import bf16_tensor_to_bits, check_close, dense_to_numpy, make_dense_layer
+    dev = torch.device("cuda")
+    fmt, H, I, E, K, T = F.FMT_BF16, 1024, 512, 8, 2, 128
+    d = make_dense_layer(fmt, E, H, I, seed=41)
+    W = L.ExpertWeights.from_dense(fmt, d["w13"], d["s13"], d["w2"], d["s2"], device=dev)
+    g = torch.Generator(device=dev).manual_seed(2)
+    x_st = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+    lg_st = torch.randn((T, E), generator=g, device=dev)
+    ids_st = torch.empty((T, K), dtype=torch.int32, device=dev)
+    wts_st = torch.empty((T, K), dtype=torch.float32, device=dev)
+    out_st = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    rt = dict(scoring="softmax", renormalize=True, logits=lg_st)
+
+    def step():
+        moe_forward(x_st, ids_st, wts_st, W, out=out_st, router=rt)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    step()
+    torch.cuda.synchronize()
+    eager = out_st.clone()
+    ids_np, wts_np = ids_st.cpu().numpy(), wts_st.cpu().numpy()
+    big = 700
+    xb = torch.randn((big, H), generator=g, device=dev).to(torch.bfloat16)
+    lb = torch.randn((big, E), generator=g, device=dev)
+    for i in range(40):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            Tb = big - 13 * (i % 7)
+            ib = torch.empty((Tb, K), dtype=torch.int32, device=dev)
+            wb = torch.empty((Tb, K), dtype=torch.float32, device=dev)
+            moe_forward(xb[:Tb], ib, wb, W, router=dict(rt, logits=lb[:Tb]))
+        torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out_st.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out_st.view(torch.int16).cpu().numpy(),
+                                      eager.view(torch.int16).cpu().numpy())
+        junk = torch.randn(1 << 20, device=dev).sum()
+        del junk
+    dn = dense_to_numpy(fmt, d)
+    ref = oracle.moe_layer(fmt, bf16_tensor_to_bits(x_st), ids_np, wts_np, E, 0, H, I,
+                           dn["w13"], dn["s13"], dn["w2"], dn["s2"])
+    check_close(eager.float().cpu().numpy(), ref, bf16_out=True, what="captured layer")

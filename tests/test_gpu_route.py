@@ -181,6 +181,34 @@ def test_lane_softmax_route_segment_bit_exact(T, E, K, renorm):
         np.testing.assert_array_equal(getattr(seg, k).cpu().numpy()[: seg.A], ref[k])
 
 
+@pytest.mark.parametrize("NS", [55, 56, 60])
+def test_lane_softmax_with_many_shared_buckets(NS):
+    """Softmax over 8 experts with enough shared experts that the buckets
+    (E + NS + 1) pass the ballot segmentation's 64: NS = 55 still fits it,
+    56 and 60 take the counting-sort segmentation.  Routing and the whole
+    segmentation bit-exact against the oracle."""
+    T, E, K = 7, 8, 2
+    rng = np.random.default_rng(NS)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[::3, 1] = logits[::3, 4]
+    dev = torch.device("cuda")
+    seg = L.segmentation(T, K, E, NS, 16, dev)
+    assert seg.small
+    ids = torch.empty((T, K), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, K), dtype=torch.float32, device=dev)
+    seg.run_small(0, ids, wts, logits=torch.from_numpy(logits).to(dev))
+    torch.cuda.synchronize()
+    rids, rwts = oracle.route_softmax_topk(logits, K, renormalize=True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_array_equal(wts.cpu().numpy().view(np.uint32), rwts.view(np.uint32))
+    ref = oracle.segment(rids, rwts, E, NS, True)
+    np.testing.assert_array_equal(seg.seg_start.cpu().numpy(), ref["seg_start"])
+    for k in ("sorted_pair", "sorted_tok", "inv"):
+        np.testing.assert_array_equal(getattr(seg, k).cpu().numpy()[: seg.A], ref[k])
+    np.testing.assert_array_equal(seg.sorted_wts.cpu().numpy()[: seg.A].view(np.uint32),
+                                  ref["sorted_wts"].view(np.uint32))
+
+
 @pytest.mark.parametrize("case", ["grouped_ties_bias", "softmax_ties", "given_ids_idmap",
                                   "grouped_bm4"])
 def test_tiny_route_segment_edge_cases(case):

@@ -139,7 +139,7 @@ def test_split_layer_matches_oracle(fmt):
         torch.cuda.synchronize()
         check_close(out.cpu().numpy(), _oracle(fmt, d, x, ids, wts, E, NS, H, I, limit),
                     bf16_out=False, what=f"{F.FMT_NAMES[fmt]} split after a swap")
-        assert split.mask.hits() > 0
+        assert split.mask.hits().item() > 0
     finally:
         torch.cuda.synchronize()
         cpu.close()

@@ -168,3 +168,26 @@ def test_slot_planes_size_what_is_derived_from_them():
     src = inspect.getsource(ExpertWeights.mx_pair_scales) + inspect.getsource(
         ExpertWeights.int8_planes)
     assert "self.n_experts" not in src
+
+
+def test_pitched_copy_refuses_bad_sizes_before_any_copy():
+    """copy_hostbuf_to_device_2d returns 0 for zero or negative heights,
+    widths and pitches and for spans past the host buffer, without queuing a
+    copy (the reference's 0-on-error contract)."""
+    from xtu_moe_amd import formats as F
+    from xtu_moe_amd.host_store import HostExpertStore
+    from xtu_moe_amd.layer import ExpertWeights
+    H, I, E = 256, 128, 3
+    g = torch.Generator().manual_seed(0)
+    w13 = torch.randn((E, 2 * I, H), generator=g) * 0.02
+    w2 = torch.randn((E, H, I), generator=g) * 0.02
+    c13, s13 = F.quantize_mxfp4(w13)
+    c2, s2 = F.quantize_mxfp4(w2)
+    W = ExpertWeights.from_dense(F.FMT_MXFP4, c13, s13, c2, s2, device="cpu")
+    st = HostExpertStore.from_weights(W, pin=False)
+    c = st.w13_cbytes
+    for h, wdt, dp, sp, off in ((-1, c, c, 2 * c, 0), (E, -c, c, 2 * c, 0), (E, c, -c, 2 * c, 0),
+                                (E, c, c, -2 * c, 0), (0, c, c, 2 * c, 0), (E, 0, c, 2 * c, 0),
+                                (E, c, c, 2 * c, -1), (E + 1, c, c, 2 * c, 0),
+                                (E, 2 * c + 1, 4 * c, 2 * c, 0)):
+        assert st.copy_hostbuf_to_device_2d(0, 0, off, 1 << 40, dp, sp, wdt, h) == 0

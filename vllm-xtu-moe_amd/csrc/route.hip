@@ -865,8 +865,9 @@ hipError_t launch_small(const SmallArgs& a, hipStream_t stream) {
     if (few && A <= 256) route_seg_small_kernel<2, 256, false, true><<<1, 256, 0, stream>>>(a);
     else if (few) route_seg_small_kernel<2, 1024, false, true><<<1, 1024, 0, stream>>>(a);
     else route_seg_small_kernel<MODE, 256><<<1, 256, 0, stream>>>(a);
-  } else if (MODE == 0 && a.E <= kLaneE && a.K <= kLaneK) {
-    // few experts: one thread per token, no routing barriers (few buckets)
+  } else if (MODE == 0 && a.E <= kLaneE && a.K <= kLaneK && few) {
+    // few experts and few buckets (shared experts included): one thread per
+    // token, no routing barriers, the ballot segmentation
     if (A <= 256) route_seg_small_kernel<0, 256, true, true><<<1, 256, 0, stream>>>(a);
     else route_seg_small_kernel<0, 1024, true, true><<<1, 1024, 0, stream>>>(a);
   } else {

@@ -39,6 +39,10 @@ hipError_t xtu_copy_2d(void* dst, size_t dpitch, const void* src, size_t spitch,
   XTU_CHECK_ARG(width <= dpitch && width <= spitch);
   XTU_CHECK_ARG(width == 0 || height == 0 || (dst && src));
   if (width == 0 || height == 0) return hipSuccess;
+  // the last row ends at (height - 1) * pitch + width on either side: reject
+  // sizes whose span does not fit a size_t (a negative count cast to size_t)
+  const size_t kMax = ~size_t(0);
+  XTU_CHECK_ARG(height - 1 <= (kMax - width) / spitch && height - 1 <= (kMax - width) / dpitch);
   return hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyDefault, stream);
 }
 

@@ -25,6 +25,23 @@ def _p(t) -> int:
     return int(t.data_ptr())
 
 
+_SIDE: dict = {}
+
+
+def side_stream(device) -> torch.cuda.Stream:
+    """One side stream per device, shared by every split layer: the layers
+    run one after another on the main stream, and each forks onto the side
+    stream after the previous layer joined back, so one stream orders them
+    all and the library's per-stream scratch is held once, not per layer."""
+    dev = torch.device(device)
+    key = str(dev)
+    s = _SIDE.get(key)
+    if s is None:
+        s = torch.cuda.Stream(device=dev)
+        _SIDE[key] = s
+    return s
+
+
 def pin_split(ids, wts, slotmap, n_local: int, hits=None, out=None):
     """(cpu_ids, cpu_w, part_ids, part_w), each shaped like ids:
     with bad = id < 0 or id >= n_local, sl = slotmap[id], res = !bad and
@@ -78,8 +95,11 @@ class PinMaskFused:
         self.part_w = part_w.view(shp)
         return cpu_ids.view(shp), cpu_w.view(shp), part_ids.view(shp)
 
-    def hits(self) -> int:
-        return int(self._hits.item())
+    def hits(self) -> torch.Tensor:
+        """The device int64 count of resident pairs since the last reset, as
+        the reference returns it (pin_mask_triton.py:146-148): callers read
+        it with ``.item()`` and reset it with ``.zero_()``."""
+        return self._hits
 
 
 class PoolSplitLayer:
@@ -92,7 +112,7 @@ class PoolSplitLayer:
             raise ValueError("pool and host engine must be the same layer shape")
         self.pool, self.cpu = pool, cpu
         self.device = torch.device(device) if device is not None else pool.dev
-        self.side = torch.cuda.Stream(device=self.device)
+        self.side = side_stream(self.device)
         self.mask = PinMaskFused(self.device)
         self.ev0, self.ev_mask, self.ev_done = (torch.cuda.Event(), torch.cuda.Event(),
                                                 torch.cuda.Event())

@@ -21,7 +21,11 @@
 * The ring-stage entries are re-exported from ``ring``.
 
 Planes may also be the device layout itself (an ``ExpertWeights``' 2-D P16
-planes, e.g. ``*pool.planes``): they are used in place.  Checkpoint planes
+planes, e.g. ``*pool.planes``): they are used in place.  A pool's or ring's
+slot planes are recognised as such (mutable, with the FP8 scale bound of
+the store that fills them, so nothing is checked per call and eager and
+captured calls take the same kernels); other device-layout planes are
+wrapped once per storage and version, like checkpoint planes.  Checkpoint planes
 on the device are packed into the device layout once and cached in a small
 LRU keyed by their storage; an entry holds the source tensors (so their
 memory cannot be reused under the key) and their in-place version counters
@@ -36,7 +40,7 @@ from collections import OrderedDict
 import torch
 
 from . import formats as F
-from .layer import DECODE_MAX_TOKENS, ExpertWeights, moe_forward
+from .layer import DECODE_MAX_TOKENS, ExpertWeights, moe_forward, slot_planes_of
 from .ring import (gpu_moe_layer_from_engine_tiled, prealloc_tile_ring,  # noqa: F401
                    stage_tiles, staging_bytes, staging_tile_experts)
 
@@ -66,9 +70,24 @@ def _packed(fmt, device, w13, s13, w2, s2, g13=None, g2=None, kmajor=False, H=No
     if w13.dim() == 2:   # already the device layout: [S, bytes] P16 planes
         if H is None or I is None:
             raise ValueError("device-layout planes need H and I")
-        return ExpertWeights(fmt, H, I, w13.shape[0], 0, w13, s13, w2, s2,
-                             None if g13 is None else g13.float(),
-                             None if g2 is None else g2.float())
+        W = slot_planes_of(w13, s13, w2, s2)
+        if W is not None and W.fmt == int(fmt):   # pool / ring slots: used as they are
+            return W
+        # other device-layout planes: built once per (storage, version) below
+        key = (fmt, str(device), "p16", int(H), int(I)) + tuple(
+            _src_key(t) for t in (w13, s13, w2, s2, g13, g2))
+        vers = tuple(None if t is None else t._version for t in (w13, s13, w2, s2, g13, g2))
+        ent = _PACKED.get(key)
+        if ent is not None and ent[2] == vers:
+            _PACKED.move_to_end(key)
+            return ent[0]
+        W = ExpertWeights(fmt, H, I, w13.shape[0], 0, w13, s13, w2, s2,
+                          None if g13 is None else g13.float(),
+                          None if g2 is None else g2.float())
+        _PACKED[key] = (W, (w13, s13, w2, s2, g13, g2), vers)
+        while len(_PACKED) > PACK_CACHE_MAX:
+            _PACKED.popitem(last=False)
+        return W
     srcs = (w13, s13, w2, s2, g13, g2)
     if not all(t is None or (t.is_cuda and t.device == device) for t in srcs):
         return _pack(fmt, device, *srcs, kmajor)   # host planes: per call

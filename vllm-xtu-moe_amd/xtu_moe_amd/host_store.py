@@ -22,7 +22,7 @@ import torch
 
 from . import _lib
 from . import formats as F
-from .layer import ExpertWeights, _p, _stream, fp8_block_scales_bounded
+from .layer import ExpertWeights, _p, _stream, fp8_block_scales_bounded, register_slot_planes
 
 PLANES = ("w13", "s13", "w2", "s2", "gs13", "gs2")
 # the reference's plane numbering for copy_hostbuf_to_device(which, ...);
@@ -155,7 +155,9 @@ class HostExpertStore:
         bytes in: height rows of width bytes, source pitch spitch, destination
         pitch dpitch; returns width*height, or 0 on a bad request."""
         src = self.host_wbuf(which, node)
-        if src is None or not height or not width:
+        src_off, dpitch, spitch = int(src_off), int(dpitch), int(spitch)
+        width, height = int(width), int(height)
+        if src is None or height <= 0 or width <= 0 or spitch <= 0 or dpitch <= 0:
             return 0
         size = src.numel() * src.element_size()
         if src_off < 0 or width > spitch or width > dpitch \
@@ -221,5 +223,8 @@ def empty_slots(fmt, H, I, n_slots, like: HostExpertStore, device) -> ExpertWeig
         src = like.planes[name]
         planes[name] = None if src is None else torch.empty((n_slots,) + tuple(src.shape[1:]),
                                                             dtype=src.dtype, device=device)
-    return ExpertWeights(fmt, H, I, n_slots, 0, planes["w13"], planes["s13"], planes["w2"],
-                         planes["s2"], planes["gs13"], planes["gs2"], mutable=True)
+    f8ok = like.fp8_scales_bounded() if int(fmt) == F.FMT_FP8 else None
+    return register_slot_planes(
+        ExpertWeights(fmt, H, I, n_slots, 0, planes["w13"], planes["s13"], planes["w2"],
+                      planes["s2"], planes["gs13"], planes["gs2"], mutable=True,
+                      fp8_scales_ok=f8ok))

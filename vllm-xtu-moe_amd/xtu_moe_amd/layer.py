@@ -64,7 +64,7 @@ class ExpertWeights:
     """
 
     def __init__(self, fmt, H, I, E, n_shared, w13, s13, w2, s2, gs13=None, gs2=None, *,
-                 mutable=False, group_k=0):
+                 mutable=False, group_k=0, fp8_scales_ok=None):
         self.fmt, self.H, self.I, self.E, self.n_shared = int(fmt), int(H), int(I), int(E), int(n_shared)
         # INT4 (WNA16): k per fp32 scale (the planes keep [N][K/group_k] per expert)
         self.group_k = int(group_k) if self.fmt == FMT_INT4 else 0
@@ -72,8 +72,10 @@ class ExpertWeights:
             raise ValueError(f"INT4 weights need group_k in {INT4_GROUPS}, got {group_k}")
         self.w13, self.s13, self.w2, self.s2, self.gs13, self.gs2 = w13, s13, w2, s2, gs13, gs2
         # mutable: the planes are restaged in place (ring / pool slots), so
-        # nothing derived from them is cached
+        # nothing derived from them is cached; their FP8 scale bound is the
+        # source's (the host store they are filled from), stated here
         self.mutable = bool(mutable)
+        self.slot_fp8_scales_ok = fp8_scales_ok
         self._i8 = None
         self._i8_fb = None
         self._mxs = None
@@ -213,6 +215,30 @@ class ExpertWeights:
         return self._i8_fb
 
 
+# Slot planes (pool, ring) by the address of their w13 plane: a caller that
+# hands their tensors to a layer entry (``*pool.planes``) gets these weights
+# back, with their FP8 scale bound, instead of a new set checked per call.
+# The planes are never freed, so an address cannot be reused under an entry.
+_SLOT_PLANES: dict = {}
+
+
+def register_slot_planes(W: "ExpertWeights") -> "ExpertWeights":
+    _SLOT_PLANES[(str(W.w13.device), W.w13.data_ptr())] = W
+    return W
+
+
+def slot_planes_of(w13, s13, w2, s2):
+    """The registered slot planes whose four tensors these are, else None."""
+    W = _SLOT_PLANES.get((str(w13.device), w13.data_ptr()))
+    if W is None:
+        return None
+    same = all(a is not None and b is not None and a.data_ptr() == b.data_ptr()
+               and tuple(a.shape) == tuple(b.shape)
+               for a, b in ((W.w13, w13), (W.s13, s13), (W.w2, w2), (W.s2, s2))
+               if not (a is None and b is None))
+    return W if same and W.w13.shape == w13.shape else None
+
+
 I8_MARKED = 0xFF   # emin byte of a weight row that takes the fp32 fallback
 
 
@@ -317,30 +343,18 @@ class _Segmentation:
         return base + 4 * int(b0), base + 4 * int(b1)
 
 
+# Scratch per (shape, device, stream), kept for the life of the process and
+# never freed: a captured HIP graph may hold their addresses, and a buffer
+# used on a stream other than the one it was allocated on must not return to
+# the caching allocator while that stream may still read it.  The streams a
+# process runs layers on are few (torch hands out streams from a fixed pool
+# per device; the split layers share one side stream per device), so this
+# is bounded by a few copies of each buffer.
 _SEG_CACHE: dict = {}
 _BUF_CACHE: dict = {}
-# Buffers replaced by a larger one.  They stay allocated for the life of the
-# process: a captured HIP graph may still hold their addresses.  Growth is
+# Buffers replaced by a larger one (kept for the same reason).  Growth is
 # geometric (power-of-two rows), so they total less than the live ones.
 _RETIRED: list = []
-# Streams that own scratch per device; past this many, the least recently
-# used stream's buffers are dropped (a stream that comes back reallocates).
-MAX_STREAMS = 8
-_STREAM_LRU: dict = {}
-
-
-def _touch_stream(device, stream: int) -> None:
-    lru = _STREAM_LRU.setdefault(str(device), [])
-    if lru and lru[-1] == stream:
-        return
-    if stream in lru:
-        lru.remove(stream)
-    lru.append(stream)
-    while len(lru) > MAX_STREAMS:
-        old = lru.pop(0)
-        for cache in (_SEG_CACHE, _BUF_CACHE):
-            for k in [k for k in cache if k[-2] == str(device) and k[-1] == old]:
-                del cache[k]
 
 
 def segmentation(T, K, E, NS, bm, device, stream=None) -> _Segmentation:
@@ -349,7 +363,6 @@ def segmentation(T, K, E, NS, bm, device, stream=None) -> _Segmentation:
     another stream gets its own.  Capacity grows to the next power of two
     of T, so varying batch sizes allocate O(log T_max) times in total."""
     st = _stream(stream)
-    _touch_stream(device, st)
     key = (K, E, NS, bm, str(device), st)
     b = _SEG_CACHE.get(key)
     if b is None or b.cap_t < T:
@@ -366,7 +379,6 @@ def _buf(name, shape, dtype, device, stream=None):
     (stream-ordered reuse; concurrent streams get their own)."""
     rows, tail = int(shape[0]), tuple(int(s) for s in shape[1:])
     st = _stream(stream)
-    _touch_stream(device, st)
     key = (name, tail, dtype, str(device), st)
     t = _BUF_CACHE.get(key)
     if t is None or t.shape[0] < rows:
@@ -468,9 +480,9 @@ def fp8_pair32_use(W, scales_ok=None) -> bool:
     LDS-staged operands (xtu_f8_pair_*): XTU_FP8_PREFILL "auto" (default) or
     "pair32", the shape fits and the block scales are bounded
     (fp8_block_scales_bounded; the kernel rescales by their ratios), checked
-    once on immutable weights and stated by the caller for slot planes (pool,
-    ring: `scales_ok`, from the host store's copy); else the 16x16x128 kernel
-    (xtu_gemm8_*, "v1")."""
+    once on immutable weights and, for slot planes (pool, ring), stated by the
+    caller (`scales_ok`) or by the planes themselves (from the host store's
+    copy); else the 16x16x128 kernel (xtu_gemm8_*, "v1")."""
     if W is None or W.fmt != FMT_FP8:
         return False
     if os.environ.get(FP8_PREFILL_ENV, "auto") == "v1":
@@ -478,7 +490,7 @@ def fp8_pair32_use(W, scales_ok=None) -> bool:
     if not bool(_lib.call("xtu_f8_pair_fits", int(W.H), int(W.I))):
         return False
     if W.mutable:
-        return bool(scales_ok)
+        return bool(scales_ok if scales_ok is not None else W.slot_fp8_scales_ok)
     return W.fp8_scales_bounded()
 
 
