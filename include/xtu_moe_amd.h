@@ -410,6 +410,24 @@ hipError_t xtu_i8_fallback(int gate_up, const void* x, const int32_t* sorted_tok
                            const int32_t* tile_hi, int max_tiles, int bm,
                            const int32_t* col_start, const int32_t* cols, void* out, float limit,
                            float alpha, float beta, hipStream_t stream);
+/* The engine's offset guard (moe_v2_packed4_w4a8.inc:436, :1361-1364: a tile
+ * with cmin + emin - 128 < -24 takes the fp32 path), restated per sorted row:
+ * xtu_i8_emin_min writes eminmin[e] = the smallest e8m0 byte of expert e's
+ * [N][K] MXFP4 matrix; xtu_i8_row_fallback then recomputes in fp32 every
+ * output column of each row whose activation exponent (crow of its token for
+ * gate_up = 1, of its act row for gate_up = 0) plus eminmin of its weight
+ * slot, minus 128, is below -24, overwriting what the integer GEMM wrote
+ * (same operands and sums as xtu_i8_fallback).  Run after the integer GEMM
+ * and xtu_i8_fallback, on the same stream. */
+hipError_t xtu_i8_emin_min(const void* s, int E, int N, int K, int32_t* eminmin,
+                           hipStream_t stream);
+hipError_t xtu_i8_row_fallback(int gate_up, const void* x, const int32_t* sorted_tok,
+                               const int32_t* crow, const int32_t* eminmin, int H, int I,
+                               const void* w, const void* s, const int32_t* slot_map,
+                               const int32_t* seg_start, const int32_t* tile_expert,
+                               const int32_t* tile_row0, const int32_t* tile_lo,
+                               const int32_t* tile_hi, int max_tiles, int bm, void* out,
+                               float limit, float alpha, float beta, hipStream_t stream);
 
 /* ------------------------------------------------ expert staging (ring / pool)
  * dst[i*dst_stride, +bytes) <- src[experts[i]*src_stride, +bytes), i < n, as

@@ -24,7 +24,9 @@
  *                                    compiled reference engine with the ALIGN
  *                                    gate on, within the layer tolerance (the
  *                                    engine's lane-sum order differs, so C is
- *                                    not bit-exact)
+ *                                    not bit-exact); the offset guard's fp32
+ *                                    rows against an engine fixture whose every
+ *                                    tile fails that guard
  */
 #include <math.h>
 #include <stdint.h>
@@ -539,15 +541,29 @@ static float i8_fallback_dot(const float* a, const uint8_t* w, const uint8_t* s,
   return (float)d;
 }
 
+/* Smallest e8m0 byte of one MXFP4 expert matrix [N][K/32]. */
+static int i8_emin_min(const uint8_t* s, int N, int K) {
+  int mn = 255;
+  for (size_t i = 0; i < (size_t)N * (K / 32); ++i)
+    if (s[i] < mn) mn = s[i];
+  return mn;
+}
+
 /* Full MXFP4 layer with INT8 activations for both GEMMs (the engine with
  * int8_activation ALIGN on, moe_v2_packed4_w4a8.inc:1341-1362): gate/up from
  * int8(x), act fp32 -> bf16, down from int8(bf16(act)).
- * Fallback (the reference's per-tile guard wtmax <= 3, :1344-1366, sends a
- * tile whose weight rows spread more than 3 e8m0 steps to its fp32 path): a
- * gate/up column pair i whose gate row i or up row i spreads more than 3, and
- * a down column h whose row spreads more than 3, are computed from the bf16
- * activation and the dequantized weights in fp32 instead.  (The reference
- * decides per CPU tile of output columns; this build decides per column.) */
+ * Fallbacks to the fp32 path (bf16 activation times the dequantized weights):
+ *  - the spread guard (wtmax <= 3, :1344-1366, a tile whose weight rows spread
+ *    more than 3 e8m0 steps takes the fp32 path): a gate/up column pair i
+ *    whose gate row i or up row i spreads more than 3, and a down column h
+ *    whose row spreads more than 3 (the reference decides per CPU tile of
+ *    output columns; this build decides per column);
+ *  - the offset guard (cmin + emin - 128 >= -24, :436, :1361-1364): a pair
+ *    whose activation row exponent crow plus the smallest e8m0 byte of the
+ *    expert's matrix, minus 128, is below -24 takes the whole gate/up (or
+ *    down) row on the fp32 path (the reference decides per block of its rows
+ *    -- one row in its per-token loop, six in the grouped one -- and over its
+ *    thread's column range; this build decides per row over the expert). */
 int xo_moe_layer_i8(int T, int K, int E, int n_shared, int H, int I, const uint16_t* x,
                     const int32_t* ids, const float* wts, const uint8_t* w13,
                     const uint8_t* s13, const uint8_t* w2, const uint8_t* s2, float limit,
@@ -558,8 +574,9 @@ int xo_moe_layer_i8(int T, int K, int E, int n_shared, int H, int I, const uint1
   float* actf = (float*)malloc(sizeof(float) * (size_t)I);
   float* y = (float*)malloc(sizeof(float) * (size_t)H);
   float* wrow = (float*)malloc(sizeof(float) * (size_t)(H > I ? H : I));
-  if (!xf || !gu || !accb || !actf || !y || !wrow) {
-    free(xf); free(gu); free(accb); free(actf); free(y); free(wrow);
+  int8_t* a8b = (int8_t*)malloc((size_t)(H > I ? H : I));
+  if (!xf || !gu || !accb || !actf || !y || !wrow || !a8b) {
+    free(xf); free(gu); free(accb); free(actf); free(y); free(wrow); free(a8b);
     return -1;
   }
   for (int t = 0; t < T; ++t) {
@@ -582,8 +599,9 @@ int xo_moe_layer_i8(int T, int K, int E, int n_shared, int H, int I, const uint1
       const uint8_t* w2e = w2 + (size_t)e * H * (I / 2);
       const uint8_t* s2e = s2 + (size_t)e * H * (I / 32);
       xo_i8_gemm(xf, 1, w13e, s13e, 2 * I, H, 1.0f, accb, gu);
+      const int g2_13 = xo_i8_quant_row(xf, H, a8b) + i8_emin_min(s13e, 2 * I, H) - 128 < -24;
       for (int i = 0; i < I; ++i) {
-        if (xo_i8_row_spread(s13e + (size_t)i * (H / 32), H) > 3 ||
+        if (g2_13 || xo_i8_row_spread(s13e + (size_t)i * (H / 32), H) > 3 ||
             xo_i8_row_spread(s13e + (size_t)(I + i) * (H / 32), H) > 3) {
           gu[i] = i8_fallback_dot(xf, w13e, s13e, 2 * I, H, i, wrow);
           gu[I + i] = i8_fallback_dot(xf, w13e, s13e, 2 * I, H, I + i, wrow);
@@ -591,12 +609,13 @@ int xo_moe_layer_i8(int T, int K, int E, int n_shared, int H, int I, const uint1
         actf[i] = bf16_round(xo_silu_gate(gu[i], gu[I + i], limit, alpha, beta));
       }
       xo_i8_gemm(actf, 1, w2e, s2e, H, I, 1.0f, accb, y);
+      const int g2_2 = xo_i8_quant_row(actf, I, a8b) + i8_emin_min(s2e, H, I) - 128 < -24;
       for (int h = 0; h < H; ++h)
-        if (xo_i8_row_spread(s2e + (size_t)h * (I / 32), I) > 3)
+        if (g2_2 || xo_i8_row_spread(s2e + (size_t)h * (I / 32), I) > 3)
           y[h] = i8_fallback_dot(actf, w2e, s2e, H, I, h, wrow);
       for (int h = 0; h < H; ++h) o[h] += w * y[h];
     }
   }
-  free(xf); free(gu); free(accb); free(actf); free(y); free(wrow);
+  free(xf); free(gu); free(accb); free(actf); free(y); free(wrow); free(a8b);
   return 0;
 }

@@ -42,7 +42,26 @@ CASES = {
     # INT8-activation x FP4-code ALIGN path of the engine (MXFP4, e8m0 spread <= 3)
     "small_mxfp4_int8": dict(fmt=F.FMT_MXFP4, E=8, NS=1, H=512, I=256, T=6, K=2, seed=15,
                              limit=7.0, int8=True),
+    # the SwiGLU-OAI activation: sigmoid scale alpha and the +beta on `up`
+    # (the engine's swiglu_alpha / swiglu_beta) with the clamp at 7
+    "small_mxfp4_oai": dict(fmt=F.FMT_MXFP4, E=8, NS=1, H=512, I=256, T=6, K=2, seed=16,
+                            limit=7.0, alpha=1.702, beta=1.0),
+    "small_fp8_oai": dict(fmt=F.FMT_FP8, E=8, NS=1, H=512, I=256, T=6, K=2, seed=17,
+                          limit=7.0, alpha=1.702, beta=1.0),
+    "small_mxfp4_int8_oai": dict(fmt=F.FMT_MXFP4, E=8, NS=1, H=512, I=256, T=6, K=2, seed=18,
+                                 limit=7.0, alpha=1.702, beta=1.0, int8=True),
+    # the ALIGN path where the engine's offset guard (cmin + emin - 128 >= -24,
+    # moe_v2_packed4_w4a8.inc:436,1361) fails on every tile: weights N(0,
+    # 0.02 * 2^-16), tokens N(0, 2^-24), so the engine computes these tiles in
+    # fp32 while the GPU's per-row-scaled int32 path takes them in INT8
+    "small_mxfp4_int8_g2": dict(fmt=F.FMT_MXFP4, E=8, NS=1, H=512, I=256, T=6, K=2, seed=19,
+                                limit=7.0, int8=True, std=0.02 * 2.0 ** -16, x_scale=2.0 ** -12),
 }
+
+
+def act_args(c: dict) -> dict:
+    """The activation parameters of a case (limit, alpha, beta)."""
+    return dict(limit=c["limit"], alpha=c.get("alpha", 1.0), beta=c.get("beta", 0.0))
 
 
 def weights_digest(d: dict) -> str:
@@ -59,7 +78,7 @@ def case_inputs(c: dict):
     import torch
 
     rng = np.random.default_rng(c["seed"] + 100)
-    x = rng.standard_normal((c["T"], c["H"])).astype(np.float32)
+    x = rng.standard_normal((c["T"], c["H"])).astype(np.float32) * np.float32(c.get("x_scale", 1.0))
     x_bits = oracle.f32_to_bf16_bits(x)
     if c.get("router") == "mixtral":
         g = torch.Generator().manual_seed(c["seed"] + 7)
@@ -72,13 +91,15 @@ def case_inputs(c: dict):
     return x_bits, ids, wts
 
 
-def main():
+def main(names=None):
     if not oracle.ref_available():
         raise SystemExit("reference engine build (oracle/_ref) missing: run oracle/build_ref.sh")
     L = oracle.ref_lib()
     for name, c in CASES.items():
+        if names and name not in names:
+            continue
         d = dense_to_numpy(c["fmt"], make_dense_layer(c["fmt"], c["E"] + c["NS"], c["H"], c["I"],
-                                                      seed=c["seed"]))
+                                                      seed=c["seed"], std=c.get("std", 0.02)))
         x_bits, ids, wts = case_inputs(c)
         T, K, E, NS = c["T"], c["K"], c["E"], c["NS"]
         # the engine takes the shared experts as always-on columns of weight 1 and
@@ -91,7 +112,7 @@ def main():
         else:
             ew = wts
         eng = oracle.RefEngine(c["fmt"], E + NS, K + NS, c["H"], c["I"], d["w13"], d["s13"],
-                               d["w2"], d["s2"], d["gs13"], d["gs2"], limit=c["limit"])
+                               d["w2"], d["s2"], d["gs13"], d["gs2"], **act_args(c))
         if c.get("int8"):
             L.xref_set_int8(1, 1 << 30)
         out = eng.forward(x_bits, eids.astype(np.uint32), ew.astype(np.float32))
@@ -105,4 +126,4 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:])

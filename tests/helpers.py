@@ -1,6 +1,7 @@
 """Shared test helpers: seeded synthetic layers and the parity tolerance."""
 from __future__ import annotations
 
+import os
 import types
 
 import numpy as np
@@ -117,3 +118,63 @@ def int4_layer(E_, H_, I_, seed):
         w13_qzeros=torch.full((E_, H_ // 128, 2 * I_ // 8), 0x77777777, dtype=torch.int32),
         top_k=3, renormalize=True, swiglu_limit=7.0)
     return d, layer
+
+
+def cover_tokens(ids, E: int, n_last: int = 8, seed: int = 0):
+    """Tokens of a batch that together route to every expert the batch uses
+    (ids in [0, E)): for n_last random experts the last token routed to them
+    (its pair sits in the expert's last, partial M tile), then a greedy cover
+    (the token reaching the most experts not yet covered, lowest index on
+    ties).  Returns (sorted tokens, the set of experts they cover)."""
+    ids = np.asarray(ids)
+    valid = (ids >= 0) & (ids < E)
+    used = set(np.unique(ids[valid]).tolist())
+    rng = np.random.default_rng(seed)
+    chosen = []
+    for e in rng.choice(sorted(used), size=min(n_last, len(used)), replace=False):
+        chosen.append(int(np.nonzero((ids == e).any(1))[0].max()))
+    covered = set(ids[chosen][valid[chosen]].tolist()) if chosen else set()
+    while covered != used:
+        left = np.array(sorted(used - covered))
+        gain = (np.isin(ids, left) & valid).sum(1)
+        t = int(np.argmax(gain))
+        chosen.append(t)
+        covered |= set(ids[t][valid[t]].tolist())
+    return sorted(set(chosen)), covered
+
+
+ORACLE_THREADS = min(16, os.cpu_count() or 1)
+
+
+def sampled_oracle(fmt, W, x, ids, wts, toks, limit=0.0, int8=False, alpha=1.0, beta=0.0):
+    """The oracle layer for the tokens `toks` of a batch on device weights W:
+    only their experts (remapped to 0..U-1) and the shared experts, at full H
+    and I, one token per call spread over host threads (the oracle's C entry
+    points release the interpreter lock)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from xtu_moe_amd.synthetic import dense_experts
+    ids_s = ids[toks].cpu().numpy()
+    wts_s = wts[toks].cpu().numpy()
+    valid = (ids_s >= 0) & (ids_s < W.E)
+    used = np.unique(ids_s[valid])
+    remap = {int(e): i for i, e in enumerate(used)}
+    cids = np.where(valid, np.vectorize(lambda e: remap.get(int(e), -1))(ids_s), -1)
+    cids = cids.astype(np.int32)
+    dn = dense_experts(W, list(used) + [W.E + s for s in range(W.n_shared)])
+    xb = bf16_tensor_to_bits(x[toks])
+    U, NS, H, I = len(used), W.n_shared, W.H, W.I
+
+    def one(i):
+        sl = slice(i, i + 1)
+        if int8:
+            return oracle.moe_layer_i8(xb[sl], cids[sl], wts_s[sl], U, NS, H, I, dn["w13"],
+                                       dn["s13"], dn["w2"], dn["s2"], limit=limit, alpha=alpha,
+                                       beta=beta)
+        return oracle.moe_layer(fmt, xb[sl], cids[sl], wts_s[sl], U, NS, H, I, dn["w13"],
+                                dn["s13"], dn["w2"], dn["s2"], dn["gs13"], dn["gs2"], limit=limit,
+                                alpha=alpha, beta=beta)
+
+    with ThreadPoolExecutor(max_workers=ORACLE_THREADS) as ex:
+        rows = list(ex.map(one, range(len(toks))))
+    return np.concatenate(rows, 0) if rows else np.zeros((0, H), np.float32)

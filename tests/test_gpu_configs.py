@@ -1,25 +1,28 @@
 """The benchmark configurations at their full shapes on the GPU, against the
-oracle (sampled tokens where the whole batch would take the CPU too long)
+oracle (where the whole batch would take the CPU too long, a set of tokens
+that covers every routed expert, chosen greedily)
 plus properties that hold at any size:
 
 * tiny Mixtral-style bf16 layer: H=1024, 8 experts, I=2048, softmax top-2
   renormalised, T=128 -- routing bit-exact and every token against the oracle;
 * Qwen3-Next shape: H=2048, I=512, 512 routed + 1 shared experts, softmax
-  top-10, SwiGLU clamp 7 -- INT8-activation x MXFP4 at T=8192 (64 sampled
-  tokens, the token-permutation bitwise property, the int32 accumulators of
-  sampled tiles bit-exact), NVFP4 at T=1, 4 and 8192, MXFP4 decode at T=1, 4;
+  top-10, SwiGLU clamp 7 -- INT8-activation x MXFP4 at T=8192 (sampled
+  tokens covering every routed expert, the token-permutation bitwise
+  property, the int32 accumulators of sampled tiles bit-exact), INT8 forced
+  at T=1 and 4, NVFP4 at T=1, 4 and 8192, MXFP4 decode at T=1, 4;
 * DeepSeek-V3 FP8 streamed prefill: 64 resident experts (+ the shared one)
   in the pool, the other 192 streamed from pinned host memory through a
   ring of 4 slots of 16 experts, Zipf(1.1)-skewed routing, T=8192 -- bitwise
-  equal to the all-resident layer, and sampled tokens against the oracle.
+  equal to the all-resident layer, and tokens covering every routed expert
+  (the last rows of eight experts' buckets among them) against the oracle.
 """
 import numpy as np
 import pytest
 import torch
 
 import oracle
-from helpers import (MAX_ABS, REL_L2, bf16_tensor_to_bits, check_close, dense_to_numpy,
-                     make_dense_layer, oracle_layer, rel_l2)
+from helpers import (MAX_ABS, REL_L2, bf16_tensor_to_bits, check_close, cover_tokens,
+                     dense_to_numpy, make_dense_layer, oracle_layer, rel_l2, sampled_oracle)
 from xtu_moe_amd import _lib
 from xtu_moe_amd import formats as F
 from xtu_moe_amd import layer as L
@@ -34,25 +37,17 @@ DEV = torch.device("cuda")
 
 
 def _sampled_oracle(fmt, W, x, ids, wts, toks, limit=0.0, int8=False):
-    """The oracle layer for the tokens `toks` of a batch: only their experts
-    (remapped to 0..U-1) and the shared experts, at full H and I."""
-    ids_s = ids[toks].cpu().numpy()
-    wts_s = wts[toks].cpu().numpy()
-    valid = (ids_s >= 0) & (ids_s < W.E)
-    used = np.unique(ids_s[valid])
-    remap = {int(e): i for i, e in enumerate(used)}
-    cids = np.where(valid, np.vectorize(lambda e: remap.get(int(e), -1))(ids_s), -1)
-    cids = cids.astype(np.int32)
-    dn = dense_experts(W, list(used) + [W.E + s for s in range(W.n_shared)])
-    xb = bf16_tensor_to_bits(x[toks])
-    if int8:
-        return oracle.moe_layer_i8(xb, cids, wts_s, len(used), W.n_shared, W.H, W.I, dn["w13"],
-                                   dn["s13"], dn["w2"], dn["s2"], limit=limit)
-    return oracle_layer(fmt, dn, xb, cids, wts_s, len(used), W.n_shared, W.H, W.I, limit=limit)
+    return sampled_oracle(fmt, W, x, ids, wts, toks, limit=limit, int8=int8)
 
 
-def _toks(T, n, seed):
-    return sorted(np.random.default_rng(seed).choice(T, size=min(n, T), replace=False).tolist())
+def _cover(ids, E, NS, seed):
+    """Tokens covering every routed expert of the batch (and the shared ones,
+    which every token uses), with the last token of 8 experts' buckets."""
+    toks, covered = cover_tokens(ids.cpu().numpy(), E, seed=seed)
+    routed = int(torch.unique(ids[(ids >= 0) & (ids < E)]).numel())
+    # every routed expert, plus the NS shared ones that each sampled token runs
+    assert len(covered) + NS == routed + NS and len(toks) > 0
+    return toks
 
 
 # ------------------------------------------------------------- tiny Mixtral
@@ -101,7 +96,7 @@ def test_qwen3_next_int8_t8192(qwen_mxfp4):
     W = qwen_mxfp4
     T = 8192
     x, logits, ids, wts = _qwen_batch(T, seed=5)
-    toks = _toks(T, 64, seed=6)
+    toks = _cover(ids, QE, QNS, seed=6)
     rids, rwts = oracle.route_softmax_topk(logits[toks].cpu().numpy(), QK)
     np.testing.assert_array_equal(ids[toks].cpu().numpy(), rids)
     np.testing.assert_array_equal(wts[toks].cpu().numpy().view(np.uint32), rwts.view(np.uint32))
@@ -159,7 +154,7 @@ def test_qwen3_next_nvfp4(T):
     x, _, ids, wts = _qwen_batch(T, seed=10 + T)
     out = moe_forward(x, ids, wts, W, swiglu_limit=QLIM, out_dtype=torch.float32)
     torch.cuda.synchronize()
-    toks = _toks(T, 48, seed=11)
+    toks = _cover(ids, QE, QNS, seed=11)
     ref = _sampled_oracle(F.FMT_NVFP4, W, x, ids, wts, toks, limit=QLIM)
     check_close(out[toks].cpu().numpy(), ref, bf16_out=False, what=f"qwen3-next nvfp4 T={T}")
     del W
@@ -178,6 +173,23 @@ def test_qwen3_next_mxfp4_decode(qwen_mxfp4, T):
     assert torch.equal(ids_o, ids) and torch.equal(wts_o, wts)
     ref = _sampled_oracle(F.FMT_MXFP4, W, x, ids, wts, list(range(T)), limit=QLIM)
     check_close(out.float().cpu().numpy(), ref, bf16_out=True, what=f"qwen3-next mxfp4 T={T}")
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_qwen3_next_int8_forced_at_decode_sizes(qwen_mxfp4, T, monkeypatch):
+    """XIAOTU_MOE_INT8_ALIGN=1 takes the INT8 ALIGN path below the 160-token
+    gate as well (the reference engine's override): T = 1 and 4 on the
+    grouped integer GEMMs, every token against the INT8 oracle."""
+    monkeypatch.setenv(L.INT8_FORCE_ENV, "1")
+    assert L.int8_align_on(T)
+    W = qwen_mxfp4
+    x, logits, ids, wts = _qwen_batch(T, seed=30 + T)
+    out, seg = moe_forward(x, ids, wts, W, int8="auto", swiglu_limit=QLIM,
+                           out_dtype=torch.float32, return_seg=True)
+    torch.cuda.synchronize()
+    assert seg.bm == 128   # the integer GEMMs' tiles, not the decode kernels'
+    ref = _sampled_oracle(F.FMT_MXFP4, W, x, ids, wts, list(range(T)), limit=QLIM, int8=True)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"qwen3-next forced int8 T={T}")
 
 
 # ---------------------------------------------------- DeepSeek-V3 streamed
@@ -207,7 +219,7 @@ def test_ds_v3_fp8_streamed_prefill():
     ref = moe_forward(x, ids, wts, W, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
-    toks = _toks(T, 8, seed=16)
+    toks = _cover(ids, E, NS, seed=16)
     want = _sampled_oracle(F.FMT_FP8, W, x, ids, wts, toks)
     check_close(out[toks].cpu().numpy(), want, bf16_out=False, what="ds-v3 fp8 streamed")
     del W, store, pool
@@ -215,6 +227,9 @@ def test_ds_v3_fp8_streamed_prefill():
 
 
 # ------------------------------------------------------ DeepSeek-V3 MXFP4 prefill
+_ORACLE_CACHE: dict = {}
+
+
 @pytest.mark.parametrize("mode", ["tri", "pair", "bf16"])
 def test_ds_v3_mxfp4_prefill_t8192(mode, monkeypatch):
     """DeepSeek-V3 shape with MXFP4 experts at T=8192, on the double-rate fp6
@@ -232,8 +247,12 @@ def test_ds_v3_mxfp4_prefill_t8192(mode, monkeypatch):
                      routed_scaling_factor=2.5)
     out = moe_forward(x, ids, wts, W, out_dtype=torch.float32)
     torch.cuda.synchronize()
-    toks = _toks(T, 6, seed=19)
-    ref = _sampled_oracle(F.FMT_MXFP4, W, x, ids, wts, toks)
+    toks = _cover(ids, E, NS, seed=19)
+    key = ("ds-v3-mxfp4", tuple(toks))
+    if key not in _ORACLE_CACHE:   # the three modes share weights, tokens and routing
+        _ORACLE_CACHE.clear()
+        _ORACLE_CACHE[key] = _sampled_oracle(F.FMT_MXFP4, W, x, ids, wts, toks)
+    ref = _ORACLE_CACHE[key]
     check_close(out[toks].cpu().numpy(), ref, bf16_out=False, what="ds-v3 mxfp4 T=8192")
     perm = torch.randperm(T, generator=torch.Generator().manual_seed(20)).to(DEV)
     out_p = moe_forward(x[perm].contiguous(), ids[perm].contiguous(), wts[perm].contiguous(), W,

@@ -7,6 +7,7 @@ import pytest
 import torch
 
 from helpers import MAX_ABS, REL_L2, rel_l2
+from golden.make_golden import act_args
 from test_golden import CASES, load_case
 from xtu_moe_amd.layer import ExpertWeights, moe_forward
 
@@ -23,9 +24,10 @@ def _run(name, path):
     W = ExpertWeights.from_dense(c["fmt"], w13, t(d["s13"]), w2, t(d["s2"]), t(d["gs13"]),
                                  t(d["gs2"]), n_shared=c["NS"], device=dev)
     x = torch.from_numpy(f["x_bits"].astype(np.int16)).view(torch.bfloat16).to(dev)
+    a = act_args(c)
     out = moe_forward(x, torch.from_numpy(f["ids"]).to(dev), torch.from_numpy(f["wts"]).to(dev),
-                      W, swiglu_limit=c["limit"], path=path, int8=bool(c.get("int8")),
-                      out_dtype=torch.float32)
+                      W, swiglu_limit=a["limit"], swiglu_alpha=a["alpha"], swiglu_beta=a["beta"],
+                      path=path, int8=bool(c.get("int8")), out_dtype=torch.float32)
     torch.cuda.synchronize()
     return out.cpu().numpy(), f["out"]
 
@@ -40,7 +42,8 @@ def test_layer_matches_reference_engine(name, path):
     assert np.max(np.abs(out - ref)) <= MAX_ABS, (name, path)
 
 
-def test_int8_layer_matches_reference_engine():
-    out, ref = _run("small_mxfp4_int8", "gemm")
-    assert rel_l2(out, ref) <= REL_L2
-    assert np.max(np.abs(out - ref)) <= MAX_ABS
+@pytest.mark.parametrize("name", sorted(n for n in CASES if CASES[n].get("int8")))
+def test_int8_layer_matches_reference_engine(name):
+    out, ref = _run(name, "gemm")
+    assert rel_l2(out, ref) <= REL_L2, name
+    assert np.max(np.abs(out - ref)) <= MAX_ABS, name

@@ -88,3 +88,37 @@ def test_int8_marked_rows_accumulators():
         np.testing.assert_array_equal(got[:, ok], ref_acc[:, ok], err_msg=f"expert {e}")
         assert (got[:, ~ok] == 0).all()
         assert (~ok).sum() == (1 if e in (1, 2) else 0)
+
+
+def test_int8_offset_guard_rows_take_fp32():
+    """Tokens scaled by 2^-20 fall past the engine's offset guard (crow + the
+    expert's smallest e8m0 byte - 128 < -24) for gate/up and, through their
+    tiny act rows, for down: their rows are recomputed whole in fp32 (they
+    match the fp32 oracle far inside the ~2e-2 the INT8 rounding would
+    leave), the other tokens stay on the integer path (the INT8 oracle)."""
+    E, NS, H, I, K, T = 8, 1, 512, 512, 2, 300
+    d = make_dense_layer(F.FMT_MXFP4, E + NS, H, I, seed=84)
+    W = ExpertWeights.from_dense(F.FMT_MXFP4, d["w13"], d["s13"], d["w2"], d["s2"], n_shared=NS,
+                                 device=DEV)
+    rng = np.random.default_rng(85)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    wts = (rng.random((T, K)) + 0.05).astype(np.float32)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(86))
+    tiny = np.zeros(T, bool)
+    tiny[rng.choice(T, size=40, replace=False)] = True
+    x[torch.from_numpy(tiny)] *= 2.0 ** -20
+    x = x.to(torch.bfloat16)
+    out = moe_forward(x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(wts).to(DEV), W,
+                      int8=True, swiglu_limit=7.0, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    dn = dense_to_numpy(F.FMT_MXFP4, d)
+    xb = bf16_tensor_to_bits(x)
+    ref8 = oracle.moe_layer_i8(xb, ids, wts, E, NS, H, I, dn["w13"], dn["s13"], dn["w2"],
+                               dn["s2"], limit=7.0)
+    check_close(o[~tiny], ref8[~tiny], bf16_out=False, what="int8 rows")
+    ref32 = oracle.moe_layer(F.FMT_MXFP4, xb[tiny], ids[tiny], wts[tiny], E, NS, H, I, dn["w13"],
+                             dn["s13"], dn["w2"], dn["s2"], limit=7.0)
+    from helpers import rel_l2
+    assert rel_l2(o[tiny], ref32) < 1e-4
+    assert rel_l2(ref8[tiny], ref32) < 1e-4      # the oracle restates the same guard

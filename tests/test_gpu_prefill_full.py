@@ -5,9 +5,10 @@ hold at any size, and sampled tokens against the oracle.
 * Token permutation: each output row is reduced in a fixed order that does
   not depend on the row's position in its M tile or on the other tokens, so
   permuting the batch permutes the output bit for bit.
-* Sampled tokens: the oracle's dequantised-fp32 layer for sixteen tokens of
-  the batch (the first, the last, one in the middle and 13 drawn at random;
-  only their experts, at full H and I); the layer's bf16 output
+* Sampled tokens: the oracle's dequantised-fp32 layer for a set of tokens
+  that routes to every expert (a greedy cover, with the last rows of eight
+  experts' buckets; plus the first, a middle and the last token; only their
+  experts, at full H and I); the layer's bf16 output
   within max-abs 2e-2 (plus half a bf16 ulp of the value) and rel-L2 5e-3.
   The FP8 prefill GEMM is exact up to fp32 rounding (e4m3 weights against
   exact e4m3 activation pairs on the scaled fp8 MFMA, fp32 accumulation, the
@@ -20,10 +21,10 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import REL_L2, bf16_tensor_to_bits, check_close, oracle_layer, rel_l2
+from helpers import REL_L2, check_close, cover_tokens, rel_l2, sampled_oracle
 from xtu_moe_amd import formats as F
 from xtu_moe_amd.layer import moe_forward, route
-from xtu_moe_amd.synthetic import dense_experts, synth_layer
+from xtu_moe_amd.synthetic import synth_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -56,17 +57,14 @@ def test_token_permutation_is_bitwise_equivariant(layer):
 
 
 def test_sampled_tokens_match_oracle(layer):
+    """Tokens that together route to every one of the 256 experts (a greedy
+    cover, with the last token of eight experts' buckets, whose pairs sit in
+    partial M tiles), plus the first, a middle and the last token."""
     W, x, ids, wts, out = layer
-    rng = np.random.default_rng(7)
-    toks = sorted({0, T // 2 + 17, T - 1, *rng.choice(T, 13, replace=False).tolist()})
-    ids_s = ids[toks].cpu().numpy()
-    used = np.unique(ids_s)
-    remap = {int(e): i for i, e in enumerate(used)}
-    cids = np.vectorize(remap.get)(ids_s).astype(np.int32)
-    U = len(used)
-    dn = dense_experts(W, list(used) + [E + s for s in range(NS)])
-    ref = oracle_layer(F.FMT_FP8, dn, bf16_tensor_to_bits(x[toks]), cids,
-                       wts[toks].cpu().numpy(), U, NS, H, I)
+    toks, covered = cover_tokens(ids.cpu().numpy(), E, seed=7)
+    assert len(covered) == E   # every routed expert (the shared one is in every token)
+    toks = sorted(set(toks) | {0, T // 2 + 17, T - 1})
+    ref = sampled_oracle(F.FMT_FP8, W, x, ids, wts, toks)
     got = out[toks]
     check_close(got.to(torch.bfloat16).float().cpu().numpy(), ref, bf16_out=True,
                 what="ds-v3 fp8 T=8192 sample (bf16 output)")

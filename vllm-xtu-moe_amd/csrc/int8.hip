@@ -445,6 +445,124 @@ __global__ __launch_bounds__(256) void i8_fallback_kernel(I8FallbackArgs a) {
   }
 }
 
+// per expert: the smallest e8m0 byte of its [N][K] matrix (every row and
+// k group, the P16 scale groups' padding excluded), written to eminmin[e]
+__global__ __launch_bounds__(256) void i8_emin_min_kernel(const uint8_t* __restrict__ s, int N,
+                                                          int K, long s_estride,
+                                                          int32_t* __restrict__ eminmin) {
+  __shared__ int red[256];
+  const int e = blockIdx.x;
+  const uint8_t* se = s + (long)e * s_estride;
+  const long nsbk = K / 128;
+  const long units = (long)N * nsbk * 4;   // (row, super-block, chunk) scale bytes
+  int mn = 255;
+  for (long u = threadIdx.x; u < units; u += 256) {
+    const int n = (int)(u / (nsbk * 4));
+    const long rem = u % (nsbk * 4);
+    const int q = (int)(rem % 4);
+    const long sb = rem / 4;
+    mn = min(mn, (int)se[scale_offset<kMXFP4>(n / 16, sb, q * 16 + n % 16, K)]);
+  }
+  red[threadIdx.x] = mn;
+  __syncthreads();
+  for (int off = 128; off >= 1; off >>= 1) {
+    if (threadIdx.x < off) red[threadIdx.x] = min(red[threadIdx.x], red[threadIdx.x + off]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) eminmin[e] = red[0];
+}
+
+// The engine's offset guard (moe_v2_packed4_w4a8.inc:436, :1361-1364): an
+// integer tile whose activation exponent plus weight exponent falls below
+// 2^-24 (crow + emin - 128 < -24) is computed on the fp32 path.  Restated
+// per row: a sorted row whose activation row exponent (crow of its token
+// for gate/up, of its act row for down) plus its expert's smallest e8m0
+// byte, minus 128, is below -24 is recomputed whole in fp32 here, after the
+// integer GEMM wrote it: every output column of the row, from the bf16
+// activations and the exactly dequantised MXFP4 weights (the operands of the
+// engine's fp32 path).  One workgroup per m tile; the activation row is
+// staged in LDS as fp32 in chunks; each thread owns output columns and sums
+// over k in order (deterministic).
+struct I8RowFallbackArgs {
+  const uint16_t* x;          // gate/up: hidden rows [T][H]; down: act rows [A][I] (bf16)
+  const int32_t* sorted_tok;  // gate/up only
+  const int32_t* crow;        // gate/up: per token [T]; down: per sorted row [A]
+  const int32_t* eminmin;     // per weight slot
+  const uint8_t* w;
+  const uint8_t* s;
+  const int32_t* seg_start;
+  const int32_t* tile_expert;
+  const int32_t* tile_row0;
+  const int32_t* tile_lo;
+  const int32_t* tile_hi;
+  const int32_t* slot_map;
+  void* out;                  // act bf16 [A][I] / y fp32 [A][H]
+  int H, I, bm;
+  float limit, alpha, beta;
+};
+
+constexpr int kI8OffMin = -24;
+
+template <bool GU>
+__global__ __launch_bounds__(256) void i8_row_fallback_kernel(I8RowFallbackArgs a) {
+  constexpr int kChunk = 2048;
+  __shared__ float xl[kChunk];
+  __shared__ int fail_rows[128];
+  __shared__ int n_fail;
+  const int tile = a.tile_lo[0] + blockIdx.x;
+  if (tile >= a.tile_hi[0]) return;
+  const int e = a.tile_expert[tile];
+  const int ws = a.slot_map ? a.slot_map[e] : e;
+  const int emn = a.eminmin[ws];
+  const int row0 = a.tile_row0[tile];
+  const int rows = min(a.bm, a.seg_start[e + 1] - row0);
+  if (threadIdx.x == 0) n_fail = 0;
+  __syncthreads();
+  for (int r = threadIdx.x; r < rows; r += 256) {
+    const long pos = row0 + r;
+    const int cr = GU ? a.crow[a.sorted_tok[pos]] : a.crow[pos];
+    if (cr + emn - 128 < kI8OffMin) fail_rows[atomicAdd(&n_fail, 1)] = r;
+  }
+  __syncthreads();
+  const int nf = n_fail;
+  if (nf == 0) return;
+  const int K = GU ? a.H : a.I;
+  const int N = GU ? 2 * a.I : a.H;
+  const int ncol = GU ? a.I : a.H;   // output columns (gate/up: column pairs)
+  const long w_es = WFmt<kMXFP4>::w_bytes(N, K), s_es = WFmt<kMXFP4>::s_bytes(N, K);
+  const uint8_t* we = a.w + (long)ws * w_es;
+  const uint8_t* se = a.s + (long)ws * s_es;
+  for (int f = 0; f < nf; ++f) {
+    const long pos = row0 + fail_rows[f];
+    const long src = GU ? (long)a.sorted_tok[pos] : pos;
+    const uint16_t* xr = a.x + src * K;
+    for (int c0 = 0; c0 < ncol; c0 += 256) {
+      const int col = c0 + threadIdx.x;
+      float g = 0.f, u = 0.f;
+      for (int k0 = 0; k0 < K; k0 += kChunk) {
+        const int kn = min(kChunk, K - k0);
+        __syncthreads();
+        for (int k = threadIdx.x; k < kn; k += 256)
+          xl[k] = __uint_as_float((uint32_t)xr[k0 + k] << 16);
+        __syncthreads();
+        if (col < ncol) {
+          for (int k = 0; k < kn; ++k) {
+            g = __builtin_fmaf(xl[k], mxfp4_at(we, se, col, k0 + k, K), g);
+            if (GU) u = __builtin_fmaf(xl[k], mxfp4_at(we, se, a.I + col, k0 + k, K), u);
+          }
+        }
+      }
+      if (col < ncol) {
+        if (GU)
+          reinterpret_cast<uint16_t*>(a.out)[pos * a.I + col] =
+              f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
+        else
+          reinterpret_cast<float*>(a.out)[pos * a.H + col] = g;
+      }
+    }
+  }
+}
+
 }  // namespace
 }  // namespace xtu
 
@@ -548,6 +666,38 @@ hipError_t xtu_i8_fallback(int gate_up, const void* x, const int32_t* sorted_tok
                    cols, out, H, I, bm, limit, alpha, beta};
   if (gate_up) i8_fallback_kernel<true><<<max_tiles, 256, 0, stream>>>(a);
   else i8_fallback_kernel<false><<<max_tiles, 256, 0, stream>>>(a);
+  return hipPeekAtLastError();
+}
+
+hipError_t xtu_i8_emin_min(const void* s, int E, int N, int K, int32_t* eminmin,
+                           hipStream_t stream) {
+  XTU_CHECK_ARG(E >= 0 && N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0);
+  if (E == 0) return hipSuccess;
+  XTU_CHECK_ARG(s && eminmin);
+  (void)hipGetLastError();
+  i8_emin_min_kernel<<<E, 256, 0, stream>>>((const uint8_t*)s, N, K, WFmt<kMXFP4>::s_bytes(N, K),
+                                             eminmin);
+  return hipPeekAtLastError();
+}
+
+hipError_t xtu_i8_row_fallback(int gate_up, const void* x, const int32_t* sorted_tok,
+                               const int32_t* crow, const int32_t* eminmin, int H, int I,
+                               const void* w, const void* s, const int32_t* slot_map,
+                               const int32_t* seg_start, const int32_t* tile_expert,
+                               const int32_t* tile_row0, const int32_t* tile_lo,
+                               const int32_t* tile_hi, int max_tiles, int bm, void* out,
+                               float limit, float alpha, float beta, hipStream_t stream) {
+  XTU_CHECK_ARG(H > 0 && I > 0 && H % 256 == 0 && I % 128 == 0 && max_tiles >= 0);
+  XTU_CHECK_ARG(bm > 0 && bm <= 128);
+  XTU_CHECK_ARG(x && crow && eminmin && w && s && seg_start && tile_expert && tile_row0 &&
+                tile_lo && tile_hi && out && (!gate_up || sorted_tok));
+  if (max_tiles == 0) return hipSuccess;
+  (void)hipGetLastError();
+  I8RowFallbackArgs a{(const uint16_t*)x, sorted_tok, crow, eminmin, (const uint8_t*)w,
+                      (const uint8_t*)s, seg_start, tile_expert, tile_row0, tile_lo, tile_hi,
+                      slot_map, out, H, I, bm, limit, alpha, beta};
+  if (gate_up) i8_row_fallback_kernel<true><<<max_tiles, 256, 0, stream>>>(a);
+  else i8_row_fallback_kernel<false><<<max_tiles, 256, 0, stream>>>(a);
   return hipPeekAtLastError();
 }
 

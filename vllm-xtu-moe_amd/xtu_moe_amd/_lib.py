@@ -103,6 +103,9 @@ SIGNATURES = {
     "xtu_cpu_engine_destroy": (_i, [_vp]),
     "xtu_i8_fallback": (_i, [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i,
                              _vp, _vp, _vp, _f, _f, _f, _vp]),
+    "xtu_i8_emin_min": (_i, [_vp, _i, _i, _i, _vp, _vp]),
+    "xtu_i8_row_fallback": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp,
+                                 _vp, _vp, _i, _i, _vp, _f, _f, _f, _vp]),
 }
 
 # entry points whose int return value is a size/count, not a status

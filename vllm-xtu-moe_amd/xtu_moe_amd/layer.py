@@ -78,6 +78,7 @@ class ExpertWeights:
         self.slot_fp8_scales_ok = fp8_scales_ok
         self._i8 = None
         self._i8_fb = None
+        self._i8_emm = None
         self._mxs = None
         self._fp8_pos = None
         if self.H % 256 or self.I % 128:
@@ -192,11 +193,17 @@ class ExpertWeights:
         out = []
         st = _stream()
         dmax = torch.zeros(1, dtype=torch.int32, device=dev)
+        emm = []
         for (w, s, N, K) in ((self.w13, self.s13, 2 * self.I, self.H), (self.w2, self.s2, self.H, self.I)):
             w8 = torch.empty((n, N * K), dtype=torch.uint8, device=dev)
             emin = torch.empty((n, N), dtype=torch.uint8, device=dev)
             _lib.call("xtu_i8_prepare", _p(w), _p(s), n, N, K, _p(w8), _p(emin), _p(dmax), st)
             out += [w8, emin]
+            # each slot's smallest e8m0 byte: the offset guard's weight side
+            mm = torch.empty(n, dtype=torch.int32, device=dev)
+            _lib.call("xtu_i8_emin_min", _p(s), n, N, K, _p(mm), st)
+            emm.append(mm)
+        self._i8_emm = tuple(emm)
         self._i8_fb = None
         if int(dmax.item()) > 3:   # marked rows: CSR lists of their output columns per slot
             I = self.I
@@ -206,6 +213,15 @@ class ExpertWeights:
             self._i8_fb = _csr_cols(m13, dev) + _csr_cols(m2, dev)
         self._i8 = tuple(out)
         return self._i8
+
+    def int8_emin_min(self):
+        """(eminmin13, eminmin2): int32 [slots], each slot's smallest e8m0 byte
+        of its gate/up and down matrices (the offset guard's weight side),
+        from the same preparation as int8_planes (for mutable planes: the
+        last one, as int8_fallback_cols)."""
+        if self._i8 is None:
+            self.int8_planes()
+        return self._i8_emm
 
     def int8_fallback_cols(self):
         """None, or (start13, cols13, start2, cols2): per weight slot, the
@@ -793,6 +809,7 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
         cra = _buf("cra", (max(A, 1),), torch.int32, dev, st)
         _lib.call("xtu_i8_quant_rows", _p(x), T, H, _p(a8x), _p(crx), st)
         fb = W.int8_fallback_cols()
+        emm13, emm2 = W.int8_emin_min()
         _lib.call("xtu_i8_gemm_gate_up", _p(a8x), _p(crx), _p(seg.sorted_tok), H, I, _p(w13_8),
                   _p(emin13), _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
                   _p(seg.tile_row0), lo, hi, seg.max_tiles, _p(act), 0, lim, al, be, st)
@@ -801,6 +818,10 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
                       _p(W.s13), _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
                       _p(seg.tile_row0), lo, hi, seg.max_tiles, seg.bm, _p(fb[0]), _p(fb[1]),
                       _p(act), lim, al, be, st)
+        # rows past the offset guard: the whole row in fp32
+        _lib.call("xtu_i8_row_fallback", 1, _p(x), _p(seg.sorted_tok), _p(crx), _p(emm13), H, I,
+                  _p(W.w13), _p(W.s13), _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
+                  _p(seg.tile_row0), lo, hi, seg.max_tiles, seg.bm, _p(act), lim, al, be, st)
         _lib.call("xtu_i8_quant_rows", _p(act), A, I, _p(a8a), _p(cra), st)
         _lib.call("xtu_i8_gemm_down", _p(a8a), _p(cra), H, I, _p(w2_8), _p(emin2), _p(slot_map),
                   _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo, hi,
@@ -809,6 +830,9 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
             _lib.call("xtu_i8_fallback", 0, _p(act), 0, H, I, _p(W.w2), _p(W.s2), _p(slot_map),
                       _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0), lo, hi,
                       seg.max_tiles, seg.bm, _p(fb[2]), _p(fb[3]), _p(y), 0.0, 1.0, 0.0, st)
+        _lib.call("xtu_i8_row_fallback", 0, _p(act), 0, _p(cra), _p(emm2), H, I, _p(W.w2),
+                  _p(W.s2), _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
+                  _p(seg.tile_row0), lo, hi, seg.max_tiles, seg.bm, _p(y), 0.0, 1.0, 0.0, st)
         return
     fmt = W.fmt
     if fp8_pair32_use(W, fp8_scales_ok):
