@@ -178,3 +178,17 @@ def sampled_oracle(fmt, W, x, ids, wts, toks, limit=0.0, int8=False, alpha=1.0, 
     with ThreadPoolExecutor(max_workers=ORACLE_THREADS) as ex:
         rows = list(ex.map(one, range(len(toks))))
     return np.concatenate(rows, 0) if rows else np.zeros((0, H), np.float32)
+
+
+def threaded_oracle(fmt, dn: dict, x_bits, ids, wts, E, NS, H, I, limit=0.0):
+    """oracle_layer over dense numpy weights, one token per call spread over
+    host threads (the weights are read in place, never copied)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    def one(t):
+        sl = slice(t, t + 1)
+        return oracle_layer(fmt, dn, x_bits[sl], ids[sl], wts[sl], E, NS, H, I, limit=limit)
+
+    with ThreadPoolExecutor(max_workers=ORACLE_THREADS) as ex:
+        rows = list(ex.map(one, range(len(ids))))
+    return np.concatenate(rows, 0) if rows else np.zeros((0, H), np.float32)

@@ -101,14 +101,34 @@ def test_ring_takes_the_engine_object_and_accumulates_into_out():
     assert st.bytes == len(set(ids[live].tolist())) * eng.host_store().expert_bytes()
 
 
-def test_ring_without_shared_home_falls_back():
+def test_ring_streams_shared_experts_without_a_pool():
+    """Without a pool the shared experts are streamed as one more tile (the
+    layer equals the all-resident one bit for bit); a layer that cannot be
+    streamed (more shared experts than a tile holds and no pool, a shape
+    mismatch) returns None before any copy is queued or any slot written."""
+    from xtu_moe_amd import ring as R
     E, NS, H, I, T, K = 16, 1, 512, 256, 40, 2
-    _, W = _layer(F.FMT_MXFP4, E, NS, H, I, seed=3)
+    d, W = _layer(F.FMT_MXFP4, E, NS, H, I, seed=3)
     x, ids, wts = _inputs(T, K, E, H, seed=4)
     store = HostExpertStore.from_weights(W)
-    assert gpu_moe_layer_from_engine_tiled(store, x, ids, wts, H, I, E, K, device=DEV,
-                                           tile_e=4) is None
+    ref = moe_forward(x, ids, wts, W, path="gemm", out_dtype=torch.float32)
+    st = RingStats()
+    out = gpu_moe_layer_from_engine_tiled(store, x, ids, wts, H, I, E, K, device=DEV, tile_e=4,
+                                          out_dtype=torch.float32, stats=st)
+    torch.cuda.synchronize()
+    st.finish()
+    routed = set(ids[(ids >= 0) & (ids < E)].tolist())
+    assert st.tiles == (len(routed) + 3) // 4 + 1
+    assert st.bytes == (len(routed) + NS) * store.expert_bytes()
+    np.testing.assert_array_equal(out.cpu().numpy(), ref.cpu().numpy())
+    # three shared experts do not fit a tile of two: refused, nothing queued
+    _, W3 = _layer(F.FMT_MXFP4, E, 3, H, I, seed=5)
+    store3 = HostExpertStore.from_weights(W3)
+    n_rings = len(R._RINGS)
+    assert gpu_moe_layer_from_engine_tiled(store3, x, ids, wts, H, I, E, K, device=DEV,
+                                           tile_e=2) is None
     assert gpu_moe_layer_from_engine_tiled(store, x, ids, wts, H + 256, I, E, K, device=DEV) is None
+    assert len(R._RINGS) == n_rings   # no ring was even allocated for them
 
 
 def _restricted(W, x, ids, wts, resident):

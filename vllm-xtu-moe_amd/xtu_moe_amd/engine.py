@@ -9,7 +9,9 @@ Mirrors the reference engine's Python binding
 buffer ABI (:1368-1437 ``shard_geometry`` / ``pin_hostbufs`` /
 ``copy_hostbuf_to_device`` / ``copy_hostbuf_to_device_2d``).  The reference engine computes on the CPU; here
 the same call runs the HIP kernels on the weights' device copy, and the
-pinned host copy serves the ring stage and the resident pool.
+pinned host copy serves the ring stage and the resident pool.  An engine
+built ``host_resident=True`` keeps the experts in the pinned host shards
+only, as the reference engine does, and streams them through the ring.
 """
 from __future__ import annotations
 
@@ -21,7 +23,7 @@ import torch
 
 from . import formats as F
 from .host_store import HostExpertStore
-from .layer import ExpertWeights, moe_forward
+from .layer import ExpertWeights, int8_align_on, moe_forward
 
 
 @dataclass
@@ -55,7 +57,13 @@ class _Engine:
     HOST = False     # weights kept in host memory, computed by the host engine
 
     def __init__(self, cfg: MOEConfigV2, w13_weight, w2_weight, w13_scale=0, w2_scale=0,
-                 w13_global_scale=0, w2_global_scale=0, device=None):
+                 w13_global_scale=0, w2_global_scale=0, device=None, host_resident=False):
+        """host_resident: keep the experts in pinned host memory only (the
+        reference engine's own residency, moe_v2.hpp:454-640, :1804-1860):
+        they are packed on the host straight into the NUMA-node shards of the
+        host store, with no device copy; forward_many then streams them
+        through the tile ring for device inputs and runs the host engine for
+        host inputs, and cpu_decode reads the same shards."""
         if cfg.expert_num <= 0 or cfg.hidden_size <= 0 or cfg.intermediate_size <= 0:
             raise ValueError("MOEConfigV2: expert_num, hidden_size, intermediate_size must be set")
         gn, gk = self.GROUP
@@ -68,14 +76,26 @@ class _Engine:
             raise ValueError("int8_activation needs MXFP4 (e8m0) weights")
         self.cfg = cfg
         opt = lambda v: None if (v is None or isinstance(v, int)) else v
-        dev = (torch.device("cpu") if self.HOST else
-               torch.device(device) if device is not None else torch.device("cuda"))
-        self.weights = ExpertWeights.from_dense(self.FMT, w13_weight, opt(w13_scale), w2_weight,
-                                                opt(w2_scale), opt(w13_global_scale),
-                                                opt(w2_global_scale), device=dev)
+        self.host_resident = bool(host_resident) and not self.HOST
+        self.device = (torch.device(device) if device is not None else
+                       (w13_weight.device if getattr(w13_weight, "is_cuda", False)
+                        else torch.device("cuda")))
+        dev = torch.device("cpu") if (self.HOST or self.host_resident) else self.device
+        W = ExpertWeights.from_dense(self.FMT, w13_weight, opt(w13_scale), w2_weight,
+                                     opt(w2_scale), opt(w13_global_scale), opt(w2_global_scale),
+                                     device=dev)
+        self.H, self.I, self.E = W.H, W.I, W.E
         self._store = None
         self._cpu = []          # host engines; the last one is current (see _host_engine)
         self._fwd = None        # host-only engine of forward_many (host-format engines)
+        if self.host_resident:
+            # the packed host copy goes straight into the pinned shards and
+            # is dropped: the shards are the only copy of the experts
+            self._store = HostExpertStore.from_weights(W, ns=self.shard_count(),
+                                                       pin=torch.cuda.is_available())
+            self.weights = None
+        else:
+            self.weights = W
 
     # ------------------------------------------------------------ forward
     def forward_many(self, qlen: int, top_k: int, expert_ids, weights, x, out):
@@ -85,10 +105,40 @@ class _Engine:
         ids = expert_ids.reshape(qlen, top_k).to(torch.int32)
         ids = torch.where(ids < 0, torch.full_like(ids, -1), ids)
         lim = c.swiglu_limit if c.activation_type == 1 else 0.0
+        if self.host_resident:
+            return self._forward_host_resident(qlen, top_k, ids, weights, x, out, lim)
         res = moe_forward(x.reshape(qlen, c.hidden_size).to(torch.bfloat16).contiguous(), ids,
                           weights.reshape(qlen, top_k).float(), self.weights, swiglu_limit=lim,
                           swiglu_alpha=c.swiglu_alpha, swiglu_beta=c.swiglu_beta,
                           out_dtype=torch.float32, int8="auto" if c.int8_activation else False, path="auto")
+        out.view(qlen, c.hidden_size).copy_(res)
+        return out
+
+    def _forward_host_resident(self, qlen, top_k, ids, weights, x, out, lim):
+        """forward_many of a host-resident engine: device inputs stream the
+        routed experts through the tile ring (the reference's long-prefill
+        path, gpu_prefill.py:2984-3095); host inputs, or a layer the ring
+        cannot take, run the host engine over the same shards."""
+        from .ring import gpu_moe_layer_from_engine_tiled
+        c = self.cfg
+        xs = x.reshape(qlen, c.hidden_size).to(torch.bfloat16).contiguous()
+        w = weights.reshape(qlen, top_k).float().contiguous()
+        res = None
+        if xs.is_cuda and not torch.cuda.is_current_stream_capturing():
+            res = gpu_moe_layer_from_engine_tiled(
+                self._store, xs, ids.to(xs.device), w.to(xs.device), self.H, self.I, self.E,
+                top_k, device=xs.device, out_dtype=torch.float32, swiglu_limit=lim,
+                swiglu_alpha=c.swiglu_alpha, swiglu_beta=c.swiglu_beta,
+                int8=bool(c.int8_activation) and int8_align_on(qlen))
+        if res is None:
+            if self._fwd is None:
+                from .cpu_experts import CpuExperts
+                self._fwd = CpuExperts.from_store(self._store, swiglu_limit=lim,
+                                                  swiglu_alpha=c.swiglu_alpha,
+                                                  swiglu_beta=c.swiglu_beta)
+            if xs.is_cuda:
+                torch.cuda.current_stream(xs.device).synchronize()
+            res = self._fwd.forward(xs.cpu(), ids.cpu(), w.cpu())
         out.view(qlen, c.hidden_size).copy_(res)
         return out
 
@@ -116,8 +166,7 @@ class _Engine:
             ns = 0
         if ns < 2:
             ns = max(1, len(glob.glob("/sys/devices/system/node/node[0-9]*")))
-        W = self.weights
-        if ns < 2 or W.I % (16 * ns) or W.H % (16 * ns):
+        if ns < 2 or self.I % (16 * ns) or self.H % (16 * ns):
             return 1
         return ns
 

@@ -215,15 +215,44 @@ class HostExpertStore:
         return moved
 
 
-def empty_slots(fmt, H, I, n_slots, like: HostExpertStore, device) -> ExpertWeights:
-    """Device planes for n_slots experts in the store's layout."""
-    planes = {"w13": torch.empty((n_slots, like.row_bytes("w13")), dtype=torch.uint8, device=device),
-              "w2": torch.empty((n_slots, like.row_bytes("w2")), dtype=torch.uint8, device=device)}
-    for name in ("s13", "s2", "gs13", "gs2"):
-        src = like.planes[name]
-        planes[name] = None if src is None else torch.empty((n_slots,) + tuple(src.shape[1:]),
-                                                            dtype=src.dtype, device=device)
-    f8ok = like.fp8_scales_bounded() if int(fmt) == F.FMT_FP8 else None
+def slot_plane_specs(fmt, H, I) -> dict:
+    """Per-expert (shape, dtype) of each device plane of a layer in format
+    `fmt` (None: the format has no such plane): the packed P16 weights and
+    scale groups, FP8's fp32 block scales, NVFP4's fp32 global scales."""
+    fmt, H, I = int(fmt), int(H), int(I)
+    u8, f32 = torch.uint8, torch.float32
+    spec = {"w13": ((2 * I * F.row_bytes(fmt, H),), u8), "w2": ((H * F.row_bytes(fmt, I),), u8),
+            "s13": None, "s2": None, "gs13": None, "gs2": None}
+    if fmt == F.FMT_FP8:
+        spec["s13"] = (((2 * I // 128) * (H // 128),), f32)
+        spec["s2"] = (((H // 128) * (I // 128),), f32)
+    elif fmt in (F.FMT_MXFP4, F.FMT_NVFP4):
+        spec["s13"] = ((F.scale_bytes(fmt, 2 * I, H),), u8)
+        spec["s2"] = ((F.scale_bytes(fmt, H, I),), u8)
+        if fmt == F.FMT_NVFP4:
+            spec["gs13"] = spec["gs2"] = ((), f32)
+    elif fmt != F.FMT_BF16:
+        raise ValueError(f"no device slot layout for format {fmt}")
+    return spec
+
+
+def empty_slots(fmt, H, I, n_slots, like: HostExpertStore | None, device) -> ExpertWeights:
+    """Device planes for n_slots experts in the store's layout (or, with no
+    store, the format's: slot_plane_specs)."""
+    if like is not None:
+        planes = {"w13": torch.empty((n_slots, like.row_bytes("w13")), dtype=torch.uint8,
+                                     device=device),
+                  "w2": torch.empty((n_slots, like.row_bytes("w2")), dtype=torch.uint8,
+                                    device=device)}
+        for name in ("s13", "s2", "gs13", "gs2"):
+            src = like.planes[name]
+            planes[name] = None if src is None else torch.empty(
+                (n_slots,) + tuple(src.shape[1:]), dtype=src.dtype, device=device)
+    else:
+        planes = {name: None if sp is None else torch.empty((n_slots,) + sp[0], dtype=sp[1],
+                                                            device=device)
+                  for name, sp in slot_plane_specs(fmt, H, I).items()}
+    f8ok = like.fp8_scales_bounded() if (like is not None and int(fmt) == F.FMT_FP8) else None
     return register_slot_planes(
         ExpertWeights(fmt, H, I, n_slots, 0, planes["w13"], planes["s13"], planes["w2"],
                       planes["s2"], planes["gs13"], planes["gs2"], mutable=True,

@@ -462,6 +462,33 @@ def int8_align_on(T: int, allowed: bool = True) -> bool:
     return m > 0 and int(T) >= m
 
 
+INT8_ENV = "XIAOTU_MOE_INT8"
+INT8_VNNI_ENV = "XIAOTU_MOE_INT8_VNNI"
+
+
+def int8_dispatch(fmt: int):
+    """Whether the quant-method hook lets a layer of this format take the
+    INT8 ALIGN path, from the reference's switches (vllm_xiaotu_moe/
+    mixed_experts.py:1457-1484): XIAOTU_MOE_INT8=0 turns it off (None: not
+    even when forced); XIAOTU_MOE_INT8_ALIGN=1 forces it at every batch size
+    (int8_align_on); XIAOTU_MOE_INT8=1 allows it from the token gate on.
+    Only MXFP4 weights qualify (e8m0 scales make the int8 weights exact).
+    Unlike the reference, whose CPU engine allows it by default for MXFP4
+    (there int8 runs ~1.5x its fp32 path), it is off by default: on the GPU
+    the MXFP4 MFMA path is faster and keeps the layer within the fp32 bar,
+    while the power-of-two per-row int8 activations leave ~2e-2 of rel-L2.
+    XIAOTU_MOE_INT8_VNNI=1 (the reference's older VNNI scheme) is refused."""
+    if int(fmt) != FMT_MXFP4:
+        return False
+    v = os.environ.get(INT8_ENV)
+    if v == "0":
+        return None
+    if os.environ.get(INT8_VNNI_ENV, "0") == "1" and os.environ.get(INT8_FORCE_ENV, "0") != "1":
+        raise NotImplementedError("XIAOTU_MOE_INT8_VNNI=1: the older int8 VNNI scheme is not "
+                                  "provided; XIAOTU_MOE_INT8_ALIGN=1 selects the ALIGN path")
+    return v == "1"
+
+
 def decode_max_tiles(A: int, max_active: int) -> int:
     """Upper bound on the 16-row tiles of a decode batch of A pairs over at
     most max_active non-empty expert buckets: a bucket of n rows has

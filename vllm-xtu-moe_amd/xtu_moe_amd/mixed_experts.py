@@ -13,9 +13,13 @@ scale attribute names and the scale groups (:3308-3476): BF16 1x1, MXFP4
 (WNA16) 1xgroup with the GPTQ / compressed-tensors repack.
 
 Here the experts run on the HIP library with the layer's weights packed once
-into the device layout (INT4 on the host engine, as the reference's
-MOE_WNA16); vLLM itself is not needed (an ``activation`` of None or a string
-name is accepted when vLLM's enum is absent).
+into the device layout when the layer is resident, or kept in pinned host
+shards behind ``host_layer.HostResidentLayer`` (tile ring for long prefill,
+pool split or host engine otherwise) when it is not (INT4 always on the
+host engine, as the reference's MOE_WNA16); vLLM itself is not needed (an
+``activation`` of None or a string name is accepted when vLLM's enum is
+absent).  The INT8 ALIGN path follows the reference's environment switches
+(``int8_dispatch``).
 """
 from __future__ import annotations
 
@@ -24,7 +28,8 @@ import enum
 import torch
 
 from . import formats as F
-from .layer import ExpertWeights, _buf as _scratch, moe_forward, route
+from .host_layer import HostResidentLayer, layer_index, resident_decision
+from .layer import ExpertWeights, _buf as _scratch, int8_align_on, int8_dispatch, moe_forward, route
 
 _ROUTING_ATTRS = ("use_grouped_topk", "renormalize", "scoring_func", "custom_routing_function",
                   "num_expert_group", "topk_group", "e_score_correction_bias",
@@ -51,6 +56,8 @@ class XiaotuExperts:
         self.moe_config, self.quant_config = moe_config, quant_config
         self._layer_ref = None
         self._weights: ExpertWeights | None = None
+        self._host_layer = None      # HostResidentLayer of a layer kept in host memory
+        self._int8_allowed = False
         self.use_grouped_topk = False
         self.renormalize = False
         self.scoring_func = "softmax"
@@ -75,14 +82,53 @@ class XiaotuExperts:
 
     # ---------------------------------------------------------- loading
     def process_weights_after_loading(self, layer) -> None:
+        """Packs the layer's experts for the kernels: into HBM when the layer
+        is resident (host_layer.resident_decision: the reference's
+        XIAOTU_MOE_GPU_RESIDENT_LAYERS list, else a device-memory budget),
+        otherwise into pinned host shards behind a HostResidentLayer (ring for
+        long prefill, pool split or host engine for the rest)."""
         self._read_layer_attrs(layer)
+        self._int8_allowed = int8_dispatch(self._fmt)
         w13, w2 = layer.w13_weight, layer.w2_weight
         s13 = self._find(layer, self._scale_attrs[0])
         s2 = self._find(layer, self._scale_attrs[1])
         g13, g2 = self._global_scales(layer)
         dev = torch.device("cuda") if not w13.is_cuda else w13.device
-        self._weights = ExpertWeights.from_dense(self._fmt, self._weight_view(w13), s13,
-                                                 self._weight_view(w2), s2, g13, g2, device=dev)
+        w13v, w2v = self._weight_view(w13), self._weight_view(w2)
+        H, I = int(w2v.shape[1]), int(w13v.shape[1]) // 2
+        nbytes = int(w13v.shape[0]) * F.expert_bytes(self._fmt, H, I)
+        if resident_decision(layer, nbytes, dev):
+            self._weights = ExpertWeights.from_dense(self._fmt, w13v, s13, w2v, s2, g13, g2,
+                                                     device=dev)
+            self._host_layer = None
+            return
+        self._weights = None
+        self._host_layer = HostResidentLayer(
+            self._fmt, w13v, s13, w2v, s2, g13, g2, device=dev, top_k=int(self.top_k or 1),
+            layer_idx=layer_index(layer), group_k=int(self._group_k),
+            swiglu_limit=float(self.swiglu_limit or 0.0),
+            swiglu_alpha=float(self.swiglu_alpha if self.swiglu_alpha is not None else 1.0),
+            swiglu_beta=float(self.swiglu_beta or 0.0))
+        self._release_device_sources(layer)
+
+    _SOURCE_ATTRS = ("w13_weight", "w2_weight", "w13_weight_scale", "w2_weight_scale",
+                     "w13_weight_scale_inv", "w2_weight_scale_inv", "w13_weight_scale_2",
+                     "w2_weight_scale_2")
+
+    def _release_device_sources(self, layer) -> None:
+        """A host-resident layer's checkpoint tensors that sit in device
+        memory are emptied once the host shards hold the experts (the
+        reference releases the source after building its engine,
+        mixed_experts.py:2083-2094): the layer's HBM then holds only its pool
+        slots.  Their shapes are kept in ``_released_shapes``."""
+        if getattr(self, "_released_shapes", None) is None:
+            self._released_shapes = {}
+        for name in self._SOURCE_ATTRS:
+            t = getattr(layer, name, None)
+            if not isinstance(t, torch.Tensor) or not t.is_cuda or t.numel() == 0:
+                continue
+            self._released_shapes[name] = tuple(t.shape)
+            t.data = torch.empty(0, dtype=t.dtype, device=t.device)
 
     def _global_scales(self, layer):
         return None, None
@@ -155,7 +201,7 @@ class XiaotuExperts:
                                       "apply_router_weight_on_input")
         if activation is not None and not self._supports_activation(activation):
             raise NotImplementedError(f"unsupported activation {activation}")
-        if self._weights is None:
+        if self._weights is None and self._host_layer is None:
             raise RuntimeError("apply called before process_weights_after_loading")
         if num_expert_group is not None:
             self.num_expert_group = num_expert_group
@@ -171,8 +217,9 @@ class XiaotuExperts:
             x = x.to(torch.bfloat16).contiguous()
         odt = hidden_states.dtype if hidden_states.dtype in (torch.bfloat16, torch.float32) \
             else torch.float32
+        H = self._weights.H if self._weights is not None else self._host_layer.H
         direct = (output is not None and output.dtype == odt and output.is_contiguous()
-                  and tuple(output.shape) == (T, self._weights.H) and output.device == x.device)
+                  and tuple(output.shape) == (T, H) and output.device == x.device)
         kw = dict(swiglu_limit=float(self.swiglu_limit or 0.0),
                   swiglu_alpha=float(self.swiglu_alpha if self.swiglu_alpha is not None else 1.0),
                   swiglu_beta=float(self.swiglu_beta or 0.0),
@@ -180,14 +227,14 @@ class XiaotuExperts:
         if topk_weights is not None and topk_ids is not None:
             res = self._experts(x, topk_ids.to(torch.int32).contiguous(),
                                 topk_weights.to(torch.float32).contiguous(), kw)
-        elif (self._monolithic and expert_map is None and self.custom_routing_function is None
-              and router_logits is not None):
+        elif (self._monolithic and self._weights is not None and expert_map is None
+              and self.custom_routing_function is None and router_logits is not None):
             # monolithic path: routing (+ segmentation, + the shared experts'
             # gate/up at decode sizes) inside the layer's own launches
             ids = _scratch("hook_ids", (T, int(self.top_k)), torch.int32, x.device)
             wts = _scratch("hook_wts", (T, int(self.top_k)), torch.float32, x.device)
             res = moe_forward(x, ids, wts, self._weights, router=self._router_args(router_logits),
-                              **kw)
+                              int8=self._int8(T), **kw)
         else:
             topk_weights, topk_ids = self._select_topk(hidden_states, router_logits)
             if expert_map is not None:
@@ -205,10 +252,24 @@ class XiaotuExperts:
     # the router logits are given (GPU formats)
     _monolithic = True
 
+    def _int8(self, T: int) -> bool:
+        """Whether a call of T tokens takes the INT8 ALIGN path (MXFP4 only;
+        int8_dispatch, then the token gate of int8_align_on)."""
+        if self._fmt != F.FMT_MXFP4 or self._int8_allowed is None:
+            return False
+        return int8_align_on(T, bool(self._int8_allowed))
+
     def _experts(self, x, ids, wts, kw):
         """The experts over routed pairs: out [T, H] (kw: swiglu_*, out,
         out_dtype)."""
-        return moe_forward(x, ids, wts, self._weights, **kw)
+        if self._host_layer is None:
+            return moe_forward(x, ids, wts, self._weights, int8=self._int8(x.shape[0]), **kw)
+        res = self._host_layer.forward(x, ids, wts, int8=self._int8(x.shape[0]))
+        out = kw.get("out")
+        if out is not None:
+            out.copy_(res)
+            return out
+        return res.to(kw.get("out_dtype", torch.float32))
 
     def _router_args(self, router_logits) -> dict:
         lg = router_logits
