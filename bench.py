@@ -63,14 +63,23 @@ WORKLOADS = {
     "qwen3-next-nvfp4": dict(fmt="nvfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
                              Ts=[1, 4, 8192], limit=7.0, int8=False, graph=True),
     "mixtral-tiny-bf16": dict(fmt="bf16", E=8, NS=0, H=1024, I=2048, K=2, router="softmax",
-                              Ts=[128], limit=0.0, int8=False, graph=True, graph_max_T=128),
+                              Ts=[128], limit=0.0, int8=False, graph=True, graph_max_T=128,
+                              bound="hbm"),
     "ds-v3-fp8-streamed": dict(fmt="fp8", E=256, NS=1, H=7168, I=2048, K=8, router="grouped",
                                Ts=[8192], limit=0.0, int8=False, graph=False, resident=64,
                                tile_e=16, nslots=4, zipf=1.1),
 }
 PCIE_GEN5_X16_GBS = 64.0   # per direction, before protocol overhead
-DEFAULT_SET = "ds-v3-mxfp4"   # decode T=1,2,4 plus the two prefill layers below
+DEFAULT_SET = "ds-v3-mxfp4"   # decode T=1,2,4 plus every configuration below
 PREFILL_SET = ("ds-v3-mxfp4-prefill", "ds-v3-fp8-prefill")
+# the default run's sub-lines: each workload's own line (roofline, cpu_baseline)
+# under config.configs, keyed by workload, with the configuration it measures
+SUITE = (("ds-v3-mxfp4-prefill", "north star: DS-V3 MXFP4 prefill T=8192"),
+         ("ds-v3-fp8-prefill", "C3: DS-V3 FP8 prefill T=8192"),
+         ("qwen3-next-int8", "C4: Qwen3-Next MXFP4, decode T=1,4 and INT8 ALIGN T=8192"),
+         ("qwen3-next-nvfp4", "C4: Qwen3-Next NVFP4 T=1,4,8192"),
+         ("mixtral-tiny-bf16", "C1: tiny Mixtral bf16 T=128"),
+         ("ds-v3-fp8-streamed", "C5: DS-V3 FP8 streamed prefill, 64 resident + 192 streamed"))
 PREFILL_STEPS = 5
 CHAIN = 8                  # layers per decode graph
 
@@ -100,15 +109,14 @@ def main():
 
     if args.workload == DEFAULT_SET:
         return bench_default(args)
-    line = bench_one(args)
-    if line is not None:
-        print(json.dumps(line), flush=True)
+    print(json.dumps(bench_one(args)), flush=True)
 
 
 def bench_default(args):
-    """The headline set: the decode workload's line (value = tok/s at T=4)
-    with the two DeepSeek-V3 prefill layers at T = 8192 (MXFP4 and FP8,
-    PREFILL_STEPS timed steps each) under config.prefill."""
+    """The headline line (the DS-V3 MXFP4 decode workload, value = tok/s at
+    T=4) with every other configuration's line under config.configs (its
+    own roofline and cpu_baseline; prefill workloads PREFILL_STEPS timed
+    steps), the two DS-V3 prefill layers also under config.prefill."""
     import gc
 
     import torch
@@ -116,21 +124,33 @@ def bench_default(args):
     a = argparse.Namespace(**vars(args))
     a.workload = "ds-v3-mxfp4-decode"
     line = bench_one(a)
-    pre = {}
-    for wl in PREFILL_SET:
+    subs = {}
+    for wl, what in SUITE:
         gc.collect()
         torch.cuda.empty_cache()
         b = argparse.Namespace(**vars(args))
-        b.workload, b.no_cpu_baseline = wl, True
-        b.steps, b.warmup = min(args.steps, PREFILL_STEPS), min(args.warmup, 2)
-        pl = bench_one(b)
-        r = pl["config"]["per_T"]["8192"]
-        pre[wl] = dict(T=8192, steps=b.steps, warmup=b.warmup, layer_ms=r["layer_ms"],
+        b.workload = wl
+        if max(WORKLOADS[wl]["Ts"]) > 16 and not WORKLOADS[wl].get("graph"):
+            b.steps, b.warmup = min(args.steps, PREFILL_STEPS), min(args.warmup, 2)
+        t0 = time.time()
+        sub = bench_one(b)
+        sub = {k: v for k, v in sub.items() if k not in ("metric", "n_gpus", "higher_is_better",
+                                                         "scaling", "vs_baseline")}
+        sub["measures"] = what
+        sub["bench_s"] = time.time() - t0
+        subs[wl] = sub
+    pre = {}
+    for wl in PREFILL_SET:
+        sl = subs[wl]
+        r = sl["config"]["per_T"]["8192"]
+        pre[wl] = dict(T=8192, steps=sl["steps"], warmup=sl["warmup"], layer_ms=r["layer_ms"],
                        tok_s=r["tok_s"], gate_up_ms=r["gate_up_ms"],
-                       gate_up_TFLOPs=r["gate_up_TFLOPs"], dtype=pl["dtype"],
-                       distinct_experts=r["distinct_experts"], roofline=pl["roofline"])
+                       gate_up_TFLOPs=r["gate_up_TFLOPs"], dtype=sl["dtype"],
+                       distinct_experts=r["distinct_experts"], roofline=sl["roofline"])
     line["config"]["workload"] = DEFAULT_SET
+    line["config"]["measures"] = "C2: DS-V3 MXFP4 decode T=1,2,4"
     line["config"]["prefill"] = pre
+    line["config"]["configs"] = subs
     print(json.dumps(line), flush=True)
 
 
@@ -173,8 +193,7 @@ def bench_one(args):
 
     cfg = WORKLOADS[args.workload]
     if "resident" in cfg:
-        streamed(args, cfg)
-        return None
+        return streamed(args, cfg)
     if args.pmc_child:
         return pmc_child(args, cfg, args.pmc_child)
     fmt = F.fmt_of(cfg["fmt"])
@@ -463,7 +482,9 @@ def bench_one(args):
                           event_overhead_us=ev_overhead * 1e3, gate_up_bytes=gu_bytes,
                           single_layer_graph_ms=single_ms, int8_activation=bool(i8),
                           layer_chain=len(chain_Ws) if chain_ms else 1,
-                          hook_layer_ms=hook_layer_ms)
+                          hook_layer_ms=hook_layer_ms,
+                          layer_hbm_frac=layer_bytes / (mean_layer / 1e3) / 1e9 / HBM_PEAK_GBS,
+                          layer_ideal_us=layer_bytes / (HBM_PEAK_GBS * 1e9) * 1e6)
         log(f"[bench] T={T}: layer {mean_layer * 1e3:.1f} us ({results[T]['layer_GBs']:.0f} GB/s; "
             f"single-layer graph {single_ms * 1e3:.1f} us"
             + (f"; through the hook's apply {hook_layer_ms * 1e3:.1f} us" if hook_layer_ms else "")
@@ -502,6 +523,12 @@ def bench_one(args):
                 if tr.get("distinct_experts"):   # the counter run's own routing
                     tr["algorithmic_bytes"] = (tr["distinct_experts"] * e_bytes13 + Th * H * 2
                                                + (Th * K + Th * NS) * I * 2)
+    elif cfg.get("bound") == "hbm":
+        # a batch whose weights outweigh its arithmetic (tiny Mixtral: 128
+        # tokens over 8 experts of 12.6 MB): the grouped GEMM against HBM
+        roof = dict(bound="hbm", achieved=r["gate_up_GBs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=r["gate_up_GBs"] / HBM_PEAK_GBS, traffic=None, kernel="moe_gemm_kernel",
+                    layer_frac=r["layer_GBs"] / HBM_PEAK_GBS)
     elif mx_tri(fmt, H, I) and not cfg["int8"] and not decode_head:
         # fp6 / fp4 A (activation triples) x e2m1 B on the double-rate
         # 32x32x64 MFMA: the fp6/fp4 peak; every algorithmic product is three
@@ -834,7 +861,7 @@ def streamed(args, cfg):
                      "kernel": "xtu_copy_experts (hipMemcpyAsync, side stream)"},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def cpu_baseline(cfg, W, T, rkw, seconds, dev):

@@ -364,6 +364,23 @@ hipError_t xtu_mx_tri_down(const uint8_t* q, const uint8_t* sq, int H, int I, co
                            const int32_t* tile_expert, const int32_t* tile_row0,
                            const int32_t* expert_tile_start, const int32_t* tile_lo,
                            const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream);
+/*   xtu_mx_duo_gate_up / _down: the same on the first two pieces of the
+ *     triples only (x ~= 2^e (p1 + p2/16), |error| <= 2^(e-6) of the 32-k
+ *     block, rms ~7.5e-4 of the values for N(0,1) rows): two double-rate
+ *     MFMAs per block and step.  No counterpart in the reference either. */
+hipError_t xtu_mx_duo_gate_up(const uint8_t* q, const uint8_t* sq, const int32_t* sorted_tok,
+                              int H, int I, const void* w13, const uint8_t* s13p, long w_estride,
+                              long s_estride, const int32_t* slot_map, const int32_t* seg_start,
+                              const int32_t* tile_expert, const int32_t* tile_row0,
+                              const int32_t* expert_tile_start, const int32_t* tile_lo,
+                              const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                              float alpha, float beta, hipStream_t stream);
+hipError_t xtu_mx_duo_down(const uint8_t* q, const uint8_t* sq, int H, int I, const void* w2,
+                           const uint8_t* s2p, long w_estride, long s_estride,
+                           const int32_t* slot_map, const int32_t* seg_start,
+                           const int32_t* tile_expert, const int32_t* tile_row0,
+                           const int32_t* expert_tile_start, const int32_t* tile_lo,
+                           const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream);
 
 /* -------------------------------------- INT8-activation x FP4-code (ALIGN) path
  * Replaces the engine's ALIGN integer path (xiaotu_moe/csrc/moe/

@@ -1,6 +1,7 @@
 """MXFP4 GEMMs on the 32x32x64 scaled MFMA, with exact e4m3 activation pairs
 (xtu_mx_pair_*) and with activation triples on the double-rate fp6 / fp4
-MFMA (xtu_mx_tri_*): the interleaved activation pairs bit-exact against the
+MFMA (xtu_mx_tri_*) or their first two pieces (xtu_mx_duo_*): the
+interleaved activation pairs bit-exact against the
 planar quantiser's, the triples bit-exact against their CPU restatement
 (tests/tri_ref.py), the step-major scale re-layout bit-exact against the
 dense scales, and the layer against the oracle in both modes over tile
@@ -24,7 +25,7 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
 
 
-@pytest.fixture(params=["pair", "tri"])
+@pytest.fixture(params=["pair", "tri", "duo"])
 def mode(request, monkeypatch):
     monkeypatch.setenv(L.MXFP4_PREFILL_ENV, request.param)
     return request.param
@@ -107,7 +108,7 @@ def _layer(fmt, E, NS, H, I, seed):
 
 
 def _on_kernel(fmt, H, I):
-    mode = "tri" if L.mx_tri(fmt, H, I) else "pair"
+    mode = L.mx_act_mode(fmt, H, I)
     return (L.mx_pair_kernel(fmt, H, I) and L.gemm_tile_m(fmt, False, H, I) == 128
             and os.environ.get(L.MXFP4_PREFILL_ENV) == mode)
 

@@ -109,3 +109,26 @@ def test_layout_round_trip_and_error_bound():
                                    q.reshape(M, -1, 64)[:, :, 24:48]], -1).reshape(M, 2 * K),
                    sq, K)
     assert np.abs(bad - xf).max() > 1e-3
+
+
+def test_first_two_pieces_error_bound():
+    """The MXFP4 prefill's "duo" activations are the triples' first two
+    pieces: x ~= 2^e (p1 + p2/16), |error| <= 2^(e-6) (half an e2m3 step of
+    the second piece, scaled), rms ~7.5e-4 of the values for N(0,1) rows --
+    inside the layer's 5e-3 bar with a wide margin; dropping the second
+    piece (a plausible indexing mistake) misses the bound."""
+    x = _rows()
+    M, K = x.shape
+    q, sq, (c1, c2, c3) = tri_split(x)
+    e = sq.astype(np.float64) - 127
+    v1, v2 = e2m3_value(c1), e2m3_value(c2)
+    two = np.exp2(e)[..., None] * (v1 + np.where((sq >= 4)[..., None], v2, 0.0) / 16)
+    xf = x.float().numpy().astype(np.float64).reshape(M, K // 32, 32)
+    err = np.abs(two - xf).max(-1)
+    ok = sq >= 8
+    assert np.all(err[ok] <= np.exp2(e - 6)[ok])
+    n = xf[:64]
+    rel = np.sqrt(((two[:64] - n) ** 2).mean() / (n ** 2).mean())
+    assert 2e-4 < rel < 1.5e-3, rel
+    one = np.exp2(e)[..., None] * v1
+    assert not np.all(np.abs(one - xf).max(-1)[ok] <= np.exp2(e - 6)[ok])

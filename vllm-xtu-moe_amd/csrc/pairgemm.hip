@@ -153,11 +153,16 @@ __global__ __launch_bounds__(256) void mx_pair_scales_kernel(const uint8_t* __re
 // ---------------------------------------------------------------------------
 // grouped GEMM
 // ---------------------------------------------------------------------------
-// TRI: activation triples (fp6, fp6, fp4 pieces, mx_tri_quant_kernel) on
-// the double-rate fp6 / fp4 x fp4 MFMA, three MFMAs per 32 x 32 block and
-// step; else exact e4m3 pairs, two MFMAs at the fp8 rate.
-template <bool GU, bool TRI, int STAGES>
+// Activation modes.  kTri: triples (fp6, fp6, fp4 pieces,
+// mx_tri_quant_kernel) on the double-rate fp6 / fp4 x fp4 MFMA, three MFMAs
+// per 32 x 32 block and step; kDuo: the same rows' first two pieces only
+// (x ~ 2^e (p1 + p2 / 16), |error| <= 2^(e-6)), two double-rate MFMAs;
+// kPair: exact e4m3 pairs, two MFMAs at the fp8 rate.
+enum { kPair = 0, kTri = 1, kDuo = 2 };
+
+template <bool GU, int MODE, int STAGES>
 __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a) {
+  constexpr bool TRI = MODE != kPair;   // the triple row layout (kTri, kDuo)
   constexpr int LEAD = STAGES - 1;   // steps of loads in flight ahead of the MFMAs
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
   // plane p = pieces 2p, 2p + 1 (k 16h.. and 32 + 16h.. of the row's hi or
   // lo 64 bytes); triples: the lane's 64 bytes of its k-half h, p1 = dwords
   // 0-5, p2 = 6-11, p3 = 12-15.
-  constexpr int kPieces = TRI ? 3 : 2;      // MFMAs per 32 x 32 block and step
+  constexpr int kPieces = MODE == kTri ? 3 : 2;   // MFMAs per 32 x 32 block and step
   constexpr int kBlockMfma = 8 * kPieces;   // per row block and step
   struct Frags {
     u32x4_t a[2][4];   // [mb][piece]
@@ -482,23 +487,27 @@ bool mx_fits(int H, int I) {
 // (K = 2048 leaves LDS for it) measured no faster at DeepSeek-V3 T = 8192
 constexpr int kStages = 3;
 
-template <bool GU, bool TRI>
+template <bool GU, int MODE>
 hipError_t launch_k(dim3 g, int K, const MxPairArgs& a, hipStream_t stream) {
-  mx_pair_gemm_kernel<GU, TRI, kStages><<<g, kPThreads, lds_bytes(kStages, K), stream>>>(a);
+  mx_pair_gemm_kernel<GU, MODE, kStages><<<g, kPThreads, lds_bytes(kStages, K), stream>>>(a);
   return hipPeekAtLastError();
 }
 
-hipError_t launch(bool gu, bool tri, const MxPairArgs& a, int max_tiles, hipStream_t stream) {
+hipError_t launch(bool gu, int mode, const MxPairArgs& a, int max_tiles, hipStream_t stream) {
   const long items = (long)max_tiles * (gu ? a.I / 256 : a.H / 512);
   const long grid = (items + 7) / 8 * 8;
   if (grid >= (1L << 31)) return hipErrorInvalidValue;
   if (grid == 0) return hipSuccess;
   const dim3 g((unsigned)grid);
   const int K = gu ? a.H : a.I;
-  if (gu && tri) return launch_k<true, true>(g, K, a, stream);
-  if (gu) return launch_k<true, false>(g, K, a, stream);
-  if (tri) return launch_k<false, true>(g, K, a, stream);
-  return launch_k<false, false>(g, K, a, stream);
+  if (gu) {
+    if (mode == kTri) return launch_k<true, kTri>(g, K, a, stream);
+    if (mode == kDuo) return launch_k<true, kDuo>(g, K, a, stream);
+    return launch_k<true, kPair>(g, K, a, stream);
+  }
+  if (mode == kTri) return launch_k<false, kTri>(g, K, a, stream);
+  if (mode == kDuo) return launch_k<false, kDuo>(g, K, a, stream);
+  return launch_k<false, kPair>(g, K, a, stream);
 }
 
 }  // namespace
@@ -537,7 +546,7 @@ hipError_t xtu_mx_pair_scales(const uint8_t* s, int E, int N, int K, long s_estr
   return hipPeekAtLastError();
 }
 
-static hipError_t gate_up(bool tri, const uint8_t* hilo, const uint8_t* shi,
+static hipError_t gate_up(int mode, const uint8_t* hilo, const uint8_t* shi,
                           const int32_t* sorted_tok, int H, int I, const void* w13,
                           const uint8_t* s13p, long w_estride, long s_estride,
                           const int32_t* slot_map, const int32_t* seg_start,
@@ -555,10 +564,10 @@ static hipError_t gate_up(bool tri, const uint8_t* hilo, const uint8_t* shi,
   const MxPairArgs a{hilo, shi, sorted_tok, (const uint8_t*)w13, s13p, seg_start, tile_expert,
                      tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, act, H, I,
                      w_estride, s_estride, limit, alpha, beta};
-  return launch(true, tri, a, max_tiles, stream);
+  return launch(true, mode, a, max_tiles, stream);
 }
 
-static hipError_t down(bool tri, const uint8_t* hilo, const uint8_t* shi, int H, int I,
+static hipError_t down(int mode, const uint8_t* hilo, const uint8_t* shi, int H, int I,
                        const void* w2, const uint8_t* s2p, long w_estride, long s_estride,
                        const int32_t* slot_map, const int32_t* seg_start,
                        const int32_t* tile_expert, const int32_t* tile_row0,
@@ -574,7 +583,7 @@ static hipError_t down(bool tri, const uint8_t* hilo, const uint8_t* shi, int H,
   const MxPairArgs a{hilo, shi, nullptr, (const uint8_t*)w2, s2p, seg_start, tile_expert,
                      tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, y, H, I,
                      w_estride, s_estride, 0.f, 1.f, 0.f};
-  return launch(false, tri, a, max_tiles, stream);
+  return launch(false, mode, a, max_tiles, stream);
 }
 
 hipError_t xtu_mx_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const int32_t* sorted_tok,
@@ -585,7 +594,7 @@ hipError_t xtu_mx_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const in
                                const int32_t* tile_lo, const int32_t* tile_hi, int max_tiles,
                                void* act, float limit, float alpha, float beta,
                                hipStream_t stream) {
-  return gate_up(false, hilo, shi, sorted_tok, H, I, w13, s13p, w_estride, s_estride, slot_map,
+  return gate_up(kPair, hilo, shi, sorted_tok, H, I, w13, s13p, w_estride, s_estride, slot_map,
                  seg_start, tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi,
                  max_tiles, act, limit, alpha, beta, stream);
 }
@@ -596,7 +605,7 @@ hipError_t xtu_mx_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int 
                             const int32_t* tile_expert, const int32_t* tile_row0,
                             const int32_t* expert_tile_start, const int32_t* tile_lo,
                             const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream) {
-  return down(false, hilo, shi, H, I, w2, s2p, w_estride, s_estride, slot_map, seg_start,
+  return down(kPair, hilo, shi, H, I, w2, s2p, w_estride, s_estride, slot_map, seg_start,
               tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi, max_tiles, y, stream);
 }
 
@@ -619,7 +628,7 @@ hipError_t xtu_mx_tri_gate_up(const uint8_t* q, const uint8_t* sq, const int32_t
                               const int32_t* expert_tile_start, const int32_t* tile_lo,
                               const int32_t* tile_hi, int max_tiles, void* act, float limit,
                               float alpha, float beta, hipStream_t stream) {
-  return gate_up(true, q, sq, sorted_tok, H, I, w13, s13p, w_estride, s_estride, slot_map,
+  return gate_up(kTri, q, sq, sorted_tok, H, I, w13, s13p, w_estride, s_estride, slot_map,
                  seg_start, tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi,
                  max_tiles, act, limit, alpha, beta, stream);
 }
@@ -630,7 +639,29 @@ hipError_t xtu_mx_tri_down(const uint8_t* q, const uint8_t* sq, int H, int I, co
                            const int32_t* tile_expert, const int32_t* tile_row0,
                            const int32_t* expert_tile_start, const int32_t* tile_lo,
                            const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream) {
-  return down(true, q, sq, H, I, w2, s2p, w_estride, s_estride, slot_map, seg_start, tile_expert,
+  return down(kTri, q, sq, H, I, w2, s2p, w_estride, s_estride, slot_map, seg_start, tile_expert,
+              tile_row0, expert_tile_start, tile_lo, tile_hi, max_tiles, y, stream);
+}
+
+hipError_t xtu_mx_duo_gate_up(const uint8_t* q, const uint8_t* sq, const int32_t* sorted_tok,
+                              int H, int I, const void* w13, const uint8_t* s13p, long w_estride,
+                              long s_estride, const int32_t* slot_map, const int32_t* seg_start,
+                              const int32_t* tile_expert, const int32_t* tile_row0,
+                              const int32_t* expert_tile_start, const int32_t* tile_lo,
+                              const int32_t* tile_hi, int max_tiles, void* act, float limit,
+                              float alpha, float beta, hipStream_t stream) {
+  return gate_up(kDuo, q, sq, sorted_tok, H, I, w13, s13p, w_estride, s_estride, slot_map,
+                 seg_start, tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi,
+                 max_tiles, act, limit, alpha, beta, stream);
+}
+
+hipError_t xtu_mx_duo_down(const uint8_t* q, const uint8_t* sq, int H, int I, const void* w2,
+                           const uint8_t* s2p, long w_estride, long s_estride,
+                           const int32_t* slot_map, const int32_t* seg_start,
+                           const int32_t* tile_expert, const int32_t* tile_row0,
+                           const int32_t* expert_tile_start, const int32_t* tile_lo,
+                           const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream) {
+  return down(kDuo, q, sq, H, I, w2, s2p, w_estride, s_estride, slot_map, seg_start, tile_expert,
               tile_row0, expert_tile_start, tile_lo, tile_hi, max_tiles, y, stream);
 }
 

@@ -65,6 +65,10 @@ SIGNATURES = {
                                 _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
     "xtu_mx_tri_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp, _vp,
                              _vp, _i, _vp, _vp]),
+    "xtu_mx_duo_gate_up": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
+                                _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
+    "xtu_mx_duo_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp, _vp,
+                             _vp, _i, _vp, _vp]),
     "xtu_fp8pair_quant": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "xtu_gemm8_gate_up": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp,
                                _vp, _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),

@@ -539,9 +539,12 @@ def fp8_pair32_use(W, scales_ok=None) -> bool:
 
 # "auto": the 32x32x64 MXFP4 kernel on activation triples (fp6/fp6/fp4
 # pieces, double-rate MFMA) where it takes the shape, else the bf16-operand
-# kernels; "tri" the same; "pair" exact e4m3 pairs (the 32x32x64 kernel where
-# it fits, else the 16x16x128 one); "bf16" the bf16-operand kernels
+# kernels; "tri" the same; "duo" the triples' first two pieces only (two
+# double-rate MFMAs instead of three); "pair" exact e4m3 pairs (the
+# 32x32x64 kernel where it fits, else the 16x16x128 one); "bf16" the
+# bf16-operand kernels
 MXFP4_PREFILL_DEFAULT = "auto"
+_TRI_MODES = ("auto", "tri", "duo")
 
 
 def _mx_fits(H: int, I: int) -> bool:
@@ -561,7 +564,7 @@ def pair_gemm(fmt: int, H: int = 0, I: int = 0) -> bool:
     if fmt != FMT_MXFP4:
         return False
     mode = os.environ.get(MXFP4_PREFILL_ENV, MXFP4_PREFILL_DEFAULT)
-    return mode == "pair" or (mode in ("auto", "tri") and _mx_fits(H, I))
+    return mode == "pair" or (mode in _TRI_MODES and _mx_fits(H, I))
 
 
 def mx_pair_kernel(fmt: int, H: int, I: int) -> bool:
@@ -574,10 +577,21 @@ def mx_pair_kernel(fmt: int, H: int, I: int) -> bool:
 
 def mx_tri(fmt: int, H: int, I: int) -> bool:
     """Whether the MXFP4 32x32x64 kernel takes activation triples (fp6, fp6,
-    fp4 pieces on the double-rate MFMA; XTU_MXFP4_PREFILL "auto" or "tri")
-    rather than exact e4m3 pairs ("pair")."""
+    fp4 pieces on the double-rate MFMA; XTU_MXFP4_PREFILL "auto", "tri" or
+    "duo") rather than exact e4m3 pairs ("pair")."""
     mode = os.environ.get(MXFP4_PREFILL_ENV, MXFP4_PREFILL_DEFAULT)
-    return mode in ("auto", "tri") and mx_pair_kernel(fmt, H, I)
+    return mode in _TRI_MODES and mx_pair_kernel(fmt, H, I)
+
+
+def mx_act_mode(fmt: int, H: int, I: int) -> str:
+    """The activation format of the MXFP4 32x32x64 kernel for this layer:
+    "tri" (three pieces), "duo" (two) or "pair" (exact e4m3 pairs); its
+    GEMM entry points are xtu_mx_<mode>_gate_up / _down and its quantiser
+    xtu_tri_quant_il (tri, duo) or xtu_pair_quant_il (pair)."""
+    if not mx_tri(fmt, H, I):
+        return "pair"
+    mode = os.environ.get(MXFP4_PREFILL_ENV, MXFP4_PREFILL_DEFAULT)
+    return "duo" if mode == "duo" else "tri"
 
 
 def gemm_tile_m(fmt: int, int8: bool = False, H: int = 0, I: int = 0, W=None,
@@ -880,16 +894,17 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
     if mx_pair_kernel(fmt, H, I):
         # activation triples (double-rate fp6/fp4 MFMA) or exact pairs,
         # interleaved, on the MXFP4 32x32x64 kernel
-        kind = "tri" if mx_tri(fmt, H, I) else "pair"
+        kind = mx_act_mode(fmt, H, I)
+        qk = "pair" if kind == "pair" else "tri"
         s13p, s2p = W.mx_pair_scales(st)
         xq = _mxpair_bufs("xm", T, H, dev, st)
         aq = _mxpair_bufs("am", A, I, dev, st)
-        _lib.call(f"xtu_{kind}_quant_il", _p(x), T, H, *[_p(t) for t in xq], st)
+        _lib.call(f"xtu_{qk}_quant_il", _p(x), T, H, *[_p(t) for t in xq], st)
         _lib.call(f"xtu_mx_{kind}_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
                   _p(W.w13), _p(s13p), 0, 0, _p(slot_map), _p(seg.seg_start),
                   _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi,
                   seg.max_tiles, _p(act), lim, al, be, st)
-        _lib.call(f"xtu_{kind}_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
+        _lib.call(f"xtu_{qk}_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
         _lib.call(f"xtu_mx_{kind}_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(s2p), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
                   _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
