@@ -185,10 +185,9 @@ def bench_one(args):
 
     from xtu_moe_amd import _lib
     from xtu_moe_amd import formats as F
-    from xtu_moe_amd.layer import (_fp8pair_bufs, _mxpair_bufs, _p, _stream, gemm_tile_m,
-                                   int8_align_on, moe_forward, mx_pair_kernel, mx_tri, pair_gemm, route,
-                                   fp8_pair32_use,
-                                   segmentation)
+    from xtu_moe_amd.layer import (_fp8pair_bufs, _mxpair_bufs, _p, _stream, fp8_pair32_use,
+                                   gemm_tile_m, int8_align_on, moe_forward, mx_act_mode,
+                                   mx_pair_kernel, mx_tri, pair_gemm, route, segmentation)
     from xtu_moe_amd.synthetic import synth_layer
 
     cfg = WORKLOADS[args.workload]
@@ -392,10 +391,11 @@ def bench_one(args):
                 f8x = _mxpair_bufs("xm", T, H, dev)
                 _lib.call("xtu_pair_quant_il", _p(x_st), T, H, *[_p(t) for t in f8x], st)
             elif not decode and not i8 and mx_pair_kernel(fmt, H, I):
-                mxk = "tri" if mx_tri(fmt, H, I) else "pair"
+                mxk = mx_act_mode(fmt, H, I)
                 mxx = _mxpair_bufs("xm", T, H, dev)
                 s13p, _ = W.mx_pair_scales()
-                _lib.call(f"xtu_{mxk}_quant_il", _p(x_st), T, H, *[_p(t) for t in mxx], st)
+                _lib.call(f"xtu_{'pair' if mxk == 'pair' else 'tri'}_quant_il", _p(x_st), T, H,
+                          *[_p(t) for t in mxx], st)
             elif not decode and not i8 and pair_gemm(fmt, H, I):
                 fp8x = _fp8pair_bufs("x8", T, H, dev)
                 _lib.call("xtu_fp8pair_quant", _p(x_st), T, H, *[_p(t) for t in fp8x], st)
@@ -530,13 +530,15 @@ def bench_one(args):
                     frac=r["gate_up_GBs"] / HBM_PEAK_GBS, traffic=None, kernel="moe_gemm_kernel",
                     layer_frac=r["layer_GBs"] / HBM_PEAK_GBS)
     elif mx_tri(fmt, H, I) and not cfg["int8"] and not decode_head:
-        # fp6 / fp4 A (activation triples) x e2m1 B on the double-rate
-        # 32x32x64 MFMA: the fp6/fp4 peak; every algorithmic product is three
-        # MFMA products (the activation's three pieces)
+        # fp6 / fp4 A (activation triples, or their first two pieces) x e2m1
+        # B on the double-rate 32x32x64 MFMA: the fp6/fp4 peak; every
+        # algorithmic product is three (two) MFMA products
         ach = r["gate_up_TFLOPs"]
+        npc = 2.0 if mx_act_mode(fmt, H, I) == "duo" else 3.0
         roof = dict(bound="mfma", achieved=ach, peak=PEAK_TFLOPS["fp4"], unit="TFLOP/s",
                     frac=ach / PEAK_TFLOPS["fp4"], traffic=None, kernel="mx_pair_gemm_kernel",
-                    mfma_issue_frac=3.0 * ach / PEAK_TFLOPS["fp4"],
+                    activation_pieces=int(npc),
+                    mfma_issue_frac=npc * ach / PEAK_TFLOPS["fp4"],
                     frac_of_fp8_peak=ach / PEAK_TFLOPS["fp8"],
                     frac_of_bf16_peak=ach / PEAK_TFLOPS["bf16"])
         prefill_traffic(roof, "mx_pair_gemm_kernel<true")
@@ -584,6 +586,8 @@ def bench_one(args):
         "vs_baseline": None,
         "dtype": {"mxfp4": ("bf16-mfma/e2m1+e8m0"
                             if decode_head or not pair_gemm(fmt, H, I)
+                            else "fp6xfp4-mfma/e2m3,e2m3-duo x e2m1+e8m0"
+                            if mx_act_mode(fmt, H, I) == "duo"
                             else "fp6xfp4-mfma/e2m3,e2m3,e2m1-triple x e2m1+e8m0"
                             if mx_tri(fmt, H, I)
                             else "fp8xfp4-mfma/e4m3-pair x e2m1+e8m0"),
@@ -617,7 +621,7 @@ def pmc_child(args, cfg, T):
     from xtu_moe_amd import _lib
     from xtu_moe_amd import formats as F
     from xtu_moe_amd.layer import (_mxpair_bufs, _p, _stream, fp8_pair32_use, gemm_tile_m,
-                                   mx_tri, route, segmentation)
+                                   mx_act_mode, mx_tri, route, segmentation)
     from xtu_moe_amd.synthetic import synth_layer
 
     fmt = F.fmt_of(cfg["fmt"])
@@ -639,7 +643,7 @@ def pmc_child(args, cfg, T):
     st = _stream()
     if prefill:
         if mx_tri(fmt, H, I):
-            kind, s13 = "mx_tri", W.mx_pair_scales(st)[0]
+            kind, s13 = "mx_" + mx_act_mode(fmt, H, I), W.mx_pair_scales(st)[0]
             qname = "xtu_tri_quant_il"
         elif fp8_pair32_use(W):
             kind, s13, qname = "f8_pair", W.s13, "xtu_pair_quant_il"

@@ -539,10 +539,12 @@ def fp8_pair32_use(W, scales_ok=None) -> bool:
 
 # "auto": the 32x32x64 MXFP4 kernel on activation triples (fp6/fp6/fp4
 # pieces, double-rate MFMA) where it takes the shape, else the bf16-operand
-# kernels; "tri" the same; "duo" the triples' first two pieces only (two
-# double-rate MFMAs instead of three); "pair" exact e4m3 pairs (the
-# 32x32x64 kernel where it fits, else the 16x16x128 one); "bf16" the
-# bf16-operand kernels
+# kernels; "tri" the same; "pair" exact e4m3 pairs (the 32x32x64 kernel
+# where it fits, else the 16x16x128 one); "bf16" the bf16-operand kernels;
+# "duo" the triples' first two pieces only (two double-rate MFMAs instead
+# of three; opt-in: measured at DeepSeek-V3 T = 8192 it is 16% faster per
+# layer but leaves max-abs 2.6e-2 against the dequantised-fp32 layer, past
+# the 2e-2 bar, so it is never chosen by default)
 MXFP4_PREFILL_DEFAULT = "auto"
 _TRI_MODES = ("auto", "tri", "duo")
 
