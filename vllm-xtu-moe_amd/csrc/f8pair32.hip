@@ -363,31 +363,64 @@ __global__ __launch_bounds__(kQThreads, 1) void f8_pair_gemm_kernel(F8PairArgs a
   else run(std::integral_constant<int, 0>{});
 
   // ---- epilogue: the last block's scale, then the 32x32 result layout
-  // (column l % 32, rows 8 (i / 4) + 4 (l / 32) + i % 4)
+  // (column l % 32, rows 8 (i / 4) + 4 (l / 32) + i % 4).  Each wave's
+  // results go through its own LDS region (the stages are free once every
+  // wave is past the K loop) and are read back as 16-byte row pieces: wide
+  // stores of whole row segments instead of one store per lane and value.
   const float sl0 = ratio[2 * nkb], sl1 = ratio[2 * nkb + 1];
+  __syncthreads();
+  if constexpr (GU) {
+    constexpr int kAP = 72;   // staged row pitch in bf16 (64 + 8)
+    uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + w * (32 * kAP);
+    uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < 2; ++mb) {
+      const int rb = 32 * (2 * mb + wm);
+      if (rb >= rows) continue;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = 32 * (2 * mb + wm) + 8 * (i / 4) + 4 * h + (i % 4);
-      if (r >= rows) continue;
-      const long prow = row0 + r;
-      if constexpr (GU) {
-        uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
+      for (int i = 0; i < 16; ++i) {
+        const int r = 8 * (i / 4) + 4 * h + (i % 4);
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          const long col = (long)nb * 128 + 64 * wn + 32 * cb + r32;
-          act[prow * a.I + col] = f32_to_bf16(silu_gate(acc[mb][cb][i] * sl0,
-                                                        acc[mb][cb + 2][i] * sl1, a.limit,
-                                                        a.alpha, a.beta));
-        }
-      } else {
-        float* y = reinterpret_cast<float*>(a.out);
-        const float sl = wn ? sl1 : sl0;
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-          y[prow * a.H + (long)nb * 256 + 128 * wn + 32 * cb + r32] = acc[mb][cb][i] * sl;
+        for (int cb = 0; cb < 2; ++cb)
+          stage[r * kAP + 32 * cb + r32] = f32_to_bf16(silu_gate(
+              acc[mb][cb][i] * sl0, acc[mb][cb + 2][i] * sl1, a.limit, a.alpha, a.beta));
       }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {   // 32 rows x 8 pieces of 8 bf16
+        const int q = 64 * j + lane, rr = q / 8, c8 = q % 8;
+        if (rb + rr < rows)
+          *reinterpret_cast<u32x4_t*>(act + (long)(row0 + rb + rr) * a.I + (long)nb * 128 +
+                                      64 * wn + 8 * c8) =
+              *reinterpret_cast<const u32x4_t*>(stage + rr * kAP + 8 * c8);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  } else {
+    constexpr int kYP = 136;   // staged row pitch in floats (128 + 8)
+    float* stage = reinterpret_cast<float*>(lds) + w * (32 * kYP);
+    float* y = reinterpret_cast<float*>(a.out);
+    const float sl = wn ? sl1 : sl0;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const int rb = 32 * (2 * mb + wm);
+      if (rb >= rows) continue;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = 8 * (i / 4) + 4 * h + (i % 4);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) stage[r * kYP + 32 * cb + r32] = acc[mb][cb][i] * sl;
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {   // 32 rows x 32 pieces of 4 floats
+        const int q = 64 * j + lane, rr = q / 32, c4 = q % 32;
+        if (rb + rr < rows)
+          *reinterpret_cast<f32x4_t*>(y + (long)(row0 + rb + rr) * a.H + (long)nb * 256 +
+                                      128 * wn + 4 * c4) =
+              *reinterpret_cast<const f32x4_t*>(stage + rr * kYP + 4 * c4);
+      }
+      __builtin_amdgcn_wave_barrier();
     }
   }
 }

@@ -289,36 +289,60 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
     float gsv = 1.0f;
     if constexpr (FMT == kNVFP4) gsv = a.gs ? a.gs[ws] : 1.0f;
     const int r16 = lane % 16, q = lane / 16;
+    // The 16x16 result (column lane % 16, rows 4 (lane / 16) + i) of each
+    // row tile goes through this wave's own LDS region (the A buffers are
+    // free once every wave is past the K loop) and is read back as 16-byte
+    // row pieces: wide stores of the wave's contiguous columns (its panels
+    // are adjacent) instead of one store per lane and value.
+    __syncthreads();
     if constexpr (GU) {
+      constexpr int NC = PW / 2 * 16;   // act columns of the wave
+      constexpr int kAP = NC + 8;       // staged row pitch (bf16)
+      uint16_t* stage = As + w * (16 * kAP);
       uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
+      const long col0 = (long)pan[0] * 16;
 #pragma unroll
-      for (int m = 0; m < NR; ++m)
+      for (int m = 0; m < NR; ++m) {
+        if (m * 16 >= rows) break;
 #pragma unroll
-        for (int p = 0; p < PW / 2; ++p) {
-          const long col = (long)pan[p] * 16 + r16;
+        for (int p = 0; p < PW / 2; ++p)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int r = m * 16 + 4 * q + i;
-            if (r < rows) {
-              const float g = acc[m][p][i] * gsv, u = acc[m][p + PW / 2][i] * gsv;
-              act[(long)(row0 + r) * a.I + col] =
-                  f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
-            }
+            const float g = acc[m][p][i] * gsv, u = acc[m][p + PW / 2][i] * gsv;
+            stage[(4 * q + i) * kAP + 16 * p + r16] =
+                f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
           }
+        __builtin_amdgcn_wave_barrier();
+        for (int j = lane; j < 16 * (NC / 8); j += 64) {   // 16 rows x NC/8 pieces
+          const int rr = j / (NC / 8), c8 = j % (NC / 8);
+          if (m * 16 + rr < rows)
+            *reinterpret_cast<u32x4_t*>(act + (long)(row0 + m * 16 + rr) * a.I + col0 + 8 * c8) =
+                *reinterpret_cast<const u32x4_t*>(stage + rr * kAP + 8 * c8);
         }
+        __builtin_amdgcn_wave_barrier();
+      }
     } else {
+      constexpr int NC = PW * 16;   // y columns of the wave
+      constexpr int kYP = NC + 4;   // staged row pitch (floats)
+      float* stage = reinterpret_cast<float*>(As) + w * (16 * kYP);
       float* y = reinterpret_cast<float*>(a.out);
+      const long col0 = (long)pan[0] * 16;
 #pragma unroll
-      for (int m = 0; m < NR; ++m)
+      for (int m = 0; m < NR; ++m) {
+        if (m * 16 >= rows) break;
 #pragma unroll
-        for (int p = 0; p < PW; ++p) {
-          const long col = (long)pan[p] * 16 + r16;
+        for (int p = 0; p < PW; ++p)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = m * 16 + 4 * q + i;
-            if (r < rows) y[(long)(row0 + r) * a.H + col] = acc[m][p][i] * gsv;
-          }
+          for (int i = 0; i < 4; ++i) stage[(4 * q + i) * kYP + 16 * p + r16] = acc[m][p][i] * gsv;
+        __builtin_amdgcn_wave_barrier();
+        for (int j = lane; j < 16 * (NC / 4); j += 64) {   // 16 rows x NC/4 pieces
+          const int rr = j / (NC / 4), c4 = j % (NC / 4);
+          if (m * 16 + rr < rows)
+            *reinterpret_cast<f32x4_t*>(y + (long)(row0 + m * 16 + rr) * a.H + col0 + 4 * c4) =
+                *reinterpret_cast<const f32x4_t*>(stage + rr * kYP + 4 * c4);
         }
+        __builtin_amdgcn_wave_barrier();
+      }
     }
   };
   if (rows > 64) run(std::integral_constant<int, kRT>{});

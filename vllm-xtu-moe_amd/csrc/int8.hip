@@ -306,6 +306,79 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8GemmArgs a) {
     }
     const int em0 = a.emin[(long)ws * N + gcol0];
     const int em1 = a.emin[(long)ws * N + gcol1];
+    if constexpr (GU) {
+      if (!a.acc_out) {
+        // act rows through LDS as for y below: the wave's 32 act columns of
+        // each row tile (bf16), read back as 16-byte pieces (8 columns), two
+        // wide stores per lane and row tile instead of sixteen 2-byte ones.
+        // A column pair with a marked row gets a value (from zero int8
+        // weights); the fp32 fallback that follows overwrites it.
+        constexpr int kAP = 40;   // LDS row pitch in bf16 (32 + 8)
+        uint16_t* stage = reinterpret_cast<uint16_t*>(Bs) + w * (32 * kAP);
+        __syncthreads();   // every wave is done with the K loop's LDS tiles
+        uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
+#pragma unroll
+        for (int m = 0; m < NT; ++m) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = (i / 4) * 8 + (lane / 32) * 4 + (i % 4);
+            const int cr = m * 32 + r < rows ? a.crow[a.sorted_tok[row0 + m * 32 + r]] : 0;
+            const float c0 = (float)acc[m][0][i] * ldexpf(1.0f, em0 - 128 + cr);
+            const float c1 = (float)acc[m][1][i] * ldexpf(1.0f, em1 - 128 + cr);
+            stage[r * kAP + ncol] = f32_to_bf16(silu_gate(c0, c1, a.limit, a.alpha, a.beta));
+          }
+          __builtin_amdgcn_wave_barrier();
+          const int r = lane / 4, c8 = lane % 4;   // 16 rows x 4 pieces per pass
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int rr = r + 16 * j;
+            if (m * 32 + rr < rows) {
+              const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&stage[rr * kAP + 8 * c8]);
+              *reinterpret_cast<u32x4_t*>(
+                  &act[(long)(row0 + m * 32 + rr) * a.I + (long)nb * 128 + 32 * w + 8 * c8]) = v;
+            }
+          }
+          __builtin_amdgcn_wave_barrier();
+        }
+        return;
+      }
+    }
+    if constexpr (!GU) {
+      if (!a.acc_out) {
+        // y rows through LDS: the wave's 32 x 64 block of each row tile is
+        // written to its own LDS region (one fp32 per lane and value, as the
+        // MFMA result lies), then read back as 16-byte row pieces, so each
+        // lane issues 8 wide stores per row tile instead of 32 scalar ones.
+        // A marked column's value (its int8 weights are zero) is written
+        // too; the fp32 fallback that follows overwrites it.
+        constexpr int kYP = 68;   // LDS row pitch in floats (64 + 4 against bank conflicts)
+        float* stage = reinterpret_cast<float*>(Bs) + w * (32 * kYP);
+        __syncthreads();   // every wave is done with the K loop's LDS tiles
+        float* y = reinterpret_cast<float*>(a.out);
+#pragma unroll
+        for (int m = 0; m < NT; ++m) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = (i / 4) * 8 + (lane / 32) * 4 + (i % 4);
+            const int cr = m * 32 + r < rows ? a.crow[row0 + m * 32 + r] : 0;
+            stage[r * kYP + ncol] = (float)acc[m][0][i] * ldexpf(1.0f, em0 - 128 + cr);
+            stage[r * kYP + 32 + ncol] = (float)acc[m][1][i] * ldexpf(1.0f, em1 - 128 + cr);
+          }
+          __builtin_amdgcn_wave_barrier();
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int q = j * 64 + lane, r = q / 16, c4 = q % 16;
+            if (m * 32 + r < rows) {
+              const f32x4_t v = *reinterpret_cast<const f32x4_t*>(&stage[r * kYP + 4 * c4]);
+              *reinterpret_cast<f32x4_t*>(
+                  &y[(long)(row0 + m * 32 + r) * a.H + (long)nb * 256 + 64 * w + 4 * c4]) = v;
+            }
+          }
+          __builtin_amdgcn_wave_barrier();
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int m = 0; m < NT; ++m)
 #pragma unroll
