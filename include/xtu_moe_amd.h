@@ -10,7 +10,9 @@
  *
  * Weight formats (fmt): 0 BF16, 1 FP8 e4m3 + 128x128 fp32 block scales,
  * 2 MXFP4 (e2m1 + e8m0 per 32 k), 3 NVFP4 (e2m1 + e4m3 per 16 k + fp32
- * per-expert global scale).  Weights are in the P16 panel layout: per
+ * second-level scales: gs13 [E][2] = gate, up -- the checkpoint's
+ * w13_weight_scale_2 [E][2], hybrid_model.py:1546-1561 -- and gs2 [E],
+ * indexed by weight slot).  Weights are in the P16 panel layout: per
  * expert, a [N][K] matrix is stored as
  * [N/16][K/SB][4][16][16 B] with SB = 128 (fp4), 64 (fp8), 32 (bf16) k per
  * super-block; fp4 scales in groups of UG super-blocks per 16-row panel,
@@ -537,7 +539,7 @@ hipError_t xtu_pin_split(const int32_t* ids, const float* wts, int n, const int3
  * bytes per expert); s13 / s2: packed scale groups (fp4), fp32 block
  * scales (fp8), or fp32 [N][K/group_k] row scales (fmt 4, INT4/WNA16:
  * value = code - 8, the engine's MOE_WNA16, moe_v2_packed4_base.inc:1-20,
- * :1594); gs13 / gs2: NVFP4 global scales.  isa: -1 best available, 0
+ * :1594); gs13 [E][2] / gs2 [E]: NVFP4 second-level scales.  isa: -1 best available, 0
  * portable, 2 AVX-512.  max_tokens > 0 allocates the pinned staging of
  * xtu_cpu_decode (max_tokens rows of max_topk pairs); 0 = host-only engine.
  * The weights are read in place and must outlive the engine. */

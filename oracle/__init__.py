@@ -151,6 +151,19 @@ def segment(ids: np.ndarray, wts: np.ndarray, E: int, n_shared: int = 0,
 
 
 # ---------------------------------------------------------------- expert math
+def gate_up_scales2(gs13):
+    """NVFP4 second-level scales of w13 as [E, 2] fp32 (gate, up): a
+    per-expert [E] vector (one scale for both halves) is repeated."""
+    if gs13 is None:
+        return None
+    g = np.asarray(gs13, np.float32)
+    if g.ndim == 1:
+        g = np.repeat(g[:, None], 2, axis=1)
+    if g.ndim != 2 or g.shape[1] != 2:
+        raise ValueError(f"gs13 must be [E] or [E, 2], got {g.shape}")
+    return np.ascontiguousarray(g)
+
+
 def moe_layer(fmt: int, x_bf16: np.ndarray, ids, wts, E: int, n_shared: int, H: int, I: int,
               w13, s13, w2, s2, gs13=None, gs2=None, limit=0.0, alpha=1.0, beta=0.0):
     """out[T][H] fp32 of the dequantized-fp32 layer (CPU-engine semantics).
@@ -161,6 +174,7 @@ def moe_layer(fmt: int, x_bf16: np.ndarray, ids, wts, E: int, n_shared: int, H: 
     wts = np.ascontiguousarray(wts, np.float32)
     T, K = ids.shape
     out = np.zeros((T, H), np.float32)
+    gs13 = gate_up_scales2(gs13)
     arrs = [np.ascontiguousarray(a) if a is not None else None for a in (w13, s13, gs13, w2, s2, gs2)]
     gk = H // s13.shape[-1] if fmt == 4 else 0
     rc = lib().xo_moe_layer_g(fmt, gk, T, K, E, n_shared, H, I, _p(x), _p(ids), _p(wts),
@@ -263,7 +277,9 @@ class RefEngine:
     fmt: FMT_BF16 / FMT_FP8 / FMT_MXFP4 / FMT_NVFP4 / FMT_INT4 (the engine's
     WNA16 traits; fp32 scales [E, N, K/group]).  For NVFP4 the e4m3 scale
     bytes are handed to the engine as fp32 (exact) with the per-expert global
-    scale passed separately, as the engine's NVFP4 traits expect.
+    scale passed separately, as the engine's NVFP4 traits expect; gate and up
+    scales given separately (gs13 [E, 2]) are folded into the fp32 group
+    scales instead, as the reference hook does.
     """
 
     def __init__(self, fmt, E, K, H, I, w13, s13, w2, s2, gs13=None, gs2=None,
@@ -277,6 +293,17 @@ class RefEngine:
             t = e4m3_table()
             s13 = t[np.asarray(s13)]
             s2 = t[np.asarray(s2)]
+            if gs13 is not None and np.asarray(gs13).ndim == 2:
+                # gate and up scales that may differ: folded into the fp32
+                # group scales per half, as the reference hook hands them to
+                # its NVFP4 engine (hybrid_model.py:1546-1563)
+                g13 = np.asarray(gs13, np.float32)
+                s13 = s13.copy()
+                s13[:, :I] *= g13[:, 0, None, None]
+                s13[:, I:] *= g13[:, 1, None, None]
+                s2 = s2 * np.asarray(gs2, np.float32)[:, None, None]
+                gs13 = np.ones(E, np.float32)
+                gs2 = np.ones(E, np.float32)
         self._keep = [np.ascontiguousarray(a) if a is not None else None
                       for a in (w13, w2, s13, s2, gs13, gs2)]
         k = self._keep

@@ -309,16 +309,18 @@ int xo_segment(const int32_t* ids, const float* wts, int T, int K, int E, int n_
 /*   1 FP8  : w13 [E][2I][H] e4m3, s13 [E][2I/128][H/128] f32 (w2 alike)     */
 /*   2 MXFP4: w13 [E][2I][H/2] e2m1 (low nibble even k), s13 [E][2I][H/32]   */
 /*            e8m0 (moe_v2_packed4_w4a8.inc:1966-2003)                        */
-/*   3 NVFP4: as MXFP4 with s13 [E][2I][H/16] e4m3 bytes and a per-expert    */
-/*            fp32 global scale gs13[E] (gpu_prefill.py:111-127, 290-297)    */
+/*   3 NVFP4: as MXFP4 with s13 [E][2I][H/16] e4m3 bytes and fp32 second-   */
+/*            level scales gs13 [E][2] (gate rows, up rows) and gs2 [E]      */
+/*            (hybrid_model.py:1546-1561 folds them into the group scales;   */
+/*            gpu_prefill.py:111-127, 290-297)                               */
 /*   4 INT4 (WNA16): nibbles as MXFP4, value = nibble - 8, times an fp32     */
 /*            scale s13 [E][2I][H/gk] (moe_v2_packed4_base.inc:4-16, :1594)  */
 /* ------------------------------------------------------------------------ */
 enum { XO_BF16 = 0, XO_FP8 = 1, XO_MXFP4 = 2, XO_NVFP4 = 3, XO_INT4 = 4 };
 
 /* dequantize row n (of N) of one expert's [N][K] weight into out[K]; gk is
- * INT4's k per scale */
-static void deq_row(int fmt, int gk, const void* w, const void* s, const float* gs, int e, int N,
+ * INT4's k per scale, g the row's NVFP4 second-level scale */
+static void deq_row(int fmt, int gk, const void* w, const void* s, float g, int e, int N,
                     int K, int n, float* out) {
   if (fmt == XO_INT4) {
     const uint8_t* r = (const uint8_t*)w + ((size_t)e * N + n) * (K / 2);
@@ -340,7 +342,6 @@ static void deq_row(int fmt, int gk, const void* w, const void* s, const float* 
     const uint8_t* r = (const uint8_t*)w + ((size_t)e * N + n) * (K / 2);
     const int gk = (fmt == XO_MXFP4) ? 32 : 16;
     const uint8_t* sc = (const uint8_t*)s + ((size_t)e * N + n) * (K / gk);
-    const float g = (fmt == XO_NVFP4 && gs) ? gs[e] : 1.0f;
     for (int k = 0; k < K; ++k) {
       const int nib = (k & 1) ? (r[k / 2] >> 4) : (r[k / 2] & 15);
       const float scale = (fmt == XO_MXFP4) ? xo_e8m0(sc[k / gk]) : xo_e4m3(sc[k / gk]) * g;
@@ -365,17 +366,21 @@ static void expert_row(int fmt, int gk, const void* w13, const void* s13, const 
                        const void* w2, const void* s2, const float* gs2, int e, int H, int I,
                        const float* xf, float limit, float alpha, float beta, float* wrow,
                        float* actf, float* y) {
+  const int nv = fmt == XO_NVFP4;
+  const float g_gate = nv && gs13 ? gs13[2 * (size_t)e] : 1.0f;
+  const float g_up = nv && gs13 ? gs13[2 * (size_t)e + 1] : 1.0f;
+  const float g_down = nv && gs2 ? gs2[e] : 1.0f;
   for (int i = 0; i < I; ++i) {
     double g = 0.0, u = 0.0;
-    deq_row(fmt, gk, w13, s13, gs13, e, 2 * I, H, i, wrow);
+    deq_row(fmt, gk, w13, s13, g_gate, e, 2 * I, H, i, wrow);
     for (int k = 0; k < H; ++k) g += (double)xf[k] * wrow[k];
-    deq_row(fmt, gk, w13, s13, gs13, e, 2 * I, H, I + i, wrow);
+    deq_row(fmt, gk, w13, s13, g_up, e, 2 * I, H, I + i, wrow);
     for (int k = 0; k < H; ++k) u += (double)xf[k] * wrow[k];
     actf[i] = bf16_round(xo_silu_gate((float)g, (float)u, limit, alpha, beta));
   }
   for (int h = 0; h < H; ++h) {
     double d = 0.0;
-    deq_row(fmt, gk, w2, s2, gs2, e, H, I, h, wrow);
+    deq_row(fmt, gk, w2, s2, g_down, e, H, I, h, wrow);
     for (int i = 0; i < I; ++i) d += (double)actf[i] * wrow[i];
     y[h] = (float)d;
   }
@@ -536,7 +541,7 @@ int xo_i8_row_spread(const uint8_t* srow, int K) {
 static float i8_fallback_dot(const float* a, const uint8_t* w, const uint8_t* s, int N, int K,
                              int n, float* wrow) {
   double d = 0.0;
-  deq_row(XO_MXFP4, 0, w, s, NULL, 0, N, K, n, wrow);
+  deq_row(XO_MXFP4, 0, w, s, 1.0f, 0, N, K, n, wrow);
   for (int k = 0; k < K; ++k) d += (double)a[k] * wrow[k];
   return (float)d;
 }

@@ -36,12 +36,17 @@ def check_close(out, ref, *, bf16_out: bool, what: str = ""):
     return r
 
 
-def make_dense_layer(fmt: int, E_total: int, H: int, I: int, seed: int = 0, std: float = 0.02):
-    """Dense checkpoint tensors (CPU torch) of E_total experts drawn N(0, std) and quantised."""
+def make_dense_layer(fmt: int, E_total: int, H: int, I: int, seed: int = 0, std: float = 0.02,
+                     split_gate_up: bool = False):
+    """Dense checkpoint tensors (CPU torch) of E_total experts drawn N(0, std)
+    and quantised; split_gate_up: NVFP4 gate and up halves quantised apart
+    (gs13 [E, 2], the two scales differ), the up half drawn at 3 std."""
     g = torch.Generator().manual_seed(seed)
     w13 = torch.randn((E_total, 2 * I, H), generator=g) * std
     w2 = torch.randn((E_total, H, I), generator=g) * std
-    w13q, s13, gs13 = F.quantize(fmt, w13)
+    if split_gate_up:
+        w13[:, I:] *= 3.0
+    w13q, s13, gs13 = (F.quantize_w13 if split_gate_up else F.quantize)(fmt, w13)
     w2q, s2, gs2 = F.quantize(fmt, w2)
     return dict(w13=w13q, s13=s13, gs13=gs13, w2=w2q, s2=s2, gs2=gs2)
 

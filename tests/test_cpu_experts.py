@@ -178,13 +178,39 @@ def test_wna16_engine_forward_many():
 
 
 def test_nvfp4_second_level_scales():
+    """w13's scale_2 comes out as [E, 2] (gate, up) whatever the checkpoint
+    gives, w1 / w3 scales that differ included; all zero is refused."""
     from xtu_moe_amd.mixed_experts import nvfp4_global_scales
     g2 = torch.tensor([0.5, 2.0])
     a, b = nvfp4_global_scales(torch.tensor([[0.5, 0.5], [1.5, 1.5]]), g2)
-    assert torch.equal(a, torch.tensor([0.5, 1.5])) and torch.equal(b, g2)
+    assert torch.equal(a, torch.tensor([[0.5, 0.5], [1.5, 1.5]])) and torch.equal(b, g2)
     a, _ = nvfp4_global_scales(torch.tensor([0.25, 4.0]), g2)
-    assert torch.equal(a, torch.tensor([0.25, 4.0]))
-    with pytest.raises(RuntimeError):          # gate and up differ
-        nvfp4_global_scales(torch.tensor([[0.5, 0.5], [1.5, 1.0]]), g2)
+    assert torch.equal(a, torch.tensor([[0.25, 0.25], [4.0, 4.0]]))
+    a, _ = nvfp4_global_scales(torch.tensor([[0.5, 0.5], [1.5, 1.0]]), g2)
+    assert torch.equal(a, torch.tensor([[0.5, 0.5], [1.5, 1.0]]))
+    with pytest.raises(ValueError):            # neither [E] nor [E, 2]
+        nvfp4_global_scales(torch.ones(2, 3), g2)
     with pytest.raises(RuntimeError):          # not loaded
         nvfp4_global_scales(torch.zeros(2, 2), g2)
+
+
+def test_host_engine_nvfp4_unequal_gate_up_scales():
+    """The host engine takes the gate panels' scale_2 from column 0 and the
+    up panels' from column 1 (the reference folds each into its half's
+    group scales, hybrid_model.py:1546-1563), against the oracle and the
+    reference engine over the folded scales."""
+    d = make_dense_layer(F.FMT_NVFP4, E, H, I, seed=31, split_gate_up=True)
+    assert d["gs13"].shape == (E, 2) and bool((d["gs13"][:, 1] > 2 * d["gs13"][:, 0]).all())
+    W = ExpertWeights.from_dense(F.FMT_NVFP4, d["w13"], d["s13"], d["w2"], d["s2"], d["gs13"],
+                                 d["gs2"], device="cpu")
+    eng = CpuExperts.from_weights(W)
+    x, ids, wts = _batch(5, 2, seed=32)
+    out = eng.forward(x, torch.from_numpy(ids), torch.from_numpy(wts))
+    dn = dense_to_numpy(F.FMT_NVFP4, d)
+    ref = _oracle(F.FMT_NVFP4, dn, x, ids, wts)
+    check_close(out.numpy(), ref, bf16_out=False, what="host engine, unequal scale_2")
+    if oracle.ref_available():
+        r = oracle.RefEngine(F.FMT_NVFP4, E, 2, H, I, dn["w13"], dn["s13"], dn["w2"], dn["s2"],
+                             dn["gs13"], dn["gs2"])
+        got = r.forward(bf16_tensor_to_bits(x), ids, wts)
+        check_close(got, ref, bf16_out=False, what="reference engine, folded scale_2")

@@ -5,8 +5,10 @@
   host engine behind the cpu_decode bridge for batches inside the pre-sized
   staging, the synchronous host forward beyond it; both against the oracle.
   The bridged apply captured in a HIP graph replays bit-identically.
-* NVFP4: weight_scale_2 given as [E, 2] (gate, up; equal, as real
-  checkpoints have them) gives the same layer as [E] and matches the oracle.
+* NVFP4: weight_scale_2 given as [E, 2] (gate, up) equal gives the same
+  layer as [E]; gate and up scales that differ (w1 / w3 quantised apart) are
+  applied per half, on the resident decode and prefill paths and on a
+  host-resident layer's host engine, against the oracle.
 """
 import numpy as np
 import pytest
@@ -83,22 +85,22 @@ def test_int4_hook_replays_in_a_graph(monkeypatch):
     del g
 
 
+def _nvfp4_layer(d, K, g13):
+    P = lambda t: torch.nn.Parameter(t, requires_grad=False)
+    return type("L", (), dict(w13_weight=P(d["w13"]), w2_weight=P(d["w2"]),
+                              w13_weight_scale=P(d["s13"]), w2_weight_scale=P(d["s2"]),
+                              w13_weight_scale_2=P(g13), w2_weight_scale_2=P(d["gs2"]),
+                              top_k=K, renormalize=True))()
+
+
 def test_nvfp4_second_level_scales_two_columns():
     E, H, I, T, K = 8, 512, 256, 20, 2
     d = make_dense_layer(F.FMT_NVFP4, E, H, I, seed=23)
-    P = lambda t: torch.nn.Parameter(t, requires_grad=False)
-
-    def layer(g13):
-        return type("L", (), dict(w13_weight=P(d["w13"]), w2_weight=P(d["w2"]),
-                                  w13_weight_scale=P(d["s13"]), w2_weight_scale=P(d["s2"]),
-                                  w13_weight_scale_2=P(g13), w2_weight_scale_2=P(d["gs2"]),
-                                  top_k=K, renormalize=True))()
-
     x, ids, wts = _inputs(T, K, E, H, seed=24)
     outs = []
     for g13 in (d["gs13"], torch.stack([d["gs13"], d["gs13"]], 1)):
         hook = XiaotuExpertsNvfp4()
-        hook.process_weights_after_loading(layer(g13))
+        hook.process_weights_after_loading(_nvfp4_layer(d, K, g13))
         outs.append(hook.apply(x.to(DEV), None, None, topk_ids=torch.from_numpy(ids).to(DEV),
                                topk_weights=torch.from_numpy(wts).to(DEV)))
     torch.cuda.synchronize()
@@ -106,6 +108,37 @@ def test_nvfp4_second_level_scales_two_columns():
     ref = oracle_layer(F.FMT_NVFP4, dense_to_numpy(F.FMT_NVFP4, d), bf16_tensor_to_bits(x), ids,
                        wts, E, 0, H, I)
     check_close(outs[1].float().cpu().numpy(), ref, bf16_out=True, what="nvfp4 [E,2] scale_2")
-    with pytest.raises(RuntimeError):
-        XiaotuExpertsNvfp4().process_weights_after_loading(
-            layer(torch.stack([d["gs13"], 2 * d["gs13"]], 1)))
+
+
+@pytest.mark.parametrize("resident", ["1", ""])
+@pytest.mark.parametrize("T", [3, 300])
+def test_nvfp4_unequal_gate_up_scales(monkeypatch, resident, T):
+    """w1 / w3 second-level scales that differ (about 3x here): each half
+    takes its own, on the decode (T = 3) and grouped-GEMM (T = 300) paths of
+    a resident layer, and through a host-resident layer (host engine at
+    T = 3, the tile ring at T = 300)."""
+    monkeypatch.setenv("XIAOTU_MOE_GPU_RESIDENT_LAYERS", resident or "99")
+    monkeypatch.setenv("VLLM_XIAOTU_GPU_PREFILL_MIN_TOKENS", "256")
+    monkeypatch.setenv("XTU_CD_PREALLOC_TOKENS", "16")
+    E, H, I, K = 8, 512, 256, 2
+    d = make_dense_layer(F.FMT_NVFP4, E, H, I, seed=25, split_gate_up=True)
+    g13 = d["gs13"]
+    assert g13.shape == (E, 2) and bool((g13[:, 1] > 2 * g13[:, 0]).all())
+    layer = _nvfp4_layer(d, K, g13)
+    layer.layer_name = "model.layers.1.mlp.experts"
+    hook = XiaotuExpertsNvfp4()
+    hook.process_weights_after_loading(layer)
+    assert (hook._host_layer is None) == bool(resident)
+    x, ids, wts = _inputs(T, K, E, H, seed=26)
+    out = hook.apply(x.to(DEV), None, None, topk_ids=torch.from_numpy(ids).to(DEV),
+                     topk_weights=torch.from_numpy(wts).to(DEV))
+    torch.cuda.synchronize()
+    if not resident:
+        assert hook._host_layer.last_path == ("ring" if T >= 256 else "host")
+    dn = dense_to_numpy(F.FMT_NVFP4, d)
+    ref = oracle_layer(F.FMT_NVFP4, dn, bf16_tensor_to_bits(x), ids, wts, E, 0, H, I)
+    check_close(out.float().cpu().numpy(), ref, bf16_out=True, what=f"nvfp4 unequal T={T}")
+    # one scale for both halves would be a wrong answer this test sees
+    dn1 = dict(dn, gs13=dn["gs13"][:, 0].copy())
+    wrong = oracle_layer(F.FMT_NVFP4, dn1, bf16_tensor_to_bits(x), ids, wts, E, 0, H, I)
+    assert float(np.abs(wrong - ref).max()) > 10 * float(np.abs(out.float().cpu().numpy() - ref).max())

@@ -116,7 +116,7 @@ struct PanelRef {
   const uint8_t* w;   // 16 rows, K/sb_k super-blocks of 1 KiB
   const uint8_t* s;   // fp4: the panel's scale groups; fp8: fp32 scales of its 128-row block;
                       // int4: fp32 scales of its first row ([16][K/gk])
-  float gs;           // NVFP4 global scale
+  float gs;           // NVFP4 second-level scale of the panel's rows
   int K;
   int gk;             // int4: k per scale
 };
@@ -473,7 +473,7 @@ struct Engine {
     P.w = d.w13[node] + (size_t)e * d.w13_estride + (up ? (size_t)ppn * 16 * rb13 : 0) +
           (size_t)lp * 16 * rb13;
     P.s = scale_of(d.s13, d.s13_estride, sg13, e, p, d.H);
-    P.gs = d.gs13 ? d.gs13[e] : 1.f;
+    P.gs = d.gs13 ? d.gs13[2 * (size_t)e + (up ? 1 : 0)] : 1.f;   // [E][2]: gate, up
     P.K = d.H;
     P.gk = d.group_k;
     return P;

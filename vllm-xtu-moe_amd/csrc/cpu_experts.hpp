@@ -37,8 +37,8 @@ struct LayerDesc {
   const uint8_t* s2 = nullptr;             // likewise for [H][I]
   int group_k = 0;                         // int4: k per scale (32, 64 or 128)
   size_t s13_estride = 0, s2_estride = 0;  // bytes per expert
-  const float* gs13 = nullptr;             // NVFP4 per-expert global scales
-  const float* gs2 = nullptr;
+  const float* gs13 = nullptr;             // NVFP4 second-level scales [E][2]: gate, up
+  const float* gs2 = nullptr;              // NVFP4 second-level scales [E]
 };
 
 // Empty string when the description is usable, else what is wrong.

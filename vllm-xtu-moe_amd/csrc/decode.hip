@@ -34,7 +34,7 @@ struct DecodeArgs {
   const uint16_t* x;         // gate/up: hidden rows [T][H]; down: act rows [A][I]
   const uint8_t* w;          // packed weights, expert-major
   const uint8_t* s;          // fp4 scales (packed) or fp8 block scales (fp32)
-  const float* gs;           // NVFP4 per-expert global scale (may be null)
+  const float* gs;           // NVFP4 second-level scales: gate/up [slot][2], down [slot] (may be null)
   const int32_t* sorted_tok;
   const int32_t* seg_start;
   const int32_t* active;     // work slots: active experts, or the 16-row tiles' experts
@@ -286,10 +286,11 @@ __device__ __forceinline__ void gate_up_epilogue(const DecodeArgs& a, f32x4_t (*
         g += red[k][l][i];
         u += red[a.ksplit + k][l][i];
       }
-      if constexpr (FMT == kNVFP4) {
-        const float gsv = a.gs ? a.gs[ws] : 1.0f;
-        g *= gsv;
-        u *= gsv;
+      if constexpr (FMT == kNVFP4) {   // second-level scales [slot][2]: gate, up
+        if (a.gs) {
+          g *= a.gs[2 * ws];
+          u *= a.gs[2 * ws + 1];
+        }
       }
       uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
       act[(long)(r0 + mm) * a.I + 16 * sub + n] =

@@ -286,8 +286,14 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
       }
     }
 
-    float gsv = 1.0f;
-    if constexpr (FMT == kNVFP4) gsv = a.gs ? a.gs[ws] : 1.0f;
+    // NVFP4 second-level scales: [slot][2] (gate, up) for gate/up, [slot] for down
+    float gsv = 1.0f, gsu = 1.0f;
+    if constexpr (FMT == kNVFP4) {
+      if (a.gs) {
+        gsv = GU ? a.gs[2 * ws] : a.gs[ws];
+        gsu = GU ? a.gs[2 * ws + 1] : gsv;
+      }
+    }
     const int r16 = lane % 16, q = lane / 16;
     // The 16x16 result (column lane % 16, rows 4 (lane / 16) + i) of each
     // row tile goes through this wave's own LDS region (the A buffers are
@@ -308,7 +314,7 @@ __global__ __launch_bounds__(kGemmThreads, WPS) void moe_gemm_kernel(GemmArgs a)
         for (int p = 0; p < PW / 2; ++p)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float g = acc[m][p][i] * gsv, u = acc[m][p + PW / 2][i] * gsv;
+            const float g = acc[m][p][i] * gsv, u = acc[m][p + PW / 2][i] * gsu;
             stage[(4 * q + i) * kAP + 16 * p + r16] =
                 f32_to_bf16(silu_gate(g, u, a.limit, a.alpha, a.beta));
           }

@@ -449,13 +449,13 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
   else run(std::integral_constant<int, 0>{});
 
   // ---- epilogue.  32x32 result lane layout: column l % 32, rows
-  // 8 (i / 4) + 4 (l / 32) + i % 4.  Each wave's results go through its own
-  // LDS region (the stages are free once every wave is past the K loop), one
-  // value per lane as the MFMA result lies, and are read back as 16-byte row
-  // pieces: wide stores of whole row segments instead of one 2- or 4-byte
-  // store per lane and value.
-  __syncthreads();
+  // 8 (i / 4) + 4 (l / 32) + i % 4.
   if constexpr (GU) {
+    // Each wave's SwiGLU rows go through its own LDS region (the stages are
+    // free once every wave is past the K loop), one value per lane as the
+    // MFMA result lies, and are read back as 16-byte row pieces: wide stores
+    // of whole row segments instead of one 2-byte store per lane and value.
+    __syncthreads();
     constexpr int kAP = 136;   // staged row pitch in bf16 (128 + 8)
     uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + w * (32 * kAP);
     uint16_t* act = reinterpret_cast<uint16_t*>(a.out);
@@ -483,31 +483,19 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
       __builtin_amdgcn_wave_barrier();
     }
   } else {
-    constexpr int kYP = 136;   // staged row pitch in floats (128 + 8)
-    float* stage = reinterpret_cast<float*>(lds) + w * (32 * kYP);
+    // fp32 y: 32 lanes store 128 contiguous bytes of a row per value, and
+    // staging these through LDS measured slower (DeepSeek-V3 down, T = 8192)
     float* y = reinterpret_cast<float*>(a.out);
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-      const int rb = 32 * (2 * mb + wm);
-      if (rb >= rows) continue;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {   // column blocks 4 half .. 4 half + 3
+      for (int i = 0; i < 16; ++i) {
+        const int r = 32 * (2 * mb + wm) + 8 * (i / 4) + 4 * h + (i % 4);
+        if (r >= rows) continue;
+        const long prow = row0 + r;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int r = 8 * (i / 4) + 4 * h + (i % 4);
-#pragma unroll
-          for (int c = 0; c < 4; ++c) stage[r * kYP + 32 * c + r32] = acc[mb][4 * half + c][i];
-        }
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {   // 32 rows x 32 pieces of 4 floats
-          const int q = 64 * j + lane, rr = q / 32, c4 = q % 32;
-          if (rb + rr < rows)
-            *reinterpret_cast<f32x4_t*>(y + (long)(row0 + rb + rr) * a.H + (long)nb * 512 +
-                                        256 * wn + 128 * half + 4 * c4) =
-                *reinterpret_cast<const f32x4_t*>(stage + rr * kYP + 4 * c4);
-        }
-        __builtin_amdgcn_wave_barrier();
+        for (int cb = 0; cb < 8; ++cb)
+          y[prow * a.H + (long)nb * 512 + 256 * wn + 32 * cb + r32] = acc[mb][cb][i];
       }
     }
   }

@@ -113,10 +113,10 @@ hipError_t xtu_pin_split(const int32_t* ids, const float* wts, int n, const int3
 // w13_nodes / w2_nodes: ns node buffers ([expert][gate rows | up rows] and
 // [expert][rows] of the node, P16; strides in bytes per expert); s13 / s2:
 // packed scale groups (fp4), fp32 block scales (fp8) or fp32 [N][K/group_k]
-// row scales (int4, format 4), per expert stride; gs13 / gs2: NVFP4 global
-// scales; group_k: int4's k per scale (32, 64, 128; else ignored).  isa: -1
-// best available, 0 portable, 2 AVX-512.  max_tokens > 0 allocates the
-// pinned staging that xtu_cpu_decode
+// row scales (int4, format 4), per expert stride; gs13 / gs2: NVFP4
+// second-level scales ([E][2] gate, up / [E]); group_k: int4's k per scale
+// (32, 64, 128; else ignored).  isa: -1 best available, 0 portable, 2
+// AVX-512.  max_tokens > 0 allocates the pinned staging that xtu_cpu_decode
 // uses (max_tokens rows, max_topk pairs per row); 0 makes a host-only engine.
 // The weights are read in place: they must outlive the engine.
 hipError_t xtu_cpu_engine_create(int fmt, int H, int I, int n_experts, int ns,

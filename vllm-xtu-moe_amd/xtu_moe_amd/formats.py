@@ -123,6 +123,20 @@ def quantize(fmt: int, w: torch.Tensor):
     return w.to(torch.bfloat16).contiguous(), None, None
 
 
+def quantize_w13(fmt: int, w13: torch.Tensor):
+    """quantize() of a gate/up weight [E, 2I, H].  NVFP4 quantises the gate
+    and up halves separately, each with its own second-level scale (gs
+    [E, 2]: gate, up), as a checkpoint's w1 / w3 are; other formats are
+    quantize() of the whole."""
+    if fmt != FMT_NVFP4:
+        return quantize(fmt, w13)
+    I = w13.shape[1] // 2
+    cg, sg, gg = quantize_nvfp4(w13[:, :I])
+    cu, su, gu = quantize_nvfp4(w13[:, I:])
+    return (torch.cat([cg, cu], 1).contiguous(), torch.cat([sg, su], 1).contiguous(),
+            torch.stack([gg, gu], 1).contiguous())
+
+
 # ---------------------------------------------------------------- dequantisers
 def e4m3_table(device=None) -> torch.Tensor:
     return torch.arange(256, dtype=torch.uint8, device=device).view(torch.float8_e4m3fn).float()

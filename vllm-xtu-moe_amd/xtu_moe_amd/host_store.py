@@ -218,7 +218,8 @@ class HostExpertStore:
 def slot_plane_specs(fmt, H, I) -> dict:
     """Per-expert (shape, dtype) of each device plane of a layer in format
     `fmt` (None: the format has no such plane): the packed P16 weights and
-    scale groups, FP8's fp32 block scales, NVFP4's fp32 global scales."""
+    scale groups, FP8's fp32 block scales, NVFP4's fp32 second-level scales
+    (gate and up for w13, one for w2)."""
     fmt, H, I = int(fmt), int(H), int(I)
     u8, f32 = torch.uint8, torch.float32
     spec = {"w13": ((2 * I * F.row_bytes(fmt, H),), u8), "w2": ((H * F.row_bytes(fmt, I),), u8),
@@ -230,7 +231,7 @@ def slot_plane_specs(fmt, H, I) -> dict:
         spec["s13"] = ((F.scale_bytes(fmt, 2 * I, H),), u8)
         spec["s2"] = ((F.scale_bytes(fmt, H, I),), u8)
         if fmt == F.FMT_NVFP4:
-            spec["gs13"] = spec["gs2"] = ((), f32)
+            spec["gs13"], spec["gs2"] = ((2,), f32), ((), f32)   # gate, up / down
     elif fmt != F.FMT_BF16:
         raise ValueError(f"no device slot layout for format {fmt}")
     return spec

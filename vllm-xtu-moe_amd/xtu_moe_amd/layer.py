@@ -54,13 +54,29 @@ def _fp8_block_scales(s):
     return s.float()
 
 
+def gate_up_scales2(gs13):
+    """NVFP4 second-level scales of w13 as fp32 [N, 2] (gate, up), the
+    layout the kernels read (gs13[2 slot], gs13[2 slot + 1]): the
+    checkpoint's w13_weight_scale_2 [E, 2] as it is, a per-expert [E]
+    vector repeated; None stays None."""
+    if gs13 is None:
+        return None
+    g = gs13.to(torch.float32)
+    if g.dim() == 1:
+        g = g[:, None].expand(-1, 2)
+    if g.dim() != 2 or g.shape[1] != 2:
+        raise ValueError(f"gate/up second-level scales must be [E] or [E, 2], got {tuple(g.shape)}")
+    return g.contiguous()
+
+
 class ExpertWeights:
     """Resident weights of one layer in the P16 panel layout.
 
     Experts [0, E) are routed; [E, E + n_shared) are shared experts that every
     token uses with weight 1.  Tensors: w13/w2 u8 [E+NS, bytes], s13/s2 (u8
-    P16 scales for fp4, fp32 block scales for fp8, None for bf16), gs13/gs2
-    fp32 [E+NS] (NVFP4 global scales) or None.
+    P16 scales for fp4, fp32 block scales for fp8, None for bf16), NVFP4
+    second-level scales gs13 fp32 [E+NS, 2] (gate, up; a [E+NS] vector is
+    taken as one scale for both halves) and gs2 fp32 [E+NS], or None.
     """
 
     def __init__(self, fmt, H, I, E, n_shared, w13, s13, w2, s2, gs13=None, gs2=None, *,
@@ -70,6 +86,7 @@ class ExpertWeights:
         self.group_k = int(group_k) if self.fmt == FMT_INT4 else 0
         if self.fmt == FMT_INT4 and self.group_k not in INT4_GROUPS:
             raise ValueError(f"INT4 weights need group_k in {INT4_GROUPS}, got {group_k}")
+        gs13 = gate_up_scales2(gs13)
         self.w13, self.s13, self.w2, self.s2, self.gs13, self.gs2 = w13, s13, w2, s2, gs13, gs2
         # mutable: the planes are restaged in place (ring / pool slots), so
         # nothing derived from them is cached; their FP8 scale bound is the

@@ -321,28 +321,26 @@ class XiaotuExpertsNvfp4(XiaotuExperts):
 
 def nvfp4_global_scales(g13, g2, where: str = "?"):
     """The per-expert fp32 second-level scales (weight_scale_2) as the
-    kernels take them: one scalar per expert for gate/up and one for down.
+    kernels take them: gate/up as [E, 2] (gate, up) and down as [E].
 
-    Checkpoints give w13's as [E] or [E, 2] (gate, up); the kernels multiply
-    the gate and up results by the same scalar, so [E, 2] is taken only when
-    the two columns are equal, and refused otherwise (taking either would be a
-    silent wrong answer), as the reference's GPU path does
-    (vllm_xiaotu_moe/hybrid_model.py:1490-1520).  All-zero scales mean the
-    loader did not fill them and are refused as well (hybrid_model.py:
-    1545-1554).  The e4m3 group scale times this scalar is the reference's
-    fold (hybrid_model.py:1522-1570: fp32 e4m3(s) * scale_2, applied to the
-    e2m1 value); the kernels form the same product."""
+    Checkpoints give w13's as [E, 2] (w1, w3) or [E]; the kernels multiply
+    the gate results by column 0 and the up results by column 1, the
+    reference's fold of scale_2 into the fp32 group scales per half
+    (vllm_xiaotu_moe/hybrid_model.py:1546-1563: fp32 e4m3(s) * scale_2,
+    applied to the e2m1 value), so w1 and w3 scales that differ are taken as
+    they are.  All-zero scales mean the loader did not fill them and are
+    refused (hybrid_model.py:1550-1556)."""
     if g13 is None or g2 is None:
         raise ValueError(f"[xtu-nvfp4] {where}: weight_scale_2 planes missing")
     g13 = g13.detach().to(torch.float32)
     g2 = g2.detach().to(torch.float32).reshape(-1)
-    if g13.dim() == 2 and g13.shape[1] > 1:
-        ne = int((g13[:, 0] != g13[:, 1:].amax(1)).sum() + (g13[:, 0] != g13[:, 1:].amin(1)).sum())
-        if ne:
-            raise RuntimeError(
-                f"[xtu-nvfp4] {where}: gate/up weight_scale_2 differ for some experts; the "
-                "kernels take one second-level scale per expert for gate and up")
-    g13 = g13[:, 0] if g13.dim() == 2 else g13.reshape(-1)
+    if g13.dim() == 2 and g13.shape[1] == 1:
+        g13 = g13.reshape(-1)
+    if g13.dim() == 1:
+        g13 = g13[:, None].expand(-1, 2)
+    if g13.dim() != 2 or g13.shape[1] != 2:
+        raise ValueError(f"[xtu-nvfp4] {where}: w13 weight_scale_2 must be [E] or [E, 2], "
+                         f"got {tuple(g13.shape)}")
     if float(g13.abs().max()) == 0.0 or float(g2.abs().max()) == 0.0:
         raise RuntimeError(f"[xtu-nvfp4] {where}: weight_scale_2 is all zero (not loaded)")
     if g13.shape[0] != g2.shape[0]:

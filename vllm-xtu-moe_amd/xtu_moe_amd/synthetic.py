@@ -20,7 +20,7 @@ def synth_layer(fmt: int, E: int, n_shared: int, H: int, I: int, *, seed: int = 
     n = E + n_shared
     g = torch.Generator(device=dev).manual_seed(seed)
 
-    def alloc(N, K):
+    def alloc(N, K, gu):
         rb = F.row_bytes(fmt, K)
         w = torch.empty((n, N * rb), dtype=torch.uint8, device=dev)
         if fmt in (F.FMT_MXFP4, F.FMT_NVFP4):
@@ -29,16 +29,18 @@ def synth_layer(fmt: int, E: int, n_shared: int, H: int, I: int, *, seed: int = 
             s = torch.empty((n, (N // 128) * (K // 128)), dtype=torch.float32, device=dev)
         else:
             s = None
-        gs = torch.empty(n, dtype=torch.float32, device=dev) if fmt == F.FMT_NVFP4 else None
+        gs = None
+        if fmt == F.FMT_NVFP4:   # gate/up: one second-level scale per half
+            gs = torch.empty((n, 2) if gu else (n,), dtype=torch.float32, device=dev)
         return w, s, gs
 
-    w13, s13, gs13 = alloc(2 * I, H)
-    w2, s2, gs2 = alloc(H, I)
+    w13, s13, gs13 = alloc(2 * I, H, True)
+    w2, s2, gs2 = alloc(H, I, False)
     for e0 in range(0, n, chunk):
         e1 = min(n, e0 + chunk)
-        for (w, s, gs, N, K) in ((w13, s13, gs13, 2 * I, H), (w2, s2, gs2, H, I)):
+        for (w, s, gs, N, K, gu) in ((w13, s13, gs13, 2 * I, H, True), (w2, s2, gs2, H, I, False)):
             dense = torch.randn((e1 - e0, N, K), generator=g, device=dev) * std
-            q, sc, gsc = F.quantize(fmt, dense)
+            q, sc, gsc = (F.quantize_w13 if gu else F.quantize)(fmt, dense)
             del dense
             w[e0:e1] = F.pack_weight(fmt, q)
             if s is not None:
