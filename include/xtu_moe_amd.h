@@ -188,6 +188,38 @@ hipError_t xtu_decode_gate_up_routed(int fmt, const void* x, int T, int H, int I
                                      void* act, float limit, float alpha, float beta,
                                      hipStream_t stream);
 
+/* Routing, segmentation and every gate/up of a tiny decode batch in one
+ * launch (the routing launch and the gate/up launch above folded together).
+ * The routing arguments are xtu_decode_route_shared's and its outputs the
+ * same (topk_ids / topk_weights and the segmentation with tiles of bm <= 16
+ * rows, for the down pass); act bf16 [A][I] gets the routed experts' SwiGLU
+ * rows in sorted order.  act_shared non-null (n_shared >= 1): the shared
+ * experts' rows go there ([n_shared][T][I], token order) from workgroups
+ * that need no routing, and the down pass is xtu_decode_down_combine with
+ * act_shared; act_shared null: the shared experts' rows are ordinary sorted
+ * rows of act.  Every routed workgroup routes the batch in LDS for itself
+ * (the same code on the same inputs, so all agree) instead of reading the
+ * routing back from memory.  max_tiles: work items per gate panel, at least
+ * b + (A - b) / bm for A = T (K + n_shared) pairs in b <= min(E, T K) +
+ * n_shared buckets, at most 64.  Replaces, for decode, the router call,
+ * _build_segmentation (gpu_prefill.py:849-887) and moe4_smallm_gu2
+ * (moe4_smallm.cu:395-413).
+ * xtu_decode_route_gate_up_ok: the shape fits (the tiny router's envelope
+ * and the gate/up fast path, as xtu_decode_route_shared_ok, but a routing
+ * wave may take several tokens and n_shared may be 0). */
+int xtu_decode_route_gate_up_ok(int fmt, int mode, int T, int E, int K, int n_group,
+                                int n_shared, int H, int I);
+hipError_t xtu_decode_route_gate_up(
+    int mode, const float* logits, const float* bias, int32_t* topk_ids, float* topk_weights,
+    int T, int E, int K, int n_group, int topk_group, float routed_scaling, int renormalize,
+    const int32_t* id_map, int n_shared, int drop_zero, int bm, int32_t* sorted_pair,
+    int32_t* sorted_tok, float* sorted_wts, int32_t* inv, int32_t* seg_start, int32_t* active,
+    int32_t* n_active, int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
+    int32_t* expert_tile_start, int fmt, const void* x, int H, int I, const void* w13,
+    const void* s13, const float* gs13, long w_estride, long s_estride, const int32_t* slot_map,
+    int max_tiles, void* act, void* act_shared, float limit, float alpha, float beta,
+    hipStream_t stream);
+
 /* Down projection with the weighted combine fused: out[t] = sum over t's live
  * pairs (t, e) of w * (act_row W2_e^T), bf16 (out_bf16 = 1) or fp32 [T][H],
  * every row written.  Replaces moe4_smallm_dn2 (moe4_smallm.cu:260-333,

@@ -291,3 +291,101 @@ def test_shared_split_misaligned_logits_fall_back(monkeypatch):
     x = torch.randn((T, H), device="cuda").to(torch.bfloat16)
     _same(_split_run(monkeypatch, True, x, W, K, router=router),
           _split_run(monkeypatch, False, x, W, K, router=router), "misaligned logits")
+
+
+# ---------------------------------------------------------------------------
+# routing, segmentation and gate/up in one launch (xtu_decode_route_gate_up)
+
+def _fr_run(monkeypatch, fused_route, split, x, W, K, **kw):
+    monkeypatch.setenv(L.FUSED_ROUTE_ENV, "1" if fused_route else "0")
+    return _split_run(monkeypatch, split, x, W, K, **kw)
+
+
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("fmt,T,H", [(F.FMT_MXFP4, 1, 512), (F.FMT_MXFP4, 2, 512),
+                                     (F.FMT_MXFP4, 4, 512), (F.FMT_MXFP4, 4, 4096),
+                                     (F.FMT_FP8, 7, 4096)])
+def test_fused_route_grouped_sigmoid(fmt, T, H, split, monkeypatch):
+    """Every gate/up workgroup routes the batch itself: routing outputs,
+    segmentation and the layer output are bitwise those of the separate
+    routing launch, with the shared expert split off or as a sorted bucket;
+    at H = 512 two waves route four tokens."""
+    E, NS, I, K = 256, 1, 256, 8
+    d, W = _layer(fmt, E, NS, H, I, seed=170 + T)
+    g = torch.Generator(device="cuda").manual_seed(171 + T)
+    logits = torch.randn((T, E), generator=g, device="cuda")
+    bias = torch.randn((E,), generator=g, device="cuda") * 0.1
+    x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    router = dict(logits=logits, scoring="sigmoid", bias=bias, n_group=8, topk_group=4,
+                  routed_scaling_factor=2.5, renormalize=True)
+    assert L._route_gate_up_ok(fmt, 1, T, E, K, router, H, I, NS)
+    a = _fr_run(monkeypatch, True, split, x, W, K, router=router)
+    b = _fr_run(monkeypatch, False, split, x, W, K, router=router)
+    _same(a, b, f"fused route T={T} split={split}")
+    out, ids, wts, _ = a
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids.cpu().numpy(),
+                       wts.cpu().numpy(), E, NS, H, I)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"fused route T={T} vs oracle")
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_fused_route_softmax_512_no_shared(T, monkeypatch):
+    fmt, E, NS, H, I, K = F.FMT_NVFP4, 512, 0, 512, 256, 10
+    _, W = _layer(fmt, E, NS, H, I, seed=180 + T)
+    g = torch.Generator(device="cuda").manual_seed(181 + T)
+    logits = torch.randn((T, E), generator=g, device="cuda")
+    x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    router = dict(logits=logits, scoring="softmax", renormalize=True)
+    assert L._route_gate_up_ok(fmt, 0, T, E, K, router, H, I, NS)
+    _same(_fr_run(monkeypatch, True, False, x, W, K, router=router),
+          _fr_run(monkeypatch, False, False, x, W, K, router=router), f"softmax 512 T={T}")
+
+
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("drop_zero", [True, False])
+def test_fused_route_given_ids_maps_two_shared(drop_zero, split, monkeypatch):
+    """Given ids (no router) through an id map, experts behind a slot map,
+    two shared experts, an invalid id, an expert listed twice, a zero
+    weight: bitwise the separate launches, and the oracle."""
+    fmt, E, NS, H, I, T, K = F.FMT_FP8, 16, 2, 2048, 256, 3, 4
+    d, _ = _layer(fmt, E, NS, H, I, seed=191)
+    order = np.arange(E + NS)[::-1].copy()
+    idx = torch.from_numpy(order)
+    rev = {k: (v[idx].contiguous() if v is not None else None) for k, v in d.items()}
+    W = ExpertWeights.from_dense(fmt, rev["w13"], rev["s13"], rev["w2"], rev["s2"], rev["gs13"],
+                                 rev["gs2"], n_shared=NS, device="cuda")
+    slot_map = torch.from_numpy(np.argsort(order).astype(np.int32)).cuda()
+    ids_np, wts_np = random_routing(T, K, E, seed=192)
+    ids_np[0, 1] = -1
+    ids_np[1, 2] = ids_np[1, 0]
+    wts_np[2, 3] = 0.0
+    ids = torch.from_numpy(ids_np).cuda()
+    wts = torch.from_numpy(wts_np).cuda()
+    id_map = torch.from_numpy(np.roll(np.arange(E), 5).astype(np.int32)).cuda()
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(193)).to(torch.bfloat16).cuda()
+    assert L._route_gate_up_ok(fmt, 2, T, E, K, None, H, I, NS)
+    kw = dict(ids=ids, wts=wts, drop_zero=drop_zero, id_map=id_map, slot_map=slot_map)
+    a = _fr_run(monkeypatch, True, split, x, W, K, **kw)
+    _same(a, _fr_run(monkeypatch, False, split, x, W, K, **kw),
+          f"given ids drop_zero={drop_zero} split={split}")
+    mapped = np.where((ids_np >= 0) & (ids_np < E), np.roll(np.arange(E), 5)[ids_np % E], -1)
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x.cpu()),
+                       mapped.astype(np.int32), wts_np, E, NS, H, I)
+    check_close(a[0].cpu().numpy(), ref, bf16_out=False, what="fused route given ids vs oracle")
+
+
+def test_fused_route_every_pair_invalid(monkeypatch):
+    """No live pair: the routed workgroups find no tile and exit; the shared
+    expert alone makes the output."""
+    fmt, E, NS, H, I, T, K = F.FMT_MXFP4, 16, 1, 512, 256, 2, 4
+    d, W = _layer(fmt, E, NS, H, I, seed=195)
+    ids = torch.full((T, K), -1, dtype=torch.int32, device="cuda")
+    wts = torch.ones((T, K), dtype=torch.float32, device="cuda")
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(196)).to(torch.bfloat16).cuda()
+    for split in (True, False):
+        a = _fr_run(monkeypatch, True, split, x, W, K, ids=ids, wts=wts)
+        _same(a, _fr_run(monkeypatch, False, split, x, W, K, ids=ids, wts=wts),
+              f"all invalid split={split}")
+        ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x.cpu()),
+                           ids.cpu().numpy(), wts.cpu().numpy(), E, NS, H, I)
+        check_close(a[0].cpu().numpy(), ref, bf16_out=False, what="all invalid vs oracle")

@@ -21,6 +21,7 @@
 // down: y is fp32; with KSPLIT = 1 each wave writes its panel directly.
 #include "route_tiny.hpp"
 #include "weight_format.hpp"
+#include <algorithm>
 
 namespace xtu {
 namespace {
@@ -452,6 +453,105 @@ __global__ __launch_bounds__(512) void decode_route_shared_kernel(tiny::SmallArg
   const int tok = min(m, a.T - 1);
   consume_round<FMT, NU, true>(r, acc, u0, u1, xs + tok * a.H + q * F::kCK, nullptr);
   gate_up_epilogue<FMT>(a, red, acc, w, lane, sh * a.T, a.T, ws, sub);
+}
+
+// Routing, segmentation and every gate/up of a decode batch in one launch.
+// Workgroups [0, n_sh): the shared experts' gate/up panels when they are
+// split off (rows to act_sh, as decode_route_shared_kernel writes them); the
+// rest route and segment the whole batch for themselves in LDS
+// (tiny::route_segment_block with STORE = false; the first one also stores
+// the routing and the segmentation for the down pass), stage the batch's x
+// rows once, then take (16-row tile, gate panel) work items item0, item0 +
+// stride, ... of the batch, each streamed as decode_gate_up_kernel's fast
+// path does.  Launched with about one resident round of these workgroups,
+// so the routing is done once per workgroup, beside the first weight
+// streams, and the routing launch and its boundary are gone.  skip: tiles at
+// the end of the tile list left out (the split-off shared experts' own).
+template <int FMT, int MODE, int EPL, int XC>
+__global__ __launch_bounds__(512) void decode_route_gate_up_kernel(tiny::SmallArgs ra,
+                                                                   DecodeArgs a, void* act_sh,
+                                                                   int n_sh, int skip) {
+  using F = WFmt<FMT>;
+  constexpr int NU = round_units<FMT>();
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // T rows x H
+  __shared__ f32x4_t red[8][kWave];
+  __shared__ __attribute__((aligned(16))) tiny::TinySmem g;
+  const int npan = a.I / 16;
+  const int ksplit = a.ksplit;
+  const int w = wave_id();
+  const uint32_t lane = threadIdx.x % kWave;
+  const int half = w / ksplit, ks = w - half * ksplit;
+  const int nunits = a.H / 128;
+  const int u0 = ks * nunits / ksplit, u1 = (ks + 1) * nunits / ksplit;
+  const int q = lane / 16, m = lane % 16;
+  const int nchunks = a.T * (a.H / 8);
+  // The batch's rows go to LDS first, all pieces in flight at once; their
+  // registers are then free for the weight stream (and the routing).  They
+  // are read only after a barrier.
+  {
+    u32x4_t xv[XC];
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+      const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
+      xv[j] = *reinterpret_cast<const u32x4_t*>(a.x + (long)cc * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+      const int cc = threadIdx.x + j * blockDim.x;
+      if (cc < nchunks) *reinterpret_cast<u32x4_t*>(xs + cc * 8) = xv[j];
+    }
+  }
+  if ((int)blockIdx.x < n_sh) {
+    // a shared expert: all T rows of the batch, in token order, no routing
+    const int sh = blockIdx.x / npan, sub = blockIdx.x - sh * npan;
+    const int e = ra.E + sh;
+    const int ws = a.slot_map ? a.slot_map[e] : e;
+    const Stream<FMT> st = make_stream<FMT>(a, ws, half ? npan + sub : sub, a.H);
+    Round<FMT, NU> r;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    __builtin_amdgcn_sched_barrier(0);
+    issue_round<FMT, NU>(r, st, u0, u1, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    consume_round<FMT, NU, true>(r, acc, u0, u1, xs + min(m, a.T - 1) * a.H + q * F::kCK,
+                                 nullptr);
+    a.out = act_sh;
+    gate_up_epilogue<FMT>(a, red, acc, w, lane, sh * a.T, a.T, ws, sub);
+    return;
+  }
+  const int first = blockIdx.x - n_sh, stride = gridDim.x - n_sh;
+  if (first == 0) tiny::route_segment_block<MODE, EPL, true>(ra, g);
+  else tiny::route_segment_block<MODE, EPL, false>(ra, g);
+  const int items = (g.act_t[g.n_act] - skip) * npan;
+  if (first >= items) return;   // whole workgroup
+  // The next item's weights are issued before this item's epilogue, whose
+  // row stores would otherwise sit in front of them in the wave's in-order
+  // memory counter.
+  auto issue = [&](Round<FMT, NU>& rr, int it, int& ws_out) {
+    const int slot = it / npan, sub = it - slot * npan;
+    const int e = g.tile_e[slot];
+    ws_out = a.slot_map ? a.slot_map[e] : e;
+    const Stream<FMT> st = make_stream<FMT>(a, ws_out, half ? npan + sub : sub, a.H);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_round<FMT, NU>(rr, st, u0, u1, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  Round<FMT, NU> r;
+  int item = first, ws = 0;
+  issue(r, item, ws);
+  while (true) {
+    const int slot = item / npan, sub = item - slot * npan;
+    const int r0 = g.tile_r[slot], na = g.tile_n[slot];
+    const int tok = g.stok[r0 + min(m, na - 1)];
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    consume_round<FMT, NU, true>(r, acc, u0, u1, xs + tok * a.H + q * F::kCK, nullptr);
+    const int next = item + stride, ws_cur = ws;
+    if (next < items) issue(r, next, ws);
+    gate_up_epilogue<FMT>(a, red, acc, w, lane, r0, na, ws_cur, sub);
+    if (next >= items) break;
+    __syncthreads();   // red is read back before the next item writes it
+    item = next;
+  }
 }
 
 template <int FMT, bool GENERIC>
@@ -981,6 +1081,75 @@ hipError_t launch_route_shared(int mode, int epl, const tiny::SmallArgs& ra, Dec
   return hipPeekAtLastError();
 }
 
+template <int FMT, int XC>
+void launch_route_gate_up_xc(int mode, int epl, dim3 grid, int bd, size_t lds,
+                             const tiny::SmallArgs& ra, const DecodeArgs& a, void* act_sh,
+                             int n_sh, int skip, hipStream_t stream) {
+  if (mode == 2) {
+    decode_route_gate_up_kernel<FMT, 2, 1, XC><<<grid, bd, lds, stream>>>(ra, a, act_sh, n_sh, skip);
+  } else if (mode == 1) {
+    if (epl == 4)
+      decode_route_gate_up_kernel<FMT, 1, 4, XC><<<grid, bd, lds, stream>>>(ra, a, act_sh, n_sh, skip);
+    else
+      decode_route_gate_up_kernel<FMT, 1, 8, XC><<<grid, bd, lds, stream>>>(ra, a, act_sh, n_sh, skip);
+  } else {
+    if (epl == 4)
+      decode_route_gate_up_kernel<FMT, 0, 4, XC><<<grid, bd, lds, stream>>>(ra, a, act_sh, n_sh, skip);
+    else
+      decode_route_gate_up_kernel<FMT, 0, 8, XC><<<grid, bd, lds, stream>>>(ra, a, act_sh, n_sh, skip);
+  }
+}
+
+// Compute units of the current device (queried once per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+constexpr size_t kLdsCu = 160 * 1024;                                      // LDS per CU
+constexpr size_t kStaticLds = 8 * kWave * 16 + sizeof(tiny::TinySmem);     // red + routing
+
+// Grid: the split-off shared experts' panels (act_sh set), then about one
+// resident round of routed workgroups looping over the batch's work items.
+template <int FMT>
+hipError_t launch_route_gate_up(int mode, int epl, const tiny::SmallArgs& ra, DecodeArgs a,
+                                void* act_sh, int max_tiles, hipStream_t stream) {
+  using F = WFmt<FMT>;
+  if (!a.w_estride) a.w_estride = F::w_bytes(2L * a.I, a.H);
+  if (!a.s_estride) a.s_estride = F::s_bytes(2L * a.I, a.H);
+  int ksplit = 0, xc = 0;
+  if (!gate_up_fast_shape<FMT>(a.T, a.H, ksplit, xc)) return hipErrorInvalidValue;
+  a.ksplit = ksplit;
+  a.rows = a.T;
+  const int bd = 128 * ksplit;
+  const int npan = a.I / 16;
+  const int n_sh = act_sh ? ra.NS * npan : 0;
+  const int skip = act_sh ? ra.NS * ((a.T + ra.bm - 1) / ra.bm) : 0;
+  const size_t lds = (size_t)a.T * a.H * 2;
+  // routed workgroups: one resident round beside the shared ones (the
+  // work items past it are looped over), never more than the items
+  const int per_cu = std::max(1, std::min<int>(1024 / bd, (int)(kLdsCu / (lds + kStaticLds))));
+  const int routed = (int)std::max<long>(
+      1, std::min<long>((long)max_tiles * npan, (long)per_cu * cu_count() - n_sh));
+  const dim3 grid(n_sh + routed);
+  switch (xc) {
+    case 1: launch_route_gate_up_xc<FMT, 1>(mode, epl, grid, bd, lds, ra, a, act_sh, n_sh, skip, stream); break;
+    case 2: launch_route_gate_up_xc<FMT, 2>(mode, epl, grid, bd, lds, ra, a, act_sh, n_sh, skip, stream); break;
+    case 4: launch_route_gate_up_xc<FMT, 4>(mode, epl, grid, bd, lds, ra, a, act_sh, n_sh, skip, stream); break;
+    default: launch_route_gate_up_xc<FMT, 8>(mode, epl, grid, bd, lds, ra, a, act_sh, n_sh, skip, stream); break;
+  }
+  return hipPeekAtLastError();
+}
+
 hipError_t dispatch_decode(int fmt, int which, DecodeArgs a, int max_active, hipStream_t stream) {
   switch (fmt) {
     case kMXFP4: return launch_decode<kMXFP4>(which, a, max_active, stream);
@@ -1094,6 +1263,70 @@ hipError_t xtu_decode_route_shared(
     case kNVFP4: return launch_route_shared<kNVFP4>(mode, epl, ra, a, stream);
     case kFP8: return launch_route_shared<kFP8>(mode, epl, ra, a, stream);
     case kBF16: return launch_route_shared<kBF16>(mode, epl, ra, a, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+int xtu_decode_route_gate_up_ok(int fmt, int mode, int T, int E, int K, int n_group,
+                                int n_shared, int H, int I) {
+  int ksplit = 0, xc = 0;
+  if (!shape_ok(fmt, H, I) || mode < 0 || mode > 2 || K < 1 || K > 16 || K > E || E < 1 ||
+      E > 1024 || n_shared < 0 || n_shared > 16 || !gate_up_fast_shape_fmt(fmt, T, H, ksplit, xc))
+    return 0;
+  if (mode == 1 && (n_group <= 0 || n_group > 64 || E % n_group)) return 0;
+  tiny::SmallArgs r{};
+  r.T = T;
+  r.K = K;
+  r.E = E;
+  r.NS = n_shared;
+  r.n_group = n_group > 0 ? n_group : 1;
+  r.renorm = 1;
+  static const float probe[4] = {0.f, 0.f, 0.f, 0.f};   // a 16-byte-aligned row stands in
+  r.logits = probe;
+  return tiny::tiny_epl(r, mode) != 0;
+}
+
+hipError_t xtu_decode_route_gate_up(
+    int mode, const float* logits, const float* bias, int32_t* topk_ids, float* topk_weights,
+    int T, int E, int K, int n_group, int topk_group, float routed_scaling, int renormalize,
+    const int32_t* id_map, int n_shared, int drop_zero, int bm, int32_t* sorted_pair,
+    int32_t* sorted_tok, float* sorted_wts, int32_t* inv, int32_t* seg_start, int32_t* active,
+    int32_t* n_active, int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
+    int32_t* expert_tile_start, int fmt, const void* x, int H, int I, const void* w13,
+    const void* s13, const float* gs13, long w_estride, long s_estride, const int32_t* slot_map,
+    int max_tiles, void* act, void* act_shared, float limit, float alpha, float beta,
+    hipStream_t stream) {
+  XTU_CHECK_ARG(xtu_decode_route_gate_up_ok(fmt, mode, T, E, K, n_group, n_shared, H, I));
+  XTU_CHECK_ARG(bm >= 1 && bm <= kMaxTok && w_estride >= 0 && s_estride >= 0);
+  // every tile of the batch needs a work item: b non-empty buckets of A
+  // pairs hold at most b + (A - b) / bm tiles (ceil(n / bm) <= 1 + (n-1) / bm)
+  {
+    const long A = (long)T * (K + n_shared);
+    const long b = std::min<long>(std::min<long>(E, (long)T * K) + n_shared, A);
+    XTU_CHECK_ARG(max_tiles >= std::min<long>(A, b + (A - b) / std::max(bm, 1)) &&
+                  max_tiles >= 1 && max_tiles <= tiny::kTinyMaxA);
+  }
+  if (mode == 1)
+    XTU_CHECK_ARG(topk_group > 0 && topk_group <= n_group && K <= topk_group * (E / n_group));
+  XTU_CHECK_ARG(topk_ids && topk_weights && (mode == 2 || logits));
+  XTU_CHECK_ARG(sorted_pair && sorted_tok && sorted_wts && inv && seg_start && active &&
+                n_active && tile_expert && tile_row0 && n_tiles && expert_tile_start);
+  XTU_CHECK_ARG(x && w13 && (fmt == kBF16 || s13) && act && (n_shared > 0 || !act_shared));
+  tiny::SmallArgs ra{logits, bias, topk_ids, topk_weights, id_map, T, K, E, n_group,
+                     topk_group, renormalize, n_shared, drop_zero, bm, routed_scaling,
+                     sorted_pair, sorted_tok, inv, seg_start, active, n_active, sorted_wts,
+                     tile_expert, tile_row0, n_tiles, expert_tile_start};
+  const int epl = tiny::tiny_epl(ra, mode);   // also checks the logit / bias alignment
+  XTU_CHECK_ARG(epl != 0);
+  (void)hipGetLastError();
+  DecodeArgs a{(const uint16_t*)x, (const uint8_t*)w13, (const uint8_t*)s13, gs13, nullptr,
+               nullptr, nullptr, nullptr, slot_map, act, nullptr, T, H, I, w_estride,
+               s_estride, limit, alpha, beta, 0, 1, 1, 0};
+  switch (fmt) {
+    case kMXFP4: return launch_route_gate_up<kMXFP4>(mode, epl, ra, a, act_shared, max_tiles, stream);
+    case kNVFP4: return launch_route_gate_up<kNVFP4>(mode, epl, ra, a, act_shared, max_tiles, stream);
+    case kFP8: return launch_route_gate_up<kFP8>(mode, epl, ra, a, act_shared, max_tiles, stream);
+    case kBF16: return launch_route_gate_up<kBF16>(mode, epl, ra, a, act_shared, max_tiles, stream);
   }
   return hipErrorInvalidValue;
 }

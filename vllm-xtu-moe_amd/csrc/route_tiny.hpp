@@ -214,8 +214,10 @@ __device__ void route_token_wave(const float* __restrict__ l, const float* __res
     w = renorm ? __fdiv_rn(my_ws, sum) * scale : my_ws * scale;
   }
   if (lane < K) {
-    ids_out[lane] = my_e;
-    wts_out[lane] = w;
+    if (ids_out) {
+      ids_out[lane] = my_e;
+      wts_out[lane] = w;
+    }
     if (ids_lds) {
       ids_lds[lane] = my_e;
       wts_lds[lane] = w;
@@ -232,26 +234,39 @@ struct TinySmem {
   int act_r[kTinyMaxA + 1];   // first row of active bucket i; [n_act] = trash start
   int act_t[kTinyMaxA + 1];   // first tile of active bucket i; [n_act] = all tiles
   int n_act;
+  // the same segmentation as the global outputs, for the workgroup's own use
+  int stok[kTinyMaxA];        // token of sorted row j
+  int tile_e[kTinyMaxA];      // bucket of tile t
+  int tile_r[kTinyMaxA];      // first sorted row of tile t
+  int tile_n[kTinyMaxA];      // rows of tile t (at most bm)
 };
 
-// MODE 0/1: wave t routes token t (E = 64 * EPL), then the segmentation;
-// MODE 2: ids/wts given.  One workgroup with blockDim.x >= 64 * T; the last
-// pass writes one bucket start per thread (any block size is correct).
-template <int MODE, int EPL>
+// MODE 0/1: wave w routes tokens w, w + waves, ... (E = 64 * EPL), then the
+// segmentation; MODE 2: ids/wts given.  One workgroup of at least one wave;
+// the last pass writes one bucket start per thread (any block size is
+// correct).
+// STORE = false: nothing is written to global memory, only the segmentation
+// in g (the LDS copy every caller gets: sorted tokens and the tile map),
+// so any number of workgroups can route the same batch for themselves and
+// agree (the same code on the same inputs).
+template <int MODE, int EPL, bool STORE = true>
 __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
   const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
   const int T = a.T, K = a.K, E = a.E, NS = a.NS;
   const int TK = T * K, A = TK + T * NS, NB = E + NS + 1, trash = E + NS;
   constexpr int BIG = 0x7fffffff;
   if (MODE < 2) {
-    if (wv < T)
-      route_token_wave<MODE, EPL>(a.logits + (long)wv * E, a.bias, K, a.n_group, a.topk_group,
-                                  a.scale, a.renorm, lane, a.ids + (long)wv * K,
-                                  a.wts + (long)wv * K, g.ids + wv * K, g.w + wv * K);
+    const int nw = blockDim.x / kWave;   // a wave routes tokens wv, wv + nw, ...
+    for (int t = wv; t < T; t += nw)
+      route_token_wave<MODE, EPL>(a.logits + (long)t * E, a.bias, K, a.n_group, a.topk_group,
+                                  a.scale, a.renorm, lane,
+                                  STORE ? a.ids + (long)t * K : nullptr,
+                                  STORE ? a.wts + (long)t * K : nullptr, g.ids + t * K,
+                                  g.w + t * K);
   } else {
-    if (tid < TK) {
-      g.ids[tid] = a.ids[tid];
-      g.w[tid] = a.wts[tid];
+    for (int p = tid; p < TK; p += blockDim.x) {
+      g.ids[p] = a.ids[p];
+      g.w[p] = a.wts[p];
     }
   }
   __syncthreads();
@@ -279,11 +294,15 @@ __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
       pos += (v[0] < key) + (v[1] < key) + (v[2] < key) + (v[3] < key);
     }
     if (lane < A) {
+      const int tk = lane < TK ? lane / K : (lane - TK) / NS;
       g.sb[pos] = b;
-      a.sorted_pair[pos] = lane;
-      a.inv[lane] = pos;
-      a.sorted_tok[pos] = lane < TK ? lane / K : (lane - TK) / NS;
-      a.sorted_wts[pos] = w;
+      g.stok[pos] = tk;
+      if constexpr (STORE) {
+        a.sorted_pair[pos] = lane;
+        a.inv[lane] = pos;
+        a.sorted_tok[pos] = tk;
+        a.sorted_wts[pos] = w;
+      }
     } else {
       g.sb[lane] = BIG;
     }
@@ -308,10 +327,17 @@ __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
       g.act_b[ai] = sbj;
       g.act_r[ai] = lane;
       g.act_t[ai] = t0;
-      a.active[ai] = sbj;
+      if constexpr (STORE) a.active[ai] = sbj;
       for (int j = 0; j < nt; ++j) {
-        a.tile_expert[t0 + j] = sbj;
-        a.tile_row0[t0 + j] = lane + j * a.bm;
+        if constexpr (STORE) {
+          a.tile_expert[t0 + j] = sbj;
+          a.tile_row0[t0 + j] = lane + j * a.bm;
+        }
+        if (t0 + j < kTinyMaxA) {   // bm >= 1: at most A <= 64 tiles
+          g.tile_e[t0 + j] = sbj;
+          g.tile_r[t0 + j] = lane + j * a.bm;
+          g.tile_n[t0 + j] = min(a.bm, cnt - j * a.bm);
+        }
       }
     }
     // rows before the trash bucket (= pairs in active buckets)
@@ -321,13 +347,16 @@ __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
       g.n_act = na;
       g.act_r[na] = __popcll(tm);
       g.act_t[na] = tot;
-      a.n_active[0] = na;
-      a.n_tiles[0] = tot;
+      if constexpr (STORE) {
+        a.n_active[0] = na;
+        a.n_tiles[0] = tot;
+      }
     }
     if (lane >= na && lane < kTinyMaxA + 4) g.act_b[lane] = BIG;
     if (lane < 4) g.act_b[kTinyMaxA + lane] = BIG;
   }
   __syncthreads();
+  if constexpr (!STORE) return;
   // per-bucket starts: i = active buckets below e; rows and tiles before e
   for (int e = tid; e <= NB; e += blockDim.x) {
     int i = 0;

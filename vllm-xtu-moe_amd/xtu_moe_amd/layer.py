@@ -28,6 +28,7 @@ SMALL_MAX_PAIRS = 1024
 # plus the three-launch segmentation is faster (measured: 95 us vs ~17 us for
 # 128 tokens over 8 experts).
 SMALL_ROUTE_MAX_TOKENS = 16
+TINY_MAX_PAIRS = 64  # pairs one workgroup routes and segments (xtu_route_segment_small's tiny path)
 LANE_ROUTE_MAX_E, LANE_ROUTE_MAX_K = 32, 8   # softmax routed by one thread per token
 
 
@@ -689,6 +690,44 @@ def _route_shared_ok(fmt, mode, T, E, K, router, H, I, NS) -> bool:
                           int(K), n_group, int(NS), int(H), int(I)))
 
 
+FUSED_ROUTE_ENV = "XTU_DECODE_FUSED_ROUTE"
+# gate/up work items (tiles x I/16 panels) up to which the one-launch routing
+# + gate/up pays: about one resident round of its workgroups.  Measured on
+# MI355X: Qwen3-Next MXFP4 T = 1 (352 items) 27.2 -> 24.9 us per layer;
+# DeepSeek-V3 T = 1 (1152) unchanged, T = 2 (2176) 75.5 -> 79.8 us, and
+# Qwen3-Next T = 4 (1280) 33.3 -> 35.6 us: each workgroup routes the batch
+# (~the routing launch's own latency) before its first weight stream.
+FUSED_ROUTE_MAX_ITEMS = 512
+
+
+def _route_gate_up_ok(fmt, mode, T, E, K, router, H, I, NS, items=None) -> bool:
+    """Whether routing, segmentation and the gate/up share one launch
+    (xtu_decode_route_gate_up: the tiny router's envelope and the gate/up
+    fast path; fp32 logits / bias rows 16-byte aligned), and, for `items`
+    gate/up work items, pay there (FUSED_ROUTE_MAX_ITEMS).
+    XTU_DECODE_FUSED_ROUTE=0 keeps separate launches, =1 fuses whenever
+    the shape fits."""
+    mode_env = os.environ.get(FUSED_ROUTE_ENV, "auto")
+    if mode_env == "0":
+        return False
+    if mode_env != "1" and items is not None and items > FUSED_ROUTE_MAX_ITEMS:
+        return False
+    n_group = 1
+    if router is not None:
+        lg, bias = router.get("logits"), router.get("bias")
+        for t in (lg, bias):
+            if t is not None and not (t.is_cuda and t.dtype == torch.float32
+                                      and t.is_contiguous() and t.data_ptr() % 16 == 0):
+                return False
+        if lg is None or tuple(lg.shape) != (T, E):
+            return False
+        if mode == 0 and not router.get("renormalize", True):
+            return False
+        n_group = int(router.get("n_group", 1))
+    return bool(_lib.call("xtu_decode_route_gate_up_ok", int(fmt), int(mode), int(T), int(E),
+                          int(K), n_group, int(NS), int(H), int(I)))
+
+
 def _mxpair_bufs(tag, M, K, dev, stream=None):
     """Interleaved activation pairs [M][2K] and their e8m0 bytes [M][K/32]."""
     return (_buf(tag + "_hilo", (max(M, 1), 2 * K), torch.uint8, dev, stream),
@@ -761,14 +800,33 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     # (they need no routing), the routed gate/up leaves them out and the fused
     # down takes their rows from act_sh
     rmode = 2 if router is None else (1 if router.get("scoring", "softmax") == "sigmoid" else 0)
+    # decode of a tiny batch: routing, segmentation and the gate/up in one
+    # launch (every gate/up workgroup routes the batch for itself)
+    fused = (path == "decode" and T > 0 and seg.small
+             and _route_gate_up_ok(fmt, rmode, T, E, K, router, H, I, NS,
+                                   items=min(seg.max_tiles, TINY_MAX_PAIRS) * (I // 16)))
     split = (path == "decode" and T > 0 and NS > 0 and seg.small
              and odt in (torch.bfloat16, torch.float32)
              and decode_fused_down_use(fmt, T, seg.A, H, I, max_active, E + NS, NS * T)
-             and _route_shared_ok(fmt, rmode, T, E, K, router, H, I, NS))
+             and (fused or _route_shared_ok(fmt, rmode, T, E, K, router, H, I, NS)))
     lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
     if split:
-        r = router or {}
         act_sh = _buf("act_sh", (NS * T, I), torch.bfloat16, dev, st)
+    if fused:
+        r = router or {}
+        act = _buf("act", (max(seg.A, 1), I), torch.bfloat16, dev, st)
+        _lib.call("xtu_decode_route_gate_up", rmode, _p(r.get("logits")), _p(r.get("bias")),
+                  _p(ids), _p(wts), T, E, K, int(r.get("n_group", 1)),
+                  int(r.get("topk_group", 1)), float(r.get("routed_scaling_factor", 1.0)),
+                  int(r.get("renormalize", True)), _p(id_map), NS, int(drop_zero), seg.bm,
+                  _p(seg.sorted_pair), _p(seg.sorted_tok), _p(seg.sorted_wts), _p(seg.inv),
+                  _p(seg.seg_start), _p(seg.active), _p(seg.n_active), _p(seg.tile_expert),
+                  _p(seg.tile_row0), _p(seg.n_tiles), _p(seg.expert_tile_start), fmt, _p(x), H,
+                  I, _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0, _p(slot_map),
+                  min(seg.max_tiles, TINY_MAX_PAIRS), _p(act), _p(act_sh) if split else 0,
+                  lim, al, be, st)
+    elif split:
+        r = router or {}
         _lib.call("xtu_decode_route_shared", rmode, _p(r.get("logits")), _p(r.get("bias")),
                   _p(ids), _p(wts), T, E, K, int(r.get("n_group", 1)),
                   int(r.get("topk_group", 1)), float(r.get("routed_scaling_factor", 1.0)),
@@ -812,7 +870,9 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     if path == "decode":
         act = _buf("act", (max(A, 1), I), torch.bfloat16, dev, st)
         max_dt = decode_max_tiles(A, max_active)
-        if split:
+        if fused:
+            pass   # the routing launch ran the gate/up too
+        elif split:
             _lib.call("xtu_decode_gate_up_routed", fmt, _p(x), T, H, I, _p(W.w13), _p(W.s13),
                       _p(W.gs13), 0, 0, _p(slot_map), _p(seg.sorted_tok), _p(seg.seg_start),
                       _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.n_tiles), max_dt, NS,
