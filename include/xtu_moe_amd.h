@@ -398,6 +398,22 @@ hipError_t xtu_mx_tri_down(const uint8_t* q, const uint8_t* sq, int H, int I, co
                            const int32_t* tile_expert, const int32_t* tile_row0,
                            const int32_t* expert_tile_start, const int32_t* tile_lo,
                            const int32_t* tile_hi, int max_tiles, float* y, hipStream_t stream);
+/* xtu_mx_{pair,tri,duo}_gate_up with the activation written straight in the
+ * down pass's operand layout (mode 0 pairs as xtu_pair_quant_il writes
+ * them, 1 and 2 triples as xtu_tri_quant_il does): act_q [A][2I] and its
+ * e8m0 bytes act_sq [A][I/32], the bytes the separate quantiser would make
+ * of the bf16 rows, which are never written.  Replaces the gate/up kernel's
+ * bf16 inter rows plus the down kernel's in-loop activation handling
+ * (gpu_prefill.py:311-390). */
+hipError_t xtu_mx_gate_up_q(int mode, const uint8_t* q, const uint8_t* sq,
+                            const int32_t* sorted_tok, int H, int I, const void* w13,
+                            const uint8_t* s13p, long w_estride, long s_estride,
+                            const int32_t* slot_map, const int32_t* seg_start,
+                            const int32_t* tile_expert, const int32_t* tile_row0,
+                            const int32_t* expert_tile_start, const int32_t* tile_lo,
+                            const int32_t* tile_hi, int max_tiles, uint8_t* act_q,
+                            uint8_t* act_sq, float limit, float alpha, float beta,
+                            hipStream_t stream);
 /*   xtu_mx_duo_gate_up / _down: the same on the first two pieces of the
  *     triples only (x ~= 2^e (p1 + p2/16), |error| <= 2^(e-6) of the 32-k
  *     block, rms ~7.5e-4 of the values for N(0,1) rows): two double-rate
@@ -515,6 +531,18 @@ hipError_t xtu_f8_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const in
                                const int32_t* expert_tile_start, const int32_t* tile_lo,
                                const int32_t* tile_hi, int max_tiles, void* act, float limit,
                                float alpha, float beta, hipStream_t stream);
+/* xtu_f8_pair_gate_up with the activation written as the down pass's exact
+ * pairs (act_hilo [A][2I], act_shi [A][I/32], the bytes xtu_pair_quant_il
+ * would make of the bf16 rows, which are never written). */
+hipError_t xtu_f8_pair_gate_up_q(const uint8_t* hilo, const uint8_t* shi,
+                                 const int32_t* sorted_tok, int H, int I, const void* w13,
+                                 const float* s13, long w_estride, long s_estride,
+                                 const int32_t* slot_map, const int32_t* seg_start,
+                                 const int32_t* tile_expert, const int32_t* tile_row0,
+                                 const int32_t* expert_tile_start, const int32_t* tile_lo,
+                                 const int32_t* tile_hi, int max_tiles, uint8_t* act_hilo,
+                                 uint8_t* act_shi, float limit, float alpha, float beta,
+                                 hipStream_t stream);
 hipError_t xtu_f8_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int I, const void* w2,
                             const float* s2, long w_estride, long s_estride,
                             const int32_t* slot_map, const int32_t* seg_start,

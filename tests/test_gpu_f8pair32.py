@@ -117,3 +117,21 @@ def test_unbounded_scales_take_the_v1_kernel(bad):
     x = torch.randn((T, H), generator=torch.Generator().manual_seed(82)).to(torch.bfloat16)
     ref = oracle_layer(FMT, dense_to_numpy(FMT, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I)
     check_close(_run(x, ids, wts, W), ref, bf16_out=False, what=f"unbounded scales ({bad})")
+
+
+@pytest.mark.parametrize("T,K,skew", [(1, 2, False), (700, 4, False), (900, 2, True)])
+def test_fused_act_pairs_are_bitwise(monkeypatch, T, K, skew):
+    """The gate/up epilogue writing the down pass's pairs
+    (xtu_f8_pair_gate_up_q) gives the layer output bitwise equal to the bf16
+    rows quantised by the separate kernel."""
+    monkeypatch.setenv(L.FP8_PREFILL_ENV, "auto")
+    E, NS, H, I = 16, 1, 1024, 512
+    d, W = _layer(E, NS, H, I, seed=150 + T, spread=8)
+    assert L.fp8_pair32_use(W)
+    ids, wts = _routing(T, K, E, 151 + T, skew)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(152 + T)).to(torch.bfloat16)
+    outs = []
+    for fused in ("1", "0"):
+        monkeypatch.setenv(L.ACT_QUANT_ENV, fused)
+        outs.append(_run(x, ids, wts, W, swiglu_limit=5.0))
+    assert np.array_equal(outs[0].view(np.int32), outs[1].view(np.int32))

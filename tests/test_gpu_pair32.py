@@ -161,3 +161,30 @@ def test_slot_map_on_mutable_planes(fmt, mode):
         out = moe_forward(xd, idd, wd, slots, path="gemm", slot_map=smap, out_dtype=torch.float32)
         torch.cuda.synchronize()
         check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"slot map round {round_}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,K,skew", [(1, 2, False), (700, 4, False), (900, 2, True)])
+def test_fused_act_quant_is_bitwise(fmt, T, K, skew, mode, monkeypatch):
+    """The gate/up epilogue writing the down pass's pairs / triples
+    (xtu_mx_gate_up_q) gives the layer output bitwise equal to the bf16 rows
+    quantised by the separate kernel, over single rows, partial and
+    multi-tile experts and a shared expert."""
+    E, NS, H, I = 16, 1, 1024, 512
+    d, W = _layer(fmt, E, NS, H, I, seed=130 + T)
+    assert _on_kernel(fmt, H, I)
+    rng = np.random.default_rng(131 + T)
+    if skew:
+        ids = np.stack([np.array([rng.integers(0, 2), rng.integers(2, E)]) for _ in range(T)])
+    else:
+        ids = np.stack([rng.permutation(E)[:K] for _ in range(T)])
+    ids = torch.from_numpy(ids.astype(np.int32)).to(DEV)
+    wts = torch.from_numpy((rng.random((T, K)) + 0.05).astype(np.float32)).to(DEV)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(132 + T)).to(torch.bfloat16)
+    outs = []
+    for fused in ("1", "0"):
+        monkeypatch.setenv(L.ACT_QUANT_ENV, fused)
+        outs.append(moe_forward(x.to(DEV), ids, wts, W, path="gemm", swiglu_limit=5.0,
+                                out_dtype=torch.float32))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32)), mode

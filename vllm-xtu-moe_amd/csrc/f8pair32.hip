@@ -73,10 +73,13 @@ struct F8PairArgs {
   const int32_t* tile_lo;
   const int32_t* tile_hi;
   const int32_t* slot_map;
-  void* out;                  // gate/up: act bf16 [A][I]; down: y fp32 [A][H]
+  void* out;                  // gate/up: act bf16 [A][I] (or its pairs [A][2I], qs set);
+                              // down: y fp32 [A][H]
   int H, I;
   long w_estride, s_estride;
   float limit, alpha, beta;
+  uint8_t* qs;                // gate/up: null, or the e8m0 bytes [A][I/32] of act written
+                              // as exact pairs for the down pass
 };
 
 template <bool GU, int STAGES>
@@ -386,13 +389,33 @@ __global__ __launch_bounds__(kQThreads, 1) void f8_pair_gemm_kernel(F8PairArgs a
               acc[mb][cb][i] * sl0, acc[mb][cb + 2][i] * sl1, a.limit, a.alpha, a.beta));
       }
       __builtin_amdgcn_wave_barrier();
+      if (a.qs) {
+        // the down pass's pairs straight from the staged bf16 rows (the
+        // values the act quantiser would read back): 32 rows x 2 blocks of
+        // 32 k, one per lane
+        const int rr = lane / 2, cb = lane % 2;
+        if (rb + rr < rows) {
+          const long row = row0 + rb + rr;
+          const int blk = nb * 4 + wn * 2 + cb;
+          uint32_t hw[8], lw[8];
+          const int sa = pair_split32(stage + rr * kAP + 32 * cb, hw, lw);
+          uint8_t* d = reinterpret_cast<uint8_t*>(a.out) + row * 2L * a.I + (blk / 2) * 128 +
+                       (blk % 2) * 32;
+          *reinterpret_cast<u32x4_t*>(d) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+          *reinterpret_cast<u32x4_t*>(d + 16) = u32x4_t{hw[4], hw[5], hw[6], hw[7]};
+          *reinterpret_cast<u32x4_t*>(d + 64) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
+          *reinterpret_cast<u32x4_t*>(d + 80) = u32x4_t{lw[4], lw[5], lw[6], lw[7]};
+          a.qs[row * (a.I / 32) + blk] = (uint8_t)sa;
+        }
+      } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {   // 32 rows x 8 pieces of 8 bf16
-        const int q = 64 * j + lane, rr = q / 8, c8 = q % 8;
-        if (rb + rr < rows)
-          *reinterpret_cast<u32x4_t*>(act + (long)(row0 + rb + rr) * a.I + (long)nb * 128 +
-                                      64 * wn + 8 * c8) =
-              *reinterpret_cast<const u32x4_t*>(stage + rr * kAP + 8 * c8);
+        for (int j = 0; j < 4; ++j) {   // 32 rows x 8 pieces of 8 bf16
+          const int q = 64 * j + lane, rr = q / 8, c8 = q % 8;
+          if (rb + rr < rows)
+            *reinterpret_cast<u32x4_t*>(act + (long)(row0 + rb + rr) * a.I + (long)nb * 128 +
+                                        64 * wn + 8 * c8) =
+                *reinterpret_cast<const u32x4_t*>(stage + rr * kAP + 8 * c8);
+        }
       }
       __builtin_amdgcn_wave_barrier();
     }
@@ -478,7 +501,29 @@ hipError_t xtu_f8_pair_gate_up(const uint8_t* hilo, const uint8_t* shi, const in
   (void)hipGetLastError();
   F8PairArgs a{hilo, shi, sorted_tok, (const uint8_t*)w13, s13, seg_start, tile_expert, tile_row0,
                expert_tile_start, tile_lo, tile_hi, slot_map, act, H, I, w_estride, s_estride,
-               limit, alpha, beta};
+               limit, alpha, beta, nullptr};
+  return f8_launch(true, a, max_tiles, stream);
+}
+
+hipError_t xtu_f8_pair_gate_up_q(const uint8_t* hilo, const uint8_t* shi,
+                                 const int32_t* sorted_tok, int H, int I, const void* w13,
+                                 const float* s13, long w_estride, long s_estride,
+                                 const int32_t* slot_map, const int32_t* seg_start,
+                                 const int32_t* tile_expert, const int32_t* tile_row0,
+                                 const int32_t* expert_tile_start, const int32_t* tile_lo,
+                                 const int32_t* tile_hi, int max_tiles, uint8_t* act_hilo,
+                                 uint8_t* act_shi, float limit, float alpha, float beta,
+                                 hipStream_t stream) {
+  XTU_CHECK_ARG(f8_fits(H, I));
+  XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
+  XTU_CHECK_ARG(2L * I * H < (1L << 32));
+  XTU_CHECK_ARG(hilo && shi && sorted_tok && w13 && s13 && seg_start && tile_expert &&
+                tile_row0 && expert_tile_start && tile_lo && tile_hi && act_hilo && act_shi);
+  if (max_tiles == 0) return hipSuccess;
+  (void)hipGetLastError();
+  F8PairArgs a{hilo, shi, sorted_tok, (const uint8_t*)w13, s13, seg_start, tile_expert, tile_row0,
+               expert_tile_start, tile_lo, tile_hi, slot_map, act_hilo, H, I, w_estride,
+               s_estride, limit, alpha, beta, act_shi};
   return f8_launch(true, a, max_tiles, stream);
 }
 
@@ -497,7 +542,7 @@ hipError_t xtu_f8_pair_down(const uint8_t* hilo, const uint8_t* shi, int H, int 
   (void)hipGetLastError();
   F8PairArgs a{hilo, shi, nullptr, (const uint8_t*)w2, s2, seg_start, tile_expert, tile_row0,
                expert_tile_start, tile_lo, tile_hi, slot_map, y, H, I, w_estride, s_estride,
-               0.f, 1.f, 0.f};
+               0.f, 1.f, 0.f, nullptr};
   return f8_launch(false, a, max_tiles, stream);
 }
 

@@ -86,10 +86,13 @@ struct MxPairArgs {
   const int32_t* tile_lo;
   const int32_t* tile_hi;
   const int32_t* slot_map;
-  void* out;                  // gate/up: act bf16 [A][I]; down: y fp32 [A][H]
+  void* out;                  // gate/up: act bf16 [A][I] (or its pairs / triples [A][2I],
+                              // qs set); down: y fp32 [A][H]
   int H, I;
   long w_estride, s_estride;
   float limit, alpha, beta;
+  uint8_t* qs;                // gate/up: null, or the e8m0 bytes [A][I/32] of act written
+                              // quantised for the down pass (pairs in kPair, else triples)
 };
 
 // ---------------------------------------------------------------------------
@@ -472,13 +475,48 @@ __global__ __launch_bounds__(kPThreads, 1) void mx_pair_gemm_kernel(MxPairArgs a
               silu_gate(acc[mb][cb][i], acc[mb][cb + 4][i], a.limit, a.alpha, a.beta));
       }
       __builtin_amdgcn_wave_barrier();
+      if (a.qs) {
+        // the down pass's operand straight from the staged bf16 rows (the
+        // values the act quantiser would read back): 32 rows x 4 blocks of
+        // 32 k, two per lane, in the pair / triple row layout
+        uint8_t* qo = reinterpret_cast<uint8_t*>(a.out);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {   // 32 rows x 16 pieces of 8 bf16
-        const int q = 64 * j + lane, rr = q / 16, c8 = q % 16;
-        if (rb + rr < rows)
-          *reinterpret_cast<u32x4_t*>(act + (long)(row0 + rb + rr) * a.I + (long)nb * 256 +
-                                      128 * wn + 8 * c8) =
-              *reinterpret_cast<const u32x4_t*>(stage + rr * kAP + 8 * c8);
+        for (int j = 0; j < 2; ++j) {
+          const int u = 64 * j + lane, rr = u / 4, cb = u % 4;
+          if (rb + rr < rows) {
+            const long row = row0 + rb + rr;
+            const int blk = nb * 8 + wn * 4 + cb;
+            const uint16_t* src = stage + rr * kAP + 32 * cb;
+            if constexpr (MODE == kPair) {
+              uint32_t hw[8], lw[8];
+              const int sa = pair_split32(src, hw, lw);
+              uint8_t* d = qo + row * 2L * a.I + (blk / 2) * 128 + (blk % 2) * 32;
+              *reinterpret_cast<u32x4_t*>(d) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+              *reinterpret_cast<u32x4_t*>(d + 16) = u32x4_t{hw[4], hw[5], hw[6], hw[7]};
+              *reinterpret_cast<u32x4_t*>(d + 64) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
+              *reinterpret_cast<u32x4_t*>(d + 80) = u32x4_t{lw[4], lw[5], lw[6], lw[7]};
+              a.qs[row * (a.I / 32) + blk] = (uint8_t)sa;
+            } else {
+              uint32_t p1[6], p2[6], p3[4];
+              const int sc = tri_split32(src, p1, p2, p3);
+              uint8_t* d = qo + row * 2L * a.I + (blk / 2) * 128 + (blk % 2) * 64;
+              *reinterpret_cast<u32x4_t*>(d) = u32x4_t{p1[0], p1[1], p1[2], p1[3]};
+              *reinterpret_cast<u32x4_t*>(d + 16) = u32x4_t{p1[4], p1[5], p2[0], p2[1]};
+              *reinterpret_cast<u32x4_t*>(d + 32) = u32x4_t{p2[2], p2[3], p2[4], p2[5]};
+              *reinterpret_cast<u32x4_t*>(d + 48) = u32x4_t{p3[0], p3[1], p3[2], p3[3]};
+              a.qs[row * (a.I / 32) + blk] = (uint8_t)sc;
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {   // 32 rows x 16 pieces of 8 bf16
+          const int q = 64 * j + lane, rr = q / 16, c8 = q % 16;
+          if (rb + rr < rows)
+            *reinterpret_cast<u32x4_t*>(act + (long)(row0 + rb + rr) * a.I + (long)nb * 256 +
+                                        128 * wn + 8 * c8) =
+                *reinterpret_cast<const u32x4_t*>(stage + rr * kAP + 8 * c8);
+        }
       }
       __builtin_amdgcn_wave_barrier();
     }
@@ -579,7 +617,8 @@ static hipError_t gate_up(int mode, const uint8_t* hilo, const uint8_t* shi,
                           const int32_t* tile_expert, const int32_t* tile_row0,
                           const int32_t* expert_tile_start, const int32_t* tile_lo,
                           const int32_t* tile_hi, int max_tiles, void* act, float limit,
-                          float alpha, float beta, hipStream_t stream) {
+                          float alpha, float beta, hipStream_t stream,
+                          uint8_t* act_scales = nullptr) {
   XTU_CHECK_ARG(mx_fits(H, I));
   XTU_CHECK_ARG(max_tiles >= 0 && max_tiles < (1 << 30) && w_estride >= 0 && s_estride >= 0);
   XTU_CHECK_ARG(w_estride < (1L << 31) && 2L * I * H < (1L << 32));
@@ -589,7 +628,7 @@ static hipError_t gate_up(int mode, const uint8_t* hilo, const uint8_t* shi,
   (void)hipGetLastError();
   const MxPairArgs a{hilo, shi, sorted_tok, (const uint8_t*)w13, s13p, seg_start, tile_expert,
                      tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, act, H, I,
-                     w_estride, s_estride, limit, alpha, beta};
+                     w_estride, s_estride, limit, alpha, beta, act_scales};
   return launch(true, mode, a, max_tiles, stream);
 }
 
@@ -608,7 +647,7 @@ static hipError_t down(int mode, const uint8_t* hilo, const uint8_t* shi, int H,
   (void)hipGetLastError();
   const MxPairArgs a{hilo, shi, nullptr, (const uint8_t*)w2, s2p, seg_start, tile_expert,
                      tile_row0, expert_tile_start, tile_lo, tile_hi, slot_map, y, H, I,
-                     w_estride, s_estride, 0.f, 1.f, 0.f};
+                     w_estride, s_estride, 0.f, 1.f, 0.f, nullptr};
   return launch(false, mode, a, max_tiles, stream);
 }
 
@@ -679,6 +718,22 @@ hipError_t xtu_mx_duo_gate_up(const uint8_t* q, const uint8_t* sq, const int32_t
   return gate_up(kDuo, q, sq, sorted_tok, H, I, w13, s13p, w_estride, s_estride, slot_map,
                  seg_start, tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi,
                  max_tiles, act, limit, alpha, beta, stream);
+}
+
+hipError_t xtu_mx_gate_up_q(int mode, const uint8_t* q, const uint8_t* sq,
+                            const int32_t* sorted_tok, int H, int I, const void* w13,
+                            const uint8_t* s13p, long w_estride, long s_estride,
+                            const int32_t* slot_map, const int32_t* seg_start,
+                            const int32_t* tile_expert, const int32_t* tile_row0,
+                            const int32_t* expert_tile_start, const int32_t* tile_lo,
+                            const int32_t* tile_hi, int max_tiles, uint8_t* act_q,
+                            uint8_t* act_sq, float limit, float alpha, float beta,
+                            hipStream_t stream) {
+  XTU_CHECK_ARG(mode == kPair || mode == kTri || mode == kDuo);
+  XTU_CHECK_ARG(act_q && act_sq);
+  return gate_up(mode, q, sq, sorted_tok, H, I, w13, s13p, w_estride, s_estride, slot_map,
+                 seg_start, tile_expert, tile_row0, expert_tile_start, tile_lo, tile_hi,
+                 max_tiles, act_q, limit, alpha, beta, stream, act_sq);
 }
 
 hipError_t xtu_mx_duo_down(const uint8_t* q, const uint8_t* sq, int H, int I, const void* w2,

@@ -70,6 +70,10 @@ SIGNATURES = {
                                 _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
     "xtu_mx_tri_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp, _vp,
                              _vp, _i, _vp, _vp]),
+    "xtu_mx_gate_up_q": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
+                              _vp, _vp, _vp, _i, _vp, _vp, _f, _f, _f, _vp]),
+    "xtu_f8_pair_gate_up_q": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
+                                   _vp, _vp, _vp, _i, _vp, _vp, _f, _f, _f, _vp]),
     "xtu_mx_duo_gate_up": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
                                 _vp, _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
     "xtu_mx_duo_down": (_i, [_vp, _vp, _i, _i, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp, _vp, _vp,

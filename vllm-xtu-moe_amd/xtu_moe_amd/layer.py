@@ -904,6 +904,18 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     return (out, seg) if return_seg else out
 
 
+ACT_QUANT_ENV = "XTU_ACT_QUANT_FUSED"
+_MX_MODE_IDS = {"pair": 0, "tri": 1, "duo": 2}   # xtu_mx_gate_up_q's mode
+
+
+def act_quant_fused() -> bool:
+    """Whether the MXFP4 / FP8 32x32x64 gate/up epilogues write the down
+    pass's activation pairs / triples themselves (the same bytes as the
+    separate quantiser over the bf16 rows, without the rows' round trip);
+    XTU_ACT_QUANT_FUSED=0 writes bf16 rows and quantises them apart."""
+    return os.environ.get(ACT_QUANT_ENV, "1") != "0"
+
+
 def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None, int8=False,
                 swiglu_limit=0.0, swiglu_alpha=1.0, swiglu_beta=0.0, stream=None,
                 fp8_scales_ok=None):
@@ -961,11 +973,17 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
         xq = _mxpair_bufs("xm", T, H, dev, st)
         aq = _mxpair_bufs("am", A, I, dev, st)
         _lib.call("xtu_pair_quant_il", _p(x), T, H, *[_p(t) for t in xq], st)
-        _lib.call("xtu_f8_pair_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
-                  _p(W.w13), _p(W.s13), 0, 0, _p(slot_map), _p(seg.seg_start),
-                  _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi,
-                  seg.max_tiles, _p(act), lim, al, be, st)
-        _lib.call("xtu_pair_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
+        if act_quant_fused():   # the gate/up epilogue writes the down pass's pairs
+            _lib.call("xtu_f8_pair_gate_up_q", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
+                      _p(W.w13), _p(W.s13), 0, 0, _p(slot_map), _p(seg.seg_start),
+                      _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo,
+                      hi, seg.max_tiles, *[_p(t) for t in aq], lim, al, be, st)
+        else:
+            _lib.call("xtu_f8_pair_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
+                      _p(W.w13), _p(W.s13), 0, 0, _p(slot_map), _p(seg.seg_start),
+                      _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo,
+                      hi, seg.max_tiles, _p(act), lim, al, be, st)
+            _lib.call("xtu_pair_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
         _lib.call("xtu_f8_pair_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(W.s2), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
                   _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
@@ -979,11 +997,18 @@ def expert_pass(x, seg, W: ExpertWeights, b0: int, b1: int, y, *, slot_map=None,
         xq = _mxpair_bufs("xm", T, H, dev, st)
         aq = _mxpair_bufs("am", A, I, dev, st)
         _lib.call(f"xtu_{qk}_quant_il", _p(x), T, H, *[_p(t) for t in xq], st)
-        _lib.call(f"xtu_mx_{kind}_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
-                  _p(W.w13), _p(s13p), 0, 0, _p(slot_map), _p(seg.seg_start),
-                  _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo, hi,
-                  seg.max_tiles, _p(act), lim, al, be, st)
-        _lib.call(f"xtu_{qk}_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
+        if act_quant_fused():   # the gate/up epilogue writes the down pass's pieces
+            _lib.call("xtu_mx_gate_up_q", _MX_MODE_IDS[kind], *[_p(t) for t in xq],
+                      _p(seg.sorted_tok), H, I, _p(W.w13), _p(s13p), 0, 0, _p(slot_map),
+                      _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
+                      _p(seg.expert_tile_start), lo, hi, seg.max_tiles, *[_p(t) for t in aq],
+                      lim, al, be, st)
+        else:
+            _lib.call(f"xtu_mx_{kind}_gate_up", *[_p(t) for t in xq], _p(seg.sorted_tok), H, I,
+                      _p(W.w13), _p(s13p), 0, 0, _p(slot_map), _p(seg.seg_start),
+                      _p(seg.tile_expert), _p(seg.tile_row0), _p(seg.expert_tile_start), lo,
+                      hi, seg.max_tiles, _p(act), lim, al, be, st)
+            _lib.call(f"xtu_{qk}_quant_il", _p(act), A, I, *[_p(t) for t in aq], st)
         _lib.call(f"xtu_mx_{kind}_down", *[_p(t) for t in aq], H, I, _p(W.w2), _p(s2p), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
                   _p(seg.expert_tile_start), lo, hi, seg.max_tiles, _p(y), st)
