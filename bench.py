@@ -3,9 +3,13 @@
 Default run (ds-v3-mxfp4): DeepSeek-V3-shaped MoE layer at decode with MXFP4
 experts (H=7168, 256 routed experts + 1 shared, I=2048, grouped-sigmoid
 routing with 8 groups / top-4 groups / top-8 and routed scaling 2.5), T = 1,
-2, 4 tokens, then the same layer at prefill T = 8192 with MXFP4 and with FP8
-(128x128 block-scaled) experts, PREFILL_STEPS timed steps each, reported
-under config.prefill with their own MFMA roofline.
+2, 4 tokens (the headline line), then every other configuration of SUITE
+(the same layer at prefill T = 8192 with MXFP4 and with FP8 (128x128
+block-scaled) experts, PREFILL_STEPS timed steps each; the Qwen3-Next layer
+with MXFP4 / INT8 ALIGN and with NVFP4 experts; the tiny Mixtral layer; the
+streamed FP8 layer), each as its own line with its own roofline and CPU
+baseline under config.configs, the two DS-V3 prefill layers also under
+config.prefill.
 A step is one pass of the layer (routing from logits -> segmentation ->
 gate/up+SwiGLU -> down -> combine) over a fresh batch of synthetic tokens
 (x ~ N(0,1) bf16, logits ~ N(0,1)), weights N(0,0.02) quantised and resident in
