@@ -29,7 +29,7 @@ The JSON line reports tokens/s at the largest T (value), the layer time, and:
                 from the reference sources) on the host cores, on a bounded
                 sample of the same workload.
 Single workloads (--workload): ds-v3-mxfp4-decode, ds-v3-mxfp4-prefill,
-ds-v3-fp8-prefill, qwen3-next-int8,
+ds-v3-fp8-prefill, qwen3-next-int8, qwen3-next-mxfp4 (INT8 ALIGN off),
 qwen3-next-nvfp4, mixtral-tiny-bf16, and ds-v3-fp8-streamed: the FP8 layer at
 T = 8192 with Zipf(1.1)-skewed router logits, the 64 most-routed experts (and
 the shared one) resident in a pool, every other routed expert streamed from
@@ -66,6 +66,9 @@ WORKLOADS = {
                             Ts=[1, 4, 8192], limit=7.0, int8=True, graph=True),
     "qwen3-next-nvfp4": dict(fmt="nvfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
                              Ts=[1, 4, 8192], limit=7.0, int8=False, graph=True),
+    # the same MXFP4 layer with INT8 ALIGN off (the default): triples at T = 8192
+    "qwen3-next-mxfp4": dict(fmt="mxfp4", E=512, NS=1, H=2048, I=512, K=10, router="softmax",
+                             Ts=[8192], limit=7.0, int8=False, graph=False),
     "mixtral-tiny-bf16": dict(fmt="bf16", E=8, NS=0, H=1024, I=2048, K=2, router="softmax",
                               Ts=[128], limit=0.0, int8=False, graph=True, graph_max_T=128,
                               bound="hbm"),
