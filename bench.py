@@ -81,7 +81,7 @@ DEFAULT_SET = "ds-v3-mxfp4"   # decode T=1,2,4 plus every configuration below
 PREFILL_SET = ("ds-v3-mxfp4-prefill", "ds-v3-fp8-prefill")
 # the default run's sub-lines: each workload's own line (roofline, cpu_baseline)
 # under config.configs, keyed by workload, with the configuration it measures
-SUITE = (("ds-v3-mxfp4-prefill", "north star: DS-V3 MXFP4 prefill T=8192"),
+SUITE = (("ds-v3-mxfp4-prefill", "DS-V3 MXFP4 prefill T=8192"),
          ("ds-v3-fp8-prefill", "C3: DS-V3 FP8 prefill T=8192"),
          ("qwen3-next-int8", "C4: Qwen3-Next MXFP4, decode T=1,4 and INT8 ALIGN T=8192"),
          ("qwen3-next-nvfp4", "C4: Qwen3-Next NVFP4 T=1,4,8192"),

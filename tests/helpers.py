@@ -10,7 +10,7 @@ import torch
 import oracle
 from xtu_moe_amd import formats as F
 
-# bf16 layer outputs vs the dequantized-fp32 oracle
+# bf16 layer outputs vs the dequantized-fp32 oracle (the parity bar)
 MAX_ABS = 2e-2
 REL_L2 = 5e-3
 
