@@ -485,23 +485,29 @@ __global__ __launch_bounds__(512) void decode_route_gate_up_kernel(tiny::SmallAr
   const int u0 = ks * nunits / ksplit, u1 = (ks + 1) * nunits / ksplit;
   const int q = lane / 16, m = lane % 16;
   const int nchunks = a.T * (a.H / 8);
-  // The batch's rows go to LDS first, all pieces in flight at once; their
-  // registers are then free for the weight stream (and the routing).  They
-  // are read only after a barrier.
-  {
-    u32x4_t xv[XC];
+  // The batch's rows, all pieces in flight at once.  A shared-expert
+  // workgroup stores them to LDS before its weight stream (their registers
+  // are then free for it); a routed one keeps up to two pieces per thread in
+  // flight during the routing and stores them after it (more, or NVFP4's
+  // wider dequantisation beside them, would cost a wave per SIMD).  They are
+  // read only after a barrier.
+  constexpr bool kLateX = XC <= 2 && FMT != kNVFP4;
+  u32x4_t xv[XC];
 #pragma unroll
-    for (int j = 0; j < XC; ++j) {
-      const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
-      xv[j] = *reinterpret_cast<const u32x4_t*>(a.x + (long)cc * 8);
-    }
+  for (int j = 0; j < XC; ++j) {
+    const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
+    xv[j] = *reinterpret_cast<const u32x4_t*>(a.x + (long)cc * 8);
+  }
+  auto stage_x = [&]() {
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
       const int cc = threadIdx.x + j * blockDim.x;
       if (cc < nchunks) *reinterpret_cast<u32x4_t*>(xs + cc * 8) = xv[j];
     }
-  }
+  };
+  if constexpr (!kLateX) stage_x();
   if ((int)blockIdx.x < n_sh) {
+    if constexpr (kLateX) stage_x();
     // a shared expert: all T rows of the batch, in token order, no routing
     const int sh = blockIdx.x / npan, sub = blockIdx.x - sh * npan;
     const int e = ra.E + sh;
@@ -524,6 +530,7 @@ __global__ __launch_bounds__(512) void decode_route_gate_up_kernel(tiny::SmallAr
   else tiny::route_segment_block<MODE, EPL, false>(ra, g);
   const int items = (g.act_t[g.n_act] - skip) * npan;
   if (first >= items) return;   // whole workgroup
+  if constexpr (kLateX) stage_x();
   // The next item's weights are issued before this item's epilogue, whose
   // row stores would otherwise sit in front of them in the wave's in-order
   // memory counter.
@@ -539,6 +546,7 @@ __global__ __launch_bounds__(512) void decode_route_gate_up_kernel(tiny::SmallAr
   Round<FMT, NU> r;
   int item = first, ws = 0;
   issue(r, item, ws);
+  __syncthreads();   // the staged rows
   while (true) {
     const int slot = item / npan, sub = item - slot * npan;
     const int r0 = g.tile_r[slot], na = g.tile_n[slot];
