@@ -389,3 +389,37 @@ def test_fused_route_every_pair_invalid(monkeypatch):
         ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x.cpu()),
                            ids.cpu().numpy(), wts.cpu().numpy(), E, NS, H, I)
         check_close(a[0].cpu().numpy(), ref, bf16_out=False, what="all invalid vs oracle")
+
+
+def test_fused_route_rejects_a_short_tile_grid():
+    """xtu_decode_route_gate_up refuses a max_tiles below the batch's tile
+    bound (a tile left without a work item would leave act rows unwritten),
+    and an act_shared without shared experts, before launching anything."""
+    from xtu_moe_amd import _lib
+    from xtu_moe_amd.layer import _p, _stream
+    fmt, E, NS, H, I, T, K = F.FMT_MXFP4, 16, 1, 512, 256, 2, 4
+    _, W = _layer(fmt, E, NS, H, I, seed=197)
+    dev = torch.device("cuda")
+    seg = L.segmentation(T, K, E, NS, L.DECODE_TILE, dev)
+    ids = torch.zeros((T, K), dtype=torch.int32, device=dev)
+    wts = torch.ones((T, K), dtype=torch.float32, device=dev)
+    x = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+    act = torch.empty((seg.A, I), dtype=torch.bfloat16, device=dev)
+    act_sh = torch.empty((NS * T, I), dtype=torch.bfloat16, device=dev)
+
+    def call(max_tiles, ns=NS, sh=act_sh):
+        return _lib.load().xtu_decode_route_gate_up(
+            2, None, None, _p(ids), _p(wts), T, E, K, 1, 1, 1.0, 1, None, ns, 1, seg.bm,
+            _p(seg.sorted_pair), _p(seg.sorted_tok), _p(seg.sorted_wts), _p(seg.inv),
+            _p(seg.seg_start), _p(seg.active), _p(seg.n_active), _p(seg.tile_expert),
+            _p(seg.tile_row0), _p(seg.n_tiles), _p(seg.expert_tile_start), fmt, _p(x), H, I,
+            _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0, None, max_tiles, _p(act),
+            _p(sh) if sh is not None else None, 0.0, 1.0, 0.0, _stream())
+
+    # T (K + NS) = 10 pairs in at most min(E, 8) + 1 = 9 buckets: at least 9 tiles
+    assert call(8) == 1                     # hipErrorInvalidValue
+    assert call(0) == 1
+    assert call(65) == 1
+    assert call(9, ns=0) == 1               # act_shared with no shared experts
+    assert call(9) == 0
+    torch.cuda.synchronize()
