@@ -1136,6 +1136,9 @@ hipError_t launch_route_gate_up(int mode, int epl, const tiny::SmallArgs& ra, De
   if (!a.s_estride) a.s_estride = F::s_bytes(2L * a.I, a.H);
   int ksplit = 0, xc = 0;
   if (!gate_up_fast_shape<FMT>(a.T, a.H, ksplit, xc)) return hipErrorInvalidValue;
+  // a routing wave per token where the workgroup can have one (at most 8
+  // waves): the K range is split further, the routing not serialised
+  while (ksplit < 4 && 2 * ksplit < a.T) ksplit *= 2;
   a.ksplit = ksplit;
   a.rows = a.T;
   const int bd = 128 * ksplit;

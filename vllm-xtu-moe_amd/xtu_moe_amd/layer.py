@@ -691,26 +691,33 @@ def _route_shared_ok(fmt, mode, T, E, K, router, H, I, NS) -> bool:
 
 
 FUSED_ROUTE_ENV = "XTU_DECODE_FUSED_ROUTE"
-# gate/up work items (tiles x I/16 panels) up to which the one-launch routing
-# + gate/up pays: about one resident round of its workgroups.  Measured on
-# MI355X: Qwen3-Next MXFP4 T = 1 (352 items) 27.2 -> 24.9 us per layer;
-# DeepSeek-V3 T = 1 (1152) unchanged, T = 2 (2176) 75.5 -> 79.8 us, and
-# Qwen3-Next T = 4 (1280) 33.3 -> 35.6 us: each workgroup routes the batch
-# (~the routing launch's own latency) before its first weight stream.
-FUSED_ROUTE_MAX_ITEMS = 512
+# gate/up weight bytes (the batch's tile bound x one expert's w13 + scales)
+# up to which the one-launch routing + gate/up pays: there the layer is
+# latency, and the routing each workgroup does beside its first weight
+# stream costs less than the routing launch and its boundary.  Measured on
+# MI355X: Qwen3-Next MXFP4 T = 1 (12 MB) 27.2 -> 24.7 us per layer, T = 4
+# (48 MB) 33.1 vs 33.4; NVFP4 T = 1 29.1 -> 27.2, T = 4 40.6 -> 37.4;
+# DeepSeek-V3 MXFP4 T = 1 (140 MB) 49.2 vs 49.1, T = 2 (265 MB) 75.5 -> 79.8,
+# T = 4 (515 MB) 130.3 -> 131.6.
+FUSED_ROUTE_MAX_BYTES = 64 << 20
 
 
-def _route_gate_up_ok(fmt, mode, T, E, K, router, H, I, NS, items=None) -> bool:
+def _w13_bytes(W) -> int:
+    """One expert's gate/up weight and scale bytes in W's planes."""
+    return sum(int(t[0].numel()) * t.element_size() for t in (W.w13, W.s13) if t is not None)
+
+
+def _route_gate_up_ok(fmt, mode, T, E, K, router, H, I, NS, gu_bytes=None) -> bool:
     """Whether routing, segmentation and the gate/up share one launch
     (xtu_decode_route_gate_up: the tiny router's envelope and the gate/up
-    fast path; fp32 logits / bias rows 16-byte aligned), and, for `items`
-    gate/up work items, pay there (FUSED_ROUTE_MAX_ITEMS).
-    XTU_DECODE_FUSED_ROUTE=0 keeps separate launches, =1 fuses whenever
-    the shape fits."""
+    fast path; fp32 logits / bias rows 16-byte aligned), and, for gu_bytes
+    of gate/up weights to stream, pay there (FUSED_ROUTE_MAX_BYTES).
+    XTU_DECODE_FUSED_ROUTE=0 keeps separate launches, =1 fuses whenever the
+    shape fits."""
     mode_env = os.environ.get(FUSED_ROUTE_ENV, "auto")
     if mode_env == "0":
         return False
-    if mode_env != "1" and items is not None and items > FUSED_ROUTE_MAX_ITEMS:
+    if mode_env != "1" and gu_bytes is not None and gu_bytes > FUSED_ROUTE_MAX_BYTES:
         return False
     n_group = 1
     if router is not None:
@@ -804,7 +811,7 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     # launch (every gate/up workgroup routes the batch for itself)
     fused = (path == "decode" and T > 0 and seg.small
              and _route_gate_up_ok(fmt, rmode, T, E, K, router, H, I, NS,
-                                   items=min(seg.max_tiles, TINY_MAX_PAIRS) * (I // 16)))
+                                   gu_bytes=min(seg.max_tiles, TINY_MAX_PAIRS) * _w13_bytes(W)))
     split = (path == "decode" and T > 0 and NS > 0 and seg.small
              and odt in (torch.bfloat16, torch.float32)
              and decode_fused_down_use(fmt, T, seg.A, H, I, max_active, E + NS, NS * T)
