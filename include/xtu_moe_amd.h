@@ -220,6 +220,39 @@ hipError_t xtu_decode_route_gate_up(
     int max_tiles, void* act, void* act_shared, float limit, float alpha, float beta,
     hipStream_t stream);
 
+/* A whole decode layer in one launch: xtu_decode_route_gate_up's routing,
+ * segmentation and gate/up (same arguments, same outputs), then, after a
+ * barrier across the launch's workgroups, xtu_decode_down_combine's down
+ * projection with the weighted combine (w2 / s2 / gs2 as there, W2 strides
+ * w2_estride / s2_estride, out bf16 or fp32 [T][H] written whole, the same
+ * per-token summation order).  The launch is one resident round of
+ * workgroups (sized by the occupancy query) so the barrier completes;
+ * barrier: xtu_decode_layer_barrier_words() words of device memory, zero
+ * before the first call; every call leaves its counters zero (the last
+ * 64-word line's first word becomes 1 if a wait ever ran out, about 0.1 s,
+ * instead of hanging).  Calls that overlap on one device must not share
+ * the barrier words.  Replaces, for decode, the router call,
+ * _build_segmentation (gpu_prefill.py:849-887), moe4_smallm_gu2 and
+ * moe4_smallm_dn2 (moe4_smallm.cu:260-333, 395-430) -- one launch instead
+ * of four.  xtu_decode_layer_ok: xtu_decode_route_gate_up_ok and the down's
+ * shape (I / 128 = 2 x the K split of the gate/up workgroup's waves over
+ * one or more panels, the act rows within 96 KiB of LDS). */
+int xtu_decode_layer_barrier_words(void);
+int xtu_decode_layer_ok(int fmt, int mode, int T, int E, int K, int n_group, int n_shared,
+                        int H, int I);
+hipError_t xtu_decode_layer(
+    int mode, const float* logits, const float* bias, int32_t* topk_ids, float* topk_weights,
+    int T, int E, int K, int n_group, int topk_group, float routed_scaling, int renormalize,
+    const int32_t* id_map, int n_shared, int drop_zero, int bm, int32_t* sorted_pair,
+    int32_t* sorted_tok, float* sorted_wts, int32_t* inv, int32_t* seg_start, int32_t* active,
+    int32_t* n_active, int32_t* tile_expert, int32_t* tile_row0, int32_t* n_tiles,
+    int32_t* expert_tile_start, int fmt, const void* x, int H, int I, const void* w13,
+    const void* s13, const float* gs13, long w13_estride, long s13_estride,
+    const int32_t* slot_map, int max_tiles, void* act, void* act_shared, float limit,
+    float alpha, float beta, const void* w2, const void* s2, const float* gs2,
+    long w2_estride, long s2_estride, void* out, int out_bf16, uint32_t* barrier,
+    hipStream_t stream);
+
 /* Down projection with the weighted combine fused: out[t] = sum over t's live
  * pairs (t, e) of w * (act_row W2_e^T), bf16 (out_bf16 = 1) or fp32 [T][H],
  * every row written.  Replaces moe4_smallm_dn2 (moe4_smallm.cu:260-333,

@@ -47,9 +47,11 @@ def test_fused_vs_oracle_and_unfused(fmt, T, H, I, monkeypatch):
     ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I)
     check_close(fused.cpu().numpy(), ref, bf16_out=False, what=f"fused fmt={fmt} T={T}")
     check_close(split.cpu().numpy(), ref, bf16_out=False, what=f"split fmt={fmt} T={T}")
-    # same products, summed in another order: a few fp32 ulps of the row scale
+    # same products, summed in another order (the fused down, in its own
+    # launch or after the one-launch layer's barrier, splits K differently):
+    # fp32 rounding, within 1e-4 of the output's scale
     scale = float(np.abs(ref).max()) + 1e-6
-    assert float((fused - split).abs().max()) <= 1e-5 * scale
+    assert float((fused - split).abs().max()) <= 1e-4 * scale
 
 
 @pytest.mark.parametrize("drop_zero", [True, False])
@@ -69,7 +71,7 @@ def test_fused_duplicates_zero_weights_invalid_ids(drop_zero, monkeypatch):
     ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids, wts, E, NS, H, I)
     check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"dup/zero drop_zero={drop_zero}")
     scale = float(np.abs(ref).max()) + 1e-6
-    assert float((out - split).abs().max()) <= 1e-5 * scale
+    assert float((out - split).abs().max()) <= 1e-4 * scale
 
 
 def test_fused_every_pair_dropped_writes_zero_rows(monkeypatch):
@@ -296,8 +298,9 @@ def test_shared_split_misaligned_logits_fall_back(monkeypatch):
 # ---------------------------------------------------------------------------
 # routing, segmentation and gate/up in one launch (xtu_decode_route_gate_up)
 
-def _fr_run(monkeypatch, fused_route, split, x, W, K, **kw):
+def _fr_run(monkeypatch, fused_route, split, x, W, K, one=False, **kw):
     monkeypatch.setenv(L.FUSED_ROUTE_ENV, "1" if fused_route else "0")
+    monkeypatch.setenv(L.ONE_LAUNCH_ENV, "1" if one else "0")
     return _split_run(monkeypatch, split, x, W, K, **kw)
 
 
@@ -423,3 +426,197 @@ def test_fused_route_rejects_a_short_tile_grid():
     assert call(9, ns=0) == 1               # act_shared with no shared experts
     assert call(9) == 0
     torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------------------
+# the whole decode layer in one launch (xtu_decode_layer): routing, gate/up,
+# a barrier across the launch's workgroups, the down with the combine
+
+def _barrier_clean():
+    """Every counter back at zero, no wait ran out (the generations move)."""
+    for t in L._BAR_CACHE.values():
+        w = t.cpu().view(-1, 64)[:, 0].tolist()
+        assert w[:9] == [0] * 9 and w[17] == 0, f"barrier words {w}"
+
+
+def _near(a, b, what):
+    """Routing and segmentation bitwise; the output the same products summed
+    over another K split of the down (fp32 rounding: within 1e-4 of the
+    output's scale, far inside the oracle bar each side is checked against)."""
+    oa, ia, wa, sa = a
+    ob, ib, wb, sb = b
+    assert torch.equal(ia, ib), f"{what}: ids"
+    assert torch.equal(wa.view(torch.int32), wb.view(torch.int32)), f"{what}: weights"
+    for f in _SEG_FIELDS:
+        ta, tb = sa[f], sb[f]
+        if ta.dtype == torch.float32:
+            ta, tb = ta.view(torch.int32), tb.view(torch.int32)
+        assert torch.equal(ta, tb), f"{what}: {f}"
+    scale = float(ob.abs().max()) + 1e-6
+    assert float((oa - ob).abs().max()) <= 1e-4 * scale, f"{what}: output"
+
+
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("fmt,T,H,I", [(F.FMT_MXFP4, 1, 512, 256), (F.FMT_MXFP4, 4, 4096, 256),
+                                       (F.FMT_NVFP4, 2, 2048, 512), (F.FMT_FP8, 3, 1024, 256),
+                                       (F.FMT_BF16, 2, 512, 512)])
+def test_one_launch_layer_grouped_sigmoid(fmt, T, H, I, split, monkeypatch):
+    E, NS, K = 256, 1, 8
+    d, W = _layer(fmt, E, NS, H, I, seed=210 + T + H)
+    g = torch.Generator(device="cuda").manual_seed(211 + T)
+    logits = torch.randn((T, E), generator=g, device="cuda")
+    bias = torch.randn((E,), generator=g, device="cuda") * 0.1
+    x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    router = dict(logits=logits, scoring="sigmoid", bias=bias, n_group=8, topk_group=4,
+                  routed_scaling_factor=2.5, renormalize=True)
+    assert L._layer_ok(fmt, 1, T, E, K, router, H, I, NS)
+    a = _fr_run(monkeypatch, True, split, x, W, K, one=True, router=router)
+    b = _fr_run(monkeypatch, True, split, x, W, K, one=False, router=router)
+    _near(a, b, f"one launch fmt={fmt} T={T} split={split}")
+    out, ids, wts, _ = a
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x), ids.cpu().numpy(),
+                       wts.cpu().numpy(), E, NS, H, I)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, what=f"one launch T={T} vs oracle")
+    _barrier_clean()
+
+
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("drop_zero", [True, False])
+def test_one_launch_given_ids_maps_two_shared(drop_zero, split, monkeypatch):
+    """Given ids through an id map, experts behind a slot map, two shared
+    experts, an invalid id, an expert listed twice, a zero weight."""
+    fmt, E, NS, H, I, T, K = F.FMT_FP8, 16, 2, 2048, 256, 3, 4
+    d, _ = _layer(fmt, E, NS, H, I, seed=221)
+    order = np.arange(E + NS)[::-1].copy()
+    idx = torch.from_numpy(order)
+    rev = {k: (v[idx].contiguous() if v is not None else None) for k, v in d.items()}
+    W = ExpertWeights.from_dense(fmt, rev["w13"], rev["s13"], rev["w2"], rev["s2"], rev["gs13"],
+                                 rev["gs2"], n_shared=NS, device="cuda")
+    slot_map = torch.from_numpy(np.argsort(order).astype(np.int32)).cuda()
+    ids_np, wts_np = random_routing(T, K, E, seed=222)
+    ids_np[0, 1] = -1
+    ids_np[1, 2] = ids_np[1, 0]
+    wts_np[2, 3] = 0.0
+    ids = torch.from_numpy(ids_np).cuda()
+    wts = torch.from_numpy(wts_np).cuda()
+    id_map = torch.from_numpy(np.roll(np.arange(E), 5).astype(np.int32)).cuda()
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(223)).to(torch.bfloat16).cuda()
+    assert L._layer_ok(fmt, 2, T, E, K, None, H, I, NS)
+    kw = dict(ids=ids, wts=wts, drop_zero=drop_zero, id_map=id_map, slot_map=slot_map)
+    a = _fr_run(monkeypatch, True, split, x, W, K, one=True, **kw)
+    _near(a, _fr_run(monkeypatch, True, split, x, W, K, one=False, **kw),
+          f"given ids drop_zero={drop_zero} split={split}")
+    mapped = np.where((ids_np >= 0) & (ids_np < E), np.roll(np.arange(E), 5)[ids_np % E], -1)
+    ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x.cpu()),
+                       mapped.astype(np.int32), wts_np, E, NS, H, I)
+    check_close(a[0].cpu().numpy(), ref, bf16_out=False, what="one launch given ids vs oracle")
+    _barrier_clean()
+
+
+def test_one_launch_every_pair_invalid(monkeypatch):
+    """No live routed pair: the shared expert alone makes the output (split or
+    as a sorted bucket); with no shared expert either, every row is zero."""
+    fmt, E, NS, H, I, T, K = F.FMT_MXFP4, 16, 1, 512, 256, 2, 4
+    d, W = _layer(fmt, E, NS, H, I, seed=225)
+    ids = torch.full((T, K), -1, dtype=torch.int32, device="cuda")
+    wts = torch.ones((T, K), dtype=torch.float32, device="cuda")
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(226)).to(torch.bfloat16).cuda()
+    assert L._layer_ok(fmt, 2, T, E, K, None, H, I, NS)
+    for split in (True, False):
+        a = _fr_run(monkeypatch, True, split, x, W, K, one=True, ids=ids, wts=wts)
+        _near(a, _fr_run(monkeypatch, True, split, x, W, K, one=False, ids=ids, wts=wts),
+              f"all invalid split={split}")
+        ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x.cpu()),
+                           ids.cpu().numpy(), wts.cpu().numpy(), E, NS, H, I)
+        check_close(a[0].cpu().numpy(), ref, bf16_out=False, what="all invalid vs oracle")
+    _, W0 = _layer(fmt, E, 0, H, I, seed=227)
+    monkeypatch.setenv(L.FUSED_ROUTE_ENV, "1")
+    monkeypatch.setenv(L.ONE_LAUNCH_ENV, "1")
+    monkeypatch.setenv(L.FUSED_DOWN_ENV, "1")
+    for dt in (torch.float32, torch.bfloat16):
+        out = torch.full((T, H), float("nan"), dtype=dt, device="cuda")
+        moe_forward(x, ids, wts, W0, path="decode", out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out.float(), torch.zeros((T, H), device="cuda"))
+    _barrier_clean()
+
+
+def test_one_launch_ds_v3_shape(monkeypatch):
+    """DeepSeek-V3 widths (H = 7168, I = 2048: eight-wave workgroups, the down
+    split eight ways) at T = 1 and 2, experts compacted to those routed."""
+    H, I, E, K = 7168, 2048, 256, 8
+    rng = np.random.default_rng(231)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(2)]).astype(np.int32)
+    wts = (rng.random((2, K)) * 0.3 + 0.05).astype(np.float32)
+    used = np.unique(ids)
+    cids = np.vectorize({int(e): i for i, e in enumerate(used)}.get)(ids).astype(np.int32)
+    U = len(used)
+    d, W = _layer(F.FMT_MXFP4, U, 1, H, I, seed=232)
+    x = torch.randn((2, H), generator=torch.Generator().manual_seed(233)).to(torch.bfloat16).cuda()
+    for T in (1, 2):
+        monkeypatch.setenv(L.ONE_LAUNCH_ENV, "1")
+        assert L._layer_ok(F.FMT_MXFP4, 2, T, U, K, None, H, I, 1)
+        xi = x[:T].contiguous()
+        it = torch.from_numpy(cids[:T].copy()).cuda()
+        wt = torch.from_numpy(wts[:T].copy()).cuda()
+        a = _fr_run(monkeypatch, True, True, xi, W, K, one=True, ids=it, wts=wt)
+        _near(a, _fr_run(monkeypatch, True, True, xi, W, K, one=False, ids=it, wts=wt),
+              f"ds-v3 one launch T={T}")
+        ref = oracle_layer(F.FMT_MXFP4, dense_to_numpy(F.FMT_MXFP4, d),
+                           bf16_tensor_to_bits(xi.cpu()), cids[:T], wts[:T], U, 1, H, I)
+        check_close(a[0].cpu().numpy(), ref, bf16_out=False, what=f"ds-v3 one launch T={T}")
+    _barrier_clean()
+
+
+def test_one_launch_back_to_back_and_graph(monkeypatch):
+    """Many launches in a row on one stream share the barrier words (each
+    leaves them reset), across batch sizes, and inside a HIP graph replayed
+    with eager calls between the replays: every result equals the first."""
+    fmt, E, NS, H, I, K = F.FMT_MXFP4, 256, 1, 2048, 512, 8
+    _, W = _layer(fmt, E, NS, H, I, seed=241)
+    g = torch.Generator(device="cuda").manual_seed(242)
+    monkeypatch.setenv(L.FUSED_ROUTE_ENV, "1")
+    monkeypatch.setenv(L.ONE_LAUNCH_ENV, "1")
+    monkeypatch.setenv(L.FUSED_DOWN_ENV, "1")
+    outs = {}
+    inputs = {}
+    for T in (1, 4, 2):
+        logits = torch.randn((T, E), generator=g, device="cuda")
+        x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+        router = dict(logits=logits, scoring="sigmoid", n_group=8, topk_group=4,
+                      routed_scaling_factor=2.5, renormalize=True)
+        assert L._layer_ok(fmt, 1, T, E, K, router, H, I, NS)
+        inputs[T] = (x, router)
+    def run(T, out=None):
+        x, router = inputs[T]
+        ids = torch.empty((T, K), dtype=torch.int32, device="cuda")
+        wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+        return moe_forward(x, ids, wts, W, path="decode", router=router, out=out,
+                           out_dtype=torch.float32)
+    for T in inputs:
+        outs[T] = run(T).clone()
+    for _ in range(20):
+        for T in (4, 1, 2):
+            assert torch.equal(run(T), outs[T]), f"back-to-back T={T}"
+    torch.cuda.synchronize()
+    _barrier_clean()
+    # graph: the layer at T = 4, replayed three times with eager calls between
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        gout = torch.empty((4, H), dtype=torch.float32, device="cuda")
+        run(4, out=gout)                     # warm the stream's buffers
+        s.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            run(4, out=gout)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(3):
+        gout.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, outs[4]), f"graph replay {i}"
+        assert torch.equal(run(1), outs[1]), f"eager between replays {i}"
+        torch.cuda.synchronize()
+    _barrier_clean()
+    assert L.barrier_timeouts() == 0

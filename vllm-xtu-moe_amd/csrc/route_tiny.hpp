@@ -239,6 +239,7 @@ struct TinySmem {
   int tile_e[kTinyMaxA];      // bucket of tile t
   int tile_r[kTinyMaxA];      // first sorted row of tile t
   int tile_n[kTinyMaxA];      // rows of tile t (at most bm)
+  float sw[kTinyMaxA];        // weight of sorted row j (1 for a shared expert's)
 };
 
 // MODE 0/1: wave w routes tokens w, w + waves, ... (E = 64 * EPL), then the
@@ -297,6 +298,7 @@ __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
       const int tk = lane < TK ? lane / K : (lane - TK) / NS;
       g.sb[pos] = b;
       g.stok[pos] = tk;
+      g.sw[pos] = w;
       if constexpr (STORE) {
         a.sorted_pair[pos] = lane;
         a.inv[lane] = pos;

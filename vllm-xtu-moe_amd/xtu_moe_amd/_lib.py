@@ -48,6 +48,13 @@ SIGNATURES = {
                                       _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                       _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp,
                                       _i, _vp, _vp, _f, _f, _f, _vp]),
+    "xtu_decode_layer_barrier_words": (_i, []),
+    "xtu_decode_layer_ok": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i]),
+    "xtu_decode_layer": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp,
+                              _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _vp, _l, _l, _vp,
+                              _i, _vp, _vp, _f, _f, _f, _vp, _vp, _vp, _l, _l, _vp, _i, _vp,
+                              _vp]),
     "xtu_decode_gate_up_routed": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp,
                                        _vp, _vp, _vp, _vp, _i, _i, _vp, _f, _f, _f, _vp]),
     "xtu_gemm_tile_m": (_i, [_i]),
@@ -128,7 +135,8 @@ _NOT_STATUS = {"xtu_version", "xtu_error_string", "xtu_segment_workspace_bytes",
                "xtu_mx_pair_fits", "xtu_mx_pair_tile_m", "xtu_f8_pair_fits",
                "xtu_f8_pair_tile_m",
                "xtu_decode_down_combine_ok", "xtu_decode_route_shared_ok",
-               "xtu_decode_route_gate_up_ok",
+               "xtu_decode_route_gate_up_ok", "xtu_decode_layer_ok",
+               "xtu_decode_layer_barrier_words",
                "xtu_i8_weight_bytes"}
 
 _LIB = None

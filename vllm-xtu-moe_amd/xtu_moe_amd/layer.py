@@ -735,6 +735,55 @@ def _route_gate_up_ok(fmt, mode, T, E, K, router, H, I, NS, gu_bytes=None) -> bo
                           int(K), n_group, int(NS), int(H), int(I)))
 
 
+ONE_LAUNCH_ENV = "XTU_DECODE_ONE_LAUNCH"
+
+
+def _layer_ok(fmt, mode, T, E, K, router, H, I, NS) -> bool:
+    """Whether a decode layer that takes the one-launch routing + gate/up and
+    the fused down + combine runs whole in one launch (xtu_decode_layer:
+    the down after a barrier across the launch's workgroups, its first
+    experts' weights loaded during the wait).  Measured on MI355X:
+    Qwen3-Next MXFP4 T = 1 24.4 -> 22.4 us per layer.  Where the separate
+    launches would not take the fused down it is not taken either (forced:
+    Qwen3-Next MXFP4 T = 4 37.5 -> 41.1 us against 33.5 without the fused
+    down; NVFP4 T = 1 27.2 against 27.4), and DeepSeek-V3 MXFP4 T = 1 (with
+    the routing forced into the gate/up launch) ran 51.9 us against 48.6.
+    XTU_DECODE_ONE_LAUNCH=0 keeps the down in its own launch."""
+    if os.environ.get(ONE_LAUNCH_ENV, "1") == "0":
+        return False
+    n_group = int(router.get("n_group", 1)) if router is not None else 1
+    return bool(_lib.call("xtu_decode_layer_ok", int(fmt), int(mode), int(T), int(E), int(K),
+                          n_group, int(NS), int(H), int(I)))
+
+
+# Grid-barrier words of the one-launch decode layer per (device, stream):
+# zeroed once, on the stream the layer runs on; every launch leaves its
+# counters zero (the last 64-word line flags a wait that ran out).  Kept for
+# the process's life, as the scratch buffers are.
+_BAR_CACHE: dict = {}
+
+
+def _barrier_words(device, stream=None):
+    st = _stream(stream)
+    key = (str(device), st)
+    t = _BAR_CACHE.get(key)
+    if t is None:
+        n = int(_lib.call("xtu_decode_layer_barrier_words"))
+        if int(torch.cuda.current_stream(device).cuda_stream) == st:
+            t = torch.zeros(n, dtype=torch.int32, device=device)
+        else:
+            with torch.cuda.stream(torch.cuda.ExternalStream(st, device=device)):
+                t = torch.zeros(n, dtype=torch.int32, device=device)
+        _BAR_CACHE[key] = t
+    return t
+
+
+def barrier_timeouts() -> int:
+    """Grid-barrier waits of the one-launch decode layer that ran out (the
+    launch could not be resident): 0 in every healthy process."""
+    return sum(int(t[-64].item()) for t in _BAR_CACHE.values())
+
+
 def _mxpair_bufs(tag, M, K, dev, stream=None):
     """Interleaved activation pairs [M][2K] and their e8m0 bytes [M][K/32]."""
     return (_buf(tag + "_hilo", (max(M, 1), 2 * K), torch.uint8, dev, stream),
@@ -819,6 +868,29 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
     if split:
         act_sh = _buf("act_sh", (NS * T, I), torch.bfloat16, dev, st)
+    # ... and the down with the weighted combine in the same launch, after a
+    # barrier across its workgroups
+    one = (fused and (split or (odt in (torch.bfloat16, torch.float32)
+                                and decode_fused_down_use(fmt, T, seg.A, H, I, max_active,
+                                                          E + NS)))
+           and _layer_ok(fmt, rmode, T, E, K, router, H, I, NS))
+    if one:
+        r = router or {}
+        act = _buf("act", (max(seg.A, 1), I), torch.bfloat16, dev, st)
+        if out is None:
+            out = torch.empty((T, H), dtype=odt, device=dev)
+        _lib.call("xtu_decode_layer", rmode, _p(r.get("logits")), _p(r.get("bias")),
+                  _p(ids), _p(wts), T, E, K, int(r.get("n_group", 1)),
+                  int(r.get("topk_group", 1)), float(r.get("routed_scaling_factor", 1.0)),
+                  int(r.get("renormalize", True)), _p(id_map), NS, int(drop_zero), seg.bm,
+                  _p(seg.sorted_pair), _p(seg.sorted_tok), _p(seg.sorted_wts), _p(seg.inv),
+                  _p(seg.seg_start), _p(seg.active), _p(seg.n_active), _p(seg.tile_expert),
+                  _p(seg.tile_row0), _p(seg.n_tiles), _p(seg.expert_tile_start), fmt, _p(x), H,
+                  I, _p(W.w13), _p(W.s13), _p(W.gs13), 0, 0, _p(slot_map),
+                  min(seg.max_tiles, TINY_MAX_PAIRS), _p(act), _p(act_sh) if split else 0,
+                  lim, al, be, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0, _p(out),
+                  int(out.dtype == torch.bfloat16), _p(_barrier_words(dev, st)), st)
+        return (out, seg) if return_seg else out
     if fused:
         r = router or {}
         act = _buf("act", (max(seg.A, 1), I), torch.bfloat16, dev, st)
