@@ -620,3 +620,44 @@ def test_one_launch_back_to_back_and_graph(monkeypatch):
         torch.cuda.synchronize()
     _barrier_clean()
     assert L.barrier_timeouts() == 0
+
+
+def test_one_launch_layer_random_shapes(monkeypatch):
+    """Seeded shapes across the one-launch layer's envelope (formats, T = 1..16,
+    top-k, zero to two shared experts, hidden and intermediate sizes, split
+    shared experts or not): routing and segmentation bitwise those of the
+    separate launches, the output within their fp32 rounding and within the
+    oracle's tolerance."""
+    rng = np.random.default_rng(301)
+    ran = 0
+    for case in range(40):
+        fmt = int(rng.choice([F.FMT_MXFP4, F.FMT_FP8, F.FMT_BF16, F.FMT_NVFP4]))
+        T = int(rng.integers(1, 17))
+        K = int(rng.integers(1, 9))
+        NS = int(rng.integers(0, 3))
+        if T * (K + NS) > 64:
+            continue
+        E = int(rng.choice([16, 24, 32]))
+        H = int(rng.choice([512, 1024, 2048]))
+        I = int(rng.choice([256, 512, 1024]))
+        split = bool(rng.integers(0, 2)) and NS > 0
+        monkeypatch.setenv(L.ONE_LAUNCH_ENV, "1")
+        if not L._layer_ok(fmt, 2, T, E, K, None, H, I, NS):
+            continue
+        d, W = _layer(fmt, E, NS, H, I, seed=310 + case)
+        ids_np, wts_np = random_routing(T, K, E, seed=320 + case)
+        ids = torch.from_numpy(ids_np).cuda()
+        wts = torch.from_numpy(wts_np).cuda()
+        x = torch.randn((T, H), generator=torch.Generator().manual_seed(330 + case)).to(
+            torch.bfloat16).cuda()
+        what = f"case {case}: fmt={fmt} T={T} K={K} NS={NS} E={E} H={H} I={I} split={split}"
+        a = _fr_run(monkeypatch, True, split, x, W, K, one=True, ids=ids, wts=wts)
+        _near(a, _fr_run(monkeypatch, True, split, x, W, K, one=False, ids=ids, wts=wts), what)
+        ref = oracle_layer(fmt, dense_to_numpy(fmt, d), bf16_tensor_to_bits(x.cpu()), ids_np,
+                           wts_np, E, NS, H, I)
+        check_close(a[0].cpu().numpy(), ref, bf16_out=False, what=what)
+        ran += 1
+        if ran == 12:
+            break
+    assert ran >= 8, f"only {ran} shapes inside the envelope"
+    _barrier_clean()
