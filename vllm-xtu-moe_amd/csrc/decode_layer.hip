@@ -37,15 +37,22 @@ namespace {
 constexpr int kBarWords = 64 * 18;
 constexpr int kBarSpin = 1 << 17;   // polls of about 1 us each before giving up
 
-__device__ __forceinline__ unsigned barrier_arrive(unsigned* bar) {
+// The group's generation before this launch's barrier, read by thread 0 at
+// the start of the launch: it cannot move before every workgroup, this one
+// included, has arrived, so reading it early keeps a memory round trip off
+// the last arrival's path.
+__device__ __forceinline__ unsigned barrier_generation(const unsigned* bar) {
+  return threadIdx.x == 0 ? __hip_atomic_load(bar + 64 * (9 + blockIdx.x % 8), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                          : 0u;
+}
+
+__device__ __forceinline__ void barrier_arrive(unsigned* bar) {
   __builtin_amdgcn_s_waitcnt(0);   // this wave's act stores are complete
   __syncthreads();
-  unsigned gen = 0;
   if (threadIdx.x == 0) {
     const unsigned g = blockIdx.x % 8, ngroups = gridDim.x < 8 ? gridDim.x : 8;
     const unsigned in_g = (gridDim.x - g + 7) / 8;
-    gen = __hip_atomic_load(bar + 64 * (9 + g), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);   // the generation is read before this arrival counts
     if (__hip_atomic_fetch_add(bar + 64 * g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
         in_g - 1) {
       __hip_atomic_store(bar + 64 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -58,7 +65,6 @@ __device__ __forceinline__ unsigned barrier_arrive(unsigned* bar) {
       }
     }
   }
-  return gen;
 }
 
 // Thread 0 polls its group's generation until it moves past gen (bounded: a
@@ -93,6 +99,7 @@ __global__ __launch_bounds__(512) void decode_layer_kernel(tiny::SmallArgs ra, D
   extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
   __shared__ f32x4_t red[8][kWave];
   __shared__ __attribute__((aligned(16))) tiny::TinySmem g;
+  const unsigned gen = barrier_generation(bar);
   route_gate_up_phase<FMT, MODE, EPL, XC, true>(ra, a, act_sh, n_sh, skip,
                                                reinterpret_cast<uint16_t*>(dyn), red, g);
 
@@ -116,12 +123,12 @@ __global__ __launch_bounds__(512) void decode_layer_kernel(tiny::SmallArgs ra, D
     }
   };
   // arrive, then issue the first down panel's weights (their loads would
-  // otherwise hold up the arrival's wait for the act stores), then wait
-  const unsigned gen = barrier_arrive(bar);
+  // otherwise hold up the arrival's wait for the act stores) and build the
+  // tables the routing in LDS gives, then wait
+  barrier_arrive(bar);
   int pg = blockIdx.x;
   if (pg >= npg) return;   // whole workgroup: nothing after the barrier
   issue_first(pg);
-  barrier_wait(bar, gen);
 
   // act rows: the sorted rows before the trash bucket (only the routed ones
   // when the shared experts' rows come from act_sh), then the shared rows
@@ -133,6 +140,31 @@ __global__ __launch_bounds__(512) void decode_layer_kernel(tiny::SmallArgs ra, D
   int* rowof = reinterpret_cast<int*>(dyn + (size_t)(d.row_cap + sh_rows) * ldx * 2);
   float* wof = reinterpret_cast<float*>(rowof + tiny::kTinyMaxA * kDcTok);
   int* eslot = reinterpret_cast<int*>(wof + tiny::kTinyMaxA * kDcTok);
+  // token -> act row and summed weight per active expert, in active order
+  // (the gate/up phase is over in every wave: the arrival's barrier)
+  for (int i = tid; i < nact * kDcTok; i += bd) {
+    rowof[i] = 0;
+    wof[i] = 0.f;
+  }
+  __syncthreads();
+  for (int j = tid; j < nact; j += bd) {
+    const int e = g.act_b[j];
+    eslot[j] = a.slot_map ? a.slot_map[e] : e;
+    if (d.act_sh && e >= e_sh) {
+      for (int t = 0; t < d.T; ++t) {
+        rowof[j * kDcTok + t] = d.row_cap + (e - e_sh) * d.T + t;
+        wof[j * kDcTok + t] = 1.0f;
+      }
+      continue;
+    }
+    for (int r = g.act_r[j]; r < g.act_r[j + 1]; ++r) {
+      const int t = g.stok[r];
+      rowof[j * kDcTok + t] = r;
+      wof[j * kDcTok + t] += g.sw[r];
+    }
+  }
+  barrier_wait(bar, gen);   // ends with a workgroup barrier: the tables are visible
+
   const int pieces = (nrows + sh_rows) * per_row;
   // device-coherent loads: the rows other workgroups wrote before the barrier
   const __amdgpu_buffer_rsrc_t ract = __builtin_amdgcn_make_buffer_rsrc(
@@ -159,28 +191,6 @@ __global__ __launch_bounds__(512) void decode_layer_kernel(tiny::SmallArgs ra, D
         const int lr = r < nrows ? r : d.row_cap + (r - nrows);
         *reinterpret_cast<u32x4_t*>(xs + lr * ldx + c8 * 8) = v[k];
       }
-    }
-  }
-  for (int i = tid; i < nact * kDcTok; i += bd) {
-    rowof[i] = 0;
-    wof[i] = 0.f;
-  }
-  __syncthreads();
-  // token -> act row and summed weight per active expert, in active order
-  for (int j = tid; j < nact; j += bd) {
-    const int e = g.act_b[j];
-    eslot[j] = a.slot_map ? a.slot_map[e] : e;
-    if (d.act_sh && e >= e_sh) {
-      for (int t = 0; t < d.T; ++t) {
-        rowof[j * kDcTok + t] = d.row_cap + (e - e_sh) * d.T + t;
-        wof[j * kDcTok + t] = 1.0f;
-      }
-      continue;
-    }
-    for (int r = g.act_r[j]; r < g.act_r[j + 1]; ++r) {
-      const int t = g.stok[r];
-      rowof[j * kDcTok + t] = r;
-      wof[j * kDcTok + t] += g.sw[r];
     }
   }
   __syncthreads();
