@@ -44,9 +44,10 @@ struct SmallArgs {
 // ---------------------------------------------------------------------------
 // Tiny batches (at most 64 pairs; routing for E = 64 * EPL, EPL = 4 or 8): one
 // wave routes one token with no workgroup barrier.  Lane l holds experts
-// [l*EPL, (l+1)*EPL).  The K choices are taken in K rounds of a wave-wide
-// maximum of order-preserving score keys; equal scores go to the lowest
-// lane, whose local choice is its lowest index, so the order is (score desc,
+// [l*EPL, (l+1)*EPL) and sorts them by (score desc, index asc) once; the K
+// choices are taken in K rounds of a wave-wide maximum of the lanes' first
+// order-preserving score keys; equal scores go to the lowest lane, whose
+// first entry is its lowest index among them, so the order is (score desc,
 // index asc) as in route_token.  Group scores (top two over a group's lanes)
 // and group ranks follow route_token's definitions; the weights use its fp32
 // sequences.  The segmentation of the <= 64 pairs works on the pair buckets
@@ -107,6 +108,36 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// Compare-exchange for a descending order: c[a] gets the larger word.
+__device__ __forceinline__ void cas_desc(uint64_t& a, uint64_t& b) {
+  const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+  a = hi;
+  b = lo;
+}
+
+// Descending sort of EPL words in registers: the optimal networks for 4 and
+// 8 (5 and 19 compare-exchanges), odd-even transposition otherwise.
+template <int EPL>
+__device__ __forceinline__ void sort_desc(uint64_t (&c)[EPL]) {
+  if constexpr (EPL != 4 && EPL != 8) {
+#pragma unroll
+    for (int r = 0; r < EPL; ++r)
+#pragma unroll
+      for (int i = r % 2; i + 1 < EPL; i += 2) cas_desc(c[i], c[i + 1]);
+  } else if constexpr (EPL == 4) {
+    cas_desc(c[0], c[1]); cas_desc(c[2], c[3]);
+    cas_desc(c[0], c[2]); cas_desc(c[1], c[3]);
+    cas_desc(c[1], c[2]);
+  } else {
+    cas_desc(c[0], c[2]); cas_desc(c[1], c[3]); cas_desc(c[4], c[6]); cas_desc(c[5], c[7]);
+    cas_desc(c[0], c[4]); cas_desc(c[1], c[5]); cas_desc(c[2], c[6]); cas_desc(c[3], c[7]);
+    cas_desc(c[0], c[1]); cas_desc(c[2], c[3]); cas_desc(c[4], c[5]); cas_desc(c[6], c[7]);
+    cas_desc(c[2], c[4]); cas_desc(c[3], c[5]);
+    cas_desc(c[1], c[4]); cas_desc(c[3], c[6]);
+    cas_desc(c[1], c[2]); cas_desc(c[3], c[4]); cas_desc(c[5], c[6]);
+  }
+}
+
 template <int MODE, int EPL>
 __device__ void route_token_wave(const float* __restrict__ l, const float* __restrict__ bias,
                                  int K, int n_group, int topk_group, float scale, int renorm,
@@ -164,42 +195,45 @@ __device__ void route_token_wave(const float* __restrict__ l, const float* __res
       for (int j = 0; j < EPL; ++j) key[j] = 0u;
     }
   }
-  // local best (lowest index among equal keys)
-  uint32_t bkey = 0u;
-  int bj = 0;
-  float bws = 0.f;
-  auto local_best = [&]() {
-    bkey = 0u;
-    bj = 0;
-    bws = 0.f;
+  // Each lane sorts its EPL entries by (key desc, index asc) once (a sorting
+  // network over 64-bit (key, EPL - 1 - index) words), so a round takes the
+  // lane's head instead of rescanning: round k takes the wave's largest head
+  // (the lowest lane among equal ones), and the winning lane drops its head.
+  uint64_t c[EPL];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      if (key[j] > bkey) {
-        bkey = key[j];
-        bj = j;
-        bws = ws[j];
-      }
-    }
-  };
-  local_best();
+  for (int j = 0; j < EPL; ++j) c[j] = (uint64_t)key[j] << 32 | (uint32_t)(EPL - 1 - j);
+  sort_desc<EPL>(c);
+  uint32_t hk[EPL];   // keys in order
+  uint32_t jpk = 0u;  // index of entry i at bits [4i, 4i + 4)
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    hk[i] = (uint32_t)(c[i] >> 32);
+    jpk |= (uint32_t)(EPL - 1 - (int)(uint32_t)c[i]) << (4 * i);
+  }
   int my_e = 0;
-  float my_ws = 0.f;
   for (int k = 0; k < K; ++k) {
-    const uint32_t gmax = wave_max_u32(bkey);
-    const unsigned long long m = __ballot(bkey == gmax);
+    const uint32_t gmax = wave_max_u32(hk[0]);
+    const unsigned long long m = __ballot(hk[0] == gmax);
     const int wl = __builtin_ctzll(m);
-    const int ek = wl * EPL + __builtin_amdgcn_readlane(bj, wl);
-    const float wk = readlane_f(bws, wl);
-    if (lane == k) {
-      my_e = ek;
-      my_ws = wk;
-    }
+    const int ek = wl * EPL + (__builtin_amdgcn_readlane((int)jpk, wl) & 15);
+    if (lane == k) my_e = ek;
     if (lane == wl) {
 #pragma unroll
-      for (int j = 0; j < EPL; ++j)
-        if (j == bj) key[j] = 0u;
-      local_best();
+      for (int i = 0; i + 1 < EPL; ++i) hk[i] = hk[i + 1];
+      hk[EPL - 1] = 0u;
+      jpk >>= 4;
     }
+  }
+  // the chosen expert's unbiased score, from the lane that holds it
+  float my_ws = 0.f;
+  {
+    const int src = my_e / EPL, js = my_e % EPL;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const float v = __shfl(ws[j], src, kWave);
+      if (j == js) my_ws = v;
+    }
+    if (lane >= K) my_ws = 0.f;
   }
   float w = 0.f;
   if (MODE == 0) {
