@@ -259,6 +259,19 @@ __device__ void route_token_wave(const float* __restrict__ l, const float* __res
   }
 }
 
+// Entries of v[0, 4 NQ) below x (the words past the live ones hold INT_MAX,
+// so only the first 4 NQ are read when the live ones are fewer).
+template <int NQ>
+__device__ __forceinline__ int count_below(const int* v, int x) {
+  int n = 0;
+#pragma unroll
+  for (int q = 0; q < 4 * NQ; q += 4) {
+    const i32x4_t u = *reinterpret_cast<const i32x4_t*>(v + q);
+    n += (u[0] < x) + (u[1] < x) + (u[2] < x) + (u[3] < x);
+  }
+  return n;
+}
+
 struct TinySmem {
   int ids[kTinyMaxA];
   float w[kTinyMaxA];
@@ -306,6 +319,11 @@ __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
   }
   __syncthreads();
   if (wv == 0) {
+    // token of pair `lane` (routed pairs t*K + k, then shared ones
+    // TK + t*NS + s), counted over the batch's tokens instead of divided
+    const int pr = lane < TK ? lane : lane - TK, per = lane < TK ? K : NS;
+    int tk = 0;
+    for (int t = 1; t < T; ++t) tk += pr >= t * per ? 1 : 0;
     // bucket of pair `lane`
     int b = BIG;
     float w = 1.0f;
@@ -316,20 +334,15 @@ __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
       b = (e < 0 || e >= E) ? trash : e;
       if (a.drop_zero && w == 0.0f) b = trash;
     } else if (lane < A) {
-      b = E + (lane - TK) % NS;
+      b = E + (pr - tk * per);
     }
     // stable position: rank of the unique key (bucket, pair) among the pairs
     const int key = lane < A ? b * kTinyMaxA + lane : BIG;
     g.bk[lane] = key;
     lds_wave_order();
-    int pos = 0;
-#pragma unroll
-    for (int q = 0; q < kTinyMaxA; q += 4) {
-      const i32x4_t v = *reinterpret_cast<const i32x4_t*>(g.bk + q);
-      pos += (v[0] < key) + (v[1] < key) + (v[2] < key) + (v[3] < key);
-    }
+    const int pos = A <= 16 ? count_below<4>(g.bk, key)
+                            : A <= 32 ? count_below<8>(g.bk, key) : count_below<16>(g.bk, key);
     if (lane < A) {
-      const int tk = lane < TK ? lane / K : (lane - TK) / NS;
       g.sb[pos] = b;
       g.stok[pos] = tk;
       g.sw[pos] = w;
@@ -356,7 +369,7 @@ __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
     const int ai = __builtin_amdgcn_mbcnt_hi((uint32_t)(fm >> 32),
                                              __builtin_amdgcn_mbcnt_lo((uint32_t)fm, 0u));
     const int na = __popcll(fm);
-    const int nt = first ? (cnt + a.bm - 1) / a.bm : 0;
+    const int nt = !first ? 0 : A <= a.bm ? 1 : (cnt + a.bm - 1) / a.bm;
     const int incl = wave_incl_scan(nt);
     const int t0 = incl - nt;
     if (first) {
@@ -394,13 +407,10 @@ __device__ void route_segment_block(const SmallArgs& a, TinySmem& g) {
   __syncthreads();
   if constexpr (!STORE) return;
   // per-bucket starts: i = active buckets below e; rows and tiles before e
+  const int na = g.n_act;
   for (int e = tid; e <= NB; e += blockDim.x) {
-    int i = 0;
-#pragma unroll
-    for (int q = 0; q < kTinyMaxA; q += 4) {
-      const i32x4_t v = *reinterpret_cast<const i32x4_t*>(g.act_b + q);
-      i += (v[0] < e) + (v[1] < e) + (v[2] < e) + (v[3] < e);
-    }
+    const int i = na <= 16 ? count_below<4>(g.act_b, e)
+                           : na <= 32 ? count_below<8>(g.act_b, e) : count_below<16>(g.act_b, e);
     a.seg_start[e] = e == NB ? A : g.act_r[i];
     a.expert_tile_start[e] = g.act_t[i];
   }
