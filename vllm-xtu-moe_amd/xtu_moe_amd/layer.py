@@ -743,7 +743,10 @@ def _layer_ok(fmt, mode, T, E, K, router, H, I, NS) -> bool:
     the fused down + combine runs whole in one launch (xtu_decode_layer:
     the down after a barrier across the launch's workgroups, its first
     experts' weights loaded during the wait).  Measured on MI355X:
-    Qwen3-Next MXFP4 T = 1 24.4 -> 22.4 us per layer.  Where the separate
+    Qwen3-Next MXFP4 T = 1 24.4 -> 22.4 us per layer (20.2 us with the
+    sorted-list wave router and the barrier generation read at launch
+    start; the same changes give the two-launch path's NVFP4 T = 1 26.2
+    us).  Where the separate
     launches would not take the fused down it is not taken either (forced:
     Qwen3-Next MXFP4 T = 4 37.5 -> 41.1 us against 33.5 without the fused
     down; NVFP4 T = 1 27.2 against 27.4), and DeepSeek-V3 MXFP4 T = 1 (with
