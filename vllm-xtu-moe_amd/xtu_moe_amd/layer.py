@@ -635,6 +635,7 @@ FUSED_DOWN_ENV = "XTU_DECODE_FUSED_DOWN"
 
 
 FUSED_DOWN_MAX_EXPERTS = 24
+NVFP4_NARROW_FUSED_MAX = 12   # NVFP4 at I < 1024: the fused down only at T = 1 scale
 
 
 def decode_fused_down_ok(fmt: int, T: int, A: int, H: int, I: int, max_active: int,
@@ -647,20 +648,24 @@ def decode_fused_down_ok(fmt: int, T: int, A: int, H: int, I: int, max_active: i
 
 
 def decode_fused_down_use(fmt: int, T: int, A: int, H: int, I: int, max_active: int,
-                          trash: int, shared_rows: int = 0) -> bool:
+                          trash: int, shared_rows: int = 0, one_launch: bool = False) -> bool:
     """Whether the decode path takes the fused down + combine.  Each of its
     waves walks every active expert, so it pays where few experts meet wide
     panels; measured (MI355X): faster for DeepSeek-V3 MXFP4 at T = 1, 2 (9 / 17
-    experts) and Qwen3-Next MXFP4 at T = 1 (11), slower with 40 experts and
-    for NVFP4 at I = 512.  XTU_DECODE_FUSED_DOWN=1 takes it whenever it fits,
-    =0 never."""
+    experts) and Qwen3-Next MXFP4 at T = 1 (11), slower with 40 experts.
+    NVFP4 at I = 512 takes it only inside the one-launch layer (one_launch:
+    the whole layer runs in xtu_decode_layer) at T = 1 scale (at most 12
+    experts): Qwen3-Next NVFP4 T = 1 25.3 against 26.0 us (two launches with
+    the separate down and combine); as a launch of its own it was slower.
+    XTU_DECODE_FUSED_DOWN=1 takes it whenever it fits, =0 never."""
     mode = os.environ.get(FUSED_DOWN_ENV, "auto")
     if mode == "0":
         return False
     if mode != "1":
         if max_active > FUSED_DOWN_MAX_EXPERTS:
             return False
-        if int(fmt) == FMT_NVFP4 and I < 1024:
+        if int(fmt) == FMT_NVFP4 and I < 1024 and (not one_launch
+                                                   or max_active > NVFP4_NARROW_FUSED_MAX):
             return False
     return decode_fused_down_ok(fmt, T, A, H, I, max_active, trash, shared_rows)
 
@@ -864,19 +869,20 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
     fused = (path == "decode" and T > 0 and seg.small
              and _route_gate_up_ok(fmt, rmode, T, E, K, router, H, I, NS,
                                    gu_bytes=min(seg.max_tiles, TINY_MAX_PAIRS) * _w13_bytes(W)))
+    layer_ok = fused and _layer_ok(fmt, rmode, T, E, K, router, H, I, NS)
     split = (path == "decode" and T > 0 and NS > 0 and seg.small
              and odt in (torch.bfloat16, torch.float32)
-             and decode_fused_down_use(fmt, T, seg.A, H, I, max_active, E + NS, NS * T)
+             and decode_fused_down_use(fmt, T, seg.A, H, I, max_active, E + NS, NS * T,
+                                       one_launch=layer_ok)
              and (fused or _route_shared_ok(fmt, rmode, T, E, K, router, H, I, NS)))
     lim, al, be = float(swiglu_limit or 0.0), float(swiglu_alpha), float(swiglu_beta)
     if split:
         act_sh = _buf("act_sh", (NS * T, I), torch.bfloat16, dev, st)
     # ... and the down with the weighted combine in the same launch, after a
     # barrier across its workgroups
-    one = (fused and (split or (odt in (torch.bfloat16, torch.float32)
-                                and decode_fused_down_use(fmt, T, seg.A, H, I, max_active,
-                                                          E + NS)))
-           and _layer_ok(fmt, rmode, T, E, K, router, H, I, NS))
+    one = layer_ok and (split or (odt in (torch.bfloat16, torch.float32)
+                                  and decode_fused_down_use(fmt, T, seg.A, H, I, max_active,
+                                                            E + NS, one_launch=True)))
     if one:
         r = router or {}
         act = _buf("act", (max(seg.A, 1), I), torch.bfloat16, dev, st)
