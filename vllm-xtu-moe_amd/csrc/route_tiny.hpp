@@ -108,7 +108,7 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-// Compare-exchange for a descending order: c[a] gets the larger word.
+// Compare-exchange for a descending order: a gets the larger word.
 __device__ __forceinline__ void cas_desc(uint64_t& a, uint64_t& b) {
   const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
   a = hi;
