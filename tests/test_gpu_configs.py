@@ -176,6 +176,25 @@ def test_qwen3_next_mxfp4_decode(qwen_mxfp4, T):
 
 
 @pytest.mark.parametrize("T", [1, 4])
+def test_qwen3_next_nvfp4_decode_routed(T):
+    """NVFP4 decode routed from logits, as the layer serves it (at T = 1 the
+    whole layer in one launch, the fused down included), against the oracle
+    and the router's ids and weights."""
+    W = synth_layer(F.FMT_NVFP4, QE, QNS, QH, QI, seed=21, device=DEV)
+    x, logits, ids, wts = _qwen_batch(T, seed=22 + T)
+    ids_o = torch.empty((T, QK), dtype=torch.int32, device=DEV)
+    wts_o = torch.empty((T, QK), dtype=torch.float32, device=DEV)
+    out = moe_forward(x, ids_o, wts_o, W, swiglu_limit=QLIM, out_dtype=torch.bfloat16,
+                      router=dict(logits=logits, scoring="softmax"))
+    torch.cuda.synchronize()
+    assert torch.equal(ids_o, ids) and torch.equal(wts_o, wts)
+    ref = _sampled_oracle(F.FMT_NVFP4, W, x, ids, wts, list(range(T)), limit=QLIM)
+    check_close(out.float().cpu().numpy(), ref, bf16_out=True, what=f"qwen3-next nvfp4 routed T={T}")
+    del W
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("T", [1, 4])
 def test_qwen3_next_int8_forced_at_decode_sizes(qwen_mxfp4, T, monkeypatch):
     """XIAOTU_MOE_INT8_ALIGN=1 takes the INT8 ALIGN path below the 160-token
     gate as well (the reference engine's override): T = 1 and 4 on the
