@@ -210,16 +210,22 @@ def test_lane_softmax_with_many_shared_buckets(NS):
 
 
 @pytest.mark.parametrize("case", ["grouped_ties_bias", "softmax_ties", "given_ids_idmap",
-                                  "grouped_bm4"])
+                                  "grouped_bm4", "grouped_e512_ties", "softmax_e256_ties"])
 def test_tiny_route_segment_edge_cases(case):
     """The one-wave-per-token path (<= 64 pairs): exact ties, bias, id_map,
-    given ids with invalid / zero-weight pairs, several tiles per bucket."""
+    given ids with invalid / zero-weight pairs, several tiles per bucket; both
+    routers at both lane widths (4 and 8 experts per lane, so each lane's
+    sorted list of tied scores is exercised at either size)."""
     dev = torch.device("cuda")
     rng = np.random.default_rng(len(case))
     T, E, K, NS, bm = 4, 256, 8, 1, 128
     id_map = None
     if case == "softmax_ties":
         E, K = 512, 10
+    if case == "grouped_e512_ties":
+        E, K = 512, 8
+    if case == "softmax_e256_ties":
+        E, K = 256, 6
     if case == "grouped_bm4":
         bm = 4
     # few distinct values: many exact ties in scores and group scores
@@ -240,7 +246,7 @@ def test_tiny_route_segment_edge_cases(case):
         ids = torch.empty((T, K), dtype=torch.int32, device=dev)
         wts = torch.empty((T, K), dtype=torch.float32, device=dev)
         lg = torch.from_numpy(logits).to(dev)
-        if case == "softmax_ties":
+        if case in ("softmax_ties", "softmax_e256_ties"):
             seg.run_small(0, ids, wts, logits=lg)
             ids_np, wts_np = oracle.route_softmax_topk(logits, K)
         else:
