@@ -148,6 +148,18 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
                            const int32_t* active, const int32_t* tile_row0,
                            const int32_t* n_active, int max_active, float* y,
                            hipStream_t stream);
+/* xtu_decode_down with y row sorted_pair[position] (the flat pair index:
+ * t*K + k, shared T*K + t*n_shared + s) instead of the sorted position, for
+ * xtu_combine_by_pair.  Same replaced code as xtu_decode_down
+ * (moe4_smallm.cu:395-430).  y holds T*(K + n_shared) rows; rows of pairs in
+ * the trash bucket are not written. */
+hipError_t xtu_decode_down_by_pair(int fmt, const void* act, int T, int H, int I, const void* w2,
+                                   const void* s2, const float* gs2, long w_estride,
+                                   long s_estride, const int32_t* slot_map,
+                                   const int32_t* seg_start, const int32_t* active,
+                                   const int32_t* tile_row0, const int32_t* n_active,
+                                   int max_active, const int32_t* sorted_pair, float* y,
+                                   hipStream_t stream);
 
 /* Routing + segmentation and the shared experts' gate/up in one launch
  * (tiny batches, n_shared >= 1): workgroup 0 does exactly what
@@ -308,6 +320,13 @@ hipError_t xtu_gemm_down(int fmt, const void* act, int H, int I, const void* w2,
 hipError_t xtu_combine(const float* y, const int32_t* inv, const float* topk_weights,
                        const int32_t* trash_start, int T, int K, int n_shared, int H, void* out,
                        int out_bf16, hipStream_t stream);
+/* xtu_combine over y rows in flat pair order (as xtu_decode_down_by_pair
+ * writes them): the same sum, skip rule and order, the row addresses taken
+ * from the pair index instead of inv (inv still decides the skip).  K in
+ * {1, 2, 4, 6, 8, 10}, n_shared <= 2; other shapes are rejected. */
+hipError_t xtu_combine_by_pair(const float* y, const int32_t* inv, const float* topk_weights,
+                               const int32_t* trash_start, int T, int K, int n_shared, int H,
+                               void* out, int out_bf16, hipStream_t stream);
 
 /* ------------------------------------------------- exact FP8 prefill GEMMs
  * FP8-weight grouped GEMMs on the scaled fp8 MFMA (16x16x128 e4m3 x e4m3),

@@ -261,6 +261,26 @@ hipError_t xtu_decode_down(int fmt, const void* act, int T, int H, int I, const 
   return dispatch_decode(fmt, 1, a, max_active, stream);
 }
 
+hipError_t xtu_decode_down_by_pair(int fmt, const void* act, int T, int H, int I, const void* w2,
+                                   const void* s2, const float* gs2, long w_estride,
+                                   long s_estride, const int32_t* slot_map,
+                                   const int32_t* seg_start, const int32_t* active,
+                                   const int32_t* tile_row0, const int32_t* n_active,
+                                   int max_active, const int32_t* sorted_pair, float* y,
+                                   hipStream_t stream) {
+  XTU_CHECK_ARG(shape_ok(fmt, H, I) && max_active >= 0 && max_active <= 65535 && T >= 0 &&
+                T <= kMaxTok);
+  XTU_CHECK_ARG(w_estride >= 0 && s_estride >= 0);
+  XTU_CHECK_ARG(act && w2 && (fmt == kBF16 || s2) && seg_start && active && n_active && y &&
+                sorted_pair);
+  if (max_active == 0 || T == 0) return hipSuccess;
+  (void)hipGetLastError();
+  DecodeArgs a{(const uint16_t*)act, (const uint8_t*)w2, (const uint8_t*)s2, gs2, nullptr,
+               seg_start, active, n_active, slot_map, y, tile_row0, T, H, I, w_estride,
+               s_estride, 0.f, 1.f, 0.f, 0, 1, 1, 0, sorted_pair};
+  return dispatch_decode(fmt, 1, a, max_active, stream);
+}
+
 int xtu_decode_route_shared_ok(int fmt, int mode, int T, int E, int K, int n_group,
                                int n_shared, int H, int I) {
   int ksplit = 0, xc = 0;

@@ -50,6 +50,8 @@ struct DecodeArgs {
   int rows;                  // rows the LDS stage holds
   int ksplit, ppb;           // waves per panel K range; panels per workgroup (down)
   int skip;                  // gate/up fast path: trailing active slots left out
+  const int32_t* pair_of;    // down: null = y row per sorted position; else y row
+                             // pair_of[position] (the flat pair index)
 };
 
 // Units issued per round: about 80 VGPRs of weights in flight per wave, and
@@ -606,6 +608,11 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
     const int cc = min((int)threadIdx.x + j * (int)blockDim.x, nchunks - 1);
     xv[j] = *reinterpret_cast<const u32x4_t*>(xsrc + cc * 8);
   }
+  // y row of each of the tile's rows, loaded with the rows (before the
+  // weights, so waiting for it does not wait for them)
+  __shared__ int yrow[kMaxTok];
+  int yr = c.r0 + (int)threadIdx.x;
+  if (a.pair_of && (int)threadIdx.x < c.na) yr = a.pair_of[c.r0 + threadIdx.x];
   const int panel = c.sub * ppb + pp;
   const Stream<FMT> st = make_stream<FMT>(a, c.ws, panel, a.I);
   Round<FMT, NU> r;
@@ -613,6 +620,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
   issue_round<FMT, NU>(r, st, u0, u1, lane);
   __builtin_amdgcn_sched_barrier(0);
   finish_stage(xs, xv, nchunks, [&](int cc) { return xsrc + cc * 8; });
+  if (threadIdx.x < kMaxTok) yrow[threadIdx.x] = yr;
   __syncthreads();
 
   const uint16_t* xa = xs + (m < nr ? m : 0) * a.I + q * F::kCK;
@@ -634,7 +642,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int mm = 4 * q + i;
-      if (mm < c.na) y[(long)(c.r0 + mm) * a.H + 16 * panel + m] = acc[i] * gsv;
+      if (mm < c.na) y[(long)yrow[mm] * a.H + 16 * panel + m] = acc[i] * gsv;
     }
     return;
   }
@@ -646,7 +654,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
       const int l = (mm / 4) * 16 + n, i = mm % 4;
       float v = 0.f;
       for (int k = 0; k < ksplit; ++k) v += red[pq * ksplit + k][l][i];
-      y[(long)(c.r0 + mm) * a.H + 16 * (c.sub * ppb + pq) + n] = v * gsv;
+      y[(long)yrow[mm] * a.H + 16 * (c.sub * ppb + pq) + n] = v * gsv;
     }
   }
 }

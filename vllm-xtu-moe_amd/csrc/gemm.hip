@@ -439,6 +439,67 @@ bool launch_combine_kn(dim3 grid, hipStream_t stream, const float* y, const int3
   return true;
 }
 
+// combine_kernel over y rows in flat pair order (pair t*K + k at row t*K + k,
+// shared pair (t, s) at row T*K + t*NS + s): the row addresses do not depend
+// on inv, so every load of a token is issued at once (one memory latency).
+// The skip test, the order and the arithmetic are combine_kernel's; the rows
+// of skipped pairs are never written and never added (a select, not a
+// multiply by zero).
+template <int KC, int NSC>
+__global__ __launch_bounds__(256) void combine_pairs_kernel(const float* __restrict__ y,
+                                                            const int32_t* __restrict__ inv,
+                                                            const float* __restrict__ wts,
+                                                            const int32_t* __restrict__ trash_start,
+                                                            int T, int H, void* out,
+                                                            int out_bf16) {
+  const int t = blockIdx.y;
+  const int h = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (h >= H) return;
+  const int trash = trash_start[0];
+  int pos[KC];
+  float w[KC];
+  f32x4_t v[KC + NSC];
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    pos[j] = inv[t * KC + j];
+    w[j] = wts[t * KC + j];
+    v[j] = __builtin_nontemporal_load(
+        reinterpret_cast<const f32x4_t*>(y + (long)(t * KC + j) * H + h));
+  }
+#pragma unroll
+  for (int s = 0; s < NSC; ++s)
+    v[KC + s] = __builtin_nontemporal_load(
+        reinterpret_cast<const f32x4_t*>(y + (long)(T * KC + t * NSC + s) * H + h));
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    const bool ok = pos[j] < trash && w[j] != 0.f;
+    acc = ok ? acc + w[j] * v[j] : acc;
+  }
+#pragma unroll
+  for (int s = 0; s < NSC; ++s) acc += v[KC + s];
+  if (out_bf16) {
+    uint16_t* o = reinterpret_cast<uint16_t*>(out) + (long)t * H + h;
+    const uint32_t lo = f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+    const uint32_t hi = f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+    *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
+  } else {
+    *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(out) + (long)t * H + h) = acc;
+  }
+}
+
+template <int KC>
+bool launch_combine_pairs_k(dim3 grid, hipStream_t stream, const float* y, const int32_t* inv,
+                            const float* w, const int32_t* trash, int T, int NS, int H, void* out,
+                            int out_bf16) {
+  switch (NS) {
+    case 0: combine_pairs_kernel<KC, 0><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, H, out, out_bf16); return true;
+    case 1: combine_pairs_kernel<KC, 1><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, H, out, out_bf16); return true;
+    case 2: combine_pairs_kernel<KC, 2><<<grid, 256, 0, stream>>>(y, inv, w, trash, T, H, out, out_bf16); return true;
+  }
+  return false;
+}
+
 template <int KC>
 bool launch_combine_k(dim3 grid, hipStream_t stream, const float* y, const int32_t* inv,
                       const float* w, const int32_t* trash, int T, int NS, int H, void* out,
@@ -612,6 +673,26 @@ hipError_t xtu_combine(const float* y, const int32_t* inv, const float* topk_wei
                             out, out_bf16))
     combine_kernel<0, 0><<<grid, 256, 0, stream>>>(y, inv, topk_weights, trash_start, T, K,
                                                    n_shared, H, out, out_bf16);
+  return hipPeekAtLastError();
+}
+
+hipError_t xtu_combine_by_pair(const float* y, const int32_t* inv, const float* topk_weights,
+                               const int32_t* trash_start, int T, int K, int n_shared, int H,
+                               void* out, int out_bf16, hipStream_t stream) {
+  XTU_CHECK_ARG(T >= 0 && T <= 65535 && H > 0 && H % 4 == 0 && n_shared >= 0 && n_shared <= 2 &&
+                (K == 1 || K == 2 || K == 4 || K == 6 || K == 8 || K == 10));
+  XTU_CHECK_ARG(T == 0 || (y && inv && out && trash_start && topk_weights));
+  if (T == 0) return hipSuccess;
+  (void)hipGetLastError();
+  const dim3 grid((H / 4 + 255) / 256, T);
+  switch (K) {
+    case 1: launch_combine_pairs_k<1>(grid, stream, y, inv, topk_weights, trash_start, T, n_shared, H, out, out_bf16); break;
+    case 2: launch_combine_pairs_k<2>(grid, stream, y, inv, topk_weights, trash_start, T, n_shared, H, out, out_bf16); break;
+    case 4: launch_combine_pairs_k<4>(grid, stream, y, inv, topk_weights, trash_start, T, n_shared, H, out, out_bf16); break;
+    case 6: launch_combine_pairs_k<6>(grid, stream, y, inv, topk_weights, trash_start, T, n_shared, H, out, out_bf16); break;
+    case 8: launch_combine_pairs_k<8>(grid, stream, y, inv, topk_weights, trash_start, T, n_shared, H, out, out_bf16); break;
+    default: launch_combine_pairs_k<10>(grid, stream, y, inv, topk_weights, trash_start, T, n_shared, H, out, out_bf16); break;
+  }
   return hipPeekAtLastError();
 }
 

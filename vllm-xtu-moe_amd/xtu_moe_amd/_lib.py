@@ -35,6 +35,9 @@ SIGNATURES = {
                                 _vp, _vp, _i, _vp, _f, _f, _f, _vp]),
     "xtu_decode_down": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp, _vp,
                              _vp, _i, _vp, _vp]),
+    "xtu_decode_down_by_pair": (_i, [_i, _vp, _i, _i, _i, _vp, _vp, _vp, _l, _l, _vp, _vp, _vp,
+                                     _vp, _vp, _i, _vp, _vp, _vp]),
+    "xtu_combine_by_pair": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
     "xtu_decode_down_combine_ok": (_i, [_i, _i, _i, _i, _i, _i, _i, _i]),
     "xtu_decode_down_combine": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _l, _l,
                                      _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp]),

@@ -671,6 +671,12 @@ def decode_fused_down_use(fmt: int, T: int, A: int, H: int, I: int, max_active: 
 
 
 SHARED_SPLIT_ENV = "XTU_DECODE_SHARED_SPLIT"
+# "0": the separate decode down writes y per sorted position and the combine
+# reads it through inv; otherwise y is written in flat pair order
+# (xtu_decode_down_by_pair) for the routers' top-k below, with up to two
+# shared experts, and the combine issues all its loads at once.
+DOWN_BY_PAIR_ENV = "XTU_DECODE_DOWN_BY_PAIR"
+COMBINE_BY_PAIR_K = (1, 2, 4, 6, 8, 10)
 
 
 def _route_shared_ok(fmt, mode, T, E, K, router, H, I, NS) -> bool:
@@ -980,6 +986,17 @@ def moe_forward(x, topk_ids, topk_weights, W: ExpertWeights, *, swiglu_limit=0.0
                       _p(out), int(out.dtype == torch.bfloat16), st)
             return (out, seg) if return_seg else out
         y = _buf("y", (max(A, 1), H), torch.float32, dev, st)
+        if (os.environ.get(DOWN_BY_PAIR_ENV, "1") != "0" and K in COMBINE_BY_PAIR_K
+                and NS <= 2 and out.dtype in (torch.bfloat16, torch.float32)):
+            # y rows in flat pair order: the combine's loads need no inv first
+            _lib.call("xtu_decode_down_by_pair", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2),
+                      _p(W.gs2), 0, 0, _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert),
+                      _p(seg.tile_row0), _p(seg.n_tiles), max_dt, _p(seg.sorted_pair), _p(y),
+                      st)
+            _lib.call("xtu_combine_by_pair", _p(y), _p(seg.inv), _p(wts),
+                      _p(seg.seg_start) + 4 * (seg.E + seg.NS), T, K, NS, H, _p(out),
+                      int(out.dtype == torch.bfloat16), st)
+            return (out, seg) if return_seg else out
         _lib.call("xtu_decode_down", fmt, _p(act), T, H, I, _p(W.w2), _p(W.s2), _p(W.gs2), 0, 0,
                   _p(slot_map), _p(seg.seg_start), _p(seg.tile_expert), _p(seg.tile_row0),
                   _p(seg.n_tiles), max_dt, _p(y), st)
